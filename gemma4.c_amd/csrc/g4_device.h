@@ -1,0 +1,100 @@
+// g4_device.h -- device-side formats and helpers shared by the gfx950 kernels.
+//
+// HBM layouts (all tensors are "planar": the bytes of every GGUF super-block
+// are kept, only their placement changes, so the download transform gives
+// back the GGUF bytes exactly):
+//
+//   Q4_K [d rows x nb blocks], 144 B/block (gemma4-4b/cpu-blas/main.c:95-100)
+//     qs plane  : d*nb*128 B.  Block word 4l+j holds GGUF qs word 8j+l, so the
+//                 8 lanes of a block read 16 contiguous bytes each and lane l
+//                 owns bytes 4l..4l+3 of every 32-byte chunk -- the lane
+//                 partition of the reference's AVX2 dot (main.c:500-523).
+//     hdr plane : d*nb*16 B, GGUF bytes 0..15 (d, dmin, scales[12]) verbatim.
+//   Q5_K [.. 176 B/block] (main.c:102-108): qs plane as Q4_K, qh plane
+//                 d*nb*32 B verbatim, hdr plane d*nb*16 B.
+//   Q6_K [.. 210 B/block] (main.c:110-115):
+//     ql plane  : d*nb*128 B; lane L=4h+u of a block owns 16 contiguous bytes
+//                 = GGUF ql[64h+8u .. +7] followed by ql[64h+32+8u .. +7].
+//     qh plane  : d*nb*64 B verbatim (lane L reads bytes 8L..8L+7).
+//     sc plane  : d*nb*16 B verbatim (int8 scales).
+//     d plane   : d*nb*2 B verbatim (fp16 d).
+//   Q8_K activations, nb blocks (main.c:118-122, private layout):
+//     qs plane  : nb*256 B; block word 8l + 4h + j holds GGUF-order word
+//                 16j + 8h + l (lane l's 32 bytes are contiguous).
+//     bsums     : nb*16 int16, then d: nb fp32.   Total nb*292 B.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define G4_QK 256
+
+namespace g4 {
+
+// ---- plane offsets ---------------------------------------------------------
+struct Q4KPlanes { size_t qs, hdr; };
+struct Q5KPlanes { size_t qs, qh, hdr; };
+struct Q6KPlanes { size_t ql, qh, sc, d; };
+
+__host__ __device__ inline Q4KPlanes q4k_planes(size_t nblocks) { return {0, nblocks * 128}; }
+__host__ __device__ inline Q5KPlanes q5k_planes(size_t nblocks) { return {0, nblocks * 128, nblocks * 160}; }
+__host__ __device__ inline Q6KPlanes q6k_planes(size_t nblocks) {
+    return {0, nblocks * 128, nblocks * 192, nblocks * 208};
+}
+__host__ __device__ inline size_t q8k_bsums_off(int nb) { return (size_t)nb * 256; }
+__host__ __device__ inline size_t q8k_d_off(int nb) { return (size_t)nb * 288; }
+
+// Q8_K qs permutation: GGUF word w = 16j + 8h + l  ->  device word 8l + 4h + j
+__host__ __device__ inline int q8k_word_dev(int w) {
+    const int j = w >> 4, h = (w >> 3) & 1, l = w & 7;
+    return 8 * l + 4 * h + j;
+}
+// Q4_K qs permutation: GGUF word 8j + l -> device word 4l + j
+__host__ __device__ inline int q4k_word_dev(int w) { return 4 * (w & 7) + (w >> 3); }
+
+// ---- exact fp16 -> fp32 (main.c:128-149) -----------------------------------
+// Integer decode so the result never depends on the hardware denorm mode:
+// a binary16 subnormal is man * 2^-24, exact in binary32.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 31u, man = h & 1023u;
+    if (e == 0) {
+        const float v = (float)man * 5.9604644775390625e-8f;   // 2^-24
+        return __uint_as_float(__float_as_uint(v) | sign);
+    }
+    const uint32_t bits = (e == 31) ? (sign | 0x7F800000u | (man << 13))
+                                    : (sign | ((e + 112u) << 23) | (man << 13));
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// 6-bit scale/min unpack in word form (main.c:490-495); sc[0..7], mn[0..7] as bytes
+__device__ __forceinline__ void unpack_scales(const uint32_t s0, const uint32_t s1, const uint32_t s2,
+                                              uint32_t& sc_lo, uint32_t& sc_hi, uint32_t& mn_lo, uint32_t& mn_hi) {
+    sc_lo = s0 & 0x3f3f3f3fu;
+    sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+    mn_lo = s1 & 0x3f3f3f3fu;
+    mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+}
+__device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xff; }
+
+// ---- cross-lane helpers (64-wide wavefronts) --------------------------------
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// GELU, tanh form, evaluated in the reference's operation order (main.c:1490-1492)
+__device__ __forceinline__ float gelu_ref(float x) {
+    const float inner = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+}  // namespace g4

@@ -1,0 +1,252 @@
+"""GPU parity: Q8_K quantization, HBM layout, K-quant / BF16 GEMVs against the
+CPU oracle (which is pinned bit-exact to the reference's own functions).
+
+Bars: Q8_K bytes, per-block int32 sums, and the Q4_K/Q5_K fp32 outputs are
+bit-exact; fp32-activation GEMVs are within 1e-5 of the result, normalised by
+sum |w * x| (the reference sums sequentially, the GPU in a tree).
+"""
+import numpy as np
+import pytest
+
+import kquant_np as kq
+import synth
+from oracle import Q8K_DTYPE
+
+pytestmark = pytest.mark.gpu
+
+P = lambda a: a.ctypes.data  # noqa: E731
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from g4 import Lib
+    L = Lib.get()
+    L.init(0)
+    return L
+
+
+def dbuf(lib, a):
+    from g4 import DBuf
+    return DBuf.from_array(lib, a)
+
+
+def gpu_q8(lib, x):
+    from g4 import DBuf
+    xd = dbuf(lib, np.ascontiguousarray(x, np.float32))
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(x.size))
+    lib.g4_quantize_row_q8_K(xd.ptr, q8.ptr, x.size)
+    return xd, q8
+
+
+def download_q8(lib, q8, k):
+    out = np.zeros(k // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(out), k)
+    return out
+
+
+def q8_cases():
+    rng = np.random.default_rng(3)
+    cases = [rng.standard_normal(2560).astype(np.float32), rng.standard_normal(10240).astype(np.float32) * 50]
+    z = np.zeros(512, np.float32)
+    z[256 + 7] = 1.0
+    cases.append(z)
+    t = rng.standard_normal(256).astype(np.float32)
+    t[10], t[20] = 3.0, -3.0
+    cases.append(t)
+    t = rng.standard_normal(256).astype(np.float32)
+    t[5], t[6] = -3.0, 3.0
+    cases.append(t)
+    h = np.zeros(256, np.float32)
+    h[0] = 127.0
+    h[1:40] = np.arange(39, dtype=np.float32) - 19.5
+    cases.append(h)
+    cases.append((rng.standard_normal(256) * 1e-30).astype(np.float32))
+    cases.append(np.full(256, -2.0, np.float32))
+    return cases
+
+
+def test_quantize_q8K_bitexact(lib, orc):
+    for x in q8_cases():
+        _, q8 = gpu_q8(lib, x)
+        got = download_q8(lib, q8, x.size)
+        assert got.tobytes() == orc.quantize_q8K(x).tobytes()
+
+
+def test_q8K_upload_download_roundtrip(lib, orc):
+    x = np.random.default_rng(4).standard_normal(2560).astype(np.float32)
+    ref = orc.quantize_q8K(x)
+    from g4 import DBuf
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(2560))
+    lib.g4_upload_q8K(q8.ptr, P(ref), 2560)
+    assert download_q8(lib, q8, 2560).tobytes() == ref.tobytes()
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("n,d", [(256, 5), (2560, 37), (10240, 3)])
+def test_layout_roundtrip(lib, qtype, n, d):
+    from g4 import download_quant, upload_quant
+    raw = synth.rand_kquant(np.random.default_rng(n + d + qtype), qtype, d, n)
+    buf = upload_quant(lib, raw, qtype, n, d)
+    back = download_quant(lib, buf, qtype, n, d)
+    assert back.tobytes() == raw.tobytes()
+    assert lib.L.g4_tensor_bytes(qtype, n, d) == raw.nbytes
+
+
+GEMV_SHAPES = [(256, 300), (2560, 10240), (2560, 2048), (2560, 512), (2048, 2560), (4096, 2560), (10240, 64),
+               (2560, 256), (2560, 1)]
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+@pytest.mark.parametrize("n,d", GEMV_SHAPES)
+def test_q45_gemv_bitexact(lib, orc, qtype, n, d):
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(1000 * qtype + n + d)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, qtype, n, d)
+    _, q8 = gpu_q8(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_quant_dot_rows(out.ptr, w.ptr, n, d, qtype, q8.ptr)
+    got = out.to_array(np.float32)
+    want = orc.mm_quant_dot_rows(raw, n, d, qtype, orc.quantize_q8K(x))
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: {got[bad[:5]]} vs {want[bad[:5]]}"
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_block_sums_exact(lib, orc, qtype):
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 96
+    rng = np.random.default_rng(7 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, qtype, n, d)
+    _, q8 = gpu_q8(lib, x)
+    S, M = DBuf(lib, 4 * d * 10), DBuf(lib, 4 * d * 10)
+    lib.g4_debug_block_sums(w.ptr, n, d, qtype, q8.ptr, S.ptr, M.ptr)
+    gS, gM = S.to_array(np.int32).reshape(d, 10), M.to_array(np.int32).reshape(d, 10)
+    q8h = orc.quantize_q8K(x)
+    bs = synth.BLOCK_BYTES[qtype]
+    for r in range(d):
+        eS, eM = kq.kquant_block_sums(raw[r].reshape(-1, bs), qtype, q8h)
+        assert np.array_equal(gS[r], eS) and np.array_equal(gM[r], eM)
+
+
+def test_vec_dot_single_row(lib, orc):
+    from g4 import DBuf, upload_quant
+    n = 2560
+    rng = np.random.default_rng(11)
+    for qtype, fn in ((12, "g4_vec_dot_q4_K_q8_K"), (13, "g4_vec_dot_q5_K_q8_K"), (14, "g4_vec_dot_q6_K_q8_K")):
+        raw = synth.rand_kquant(rng, qtype, 1, n)
+        x = rng.standard_normal(n).astype(np.float32)
+        w = upload_quant(lib, raw, qtype, n, 1)
+        _, q8 = gpu_q8(lib, x)
+        out = DBuf(lib, 4)
+        getattr(lib, fn)(n, w.ptr, q8.ptr, out.ptr)
+        q8h = orc.quantize_q8K(x)
+        f = {12: orc.L.or_vec_dot_q4K_q8K, 13: orc.L.or_vec_dot_q5K_q8K, 14: orc.L.or_vec_dot_q6K_q8K}[qtype]
+        want = np.float32(f(n, P(raw), P(q8h)))
+        assert out.to_array(np.float32)[0].tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("n,d", [(2560, 512), (10240, 2560), (2560, 8192), (256, 40)])
+def test_q6K_f32_gemv(lib, orc, n, d):
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(n * 3 + d)
+    raw = synth.rand_q6K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, 14, n, d)
+    xd = dbuf(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_quant_rows(out.ptr, xd.ptr, w.ptr, n, d, 14)
+    got = out.to_array(np.float32)
+    want = orc.mm_quant_rows(x, raw, n, d, 14)
+    W = np.abs(kq.dequant_f64(raw.reshape(-1, 210), 14).reshape(d, n))
+    mag = W @ np.abs(x.astype(np.float64))
+    err = np.abs(got.astype(np.float64) - want) / mag
+    assert err.max() <= 1e-5, err.max()
+
+
+def test_q6K_softcap(lib, orc):
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 4096
+    rng = np.random.default_rng(2)
+    raw = synth.rand_q6K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, 14, n, d)
+    xd = dbuf(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_quant_rows_softcap(out.ptr, xd.ptr, w.ptr, n, d, 14, 30.0)
+    got = out.to_array(np.float32)
+    raw_l = orc.mm_quant_rows(x, raw, n, d, 14)
+    want = (np.float32(30.0) * np.tanh(raw_l * np.float32(1.0 / 30.0))).astype(np.float32)
+    # the cap's derivative is <= 1, so the GEMV bar (1e-5 of sum |w*x|) carries
+    # over; a few ulps of 30 cover tanhf itself
+    W = np.abs(kq.dequant_f64(raw.reshape(-1, 210), 14).reshape(d, n))
+    mag = W @ np.abs(x.astype(np.float64))
+    assert (np.abs(got - want) <= 1e-5 * mag + 1e-5).all()
+
+
+def test_q6K_q8K_gemv_bitexact(lib, orc):
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 3000
+    rng = np.random.default_rng(21)
+    raw = synth.rand_q6K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, 14, n, d)
+    _, q8 = gpu_q8(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_quant_dot_rows(out.ptr, w.ptr, n, d, 14, q8.ptr)
+    want = orc.mm_quant_dot_rows(raw, n, d, 14, orc.quantize_q8K(x))
+    assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,d", [(2560, 10752), (256, 100), (4096, 33)])
+def test_bf16_gemv(lib, orc, n, d):
+    from g4 import DBuf
+    rng = np.random.default_rng(n + d)
+    wh = synth.rand_bf16(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w, xd, out = dbuf(lib, wh), dbuf(lib, x), DBuf(lib, 4 * d)
+    lib.g4_mm_bf16(out.ptr, xd.ptr, w.ptr, n, d)
+    got = out.to_array(np.float32)
+    want = orc.mm_bf16(x, wh, n, d)
+    W = (wh.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    mag = np.abs(W) @ np.abs(x.astype(np.float64))
+    assert (np.abs(got - want) <= 1e-5 * mag).all()
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_gate_up_gelu(lib, orc, qtype):
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 10240
+    rng = np.random.default_rng(31 + qtype)
+    g_raw = synth.rand_kquant(rng, qtype, d, n)
+    u_raw = synth.rand_kquant(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    gw, uw = upload_quant(lib, g_raw, qtype, n, d), upload_quant(lib, u_raw, qtype, n, d)
+    _, q8 = gpu_q8(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_gate_up_gelu(out.ptr, gw.ptr, uw.ptr, n, d, qtype, q8.ptr)
+    q8h = orc.quantize_q8K(x)
+    g = orc.mm_quant_dot_rows(g_raw, n, d, qtype, q8h)
+    u = orc.mm_quant_dot_rows(u_raw, n, d, qtype, q8h)
+    want = np.array([orc.L.or_gelu(float(v)) for v in g], np.float32) * u
+    got = out.to_array(np.float32)
+    # gate and up are bit-exact; only tanhf (device libm vs glibc) may differ by ulps
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+
+
+def test_mm_dispatch(lib, orc):
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 512
+    rng = np.random.default_rng(41)
+    raw = synth.rand_q4K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, 12, n, d)
+    xd = dbuf(lib, x)
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(n))
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm(out.ptr, xd.ptr, w.ptr, n, d, 12, q8.ptr, 0)
+    want = orc.mm_quant_dot_rows(raw, n, d, 12, orc.quantize_q8K(x))
+    assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
