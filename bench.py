@@ -1,0 +1,332 @@
+#!/usr/bin/env python3
+"""Benchmark of the Gemma 4 E4B decode-step hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Workloads (synthetic inputs, generated from fixed seeds on the host):
+  decode  full E4B-shape forward: 42 layers, hidden 2560, FFN 10240, vocab
+          262144, Q4_K_M weight mix, random init; a step is one decode token
+          (the default; the metric's workload)
+  gemv    one Q4_K x Q8_K GEMV 10240x2560 (seed 0)
+  layer   one decoder layer's projections at hidden 2560 (seed 1)
+  lmhead  tied LM head, Q6_K 262144x2560 times an fp32 hidden vector, with the
+          30*tanh(l/30) soft-cap (seed 2)
+  attn    ISWA decode attention over an fp32 KV cache (seed 3)
+
+Prints ONE JSON line.  `value` is whole-job throughput with inputs resident
+in HBM; `roofline` is the dominant kernel's algorithmic bytes over its average
+launch time (HIP events on the library stream); `cpu_baseline` times the
+reference CPU path on a bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "gemma4.c_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 512 << 20        # rotate through this many distinct bytes to defeat the 256 MB Infinity Cache
+METRIC = "decode tok/s at E4B shape (1 GPU); K-quant GEMV GB/s as % of HBM peak"
+
+
+def cpu_threads() -> int:
+    v = os.environ.get("OMP_NUM_THREADS")
+    if v and v.isdigit():
+        return int(v)
+    return min(16, os.cpu_count() or 1)
+
+
+class Timer:
+    """HIP events on the library stream around a region."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        lib.check(lib.L.g4_event_create(C.byref(self.a)))
+        lib.check(lib.L.g4_event_create(C.byref(self.b)))
+
+    def start(self):
+        self.lib.check(self.lib.L.g4_event_record(self.a))
+
+    def stop_ms(self) -> float:
+        self.lib.check(self.lib.L.g4_event_record(self.b))
+        ms = C.c_float()
+        self.lib.check(self.lib.L.g4_event_elapsed_ms(self.a, self.b, C.byref(ms)))
+        return ms.value
+
+
+def roofline(bytes_per_launch: float, sec_per_launch: float) -> dict:
+    gbs = bytes_per_launch / sec_per_launch / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+
+
+# ---------------------------------------------------------------------------
+# GEMV workloads
+# ---------------------------------------------------------------------------
+def _copies(nbytes: int) -> int:
+    return max(2, -(-MALL_BYTES // nbytes))
+
+
+def bench_gemv(lib, g4, synth, args):
+    """Q4_K x Q8_K GEMV 10240x2560; rotates weight copies so every launch reads HBM."""
+    n, d = 2560, 10240
+    rng = np.random.default_rng(0)
+    raw = synth.rand_q4K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    ncp = _copies(raw.nbytes)
+    ws = [g4.upload_quant(lib, raw, g4.Q4_K, n, d) for _ in range(ncp)]
+    xd = g4.DBuf.from_array(lib, x)
+    q8 = g4.DBuf(lib, lib.L.g4_q8K_bytes(n))
+    out = g4.DBuf(lib, 4 * d)
+    lib.g4_quantize_row_q8_K(xd.ptr, q8.ptr, n)
+    L = lib.L
+
+    def step(i):
+        L.g4_mm_quant_dot_rows(out.ptr, ws[i % ncp].ptr, n, d, g4.Q4_K, q8.ptr)
+
+    launches = 1
+    algo = raw.nbytes + lib.L.g4_q8K_bytes(n) + 4 * d
+    ms = _time_steps(lib, step, args)
+    per_launch = ms / 1e3 / args.steps / launches
+    res = {
+        "value": round(algo / per_launch / 1e9, 1), "unit": "GB/s", "higher_is_better": True,
+        "ms_per_step": ms / args.steps, "dtype": "int8xu4->int32, fp32 combine",
+        "config": {"workload": "Q4_K x Q8_K GEMV 10240x2560 (seed 0), batch 1", "rows": d, "n": n,
+                   "weight_copies_rotated": ncp},
+        "roofline": dict(roofline(algo, per_launch), kernel="gemv_q45k_kernel", bytes_per_launch=algo),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_gemv_baseline(raw, x, n, d, algo)
+    return res
+
+
+def cpu_gemv_baseline(raw, x, n, d, algo):
+    import oracle as orc_mod
+    thr = cpu_threads()
+    if orc_mod.Ref.available():
+        ref = orc_mod.Ref()
+        kind = "reference"
+        q8 = np.zeros(n // 256, orc_mod.Q8K_DTYPE)
+        o = np.empty(d, np.float32)
+
+        def run():
+            ref.L.ref_quantize_row_q8_K(x.ctypes.data, q8.ctypes.data, n)
+            ref.L.ref_mm_quant_dot_rows(o.ctypes.data, raw.ctypes.data, n, d, 12, q8.ctypes.data)
+    else:
+        orc = orc_mod.Oracle()
+        kind = "port"
+
+        def run():
+            q8 = orc.quantize_q8K(x)
+            orc.mm_quant_dot_rows(raw, n, d, 12, q8)
+    for _ in range(3):
+        run()
+    ts = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end or len(ts) < 20:
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(algo / med / 1e9, 2), "unit": "GB/s", "cores": thr, "kind": kind,
+            "sample": f"quantize_row_q8_K + mm_quant_dot_rows (Q4_K 10240x2560), median of {len(ts)} runs "
+                      f"after 3 warm-ups, OpenMP {thr} threads"}
+
+
+def bench_lmhead(lib, g4, synth, args):
+    """Tied LM head: Q6_K 262144x2560 x fp32 hidden, fused soft-cap (550 MB > MALL)."""
+    n, d = 2560, 262144
+    rng = np.random.default_rng(2)
+    raw = synth.rand_q6K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = g4.upload_quant(lib, raw, g4.Q6_K, n, d)
+    xd = g4.DBuf.from_array(lib, x)
+    out = g4.DBuf(lib, 4 * d)
+    L = lib.L
+
+    def step(i):
+        L.g4_mm_quant_rows_softcap(out.ptr, xd.ptr, w.ptr, n, d, g4.Q6_K, C.c_float(30.0))
+
+    algo = raw.nbytes + 4 * n + 4 * d
+    ms = _time_steps(lib, step, args)
+    per = ms / 1e3 / args.steps
+    res = {
+        "value": round(algo / per / 1e9, 1), "unit": "GB/s", "higher_is_better": True,
+        "ms_per_step": ms / args.steps, "dtype": "f32",
+        "config": {"workload": "tied LM head Q6_K 262144x2560 x fp32, softcap 30 (seed 2)"},
+        "roofline": dict(roofline(algo, per), kernel="gemv_q6k_f32_kernel", bytes_per_launch=algo),
+    }
+    return res
+
+
+def _gguf_e4b(synth, seed: int = 4) -> str:
+    """The synthetic E4B-shape GGUF (about 5.4 GB), written once per machine."""
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
+    path = os.path.join(d, f"g4_e4b_seed{seed}.gguf")
+    if not os.path.exists(path):
+        tmp = path + f".{os.getpid()}.part"
+        synth.write_model_gguf(tmp, synth.E4B, seed)
+        os.replace(tmp, path)
+    return path
+
+
+def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):
+    """The dominant decode kernel at its decode shape: fused gate/up GELU GEMV,
+    Q4_K 2 x 10240x2560 against one Q8_K vector, rotating weight copies (>= 512
+    MB) so every launch streams from HBM.  HIP events on the library stream."""
+    n, d = 2560, 10240
+    rng = np.random.default_rng(1)
+    g_raw = synth.rand_q4K(rng, d, n)
+    u_raw = synth.rand_q4K(rng, d, n)
+    ncp = _copies(2 * g_raw.nbytes)
+    gs = [g4.upload_quant(lib, g_raw, g4.Q4_K, n, d) for _ in range(ncp)]
+    us = [g4.upload_quant(lib, u_raw, g4.Q4_K, n, d) for _ in range(ncp)]
+    x = g4.DBuf.from_array(lib, rng.standard_normal(n).astype(np.float32))
+    q8 = g4.DBuf(lib, lib.L.g4_q8K_bytes(n))
+    hb = g4.DBuf(lib, 4 * d)
+    lib.g4_quantize_row_q8_K(x.ptr, q8.ptr, n)
+    L = lib.L
+
+    def step(i):
+        L.g4_mm_gate_up_gelu(hb.ptr, gs[i % ncp].ptr, us[i % ncp].ptr, n, d, g4.Q4_K, q8.ptr)
+
+    class A:
+        warmup, steps = 20, n_launch
+    ms = _time_steps(lib, step, A)
+    per = ms / 1e3 / n_launch
+    algo = 2 * g_raw.nbytes + lib.L.g4_q8K_bytes(n) + 4 * d
+    return dict(roofline(algo, per), kernel="gemv_q45k_kernel<gate|up, GELU> 2x10240x2560 Q4_K",
+                bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
+
+
+def _log(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def bench_decode(lib, g4, synth, args):
+    """Full synthetic E4B-shape decode: 42 layers, dim 2560, FFN 10240, vocab
+    262144, Q4_K_M mix; 512-token prompt prefilled token by token, then greedy
+    decode steps replayed as one HIP graph per token."""
+    t0 = time.perf_counter()
+    _log("synthetic E4B-shape GGUF (seed 4)")
+    path = _gguf_e4b(synth)
+    t_gen = time.perf_counter() - t0
+    _log(f"GGUF ready in {t_gen:.1f} s; loading into HBM")
+    eng = g4.Engine(path, max_seq=1024)
+    rng = np.random.default_rng(4)
+    n_prompt = 512
+    prompt = rng.integers(0, eng.vocab, n_prompt).astype(np.int32)
+    # prefill (token-serial, as generate() does), then the timed decode
+    _log("prefill 511 tokens")
+    t1 = time.perf_counter()
+    for pos in range(n_prompt - 1):
+        eng.forward(int(prompt[pos]), pos, 0)
+    t_prefill = time.perf_counter() - t1
+    assert n_prompt - 1 + args.warmup + args.steps <= eng.max_seq
+    tok = int(prompt[-1])
+    use_graph = not args.no_graph
+    _, _ = eng.decode_steps(tok, n_prompt - 1, args.warmup, use_graph=use_graph)
+    # timed: K graph replays from position 511 + W; events bracket the region
+    lib.L.g4_set_stream(None)
+    toks, sec = eng.decode_steps(tok, n_prompt - 1 + args.warmup, args.steps, use_graph=use_graph, record=False)
+    tps = args.steps / sec
+    _log(f"decode {args.steps} steps: {tps:.1f} tok/s")
+    eng.close()
+    res = {
+        "value": round(tps, 2), "unit": "tok/s", "higher_is_better": True,
+        "ms_per_step": sec * 1e3 / args.steps, "dtype": "int8xu4/u6->int32 + f32 (Q4_K_M weights)",
+        "config": {"workload": "synthetic E4B-shape greedy decode (42 layers, hidden 2560, FFN 10240, 8q/2kv heads, "
+                               "head_dim 256/512, window 512, last 18 layers shared-KV, vocab 262144 tied Q6_K head, "
+                               "Q4_K_M mix, seed 4); prompt 512 tokens prefilled token-serially, then decode",
+                   "positions": [n_prompt - 1 + args.warmup, n_prompt - 1 + args.warmup + args.steps],
+                   "graph": use_graph, "weights_bytes_per_token": synth.decode_weight_bytes(synth.E4B),
+                   "prefill_tok_s_token_serial": round((n_prompt - 1) / t_prefill, 1),
+                   "gguf_write_s": round(t_gen, 1)},
+    }
+    _log("dominant-kernel roofline")
+    res["roofline"] = _gate_up_roofline(lib, g4, synth)
+    res["decode_hbm_GBps"] = round(synth.decode_weight_bytes(synth.E4B) * tps / 1e9, 1)
+    if not args.no_cpu:
+        _log("CPU baseline (oracle forward)")
+        res["cpu_baseline"] = cpu_decode_baseline(path)
+    return res
+
+
+def cpu_decode_baseline(path: str, steps: int = 6) -> dict:
+    """The oracle's forward() (the C restatement of main.c:1838-2029, OpenMP)
+    on the same GGUF: a 4-token prompt, then `steps` greedy decode steps."""
+    import oracle as orc_mod
+    thr = cpu_threads()
+    om = orc_mod.OracleModel(orc_mod.Oracle(), path, max_seq=64)
+    prompt = np.array([2, 105, 9731, 107], np.int32)
+    toks, pf, dec = om.generate_greedy(prompt, steps)
+    om.close()
+    n = max(len(toks), 1)
+    return {"value": round(n / dec, 3) if dec > 0 else None, "unit": "tok/s", "cores": thr, "kind": "port",
+            "sample": f"oracle forward() (C restatement of the reference, gcc -O3 -std=c11, OpenMP {thr} threads, "
+                      f"plain-loop sgemv): {n} greedy decode steps after a 4-token prompt on the same GGUF"}
+
+
+def _time_steps(lib, step, args) -> float:
+    for i in range(args.warmup):
+        step(i)
+    lib.g4_sync()
+    t = Timer(lib)
+    t.start()
+    for i in range(args.steps):
+        step(i)
+    ms = t.stop_ms()
+    lib.g4_sync()
+    return ms
+
+
+WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "lmhead": bench_lmhead}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true", help="decode with eager launches instead of one HIP graph "
+                    "per token (same kernels; for profilers that do not follow graph launches)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path is single-GPU; multi-GPU sharding is a design note only)", file=sys.stderr)
+        return 2
+    if args.steps is None:
+        args.steps = 128 if args.workload == "decode" else 200
+    if args.warmup is None:
+        args.warmup = 8 if args.workload == "decode" else 20
+    import g4
+    import synth
+    lib = g4.Lib.get()
+    lib.init(0)
+    t0 = time.perf_counter()
+    res = WORKLOADS[args.workload](lib, g4, synth, args)
+    line = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res.pop("ms_per_step"), 6),
+            "higher_is_better": res.pop("higher_is_better"), "scaling": "weak", "vs_baseline": None,
+            "dtype": res.pop("dtype"), "data": "synthetic"}
+    line.update(res)
+    line["wall_s"] = round(time.perf_counter() - t0, 1)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,455 @@
+// attn.hip -- Neox RoPE, KV-cache append and ISWA decode attention on gfx950.
+//
+// Reference (gemma4-4b/cpu-blas/main.c):
+//   apply_rope_neox            1725-1745
+//   per-head norms, KV append  1886-1904 (K: k_norm, RoPE, store; V: unweighted
+//                              norm, store; Q: q_norm, RoPE)
+//   attention block            1909-1950: t_start = max(0, pos+1-window) on
+//                              sliding-window layers; per head s = scale*K.q,
+//                              softmax, o = V^T p; GQA head h reads kv head
+//                              h / (n_heads/n_kv); shared-KV layers read the
+//                              donor's cache (main.c:743-746).
+//
+// KV cache in HBM: one buffer per storing layer and per K/V, slot-major
+// [slots][kv_stride] fp32.  Full-attention layers use slot = pos; sliding-
+// window layers keep a ring of `ring` slots (slot = pos % ring), which holds
+// exactly the window the reference reads from its flat cache.
+//
+// Decode attention is split over the time axis: workgroup (c, kvh) scores one
+// chunk of the window for all q heads of kv head kvh (the K/V rows are read
+// once for the GQA group), keeps (max, sum, o) of its chunk, and a merge
+// kernel combines the chunks by log-sum-exp.  Equal to the reference's
+// softmax-then-PV up to fp32 rounding.
+#include "g4_device.h"
+#include "g4_internal.h"
+
+namespace g4 {
+
+// ---- RoPE ----------------------------------------------------------------
+// Rotate pairs (j, j + hd/2), j < n_rot/2, of one head held in LDS.  The
+// angle of pair j is the reference's chain theta_0 = pos, theta_j =
+// theta_{j-1} * ts (one rounding per step), angle = (fs * theta_j) / ff[j].
+__device__ __forceinline__ void rope_head_lds(float* seg, int hd, int n_rot, int pos, float ts, float fs,
+                                              const float* __restrict__ ff) {
+    const int half = hd / 2;
+    for (int j = threadIdx.x; j < n_rot / 2; j += blockDim.x) {
+        float theta = (float)pos;
+        for (int i = 0; i < j; i++) theta *= ts;
+        const float f = ff ? ff[j] : 1.0f;
+        const float angle = (fs * theta) / f;
+        const float cr = cosf(angle), ci = sinf(angle);
+        const float v0 = seg[j], v1 = seg[j + half];
+        seg[j] = v0 * cr - v1 * ci;
+        seg[j + half] = v0 * ci + v1 * cr;
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ vec, int hd, int n_rot, int pos, float ts,
+                                                   float fs, const float* __restrict__ ff) {
+    extern __shared__ __align__(16) float seg[];
+    float* g = vec + (size_t)blockIdx.x * hd;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) seg[i] = g[i];
+    __syncthreads();
+    rope_head_lds(seg, hd, n_rot, pos, ts, fs, ff);
+    __syncthreads();
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) g[i] = seg[i];
+}
+
+// ---- per-head norms + RoPE + KV append (main.c:1886-1904) -----------------
+struct QKVArgs {
+    float* q;              // n_heads*hd, normalised and rotated in place
+    const float* q_norm;
+    const float* k;        // n_kv*hd (nullptr: layer stores no KV)
+    const float* v;
+    const float* k_norm;
+    float* kc;             // slot 0 of this layer's K cache
+    float* vc;
+    const int* dpos;       // device position (nullptr: use pos)
+    const float* ff;       // rope freq factors (nullptr = 1)
+    int pos, n_heads, n_kv, hd, n_rot, kv_stride, ring;
+    float ts, fs, eps;
+};
+
+__global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
+    extern __shared__ __align__(16) float seg[];
+    __shared__ float red[16];
+    const int b = blockIdx.x, hd = a.hd;
+    const int pos = a.dpos ? *a.dpos : a.pos;
+    const float* src;
+    const float* w;
+    int kind;   // 0 = q, 1 = k, 2 = v
+    int head;
+    if (b < a.n_heads) { kind = 0; head = b; src = a.q + (size_t)head * hd; w = a.q_norm; }
+    else if (b < a.n_heads + a.n_kv) { kind = 1; head = b - a.n_heads; src = a.k + (size_t)head * hd; w = a.k_norm; }
+    else { kind = 2; head = b - a.n_heads - a.n_kv; src = a.v + (size_t)head * hd; w = nullptr; }
+
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        const float t = src[i];
+        seg[i] = t;
+        ss += t * t;
+    }
+    ss = block_sum(ss, red);
+    const float s = 1.0f / sqrtf(ss / (float)hd + a.eps);
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) seg[i] = w ? seg[i] * (s * w[i]) : seg[i] * s;
+    __syncthreads();
+    if (kind != 2) {
+        rope_head_lds(seg, hd, a.n_rot, pos, a.ts, a.fs, a.ff);
+        __syncthreads();
+    }
+    float* dst;
+    if (kind == 0) {
+        dst = a.q + (size_t)head * hd;
+    } else {
+        const int slot = a.ring > 0 ? pos % a.ring : pos;
+        dst = (kind == 1 ? a.kc : a.vc) + (size_t)slot * a.kv_stride + (size_t)head * hd;
+    }
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) dst[i] = seg[i];
+}
+
+// ---- split-T decode attention --------------------------------------------
+struct AttnArgs {
+    const float* q;        // n_heads*hd
+    const float* kc;       // slot 0 of the source layer's cache
+    const float* vc;
+    const int* dpos;       // device position (nullptr: t_start/nwin below)
+    float* part;           // [n_heads][G][hd+2] partials
+    float* out;            // n_heads*hd
+    uint8_t* q8;           // optional Q8_K of out (n_heads*hd/256 blocks)
+    int t_start, nwin;     // used when dpos == nullptr
+    int window;            // used with dpos: 0 = full attention
+    int kv_stride, ring, n_heads, n_kv, hd, G;
+    float scale;
+};
+
+constexpr int kAttnThreads = 256;
+constexpr int kChunkMax = 1024;     // positions per workgroup
+
+// float offset of the (max, sum) pairs in the partial kernel's LDS
+__host__ __device__ inline int attn_ml_offset(int hd, int kvm) {
+    const int a = kvm * hd + kvm * kChunkMax, b = 4 * kvm * hd;
+    return a > b ? a : b;
+}
+
+__device__ __forceinline__ void attn_window(const AttnArgs& a, int& t0, int& nwin) {
+    if (a.dpos) {
+        const int pos = *a.dpos;
+        t0 = a.window > 0 ? max(0, pos + 1 - a.window) : 0;
+        nwin = pos + 1 - t0;
+    } else {
+        t0 = a.t_start;
+        nwin = a.nwin;
+    }
+}
+
+__device__ __forceinline__ float dot4(const float4 a, const float4 b, float acc) {
+    acc = __builtin_fmaf(a.x, b.x, acc);
+    acc = __builtin_fmaf(a.y, b.y, acc);
+    acc = __builtin_fmaf(a.z, b.z, acc);
+    return __builtin_fmaf(a.w, b.w, acc);
+}
+
+// LDS: q [kvm][HD] | scores [kvm][kChunkMax], reused by the PV reduction as
+// [4 waves][kvm][HD]; the per-head (max, sum) pairs [2*kvm] sit after both
+// (attn_ml_offset), so the reduction cannot overwrite them.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    constexpr int KPL = HD / 64;          // float4 per 16-lane slice of a row
+    const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int kvm = a.n_heads / a.n_kv;
+    int t0, nwin;
+    attn_window(a, t0, nwin);
+    const int cs = (nwin + a.G - 1) / a.G;
+    const int cb = t0 + c * cs;
+    // the launcher sizes G so that a chunk fits kChunkMax; the clamp only keeps
+    // LDS accesses in bounds
+    const int cnt = min(kChunkMax, max(0, min(cb + cs, t0 + nwin) - cb));
+    float* qs = sm;
+    float* sc = sm + kvm * HD;
+    float* ml = sm + attn_ml_offset(HD, kvm);
+    const float* qsrc = a.q + (size_t)kvh * kvm * HD;
+    for (int i = tid; i < kvm * HD; i += kAttnThreads) qs[i] = qsrc[i];
+    __syncthreads();
+
+    // phase 1: scores, one position per 16-lane subgroup
+    const int sub = tid >> 4, sl = tid & 15;
+    for (int t = sub; t < cnt; t += kAttnThreads / 16) {
+        const int tt = cb + t;
+        const int slot = a.ring > 0 ? tt % a.ring : tt;
+        const float4* kr = reinterpret_cast<const float4*>(a.kc + (size_t)slot * a.kv_stride + (size_t)kvh * HD);
+        float4 kv[KPL];
+#pragma unroll
+        for (int k = 0; k < KPL; k++) kv[k] = kr[sl + 16 * k];
+        for (int h = 0; h < kvm; h++) {
+            const float4* qh = reinterpret_cast<const float4*>(qs + h * HD);
+            float d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KPL; k++) d = dot4(kv[k], qh[sl + 16 * k], d);
+            d += __shfl_xor(d, 8, 64);
+            d += __shfl_xor(d, 4, 64);
+            d += __shfl_xor(d, 2, 64);
+            d += __shfl_xor(d, 1, 64);
+            if (sl == 0) sc[h * kChunkMax + t] = a.scale * d;
+        }
+    }
+    __syncthreads();
+
+    // phase 2: chunk max / exp / sum per head (one wave per head)
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int h = wave; h < kvm; h += kAttnThreads / 64) {
+        float* s = sc + h * kChunkMax;
+        float m = -INFINITY;
+        for (int t = lane; t < cnt; t += 64) m = fmaxf(m, s[t]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int t = lane; t < cnt; t += 64) {
+            const float e = expf(s[t] - m);
+            s[t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    }
+    __syncthreads();
+
+    // phase 3: o[h] = sum_t p[h][t] V[t]; wave w takes t = w, w+4, ...
+    constexpr int VPL = HD / 256;        // float4 per lane of a row
+    float4 acc[8][VPL];
+#pragma unroll
+    for (int h = 0; h < 8; h++)
+#pragma unroll
+        for (int k = 0; k < VPL; k++) acc[h][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = wave; t < cnt; t += kAttnThreads / 64) {
+        const int tt = cb + t;
+        const int slot = a.ring > 0 ? tt % a.ring : tt;
+        const float4* vr = reinterpret_cast<const float4*>(a.vc + (size_t)slot * a.kv_stride + (size_t)kvh * HD);
+        float4 vv[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; k++) vv[k] = vr[lane + 64 * k];
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+            if (h < kvm) {
+                const float p = sc[h * kChunkMax + t];
+#pragma unroll
+                for (int k = 0; k < VPL; k++) {
+                    acc[h][k].x = __builtin_fmaf(p, vv[k].x, acc[h][k].x);
+                    acc[h][k].y = __builtin_fmaf(p, vv[k].y, acc[h][k].y);
+                    acc[h][k].z = __builtin_fmaf(p, vv[k].z, acc[h][k].z);
+                    acc[h][k].w = __builtin_fmaf(p, vv[k].w, acc[h][k].w);
+                }
+            }
+        }
+    }
+    __syncthreads();   // scores are dead; reuse q+scores for the cross-wave sum
+    float* rs = sm;    // [4][kvm][HD]
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+        if (h < kvm) {
+#pragma unroll
+            for (int k = 0; k < VPL; k++)
+                reinterpret_cast<float4*>(rs + ((size_t)wave * kvm + h) * HD)[lane + 64 * k] = acc[h][k];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < kvm * HD; i += kAttnThreads) {
+        const int h = i / HD, dd = i - h * HD;
+        float o = 0.0f;
+        for (int w = 0; w < kAttnThreads / 64; w++) o += rs[((size_t)w * kvm + h) * HD + dd];
+        float* p = a.part + ((size_t)(kvh * kvm + h) * a.G + c) * (HD + 2);
+        p[dd] = o;
+        if (dd == 0) { p[HD] = cnt > 0 ? ml[2 * h] : -INFINITY; p[HD + 1] = cnt > 0 ? ml[2 * h + 1] : 0.0f; }
+    }
+}
+
+// one workgroup of HD threads per q head
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
+    __shared__ __align__(16) float o[HD];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const float* p = a.part + (size_t)h * a.G * (HD + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < a.G; c++) M = fmaxf(M, p[(size_t)c * (HD + 2) + HD]);
+    float L = 0.0f, acc = 0.0f;
+    for (int c = 0; c < a.G; c++) {
+        const float* pc = p + (size_t)c * (HD + 2);
+        const float l = pc[HD + 1];
+        if (l > 0.0f) {
+            const float f = expf(pc[HD] - M);
+            L += l * f;
+            acc = __builtin_fmaf(pc[tid], f, acc);
+        }
+    }
+    const float r = L > 0.0f ? acc / L : 0.0f;
+    a.out[(size_t)h * HD + tid] = r;
+    if (a.q8) {
+        o[tid] = r;
+        __syncthreads();
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave < HD / 256) {
+            const float4 f = reinterpret_cast<const float4*>(o + wave * 256)[lane];
+            const float v[4] = {f.x, f.y, f.z, f.w};
+            quantize_block_wave(v, lane, a.q8, a.n_heads * HD / 256, h * (HD / 256) + wave);
+        }
+    }
+}
+
+size_t attn_lds(int hd, int kvm) { return 4 * ((size_t)attn_ml_offset(hd, kvm) + 2 * (size_t)kvm); }
+
+int launch_attn(const AttnArgs& a) {
+    const int kvm = a.n_heads / a.n_kv;
+    const dim3 g1(a.G, a.n_kv);
+    const size_t lds = attn_lds(a.hd, kvm);
+    if (a.hd == 256) {
+        hipLaunchKernelGGL(attn_partial_kernel<256>, g1, dim3(kAttnThreads), lds, g4_stream(), a);
+        hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads), dim3(256), 0, g4_stream(), a);
+    } else {
+        hipLaunchKernelGGL(attn_partial_kernel<512>, g1, dim3(kAttnThreads), lds, g4_stream(), a);
+        hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads), dim3(512), 0, g4_stream(), a);
+    }
+    return g4_check_launch("attn_partial_kernel/attn_merge_kernel");
+}
+
+int check_attn_shape(const char* who, int n_heads, int n_kv, int hd) {
+    if (hd != 256 && hd != 512) return g4_fail(G4_ERR_ARG, "%s: head_dim %d unsupported (256 or 512)", who, hd);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8)
+        return g4_fail(G4_ERR_ARG, "%s: n_heads=%d n_kv=%d (need n_heads/n_kv in 1..8)", who, n_heads, n_kv);
+    if (attn_lds(hd, n_heads / n_kv) > 65536)
+        return g4_fail(G4_ERR_ARG, "%s: %d q heads per kv head at head_dim %d exceed the LDS budget", who,
+                       n_heads / n_kv, hd);
+    return G4_OK;
+}
+
+// library-owned partials buffer for the host-position entry points
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+int workspace(size_t bytes, float** p) {
+    if (bytes > g_ws_bytes) {
+        if (g_ws) {
+            G4_HIP(hipStreamSynchronize(g4_stream()));
+            G4_HIP(hipFree(g_ws));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+        }
+        if (hipMalloc(&g_ws, bytes) != hipSuccess) return g4_fail(G4_ERR_NOMEM, "attention workspace (%zu B)", bytes);
+        g_ws_bytes = bytes;
+    }
+    *p = (float*)g_ws;
+    return G4_OK;
+}
+
+int chunks_for(int nwin) {
+    int G = (nwin + 127) / 128;        // ~128 positions per workgroup
+    if (G < 1) G = 1;
+    if (G > 512) G = 512;
+    while ((nwin + G - 1) / G > kChunkMax) G++;
+    return G;
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+// ---------------------------------------------------------------------------
+// entry points
+// ---------------------------------------------------------------------------
+extern "C" int g4_apply_rope_neox(float* vec, int n_heads, int head_dim, int n_rot, int pos, float freq_base,
+                                  float freq_scale, const float* freq_factors) {
+    G4_CHECK_ARG(vec && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0, "g4_apply_rope_neox: bad arguments");
+    G4_CHECK_ARG(n_rot >= 0 && n_rot <= head_dim, "g4_apply_rope_neox: n_rot=%d > head_dim=%d", n_rot, head_dim);
+    // theta scale on the host with the C library's powf, as main.c:1727
+    const float ts = powf(freq_base, -2.0f / (float)n_rot);
+    hipLaunchKernelGGL(rope_kernel, dim3(n_heads), dim3(256), (size_t)head_dim * 4, g4_stream(), vec, head_dim,
+                       n_rot, pos, ts, freq_scale, freq_factors);
+    return g4_check_launch("rope_kernel");
+}
+
+extern "C" int g4_qkv_post(float* q, const float* q_norm, const float* k, const float* v, const float* k_norm, float* kc,
+                float* vc, int kv_stride, int ring, const int* dpos, int pos, int n_heads, int n_kv, int hd,
+                int n_rot, float freq_base, float freq_scale, const float* ff, float eps) {
+    G4_CHECK_ARG(q && q_norm && hd > 0 && hd <= 1024 && n_rot <= hd, "qkv_post: bad arguments");
+    G4_CHECK_ARG(!k || (v && k_norm && kc && vc && kv_stride >= n_kv * hd), "qkv_post: bad K/V arguments");
+    QKVArgs a;
+    a.q = q; a.q_norm = q_norm; a.k = k; a.v = v; a.k_norm = k_norm; a.kc = kc; a.vc = vc;
+    a.dpos = dpos; a.ff = ff; a.pos = pos; a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.n_rot = n_rot;
+    a.kv_stride = kv_stride; a.ring = ring;
+    a.ts = powf(freq_base, -2.0f / (float)n_rot);
+    a.fs = freq_scale; a.eps = eps;
+    const int grid = n_heads + (k ? 2 * n_kv : 0);
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(grid), dim3(256), (size_t)hd * 4, g4_stream(), a);
+    return g4_check_launch("qkv_post_kernel");
+}
+
+extern "C" int g4_kv_append_rope(float* k, float* v, const float* k_norm, float* kc, float* vc, int kv_stride,
+                                 int ring, int pos, int n_kv, int hd, int n_rot, float freq_base, float freq_scale,
+                                 const float* freq_factors, float eps) {
+    G4_CHECK_ARG(k && v && k_norm && kc && vc && n_kv > 0 && pos >= 0, "g4_kv_append_rope: bad arguments");
+    G4_CHECK_ARG(kv_stride >= n_kv * hd, "g4_kv_append_rope: kv_stride %d < n_kv*hd", kv_stride);
+    QKVArgs a;
+    a.q = nullptr; a.q_norm = nullptr; a.k = k; a.v = v; a.k_norm = k_norm; a.kc = kc; a.vc = vc;
+    a.dpos = nullptr; a.ff = freq_factors; a.pos = pos; a.n_heads = 0; a.n_kv = n_kv; a.hd = hd; a.n_rot = n_rot;
+    a.kv_stride = kv_stride; a.ring = ring;
+    a.ts = powf(freq_base, -2.0f / (float)n_rot);
+    a.fs = freq_scale; a.eps = eps;
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(2 * n_kv), dim3(256), (size_t)hd * 4, g4_stream(), a);
+    return g4_check_launch("qkv_post_kernel");
+}
+
+static int attn_common(const char* who, AttnArgs& a) {
+    int rc = check_attn_shape(who, a.n_heads, a.n_kv, a.hd);
+    if (rc) return rc;
+    G4_CHECK_ARG(a.q && a.kc && a.vc && a.out, "%s: null pointer", who);
+    G4_CHECK_ARG(a.kv_stride >= a.n_kv * a.hd, "%s: kv_stride %d < n_kv*hd", who, a.kv_stride);
+    float* ws = nullptr;
+    rc = workspace((size_t)a.n_heads * a.G * (a.hd + 2) * 4, &ws);
+    if (rc) return rc;
+    a.part = ws;
+    return launch_attn(a);
+}
+
+// The attention block of main.c:1909-1950 over a flat cache (position t at
+// kc + t*kv_stride), positions t_start .. t_start+nwin-1.
+extern "C" int g4_attn_decode(const float* q, const float* kc, const float* vc, int kv_stride, int t_start,
+                              int nwin, int n_heads, int n_kv, int hd, float attn_scale, float* out) {
+    G4_CHECK_ARG(t_start >= 0 && nwin >= 0, "g4_attn_decode: t_start=%d nwin=%d", t_start, nwin);
+    AttnArgs a = {};
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = nullptr; a.out = out; a.q8 = nullptr;
+    a.t_start = t_start; a.nwin = nwin; a.window = 0; a.kv_stride = kv_stride; a.ring = 0;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = chunks_for(nwin);
+    return attn_common("g4_attn_decode", a);
+}
+
+// Same block over a ring cache of `ring` slots (slot = t % ring) at position
+// pos with a sliding window (window <= ring; 0 = full attention, then ring
+// must be 0 or >= pos+1).
+extern "C" int g4_attn_decode_ring(const float* q, const float* kc, const float* vc, int kv_stride, int ring,
+                                   int pos, int window, int n_heads, int n_kv, int hd, float attn_scale, float* out) {
+    G4_CHECK_ARG(pos >= 0 && ring >= 0 && window >= 0, "g4_attn_decode_ring: bad pos/ring/window");
+    const int t0 = window > 0 ? (pos + 1 - window > 0 ? pos + 1 - window : 0) : 0;
+    const int nwin = pos + 1 - t0;
+    G4_CHECK_ARG(ring == 0 || nwin <= ring, "g4_attn_decode_ring: window %d exceeds ring %d", nwin, ring);
+    AttnArgs a = {};
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = nullptr; a.out = out; a.q8 = nullptr;
+    a.t_start = t0; a.nwin = nwin; a.window = window; a.kv_stride = kv_stride; a.ring = ring;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = chunks_for(nwin);
+    return attn_common("g4_attn_decode_ring", a);
+}
+
+// Engine form: position read from device memory, fixed chunk count G (so a
+// captured graph stays valid as pos advances), caller-owned partials buffer
+// of g4_attn_part_bytes(n_heads, hd, G) bytes, optional fused Q8_K output.
+extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) { return (size_t)n_heads * G * (hd + 2) * 4; }
+
+extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* vc, int kv_stride, int ring, const int* dpos,
+                       int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float* part, float* out,
+                       void* q8) {
+    int rc = check_attn_shape("attn_decode_dev", n_heads, n_kv, hd);
+    if (rc) return rc;
+    G4_CHECK_ARG(q && kc && vc && dpos && part && out && G >= 1, "attn_decode_dev: bad arguments");
+    AttnArgs a = {};
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = dpos; a.part = part; a.out = out; a.q8 = (uint8_t*)q8;
+    a.window = window; a.kv_stride = kv_stride; a.ring = ring;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
+    return launch_attn(a);
+}

@@ -91,10 +91,69 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Sum over the whole workgroup (blockDim.x a multiple of 64, <= 1024); every
+// thread gets the total.  red must hold 16 floats; it is reusable after return.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
 // GELU, tanh form, evaluated in the reference's operation order (main.c:1490-1492)
 __device__ __forceinline__ float gelu_ref(float x) {
     const float inner = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
     return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// ---- Q8_K quantization of one 256-element block by one wavefront ----------
+// (quantize_row_q8_K, gemma4-4b/cpu-blas/main.c:247-340)
+// Quantize one 256-block held as 4 floats per lane; writes the device Q8_K
+// layout (qs permuted, bsums, d).  Every lane of the wave must call it.
+__device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, uint8_t* __restrict__ y,
+                                                    int nb, int b) {
+    // local first max of |x| over this lane's 4 elements
+    float amax = 0.0f, maxv = 0.0f;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float a = fabsf(v[e]);
+        if (a > amax) { amax = a; maxv = v[e]; idx = 4 * lane + e; }
+    }
+    // wave argmax: larger |x|, ties to the smaller index (total order)
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float oa = __shfl_xor(amax, m, 64);
+        const float ov = __shfl_xor(maxv, m, 64);
+        const int oi = __shfl_xor(idx, m, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; maxv = ov; idx = oi; }
+    }
+    int8_t q[4];
+    float dval = 0.0f;
+    if (amax == 0.0f) {
+        q[0] = q[1] = q[2] = q[3] = 0;
+    } else {
+        const float iscale = -127.0f / maxv;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int r = (int)rintf(iscale * v[e]);
+            q[e] = (int8_t)(r > 127 ? 127 : r);
+        }
+        dval = 1.0f / iscale;
+    }
+    const uint32_t word = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
+                          ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+    reinterpret_cast<uint32_t*>(y + (size_t)b * 256)[q8k_word_dev(lane)] = word;
+    // bsums: 16 elements = 4 lanes
+    int s = (int)q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(y + q8k_bsums_off(nb))[b * 16 + (lane >> 2)] = (int16_t)s;
+    if (lane == 0) reinterpret_cast<float*>(y + q8k_d_off(nb))[b] = dval;
 }
 
 }  // namespace g4

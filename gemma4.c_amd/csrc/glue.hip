@@ -1,0 +1,265 @@
+// glue.hip -- per-token step glue on gfx950: embedding lookup, the
+// per-layer-embedding (PLE) input, the PLE gate, greedy argmax.
+//
+// Reference (gemma4-4b/cpu-blas/main.c):
+//   emb_lookup       1696-1723 (row dequantized with dequant_q*_k, 172-237)
+//   x *= sqrtf(dim)  1849-1854
+//   build_ple        1747-1778
+//   PLE gate         1988-1993: g = gelu(g); g *= ple[l]
+//   greedy sampling  2045-2049: first index of the maximum
+//
+// Quantized tables are in the planar HBM layout (g4_device.h); the element
+// values are the reference's dequantized fp32 values bit for bit.
+#include "g4_device.h"
+#include "g4_internal.h"
+
+namespace g4 {
+
+// element e (0..255) of block blk of a planar K-quant tensor with nblk blocks;
+// the fp32 value dequant_q*_k produces (main.c:172-237)
+__device__ float dequant_elem(const uint8_t* __restrict__ w, int type, size_t nblk, size_t blk, int e) {
+    if (type == G4_Q6_K) {
+        const Q6KPlanes p = q6k_planes(nblk);
+        const int h = e >> 7, idx = e & 127, k = idx >> 5, l = idx & 31;
+        const int gq = 64 * h + (k & 1) * 32 + l;            // GGUF ql byte
+        const int r = gq & 63, u = (r & 31) >> 3, c = (r & 7) + (r >= 32 ? 8 : 0);
+        const uint8_t qlb = w[p.ql + blk * 128 + 16 * (4 * h + u) + c];
+        const uint8_t qhb = w[p.qh + blk * 64 + 32 * h + l];
+        const int lo = k < 2 ? (qlb & 15) : (qlb >> 4);
+        const int q = (int)(int8_t)(lo | (((qhb >> (2 * k)) & 3) << 4)) - 32;
+        const int8_t sc = (int8_t)w[p.sc + blk * 16 + 8 * h + (l >> 4) + 2 * k];
+        const float d = f16_to_f32(*reinterpret_cast<const uint16_t*>(w + p.d + blk * 2));
+        return d * (float)sc * (float)q;
+    }
+    // Q4_K / Q5_K: element e is in 64-group c = e/64, nibble half hi = (e/32)&1
+    const bool q5 = type == G4_Q5_K;
+    const size_t hdr_off = q5 ? q5k_planes(nblk).hdr : q4k_planes(nblk).hdr;
+    const uint8_t* hdr = w + hdr_off + blk * 16;
+    const int c = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    const int gw = (32 * c + l) >> 2;                          // GGUF qs word
+    const uint8_t qb = w[blk * 128 + 4 * q4k_word_dev(gw) + (l & 3)];
+    int q = hi ? (qb >> 4) : (qb & 15);
+    if (q5) {
+        const uint8_t qh = w[q5k_planes(nblk).qh + blk * 32 + l];
+        if (qh & (1u << (2 * c + hi))) q += 16;
+    }
+    const int j = 2 * c + hi;
+    int sc, m;
+    const uint8_t* s = hdr + 4;
+    if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+    else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+    const float d = f16_to_f32(*reinterpret_cast<const uint16_t*>(hdr));
+    const float mn = f16_to_f32(*reinterpret_cast<const uint16_t*>(hdr + 2));
+    const float d1 = d * (float)sc, m1 = mn * (float)m;
+    return d1 * (float)q - m1;
+}
+
+// one row of a table (row length dim) -> fp32, times scale
+__device__ float table_elem(const void* w, int type, int rows, int dim, int row, int i) {
+    switch (type) {
+    case G4_F32: return reinterpret_cast<const float*>(w)[(size_t)row * dim + i];
+    case G4_F16: return f16_to_f32(reinterpret_cast<const uint16_t*>(w)[(size_t)row * dim + i]);
+    case G4_BF16: return bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[(size_t)row * dim + i]);
+    default: {
+        const int nb = dim / 256;
+        return dequant_elem((const uint8_t*)w, type, (size_t)rows * nb, (size_t)row * nb + i / 256, i & 255);
+    }
+    }
+}
+
+__global__ __launch_bounds__(256) void emb_lookup_kernel(float* __restrict__ o, const void* w, int type, int rows,
+                                                         int dim, const int* dtok, int tok, int use_scale,
+                                                         float scale) {
+    const int id = dtok ? *dtok : tok;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim || id < 0 || id >= rows) return;
+    const float v = table_elem(w, type, rows, dim, id, i);
+    o[i] = use_scale ? v * scale : v;
+}
+
+// build_ple after the context projection (main.c:1751-1777): workgroup l
+// owns slice l of pd elements.
+//   row  = emb_lookup(ple_tok, token)[l*pd + i] * sc_tok
+//   ctx  = rmsnorm(ctx[l*pd + i] * sc_ctx, proj_norm)
+//   ple  = (row + ctx) * mix
+struct PleArgs {
+    const void* ple_tok;
+    const float* ctx;
+    const float* proj_norm;
+    float* ple;
+    const int* dtok;
+    int tok, type, rows, pd, L;
+    float sc_tok, sc_ctx, mix, eps;
+};
+
+__global__ __launch_bounds__(256) void ple_finish_kernel(PleArgs a) {
+    extern __shared__ __align__(16) float c[];
+    __shared__ float red[16];
+    const int l = blockIdx.x, pd = a.pd;
+    const int id = a.dtok ? *a.dtok : a.tok;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < pd; i += blockDim.x) {
+        const float v = a.ctx[(size_t)l * pd + i] * a.sc_ctx;
+        c[i] = v;
+        ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    const float s = 1.0f / sqrtf(ss / (float)pd + a.eps);
+    if (id < 0 || id >= a.rows) return;
+    for (int i = threadIdx.x; i < pd; i += blockDim.x) {
+        const float ctxn = (c[i] * s) * a.proj_norm[i];
+        const float row = table_elem(a.ple_tok, a.type, a.rows, pd * a.L, id, l * pd + i) * a.sc_tok;
+        a.ple[(size_t)l * pd + i] = (row + ctxn) * a.mix;
+    }
+}
+
+// g = gelu(g) * ple (main.c:1989-1993), then Q8_K of g for the next GEMV
+__global__ __launch_bounds__(256) void gelu_mul_quant_kernel(float* __restrict__ g, const float* __restrict__ ple,
+                                                             int n, uint8_t* __restrict__ q8) {
+    const int lane = threadIdx.x & 63;
+    const int nb = n / 256;
+    for (int b = threadIdx.x >> 6; b < nb; b += blockDim.x >> 6) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = b * 256 + 4 * lane + e;
+            const float t = gelu_ref(g[i]);
+            v[e] = t * ple[i];
+            g[i] = v[e];
+        }
+        if (q8) quantize_block_wave(v, lane, q8, nb, b);
+    }
+}
+
+// ---- argmax, first index of the maximum ------------------------------------
+// key = order-preserving bits of the value (high word) and ~index (low word):
+// the largest key is the largest value at its smallest index.  -0.0 is taken
+// as +0.0 so that equal values compare equal, as the C comparison does.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)i);
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+__device__ unsigned long long block_max_u64(unsigned long long k, unsigned long long* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    k = wave_max_u64(k);
+    if (lane == 0) red[w] = k;
+    __syncthreads();
+    unsigned long long t = 0;
+    for (int i = 0; i < nw; i++) t = red[i] > t ? red[i] : t;
+    return t;
+}
+
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxPer = 4096;   // elements per partial workgroup
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const float* __restrict__ v, int n,
+                                                                        unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[4];
+    const int base = blockIdx.x * kArgmaxPer;
+    unsigned long long k = 0;
+    for (int i = base + threadIdx.x; i < min(n, base + kArgmaxPer); i += kArgmaxThreads) {
+        const unsigned long long t = argmax_key(v[i], i);
+        k = t > k ? t : k;
+    }
+    k = block_max_u64(k, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = k;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const unsigned long long* __restrict__ part,
+                                                                      int np, int* __restrict__ out,
+                                                                      int* __restrict__ dtok, int* __restrict__ dpos) {
+    __shared__ unsigned long long red[4];
+    unsigned long long k = 0;
+    for (int i = threadIdx.x; i < np; i += kArgmaxThreads) k = part[i] > k ? part[i] : k;
+    k = block_max_u64(k, red);
+    if (threadIdx.x == 0) {
+        const int idx = (int)(~(uint32_t)(k & 0xffffffffu));
+        if (out) *out = idx;
+        if (dtok) *dtok = idx;
+        if (dpos) *dpos = *dpos + 1;
+    }
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+static bool table_type_ok(int type) {
+    return type == G4_F32 || type == G4_F16 || type == G4_BF16 || type == G4_Q4_K || type == G4_Q5_K ||
+           type == G4_Q6_K;
+}
+
+// emb_lookup(float *o, const void *w, int type, int id, int dim), main.c:1696;
+// rows = the table's row count (bounds check; the reference trusts id).
+extern "C" int g4_emb_lookup(float* o, const void* w, int type, int rows, int id, int dim) {
+    G4_CHECK_ARG(o && w && dim > 0 && rows > 0, "g4_emb_lookup: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    G4_CHECK_ARG(id >= 0 && id < rows, "g4_emb_lookup: id %d out of range (%d rows)", id, rows);
+    G4_CHECK_ARG(type < G4_Q4_K || type == G4_BF16 || dim % 256 == 0, "g4_emb_lookup: dim %d", dim);
+    hipLaunchKernelGGL(emb_lookup_kernel, dim3((dim + 255) / 256), dim3(256), 0, g4_stream(), o, w, type, rows, dim,
+                       nullptr, id, 0, 1.0f);
+    return g4_check_launch("emb_lookup_kernel");
+}
+
+// Engine form: token from device memory, result times `scale` (main.c:1849-1854).
+extern "C" int g4_emb_lookup_dev(float* o, const void* w, int type, int rows, const int* dtok, int dim, float scale) {
+    G4_CHECK_ARG(o && w && dtok && dim > 0 && rows > 0, "g4_emb_lookup_dev: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    hipLaunchKernelGGL(emb_lookup_kernel, dim3((dim + 255) / 256), dim3(256), 0, g4_stream(), o, w, type, rows, dim,
+                       dtok, 0, 1, scale);
+    return g4_check_launch("emb_lookup_kernel");
+}
+
+extern "C" int g4_ple_finish(float* ple, const float* ctx, const void* ple_tok, int type, int rows, const float* proj_norm,
+                             const int* dtok, int tok, int pd, int L, float sc_tok, float sc_ctx, float mix, float eps) {
+    G4_CHECK_ARG(ple && ctx && ple_tok && proj_norm && pd > 0 && pd <= 4096 && L > 0, "g4_ple_finish: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    PleArgs a{ple_tok, ctx, proj_norm, ple, dtok, tok, type, rows, pd, L, sc_tok, sc_ctx, mix, eps};
+    hipLaunchKernelGGL(ple_finish_kernel, dim3(L), dim3(256), (size_t)pd * 4, g4_stream(), a);
+    return g4_check_launch("ple_finish_kernel");
+}
+
+extern "C" int g4_gelu_mul_quant(float* g, const float* ple, int n, void* q8) {
+    G4_CHECK_ARG(g && ple && n > 0 && n % 256 == 0, "g4_gelu_mul_quant: n=%d must be a multiple of 256", n);
+    hipLaunchKernelGGL(gelu_mul_quant_kernel, dim3(1), dim3(256), 0, g4_stream(), g, ple, n, (uint8_t*)q8);
+    return g4_check_launch("gelu_mul_quant_kernel");
+}
+
+extern "C" size_t g4_argmax_part_bytes(int n) { return (size_t)((n + kArgmaxPer - 1) / kArgmaxPer) * 8; }
+
+// first index of the maximum of v[0..n) (main.c:2045-2049) -> *out (device
+// int); with dtok/dpos (device, nullable) also stores the token as the next
+// step's input and advances the position.  part: g4_argmax_part_bytes(n).
+extern "C" int g4_argmax(const float* v, int n, int* out, void* part, int* dtok, int* dpos) {
+    G4_CHECK_ARG(v && n > 0 && part, "g4_argmax: bad arguments");
+    const int np = (n + kArgmaxPer - 1) / kArgmaxPer;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(np), dim3(kArgmaxThreads), 0, g4_stream(), v, n,
+                       (unsigned long long*)part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, g4_stream(),
+                       (const unsigned long long*)part, np, out, dtok, dpos);
+    return g4_check_launch("argmax kernels");
+}
+
+// ---- step scalars -----------------------------------------------------------
+__global__ void store_i32x2_kernel(int* __restrict__ dst, int a, int b) {
+    if (threadIdx.x == 0) { dst[0] = a; dst[1] = b; }
+}
+
+// dst[0] = a, dst[1] = b, ordered on the library stream (no host staging buffer,
+// so consecutive calls never race with their own copies)
+extern "C" int g4_store_i32x2(int* dst, int a, int b) {
+    G4_CHECK_ARG(dst, "g4_store_i32x2: null pointer");
+    hipLaunchKernelGGL(store_i32x2_kernel, dim3(1), dim3(64), 0, g4_stream(), dst, a, b);
+    return g4_check_launch("store_i32x2_kernel");
+}

@@ -1,0 +1,163 @@
+// norm.hip -- RMSNorm family on gfx950, plus the fused residual/norm/quantize
+// step kernel of the decode engine.
+//
+// Reference operations (gemma4-4b/cpu-blas/main.c):
+//   rmsnorm                       1451-1456: o[i] = (x[i] * s) * w[i]
+//   rmsnorm_head_inplace          1458-1466: v[i] = v[i] * (s * w[i])
+//   rmsnorm_head_noweight_inplace 1468-1476: v[i] = v[i] * s
+// with s = 1 / sqrtf(sum(x^2) / n + eps).  The elementwise products are
+// evaluated in the reference's order; the sum of squares is a tree (the
+// reference sums sequentially), so results agree to fp32 tolerance.
+#include "g4_device.h"
+#include "g4_internal.h"
+
+namespace g4 {
+
+constexpr int kNormThreads = 1024;
+
+// rms scale of x[0..n) by the whole workgroup
+__device__ __forceinline__ float rms_scale(const float* __restrict__ x, int n, float eps, float* red) {
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(float* __restrict__ o, const float* __restrict__ x,
+                                                               const float* __restrict__ w, int n, float eps) {
+    __shared__ float red[16];
+    const float s = rms_scale(x, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = (x[i] * s) * w[i];
+}
+
+// one workgroup per head; w == nullptr is the no-weight variant
+__global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict__ v, const float* __restrict__ w, int hd,
+                                                            float eps) {
+    __shared__ float red[16];
+    float* seg = v + (size_t)blockIdx.x * hd;
+    const float s = rms_scale(seg, hd, eps, red);
+    __syncthreads();   // every thread has read seg before it is overwritten
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) seg[i] = w ? seg[i] * (s * w[i]) : seg[i] * s;
+}
+
+// ---------------------------------------------------------------------------
+// Fused step kernel (one workgroup, n <= kResidualMax):
+//   if y:       x[i] = x[i] + (y[i] * s_y) * w_post[i]        (main.c:1960-1962,
+//               1982-1984, 1995-1997: post-norm then residual add)
+//   if oscale:  x[i] = x[i] * oscale[0]                       (main.c:1999-2003)
+//   if w_next:  xb2[i] = (x[i] * s_x) * w_next[i]             (main.c:1878, 1973)
+//   if q8:      q8 = quantize_row_q8_K(qsrc == 0 ? xb2 : x)   (main.c:1884, 1975)
+// ---------------------------------------------------------------------------
+constexpr int kResidualMax = 16384;
+
+struct ResidualArgs {
+    float* x;
+    const float* y;
+    const float* w_post;
+    const float* oscale;
+    const float* w_next;
+    float* xb2;
+    uint8_t* q8;
+    int qsrc;
+    int n;
+    float eps;
+};
+
+__global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArgs a) {
+    extern __shared__ __align__(16) float buf[];   // n floats: the vector to quantize
+    __shared__ float red[16];
+    const int n = a.n;
+    float* x = a.x;
+    if (a.y) {
+        const float sy = rms_scale(a.y, n, a.eps, red);
+        const float sc = a.oscale ? a.oscale[0] : 1.0f;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            float v = x[i] + (a.y[i] * sy) * a.w_post[i];
+            if (a.oscale) v = v * sc;
+            x[i] = v;
+            buf[i] = v;
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = x[i];
+    }
+    __syncthreads();
+    if (a.w_next) {
+        const float sx = rms_scale(buf, n, a.eps, red);
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float v = (buf[i] * sx) * a.w_next[i];
+            if (a.xb2) a.xb2[i] = v;
+            if (a.qsrc == 0) buf[i] = v;
+        }
+        __syncthreads();
+    }
+    if (a.q8) {
+        const int nb = n / 256, lane = threadIdx.x & 63;
+        for (int b = threadIdx.x >> 6; b < nb; b += blockDim.x >> 6) {
+            const float4 f = reinterpret_cast<const float4*>(buf + (size_t)b * 256)[lane];
+            const float v[4] = {f.x, f.y, f.z, f.w};
+            quantize_block_wave(v, lane, a.q8, nb, b);
+        }
+    }
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, const float* oscale, const float* w_next,
+                     float* xb2, void* q8, int qsrc, int n, float eps) {
+    G4_CHECK_ARG(x && n > 0 && n <= kResidualMax, "residual_norm: bad x or n=%d", n);
+    G4_CHECK_ARG(!y || w_post, "residual_norm: y without w_post");
+    G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm: n=%d not a multiple of 256 for Q8_K", n);
+    G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm: quantizing xb2 needs w_next");
+    ResidualArgs a{x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kNormThreads), (size_t)n * 4, g4_stream(), a);
+    return g4_check_launch("residual_norm_kernel");
+}
+
+extern "C" int g4_rmsnorm(float* o, const float* x, const float* w, int n, float eps) {
+    G4_CHECK_ARG(o && x && w && n > 0, "g4_rmsnorm: bad arguments (n=%d)", n);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, g4_stream(), o, x, w, n, eps);
+    return g4_check_launch("rmsnorm_kernel");
+}
+
+extern "C" int g4_rmsnorm_head_inplace(float* v, const float* w, int n_heads, int hd, float eps) {
+    G4_CHECK_ARG(v && w && n_heads > 0 && hd > 0, "g4_rmsnorm_head_inplace: bad arguments");
+    hipLaunchKernelGGL(rmsnorm_heads_kernel, dim3(n_heads), dim3(256), 0, g4_stream(), v, w, hd, eps);
+    return g4_check_launch("rmsnorm_heads_kernel");
+}
+
+extern "C" int g4_rmsnorm_head_noweight_inplace(float* v, int n_heads, int hd, float eps) {
+    G4_CHECK_ARG(v && n_heads > 0 && hd > 0, "g4_rmsnorm_head_noweight_inplace: bad arguments");
+    hipLaunchKernelGGL(rmsnorm_heads_kernel, dim3(n_heads), dim3(256), 0, g4_stream(), v, nullptr, hd, eps);
+    return g4_check_launch("rmsnorm_heads_kernel");
+}
+
+// softmax(float *x, int n), main.c:1478-1488: max, x = expf(x - max), divide
+// by the sum (one workgroup; the sum is a tree)
+__global__ __launch_bounds__(kNormThreads) void softmax_kernel(float* __restrict__ x, int n) {
+    __shared__ float red[16];
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, x[i]);
+    m = wave_max(m);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float e = expf(x[i] - mx);
+        x[i] = e;
+        s += e;
+    }
+    s = block_sum(s, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = x[i] / s;
+}
+
+extern "C" int g4_softmax(float* x, int n) {
+    G4_CHECK_ARG(x && n > 0, "g4_softmax: bad arguments");
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(kNormThreads), 0, g4_stream(), x, n);
+    return g4_check_launch("softmax_kernel");
+}

@@ -100,3 +100,47 @@ extern "C" int g4_event_elapsed_ms(void* start, void* stop, float* ms) {
     G4_HIP(hipEventSynchronize((hipEvent_t)stop));
     return g4_hip_status(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
 }
+
+extern "C" int g4_memcpy_h2d_async(void* dst, const void* src, size_t bytes) {
+    G4_CHECK_ARG(dst && src, "g4_memcpy_h2d_async: null pointer");
+    return g4_hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+}
+extern "C" int g4_memcpy_d2h_async(void* dst, const void* src, size_t bytes) {
+    G4_CHECK_ARG(dst && src, "g4_memcpy_d2h_async: null pointer");
+    return g4_hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+}
+extern "C" int g4_host_alloc(void** p, size_t bytes) {
+    G4_CHECK_ARG(p && bytes, "g4_host_alloc: bad arguments");
+    return g4_hip_status(hipHostMalloc(p, bytes, hipHostMallocDefault));
+}
+extern "C" int g4_host_free(void* p) { return p ? g4_hip_status(hipHostFree(p)) : G4_OK; }
+
+// ---- streams and graphs: a decode step is captured once and replayed ---------
+extern "C" int g4_stream_create(void** s) {
+    G4_CHECK_ARG(s, "g4_stream_create: null pointer");
+    return g4_hip_status(hipStreamCreateWithFlags((hipStream_t*)s, hipStreamNonBlocking));
+}
+extern "C" int g4_stream_destroy(void* s) { return s ? g4_hip_status(hipStreamDestroy((hipStream_t)s)) : G4_OK; }
+
+extern "C" int g4_graph_begin(void) {
+    if (!g_stream) return g4_fail(G4_ERR_STATE, "g4_graph_begin: capture needs a created stream (g4_set_stream)");
+    return g4_hip_status(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+}
+extern "C" int g4_graph_end(void** exec) {
+    G4_CHECK_ARG(exec, "g4_graph_end: null pointer");
+    hipGraph_t g = nullptr;
+    G4_HIP(hipStreamEndCapture(g_stream, &g));
+    hipGraphExec_t e = nullptr;
+    int rc = g4_hip_status(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
+    (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    *exec = (void*)e;
+    return G4_OK;
+}
+extern "C" int g4_graph_launch(void* exec) {
+    G4_CHECK_ARG(exec, "g4_graph_launch: null graph");
+    return g4_hip_status(hipGraphLaunch((hipGraphExec_t)exec, g_stream));
+}
+extern "C" int g4_graph_destroy(void* exec) {
+    return exec ? g4_hip_status(hipGraphExecDestroy((hipGraphExec_t)exec)) : G4_OK;
+}

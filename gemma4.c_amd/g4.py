@@ -57,6 +57,52 @@ _SIGS = {
     "g4_mm_gate_up_gelu": (I, [VP, VP, VP, I, I, I, VP]),
     "g4_debug_block_sums": (I, [VP, I, I, I, VP, VP, VP]),
     "g4_set_gemv_occupancy": (I, [I]),
+    "g4_rmsnorm": (I, [VP, VP, VP, I, F]),
+    "g4_rmsnorm_head_inplace": (I, [VP, VP, I, I, F]),
+    "g4_rmsnorm_head_noweight_inplace": (I, [VP, I, I, F]),
+    "g4_apply_rope_neox": (I, [VP, I, I, I, I, F, F, VP]),
+    "g4_kv_append_rope": (I, [VP, VP, VP, VP, VP, I, I, I, I, I, I, F, F, VP, F]),
+    "g4_attn_decode": (I, [VP, VP, VP, I, I, I, I, I, I, F, VP]),
+    "g4_attn_decode_ring": (I, [VP, VP, VP, I, I, I, I, I, I, I, F, VP]),
+    "g4_softmax": (I, [VP, I]),
+    "g4_emb_lookup": (I, [VP, VP, I, I, I, I]),
+    "g4_argmax_part_bytes": (SZ, [I]),
+    "g4_argmax": (I, [VP, I, VP, VP, VP, VP]),
+    "g4_residual_norm": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, F]),
+    "g4_qkv_post": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, F, F, VP, F]),
+    "g4_attn_part_bytes": (SZ, [I, I, I]),
+    "g4_attn_decode_dev": (I, [VP, VP, VP, I, I, VP, I, I, I, I, F, I, VP, VP, VP]),
+    "g4_emb_lookup_dev": (I, [VP, VP, I, I, VP, I, F]),
+    "g4_ple_finish": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
+    "g4_gelu_mul_quant": (I, [VP, VP, I, VP]),
+    "g4_store_i32x2": (I, [VP, I, I]),
+    "g4_memcpy_h2d_async": (I, [VP, VP, SZ]),
+    "g4_memcpy_d2h_async": (I, [VP, VP, SZ]),
+    "g4_host_alloc": (I, [C.POINTER(VP), SZ]),
+    "g4_host_free": (I, [VP]),
+    "g4_stream_create": (I, [C.POINTER(VP)]),
+    "g4_stream_destroy": (I, [VP]),
+    "g4_graph_begin": (I, []),
+    "g4_graph_end": (I, [C.POINTER(VP)]),
+    "g4_graph_launch": (I, [VP]),
+    "g4_graph_destroy": (I, [VP]),
+}
+
+_ENGINE_SIGS = {
+    "g4e_open_image": (I, [VP, SZ, I, I, C.POINTER(VP)]),
+    "g4e_check_image": (I, [VP, SZ, I, VP]),
+    "g4e_open_file": (I, [C.c_char_p, I, I, C.POINTER(VP)]),
+    "g4e_close": (None, [VP]),
+    "g4e_last_error": (C.c_char_p, []),
+    "g4e_config": (None, [VP, VP]),
+    "g4e_forward": (I, [VP, I, I, I]),
+    "g4e_read_logits": (I, [VP, VP]),
+    "g4e_read_x": (I, [VP, VP]),
+    "g4e_argmax": (I, [VP, C.POINTER(I)]),
+    "g4e_set_trace": (I, [VP, I]),
+    "g4e_layer_x": (C.POINTER(F), [VP]),
+    "g4e_generate_greedy": (I, [VP, VP, I, I, VP, C.POINTER(C.c_double), C.POINTER(C.c_double), I]),
+    "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
 }
 
 
@@ -169,3 +215,105 @@ def download_quant(lib: Lib, buf: DBuf, qtype: int, n: int, d: int) -> np.ndarra
     out = np.empty(lib.L.g4_tensor_bytes(qtype, n, d), np.uint8)
     lib.check(lib.L.g4_download_quant(out.ctypes.data, buf.ptr, qtype, n, d))
     return out
+
+
+class EngineLib:
+    """libg4engine.so (host/engine.h)."""
+    _inst = None
+
+    def __init__(self, path: str = ENGINE_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+        Lib.get()   # load libg4hip.so first (the engine links to it)
+        self.L = C.CDLL(path)
+        for name, (res, args) in _ENGINE_SIGS.items():
+            f = getattr(self.L, name)
+            f.restype = res
+            f.argtypes = args
+
+    @classmethod
+    def get(cls) -> "EngineLib":
+        if cls._inst is None:
+            cls._inst = EngineLib()
+        return cls._inst
+
+    def check(self, rc: int) -> None:
+        if rc != G4_OK:
+            raise G4Error(rc, self.L.g4e_last_error().decode())
+
+    def check_image(self, data, max_seq: int = 0) -> list[int]:
+        buf = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data
+        out = np.zeros(9, np.int32)
+        self.check(self.L.g4e_check_image(buf.ctypes.data, buf.size, max_seq, out.ctypes.data))
+        return [int(v) for v in out]
+
+
+class Engine:
+    """A model opened by the C engine; forward/generate run on the GPU."""
+
+    def __init__(self, path_or_image, max_seq: int = 0, device: int = 0):
+        self.E = EngineLib.get()
+        h = VP()
+        if isinstance(path_or_image, (str, bytes, os.PathLike)):
+            self.E.check(self.E.L.g4e_open_file(os.fsencode(path_or_image), max_seq, device, C.byref(h)))
+        else:
+            a = np.ascontiguousarray(path_or_image).view(np.uint8).reshape(-1)
+            self.E.check(self.E.L.g4e_open_image(a.ctypes.data, a.size, max_seq, device, C.byref(h)))
+        self.h = h.value
+        cfg = np.zeros(9, np.int32)
+        self.E.L.g4e_config(self.h, cfg.ctypes.data)
+        (self.dim, self.hidden, self.n_layers, self.n_heads, self.n_kv, self.vocab,
+         self.max_seq, self.ple_dim, self.window) = [int(v) for v in cfg]
+
+    def forward(self, token: int, pos: int, lm_mode: int = 1) -> None:
+        self.E.check(self.E.L.g4e_forward(self.h, token, pos, lm_mode))
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        self.E.check(self.E.L.g4e_read_logits(self.h, out.ctypes.data))
+        return out
+
+    def x(self) -> np.ndarray:
+        out = np.empty(self.dim, np.float32)
+        self.E.check(self.E.L.g4e_read_x(self.h, out.ctypes.data))
+        return out
+
+    def argmax(self) -> int:
+        t = C.c_int()
+        self.E.check(self.E.L.g4e_argmax(self.h, C.byref(t)))
+        return t.value
+
+    def set_trace(self, on: bool) -> None:
+        self.E.check(self.E.L.g4e_set_trace(self.h, int(on)))
+
+    def layer_x(self) -> np.ndarray:
+        p = self.E.L.g4e_layer_x(self.h)
+        return np.ctypeslib.as_array(p, (self.n_layers + 1, self.dim)).copy()
+
+    def generate_greedy(self, prompt, max_new: int, use_graph: bool = True):
+        pr = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max_new + 1, np.int32)
+        ps, ds = C.c_double(), C.c_double()
+        n = self.E.L.g4e_generate_greedy(self.h, pr.ctypes.data, pr.size, max_new, out.ctypes.data,
+                                         C.byref(ps), C.byref(ds), int(use_graph))
+        if n < 0:
+            self.E.check(-n)
+        return out[:n].copy(), ps.value, ds.value
+
+    def decode_steps(self, token: int, pos0: int, steps: int, use_graph: bool = True, record: bool = False):
+        out = np.zeros(max(steps, 1), np.int32)
+        sec = C.c_double()
+        self.E.check(self.E.L.g4e_decode_steps(self.h, token, pos0, steps, int(use_graph),
+                                               out.ctypes.data if record else None, C.byref(sec)))
+        return (out[:steps].copy() if record else None), sec.value
+
+    def close(self) -> None:
+        if self.h:
+            self.E.L.g4e_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

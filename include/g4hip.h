@@ -118,6 +118,107 @@ int g4_mm_gate_up_gelu(float *hb, const void *gate, const void *up, int n, int d
 /* Debug: per-block exact integer sums S_b, M_b (int32, d*nb each) of
  * Q4_K/Q5_K x Q8_K (main.c:500-523 summed over lanes). */
 int g4_debug_block_sums(const void *w, int n, int d, int type, const void *q8, int32_t *S, int32_t *M);
+/* logits_tied's GEMV + soft-cap (main.c:1788-1795): o = cap*tanh(W.x / cap) */
+int g4_mm_quant_rows_softcap(float *o, const float *x, const void *w, int n, int d, int type, float cap);
+/* tiling knob of the K-quant GEMVs (workgroups per CU targeted; default 4) */
+int g4_set_gemv_occupancy(int wg_per_cu);
+
+/* ---------------------------------------------------------------------------
+ * Norms, RoPE, attention (main.c:1451-1488, 1725-1745, 1886-1950)
+ * ------------------------------------------------------------------------- */
+/* rmsnorm(float *o, const float *x, const float *w, int n, float eps), main.c:1451 */
+int g4_rmsnorm(float *o, const float *x, const float *w, int n, float eps);
+/* rmsnorm_head_inplace(float *v, const float *w, int n_heads, int hd, float eps), main.c:1458 */
+int g4_rmsnorm_head_inplace(float *v, const float *w, int n_heads, int hd, float eps);
+/* rmsnorm_head_noweight_inplace(float *v, int n_heads, int hd, float eps), main.c:1468 */
+int g4_rmsnorm_head_noweight_inplace(float *v, int n_heads, int hd, float eps);
+/* apply_rope_neox(float *vec, int n_heads, int head_dim, int n_rot, int pos,
+ * float freq_base, float freq_scale, const float *freq_factors), main.c:1725 */
+int g4_apply_rope_neox(float *vec, int n_heads, int head_dim, int n_rot, int pos, float freq_base, float freq_scale,
+                       const float *freq_factors);
+/* K/V append of main.c:1895-1904: k <- RoPE(rmsnorm_head(k, k_norm)), v <-
+ * rmsnorm_head_noweight(v), stored at slot (ring ? pos % ring : pos) of
+ * kc/vc (row stride kv_stride floats).  k and v are left unchanged. */
+int g4_kv_append_rope(float *k, float *v, const float *k_norm, float *kc, float *vc, int kv_stride, int ring, int pos,
+                      int n_kv, int hd, int n_rot, float freq_base, float freq_scale, const float *freq_factors,
+                      float eps);
+/* The attention block of main.c:1909-1950 (inline in forward(), no function
+ * of its own there): per q head h, s_t = attn_scale * K[t].q_h over
+ * t = t_start .. t_start+nwin-1 of kv head h/(n_heads/n_kv), softmax, o_h =
+ * sum_t p_t V[t].  kc/vc: position 0 of a flat cache, row stride kv_stride
+ * floats (main.c:1798-1809 uses 1024).  hd in {256, 512}. */
+int g4_attn_decode(const float *q, const float *kc, const float *vc, int kv_stride, int t_start, int nwin, int n_heads,
+                   int n_kv, int hd, float attn_scale, float *out);
+/* Same block over a ring cache of `ring` slots (slot = t % ring) with the
+ * sliding window of main.c:1910-1915 (window 0 = full attention). */
+int g4_attn_decode_ring(const float *q, const float *kc, const float *vc, int kv_stride, int ring, int pos, int window,
+                        int n_heads, int n_kv, int hd, float attn_scale, float *out);
+/* softmax(float *x, int n), main.c:1478 */
+int g4_softmax(float *x, int n);
+
+/* ---------------------------------------------------------------------------
+ * Step glue (main.c:1696-1778, 1988-1993, 2045-2049)
+ * ------------------------------------------------------------------------- */
+/* emb_lookup(float *o, const void *w, int type, int id, int dim), main.c:1696;
+ * rows = the table's row count (checked; the reference trusts id). */
+int g4_emb_lookup(float *o, const void *w, int type, int rows, int id, int dim);
+/* first index of the maximum of v[0..n) (sample_token, temp <= 0,
+ * main.c:2045-2049) -> *out (device int).  part: g4_argmax_part_bytes(n)
+ * device bytes.  dtok/dpos (device, nullable): also store the token as the
+ * next step's input and advance the position by one. */
+size_t g4_argmax_part_bytes(int n);
+int    g4_argmax(const float *v, int n, int *out, void *part, int *dtok, int *dpos);
+
+/* ---------------------------------------------------------------------------
+ * Engine step kernels: fusions of consecutive statements of forward()
+ * (main.c:1838-2029) whose position/token come from device memory, so that a
+ * captured graph of one decode step is valid at every position.
+ * ------------------------------------------------------------------------- */
+/* x += rmsnorm(y, w_post) (if y); x *= oscale[0] (if oscale); xb2 =
+ * rmsnorm(x, w_next) (if w_next); q8 = Q8_K(qsrc ? x : xb2) (if q8).
+ * main.c:1960-1962, 1982-1984, 1995-2003, 1878-1884, 1973-1975, 2021. */
+int g4_residual_norm(float *x, const float *y, const float *w_post, const float *oscale, const float *w_next,
+                     float *xb2, void *q8, int qsrc, int n, float eps);
+/* main.c:1886-1904: q heads q_norm + RoPE in place; if k: k heads k_norm +
+ * RoPE and v heads unweighted norm, stored at slot (ring ? pos%ring : pos);
+ * pos = *dpos if dpos else pos. */
+int g4_qkv_post(float *q, const float *q_norm, const float *k, const float *v, const float *k_norm, float *kc,
+                float *vc, int kv_stride, int ring, const int *dpos, int pos, int n_heads, int n_kv, int hd, int n_rot,
+                float freq_base, float freq_scale, const float *ff, float eps);
+/* attention block with pos = *dpos, t_start = max(0, pos+1-window) (window 0:
+ * 0), G time chunks (fixed; <= 1024 positions each), partials buffer of
+ * g4_attn_part_bytes(n_heads, hd, G) bytes, optional Q8_K of the output. */
+size_t g4_attn_part_bytes(int n_heads, int hd, int G);
+int    g4_attn_decode_dev(const float *q, const float *kc, const float *vc, int kv_stride, int ring, const int *dpos,
+                          int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float *part, float *out,
+                          void *q8);
+/* x = emb_lookup(w, *dtok) * scale (main.c:1849-1854) */
+int g4_emb_lookup_dev(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale);
+/* build_ple after its projection (main.c:1751-1777): ple[l*pd+i] =
+ * (emb(ple_tok, tok)[l*pd+i]*sc_tok + rmsnorm(ctx[l*pd..]*sc_ctx, norm)[i]) * mix;
+ * tok = *dtok if dtok else tok. */
+int g4_ple_finish(float *ple, const float *ctx, const void *ple_tok, int type, int rows, const float *proj_norm,
+                  const int *dtok, int tok, int pd, int L, float sc_tok, float sc_ctx, float mix, float eps);
+/* g = gelu(g) * ple, then q8 = Q8_K(g) if q8 (main.c:1989-1993) */
+int g4_gelu_mul_quant(float *g, const float *ple, int n, void *q8);
+/* dst[0] = a, dst[1] = b on the library stream (the step's token and position) */
+int g4_store_i32x2(int *dst, int a, int b);
+
+/* ---------------------------------------------------------------------------
+ * Streams, graphs, copies
+ * ------------------------------------------------------------------------- */
+int g4_memcpy_h2d_async(void *dst, const void *src, size_t bytes);
+int g4_memcpy_d2h_async(void *dst, const void *src, size_t bytes);
+int g4_host_alloc(void **p, size_t bytes);   /* pinned host memory */
+int g4_host_free(void *p);
+int g4_stream_create(void **stream);
+int g4_stream_destroy(void *stream);
+/* capture the library stream's work into a graph (the stream must be a
+ * created one, not the null stream) */
+int g4_graph_begin(void);
+int g4_graph_end(void **graph_exec);
+int g4_graph_launch(void *graph_exec);
+int g4_graph_destroy(void *graph_exec);
 
 #ifdef __cplusplus
 }

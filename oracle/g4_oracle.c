@@ -768,6 +768,7 @@ struct or_model {
     float *kc, *vc;
     or_q8K *q8;
     float *stats; /* n_layers*3 + 8 */
+    float *layer_x; /* n_layers*dim: x after each layer of the last forward */
 };
 
 typedef struct { const uint8_t *d; uint64_t p, size; int bad; } or_rd;
@@ -1000,6 +1001,7 @@ or_model *or_model_open(const uint8_t *data, size_t size, int max_seq, char *err
     const int q8n = (m->hidden > OR_MAX_Q_DIM ? m->hidden : OR_MAX_Q_DIM) / OR_QK_K + 1;
     m->q8 = (or_q8K *)calloc((size_t)q8n, sizeof(or_q8K));
     m->stats = (float *)calloc((size_t)L * 3 + 8, 4);
+    m->layer_x = (float *)calloc((size_t)L * m->dim, 4);
     if (!m->kc || !m->vc) { or_model_close(m); set_err(err, errlen, "out of memory"); return NULL; }
     return m;
 }
@@ -1013,7 +1015,7 @@ void or_model_close(or_model *m) {
     free(m->down); free(m->inp_gate); free(m->proj);
     free(m->x); free(m->xb); free(m->xb2); free(m->hb); free(m->hb2); free(m->q); free(m->k);
     free(m->v); free(m->q_out); free(m->ple); free(m->ple_ctx); free(m->ple_gate); free(m->att);
-    free(m->logits); free(m->kc); free(m->vc); free(m->q8); free(m->stats);
+    free(m->logits); free(m->kc); free(m->vc); free(m->q8); free(m->stats); free(m->layer_x);
     free(m);
 }
 
@@ -1025,6 +1027,7 @@ void or_model_config(const or_model *m, int out[9]) {
 const float *or_model_logits(const or_model *m) { return m->logits; }
 const float *or_model_x(const or_model *m) { return m->x; }
 const float *or_model_layer_stats(const or_model *m) { return m->stats; }
+const float *or_model_layer_x(const or_model *m) { return m->layer_x; }
 
 /* main.c:1747-1778 */
 static void build_ple(or_model *m, int token) {
@@ -1043,90 +1046,89 @@ static void build_ple(or_model *m, int token) {
     free(row);
 }
 
-/* main.c:1838-2029 (debug dumps replaced by the stats array) */
-int or_forward(or_model *m, int token, int pos, int lm_mode) {
+/* One decoder layer of forward() (main.c:1865-2011) on m->x; x_before is
+ * dim floats of scratch. */
+static int layer_step(or_model *m, int l, int pos, float *x_before) {
     const int dim = m->dim, hidden = m->hidden, nh = m->n_heads, nkv = m->n_kv;
-    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= m->vocab) return -1;
-    if (or_emb_lookup(m->x, m->embd.p, m->embd.type, token, dim)) return -1;
-    const float es = sqrtf((float)dim);
-    for (int i = 0; i < dim; i++) m->x[i] = m->x[i] * es;
-    build_ple(m, token);
-    float *x_before = (float *)malloc((size_t)dim * sizeof(float));
-    for (int l = 0; l < m->n_layers; l++) {
-        const int hd = layer_hd(m, l), q_dim = nh * hd, kv_dim = nkv * hd;
-        const int swa = is_swa(m, l);
-        const int n_rot = swa ? m->rot_swa : m->rot_full;
-        const float base = swa ? m->theta_swa : m->theta;
-        const float *ff = swa ? NULL : m->rope_freqs;
-        memcpy(x_before, m->x, (size_t)dim * sizeof(float));
-        or_rmsnorm(m->xb2, m->x, m->attn_norm[l], dim, m->eps);
-        const int q8_att = (m->wq[l].type == OR_Q4_K || m->wq[l].type == OR_Q5_K);
-        if (q8_att) or_quantize_q8K(m->xb2, m->q8, dim);
-        if (or_mm(m->q, m->xb2, m->wq[l].p, dim, q_dim, m->wq[l].type, m->q8, q8_att)) goto fail;
-        or_rmsnorm_head_inplace(m->q, m->q_norm[l], nh, hd, m->eps);
-        or_apply_rope_neox(m->q, nh, hd, n_rot, pos, base, 1.0f, ff);
-        const int src = kv_source(m, l);
-        if (l < OR_N_LAYER_KV) {
-            if (or_mm(m->k, m->xb2, m->wk[l].p, dim, kv_dim, m->wk[l].type, m->q8, q8_att)) goto fail;
-            if (or_mm(m->v, m->xb2, m->wv[l].p, dim, kv_dim, m->wv[l].type, m->q8, q8_att)) goto fail;
-            or_rmsnorm_head_inplace(m->k, m->k_norm[l], nkv, hd, m->eps);
-            or_rmsnorm_head_noweight_inplace(m->v, nkv, hd, m->eps);
-            or_apply_rope_neox(m->k, nkv, hd, n_rot, pos, base, 1.0f, ff);
-            const size_t off = ((size_t)l * m->max_seq + pos) * OR_MAX_KV_DIM;
-            memcpy(m->kc + off, m->k, (size_t)kv_dim * sizeof(float));
-            memcpy(m->vc + off, m->v, (size_t)kv_dim * sizeof(float));
-            if (l == 0) {
-                float s, q2, a;
-                or_hidden_stats(m->k, kv_dim, &s, &q2, &a);
-                m->stats[(size_t)m->n_layers * 3 + 0] = s;
-                m->stats[(size_t)m->n_layers * 3 + 1] = q2;
-                m->stats[(size_t)m->n_layers * 3 + 2] = a;
-            }
-        }
-        const int src_hd = layer_hd(m, src);
-        int t_start = 0;
-        if (swa) { t_start = pos + 1 - m->window; if (t_start < 0) t_start = 0; }
-        const int nwin = pos + 1 - t_start;
-        (void)src_hd;
-        const float *kc0 = m->kc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
-        const float *vc0 = m->vc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
-        or_attn_decode(m->q, kc0, vc0, OR_MAX_KV_DIM, t_start, nwin, nh, nkv, hd, 1.0f, m->att, m->q_out);
+    const int hd = layer_hd(m, l), q_dim = nh * hd, kv_dim = nkv * hd;
+    const int swa = is_swa(m, l);
+    const int n_rot = swa ? m->rot_swa : m->rot_full;
+    const float base = swa ? m->theta_swa : m->theta;
+    const float *ff = swa ? NULL : m->rope_freqs;
+    memcpy(x_before, m->x, (size_t)dim * sizeof(float));
+    or_rmsnorm(m->xb2, m->x, m->attn_norm[l], dim, m->eps);
+    const int q8_att = (m->wq[l].type == OR_Q4_K || m->wq[l].type == OR_Q5_K);
+    if (q8_att) or_quantize_q8K(m->xb2, m->q8, dim);
+    if (or_mm(m->q, m->xb2, m->wq[l].p, dim, q_dim, m->wq[l].type, m->q8, q8_att)) return -1;
+    or_rmsnorm_head_inplace(m->q, m->q_norm[l], nh, hd, m->eps);
+    or_apply_rope_neox(m->q, nh, hd, n_rot, pos, base, 1.0f, ff);
+    const int src = kv_source(m, l);
+    if (l < OR_N_LAYER_KV) {
+        if (or_mm(m->k, m->xb2, m->wk[l].p, dim, kv_dim, m->wk[l].type, m->q8, q8_att)) return -1;
+        if (or_mm(m->v, m->xb2, m->wv[l].p, dim, kv_dim, m->wv[l].type, m->q8, q8_att)) return -1;
+        or_rmsnorm_head_inplace(m->k, m->k_norm[l], nkv, hd, m->eps);
+        or_rmsnorm_head_noweight_inplace(m->v, nkv, hd, m->eps);
+        or_apply_rope_neox(m->k, nkv, hd, n_rot, pos, base, 1.0f, ff);
+        const size_t off = ((size_t)l * m->max_seq + pos) * OR_MAX_KV_DIM;
+        memcpy(m->kc + off, m->k, (size_t)kv_dim * sizeof(float));
+        memcpy(m->vc + off, m->v, (size_t)kv_dim * sizeof(float));
         if (l == 0) {
             float s, q2, a;
-            or_hidden_stats(m->q_out, q_dim, &s, &q2, &a);
-            m->stats[(size_t)m->n_layers * 3 + 3] = s;
-            m->stats[(size_t)m->n_layers * 3 + 4] = q2;
-            m->stats[(size_t)m->n_layers * 3 + 5] = a;
+            or_hidden_stats(m->k, kv_dim, &s, &q2, &a);
+            m->stats[(size_t)m->n_layers * 3 + 0] = s;
+            m->stats[(size_t)m->n_layers * 3 + 1] = q2;
+            m->stats[(size_t)m->n_layers * 3 + 2] = a;
         }
-        if (or_mm(m->xb2, m->q_out, m->wo[l].p, q_dim, dim, m->wo[l].type, m->q8, 0)) goto fail;
-        or_rmsnorm(m->xb2, m->xb2, m->post_attn_norm[l], dim, m->eps);
-        for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
-        memcpy(x_before, m->x, (size_t)dim * sizeof(float));
-        or_rmsnorm(m->xb2, m->x, m->ffn_norm[l], dim, m->eps);
-        const int q8_ffn = (m->gate[l].type == OR_Q4_K || m->gate[l].type == OR_Q5_K);
-        if (q8_ffn) or_quantize_q8K(m->xb2, m->q8, dim);
-        if (or_mm(m->hb, m->xb2, m->gate[l].p, dim, hidden, m->gate[l].type, m->q8, q8_ffn)) goto fail;
-        if (or_mm(m->hb2, m->xb2, m->up[l].p, dim, hidden, m->up[l].type, m->q8, q8_ffn)) goto fail;
-        for (int i = 0; i < hidden; i++) m->hb[i] = or_gelu(m->hb[i]) * m->hb2[i];
-        if (or_mm(m->xb2, m->hb, m->down[l].p, hidden, dim, m->down[l].type, m->q8, 0)) goto fail;
-        or_rmsnorm(m->xb2, m->xb2, m->post_ffw_norm[l], dim, m->eps);
-        for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
-        memcpy(x_before, m->x, (size_t)dim * sizeof(float));
-        if (or_mm(m->ple_gate, m->x, m->inp_gate[l].p, dim, m->ple_dim, m->inp_gate[l].type, m->q8, 0)) goto fail;
-        for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = or_gelu(m->ple_gate[i]);
-        const float *ple_l = m->ple + (size_t)l * m->ple_dim;
-        for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = m->ple_gate[i] * ple_l[i];
-        if (or_mm(m->xb2, m->ple_gate, m->proj[l].p, m->ple_dim, dim, m->proj[l].type, m->q8, 0)) goto fail;
-        or_rmsnorm(m->xb2, m->xb2, m->post_norm[l], dim, m->eps);
-        for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
-        if (m->out_scale[l]) {
-            const float sc = m->out_scale[l][0];
-            for (int i = 0; i < dim; i++) m->x[i] = m->x[i] * sc;
-        }
-        or_hidden_stats(m->x, dim, &m->stats[3 * l], &m->stats[3 * l + 1], &m->stats[3 * l + 2]);
     }
-    free(x_before);
-    if (lm_mode == 0) return 0;
+    const int src_hd = layer_hd(m, src);
+    int t_start = 0;
+    if (swa) { t_start = pos + 1 - m->window; if (t_start < 0) t_start = 0; }
+    const int nwin = pos + 1 - t_start;
+    (void)src_hd;
+    const float *kc0 = m->kc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
+    const float *vc0 = m->vc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
+    or_attn_decode(m->q, kc0, vc0, OR_MAX_KV_DIM, t_start, nwin, nh, nkv, hd, 1.0f, m->att, m->q_out);
+    if (l == 0) {
+        float s, q2, a;
+        or_hidden_stats(m->q_out, q_dim, &s, &q2, &a);
+        m->stats[(size_t)m->n_layers * 3 + 3] = s;
+        m->stats[(size_t)m->n_layers * 3 + 4] = q2;
+        m->stats[(size_t)m->n_layers * 3 + 5] = a;
+    }
+    if (or_mm(m->xb2, m->q_out, m->wo[l].p, q_dim, dim, m->wo[l].type, m->q8, 0)) return -1;
+    or_rmsnorm(m->xb2, m->xb2, m->post_attn_norm[l], dim, m->eps);
+    for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
+    memcpy(x_before, m->x, (size_t)dim * sizeof(float));
+    or_rmsnorm(m->xb2, m->x, m->ffn_norm[l], dim, m->eps);
+    const int q8_ffn = (m->gate[l].type == OR_Q4_K || m->gate[l].type == OR_Q5_K);
+    if (q8_ffn) or_quantize_q8K(m->xb2, m->q8, dim);
+    if (or_mm(m->hb, m->xb2, m->gate[l].p, dim, hidden, m->gate[l].type, m->q8, q8_ffn)) return -1;
+    if (or_mm(m->hb2, m->xb2, m->up[l].p, dim, hidden, m->up[l].type, m->q8, q8_ffn)) return -1;
+    for (int i = 0; i < hidden; i++) m->hb[i] = or_gelu(m->hb[i]) * m->hb2[i];
+    if (or_mm(m->xb2, m->hb, m->down[l].p, hidden, dim, m->down[l].type, m->q8, 0)) return -1;
+    or_rmsnorm(m->xb2, m->xb2, m->post_ffw_norm[l], dim, m->eps);
+    for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
+    memcpy(x_before, m->x, (size_t)dim * sizeof(float));
+    if (or_mm(m->ple_gate, m->x, m->inp_gate[l].p, dim, m->ple_dim, m->inp_gate[l].type, m->q8, 0)) return -1;
+    for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = or_gelu(m->ple_gate[i]);
+    const float *ple_l = m->ple + (size_t)l * m->ple_dim;
+    for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = m->ple_gate[i] * ple_l[i];
+    if (or_mm(m->xb2, m->ple_gate, m->proj[l].p, m->ple_dim, dim, m->proj[l].type, m->q8, 0)) return -1;
+    or_rmsnorm(m->xb2, m->xb2, m->post_norm[l], dim, m->eps);
+    for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
+    if (m->out_scale[l]) {
+        const float sc = m->out_scale[l][0];
+        for (int i = 0; i < dim; i++) m->x[i] = m->x[i] * sc;
+    }
+    or_hidden_stats(m->x, dim, &m->stats[3 * l], &m->stats[3 * l + 1], &m->stats[3 * l + 2]);
+    if (m->layer_x) memcpy(m->layer_x + (size_t)l * dim, m->x, (size_t)dim * sizeof(float));
+    return 0;
+}
+
+/* main.c:2021-2028: final norm and logits_tied (lm_mode 2 is unreachable with
+ * softcap > 0) */
+static int lm_head(or_model *m) {
+    const int dim = m->dim;
     or_rmsnorm(m->x, m->x, m->norm_out, dim, m->eps);
     /* logits_tied, main.c:1780-1796 (lm_mode 2 is unreachable with softcap > 0) */
     if (or_mm(m->logits, m->x, m->embd.p, dim, m->vocab, m->embd.type, m->q8, 0)) return -1;
@@ -1136,9 +1138,49 @@ int or_forward(or_model *m, int token, int pos, int lm_mode) {
         for (int i = 0; i < m->vocab; i++) m->logits[i] = cap * tanhf(m->logits[i] * inv);
     }
     return 0;
-fail:
+}
+
+static int embed_ple(or_model *m, int token, int pos) {
+    const int dim = m->dim;
+    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= m->vocab) return -1;
+    if (or_emb_lookup(m->x, m->embd.p, m->embd.type, token, dim)) return -1;
+    const float es = sqrtf((float)dim);
+    for (int i = 0; i < dim; i++) m->x[i] = m->x[i] * es;
+    build_ple(m, token);
+    return 0;
+}
+
+/* main.c:1838-2029 (debug dumps replaced by the stats array) */
+int or_forward(or_model *m, int token, int pos, int lm_mode) {
+    if (embed_ple(m, token, pos)) return -1;
+    float *x_before = (float *)malloc((size_t)m->dim * sizeof(float));
+    for (int l = 0; l < m->n_layers; l++) {
+        if (layer_step(m, l, pos, x_before)) { free(x_before); return -1; }
+    }
     free(x_before);
-    return -1;
+    if (lm_mode == 0) return 0;
+    return lm_head(m);
+}
+
+/* forward() with every layer's input taken from x_in ((n_layers+1) x dim:
+ * row 0 is the input of layer 0, row l+1 the input of layer l+1, row
+ * n_layers the input of the final norm).  Layer l's output goes to row l of
+ * x_out (n_layers x dim).  The KV cache is written from the injected inputs,
+ * so each layer is checked in isolation against a device run that produced
+ * x_in.  The embedding of the token is still computed (build_ple uses it). */
+int or_forward_inject(or_model *m, int token, int pos, int lm_mode, const float *x_in, float *x_out) {
+    const int dim = m->dim;
+    if (embed_ple(m, token, pos)) return -1;
+    float *x_before = (float *)malloc((size_t)dim * sizeof(float));
+    for (int l = 0; l < m->n_layers; l++) {
+        memcpy(m->x, x_in + (size_t)l * dim, (size_t)dim * sizeof(float));
+        if (layer_step(m, l, pos, x_before)) { free(x_before); return -1; }
+        memcpy(x_out + (size_t)l * dim, m->x, (size_t)dim * sizeof(float));
+    }
+    free(x_before);
+    if (lm_mode == 0) return 0;
+    memcpy(m->x, x_in + (size_t)m->n_layers * dim, (size_t)dim * sizeof(float));
+    return lm_head(m);
 }
 
 static double now_s(void) {

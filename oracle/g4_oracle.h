@@ -136,11 +136,18 @@ void      or_model_close(or_model *m);
 /* config query: dim, hidden, n_layers, n_heads, n_kv, vocab, max_seq, ple_dim, window */
 void      or_model_config(const or_model *m, int out[9]);
 int       or_forward(or_model *m, int token, int pos, int lm_mode);   /* main.c:1838-2029 */
+/* forward() with layer inputs injected: x_in is (n_layers+1) x dim (row l =
+ * input of layer l, row n_layers = input of the final norm); x_out gets each
+ * layer's output (n_layers x dim).  Checks every layer of a device run in
+ * isolation. */
+int       or_forward_inject(or_model *m, int token, int pos, int lm_mode, const float *x_in, float *x_out);
 const float *or_model_logits(const or_model *m);
 const float *or_model_x(const or_model *m);
 /* Per-layer fingerprints captured during the last forward (sum,l2,max per layer
  * after the layer, plus K_store and q_out of layer 0). n_layers*3 floats. */
 const float *or_model_layer_stats(const or_model *m);
+/* x after every layer of the last forward (n_layers*dim floats) */
+const float *or_model_layer_x(const or_model *m);
 /* Greedy generation loop (main.c:2335-2488 with temp=0): prompt is fed
  * token-serially, then max_new tokens are produced.  out_tokens receives
  * the generated ids; returns the count.  Stops on eos/eot. */

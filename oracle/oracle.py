@@ -81,9 +81,11 @@ class Oracle:
             "or_model_close": (None, [VP]),
             "or_model_config": (None, [VP, VP]),
             "or_forward": (C.c_int, [VP, C.c_int, C.c_int, C.c_int]),
+            "or_forward_inject": (C.c_int, [VP, C.c_int, C.c_int, C.c_int, VP, VP]),
             "or_model_logits": (VP, [VP]),
             "or_model_x": (VP, [VP]),
             "or_model_layer_stats": (VP, [VP]),
+            "or_model_layer_x": (VP, [VP]),
             "or_generate_greedy": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, VP, VP]),
         }
         for name, (res, args) in sig.items():
@@ -172,6 +174,15 @@ class OracleModel:
         if self.o.L.or_forward(self.h, token, pos, lm_mode) != 0:
             raise RuntimeError("or_forward failed")
 
+    def forward_inject(self, token: int, pos: int, lm_mode: int, x_in: np.ndarray) -> np.ndarray:
+        """Each layer run from the given input rows; returns the layer outputs."""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        assert x_in.shape == (self.n_layers + 1, self.dim)
+        out = np.empty((self.n_layers, self.dim), np.float32)
+        if self.o.L.or_forward_inject(self.h, token, pos, lm_mode, _ptr(x_in), _ptr(out)) != 0:
+            raise RuntimeError("or_forward_inject failed")
+        return out
+
     def logits(self) -> np.ndarray:
         p = self.o.L.or_model_logits(self.h)
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (self.vocab,)).copy()
@@ -183,6 +194,10 @@ class OracleModel:
     def layer_stats(self) -> np.ndarray:
         p = self.o.L.or_model_layer_stats(self.h)
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (self.n_layers * 3 + 8,)).copy()
+
+    def layer_x(self) -> np.ndarray:
+        p = self.o.L.or_model_layer_x(self.h)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (self.n_layers, self.dim)).copy()
 
     def generate_greedy(self, prompt, max_new):
         pr = np.ascontiguousarray(prompt, np.int32)

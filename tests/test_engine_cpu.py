@@ -1,0 +1,101 @@
+"""CPU-side checks of the C engine's GGUF path (no GPU): parse_gguf's metadata
+defaults and the tensor checks of load_weights turn every malformed input the
+reference would exit(1) on (main.c:843, 1396-1399, 1690-1692) into a status
+code, before any device work."""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import synth
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import g4
+    return g4.EngineLib.get()
+
+
+def _image(tmp_path, shape, tensors=None, kvs=None, name="m.gguf"):
+    p = str(tmp_path / name)
+    synth.write_gguf(p, kvs if kvs is not None else synth.model_kvs(shape),
+                     tensors if tensors is not None else synth.model_tensors(shape), seed=3)
+    return np.fromfile(p, np.uint8)
+
+
+def test_check_image_ok(tmp_path, eng):
+    s = synth.tiny_shape()
+    img = _image(tmp_path, s)
+    cfg = eng.check_image(img)
+    assert cfg == [s.dim, s.hidden, s.n_layers, s.n_heads, s.n_kv, s.vocab, s.context, s.ple_dim, s.window]
+    assert eng.check_image(img, max_seq=32)[6] == 32
+
+
+def _expect(eng, img, code, text):
+    import g4
+    with pytest.raises(g4.G4Error) as e:
+        eng.check_image(img)
+    assert e.value.code == code
+    assert text in str(e.value)
+
+
+def test_bad_magic_and_truncation(tmp_path, eng):
+    import g4
+    img = _image(tmp_path, synth.tiny_shape())
+    bad = img.copy()
+    bad[0] ^= 0xFF
+    _expect(eng, bad, g4.G4_ERR_FORMAT, "invalid GGUF magic")
+    _expect(eng, img[:100].copy(), g4.G4_ERR_FORMAT, "truncated")
+    _expect(eng, img[: img.size // 2].copy(), g4.G4_ERR_FORMAT, "past the end")
+    _expect(eng, img[:10].copy(), g4.G4_ERR_FORMAT, "invalid GGUF magic")
+
+
+def _tensors_with(shape, name, **change):
+    ts = synth.model_tensors(shape)
+    out = []
+    for t in ts:
+        if t.name == name:
+            if change.get("drop"):
+                continue
+            t = dataclasses.replace(t, **{k: v for k, v in change.items() if k != "drop"})
+        out.append(t)
+    return out
+
+
+def test_unsupported_type(tmp_path, eng):
+    import g4
+    s = synth.tiny_shape()
+    ts = _tensors_with(s, "blk.3.attn_norm.weight", qtype=synth.F16,
+                       make=lambda r: np.ones(s.dim, np.float16))
+    _expect(eng, _image(tmp_path, s, ts), g4.G4_ERR_TYPE, "Unsupported tensor type 1 for blk.3.attn_norm.weight")
+
+
+def test_wrong_shape_and_missing(tmp_path, eng):
+    import g4
+    s = synth.tiny_shape()
+    ts = _tensors_with(s, "blk.2.attn_q.weight", ne=(s.dim, s.n_heads * s.hd_swa + 256),
+                       make=lambda r: synth.rand_q4K(r, s.n_heads * s.hd_swa + 256, s.dim))
+    _expect(eng, _image(tmp_path, s, ts), g4.G4_ERR_FORMAT, "blk.2.attn_q.weight: shape")
+    ts = _tensors_with(s, "blk.7.ffn_down.weight", drop=True)
+    _expect(eng, _image(tmp_path, s, ts, name="m2.gguf"), g4.G4_ERR_FORMAT, "missing tensor blk.7.ffn_down.weight")
+    ts = _tensors_with(s, "output_norm.weight", drop=True)
+    _expect(eng, _image(tmp_path, s, ts, name="m3.gguf"), g4.G4_ERR_FORMAT, "missing tensor output_norm.weight")
+
+
+def test_token_embd_must_be_q6K(tmp_path, eng):
+    import g4
+    s = synth.tiny_shape()
+    ts = _tensors_with(s, "token_embd.weight", qtype=synth.F32, ne=(s.dim, s.vocab),
+                       make=lambda r: np.zeros((s.vocab, s.dim), np.float32))
+    _expect(eng, _image(tmp_path, s, ts), g4.G4_ERR_TYPE, "token_embd.weight")
+
+
+def test_open_without_gpu_fails_cleanly(tmp_path, eng):
+    """No HIP device here: opening reports G4_ERR_NODEV instead of crashing."""
+    import g4
+    if g4.Lib.get().L.g4_init(0) == g4.G4_OK:
+        pytest.skip("a GPU is present")
+    img = _image(tmp_path, synth.tiny_shape())
+    with pytest.raises(g4.G4Error) as e:
+        g4.Engine(img)
+    assert e.value.code == g4.G4_ERR_NODEV

@@ -1,0 +1,326 @@
+"""GPU parity of the decode-step kernels other than the GEMVs: RMSNorm family,
+Neox RoPE, KV append, ISWA decode attention, embedding lookup, the PLE input,
+GELU gate, argmax, and the fused residual/norm/quantize kernel -- against the
+CPU oracle (pinned to the reference's own functions, tests/test_oracle.py).
+
+Bars: bit-exact where the operation order is the reference's (embedding
+lookup, argmax, Q8_K of a given fp32 vector); fp32 reductions that the GPU
+sums as a tree are held to a stated relative tolerance; attention to 1e-4 of
+max|o| (the north-star bar for attention outputs).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+from oracle import Q8K_DTYPE
+
+pytestmark = pytest.mark.gpu
+
+P = lambda a: a.ctypes.data  # noqa: E731
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from g4 import Lib
+    L = Lib.get()
+    L.init(0)
+    L.L.g4_set_stream(None)
+    return L
+
+
+def dbuf(lib, a):
+    from g4 import DBuf
+    return DBuf.from_array(lib, np.ascontiguousarray(a))
+
+
+def empty(lib, nbytes):
+    from g4 import DBuf
+    return DBuf(lib, nbytes)
+
+
+def rel_err(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+# ---------------------------------------------------------------------------
+# norms, softmax
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [256, 2560, 10240, 333])
+def test_rmsnorm(lib, orc, n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    xd, wd, od = dbuf(lib, x), dbuf(lib, w), empty(lib, 4 * n)
+    lib.g4_rmsnorm(od.ptr, xd.ptr, wd.ptr, n, C.c_float(1e-6))
+    got = od.to_array(np.float32)
+    want = orc.rmsnorm(x, w)
+    # only the scale s differs (tree vs sequential sum of squares): a few ulps
+    assert rel_err(got, want) < 2e-6
+
+
+@pytest.mark.parametrize("hd,nh", [(256, 8), (512, 8), (256, 2)])
+def test_rmsnorm_heads(lib, orc, hd, nh):
+    rng = np.random.default_rng(hd + nh)
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    a = v.copy()
+    orc.L.or_rmsnorm_head_inplace(P(a), P(w), nh, hd, C.c_float(1e-6))
+    b = v.copy()
+    orc.L.or_rmsnorm_head_noweight_inplace(P(b), nh, hd, C.c_float(1e-6))
+    vd, wd = dbuf(lib, v), dbuf(lib, w)
+    lib.g4_rmsnorm_head_inplace(vd.ptr, wd.ptr, nh, hd, C.c_float(1e-6))
+    assert rel_err(vd.to_array(np.float32), a) < 2e-6
+    vd2 = dbuf(lib, v)
+    lib.g4_rmsnorm_head_noweight_inplace(vd2.ptr, nh, hd, C.c_float(1e-6))
+    assert rel_err(vd2.to_array(np.float32), b) < 2e-6
+
+
+def test_softmax(lib, orc):
+    rng = np.random.default_rng(9)
+    for n in (1, 7, 512, 4097):
+        x = (rng.standard_normal(n) * 8).astype(np.float32)
+        want = x.copy()
+        orc.L.or_softmax(P(want), n)
+        xd = dbuf(lib, x)
+        lib.g4_softmax(xd.ptr, n)
+        got = xd.to_array(np.float32)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-7 * want.max())
+
+
+# ---------------------------------------------------------------------------
+# RoPE: the angle chain is replayed exactly; only cosf/sinf may differ by ulps
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("hd,n_rot,base,use_ff", [(256, 256, 1e4, False), (512, 512, 1e6, True), (512, 512, 1e6, False),
+                                                  (256, 128, 1e4, False)])
+@pytest.mark.parametrize("pos", [0, 1, 7, 511, 4095, 32767])
+def test_rope(lib, orc, hd, n_rot, base, use_ff, pos):
+    rng = np.random.default_rng(hd + pos)
+    nh = 8
+    v = rng.standard_normal(nh * hd).astype(np.float32)
+    ff = rng.uniform(1.0, 4.0, n_rot // 2).astype(np.float32) if use_ff else None
+    want = orc.rope(v, nh, hd, n_rot, pos, base, ff)
+    vd = dbuf(lib, v)
+    ffd = dbuf(lib, ff) if use_ff else None
+    lib.g4_apply_rope_neox(vd.ptr, nh, hd, n_rot, pos, C.c_float(base), C.c_float(1.0), ffd.ptr if use_ff else None)
+    got = vd.to_array(np.float32)
+    if pos == 0:
+        assert np.array_equal(got, v)     # identity at pos 0 (design.md:524-534)
+    assert np.max(np.abs(got - want)) <= 4e-6 * np.max(np.abs(v))
+
+
+# ---------------------------------------------------------------------------
+# KV append + attention
+# ---------------------------------------------------------------------------
+def _attn_case(lib, orc, hd, n_heads, n_kv, T, t_start, scale, seed):
+    rng = np.random.default_rng(seed)
+    kv_dim = n_kv * hd
+    kc = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    vc = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    # typical post-norm magnitudes: |q|,|k| ~ sqrt(hd); scale keeps softmax non-degenerate
+    want = orc.attn(q, kc, vc, kv_dim, t_start, T - t_start, n_heads, n_kv, hd, scale)
+    qd, kd, vd, od = dbuf(lib, q), dbuf(lib, kc), dbuf(lib, vc), empty(lib, 4 * n_heads * hd)
+    lib.g4_attn_decode(qd.ptr, kd.ptr, vd.ptr, kv_dim, t_start, T - t_start, n_heads, n_kv, hd, C.c_float(scale), od.ptr)
+    return od.to_array(np.float32), want
+
+
+@pytest.mark.parametrize("hd", [256, 512])
+@pytest.mark.parametrize("T,t_start", [(1, 0), (2, 0), (37, 0), (512, 0), (700, 188), (4096, 0), (5000, 4488)])
+@pytest.mark.parametrize("scale", [1.0, 1.0 / 16])
+def test_attn_decode_flat(lib, orc, hd, T, t_start, scale):
+    got, want = _attn_case(lib, orc, hd, 8, 2, T, t_start, scale, seed=T + hd)
+    assert rel_err(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(2, 1), (8, 8), (4, 2)])
+def test_attn_decode_gqa_shapes(lib, orc, n_heads, n_kv):
+    got, want = _attn_case(lib, orc, 256, n_heads, n_kv, 300, 0, 1.0 / 16, seed=n_heads * 10 + n_kv)
+    assert rel_err(got, want) < 1e-4
+
+
+def test_attn_decode_long(lib, orc):
+    # a global layer at context 32768 (many chunks, log-sum-exp merge)
+    got, want = _attn_case(lib, orc, 256, 8, 2, 32768, 0, 1.0 / 16, seed=32768)
+    assert rel_err(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("hd,window,pos", [(256, 512, 100), (256, 512, 511), (256, 512, 512), (256, 512, 1500),
+                                           (512, 8, 30)])
+def test_kv_append_and_ring_attention(lib, orc, hd, window, pos):
+    """Ring-buffer cache (slot = t % window) against the reference's flat cache
+    (main.c:1798-1809), with the append of main.c:1895-1904 at every position."""
+    rng = np.random.default_rng(pos + hd)
+    n_heads, n_kv, eps = 8, 2, 1e-6
+    kv_dim = n_kv * hd
+    base = 1e4
+    k_norm = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    flat_k = np.zeros((pos + 1, kv_dim), np.float32)
+    flat_v = np.zeros((pos + 1, kv_dim), np.float32)
+    ring_k, ring_v = empty(lib, 4 * window * kv_dim), empty(lib, 4 * window * kv_dim)
+    knd = dbuf(lib, k_norm)
+    for t in range(pos + 1):
+        k = rng.standard_normal(kv_dim).astype(np.float32)
+        v = rng.standard_normal(kv_dim).astype(np.float32)
+        kk = k.copy()
+        orc.L.or_rmsnorm_head_inplace(P(kk), P(k_norm), n_kv, hd, C.c_float(eps))
+        kk = orc.rope(kk, n_kv, hd, hd, t, base)
+        vv = v.copy()
+        orc.L.or_rmsnorm_head_noweight_inplace(P(vv), n_kv, hd, C.c_float(eps))
+        flat_k[t], flat_v[t] = kk, vv
+        if t >= pos + 1 - window:
+            kd, vd = dbuf(lib, k), dbuf(lib, v)
+            lib.g4_kv_append_rope(kd.ptr, vd.ptr, knd.ptr, ring_k.ptr, ring_v.ptr, kv_dim, window, t, n_kv, hd, hd,
+                                  C.c_float(base), C.c_float(1.0), None, C.c_float(eps))
+    # the appended slot holds the normalised, rotated K and the normalised V
+    slot = pos % window
+    rk = ring_k.to_array(np.float32).reshape(window, kv_dim)
+    rv = ring_v.to_array(np.float32).reshape(window, kv_dim)
+    assert np.max(np.abs(rk[slot] - flat_k[pos])) < 1e-5
+    assert np.max(np.abs(rv[slot] - flat_v[pos])) < 1e-5
+    q = rng.standard_normal(n_heads * hd).astype(np.float32)
+    t_start = max(0, pos + 1 - window)
+    want = orc.attn(q, flat_k, flat_v, kv_dim, t_start, pos + 1 - t_start, n_heads, n_kv, hd, 1.0)
+    qd, od = dbuf(lib, q), empty(lib, 4 * n_heads * hd)
+    lib.g4_attn_decode_ring(qd.ptr, ring_k.ptr, ring_v.ptr, kv_dim, window, pos, window, n_heads, n_kv, hd,
+                            C.c_float(1.0), od.ptr)
+    assert rel_err(od.to_array(np.float32), want) < 1e-4
+
+
+def test_attn_dev_fused_quant(lib, orc):
+    """Engine form: device position, fixed chunk count, fused Q8_K output."""
+    rng = np.random.default_rng(77)
+    hd, nh, nkv, T = 512, 8, 2, 900
+    kv_dim = nkv * hd
+    kc = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    vc = rng.standard_normal((T, kv_dim)).astype(np.float32)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    pos = 640
+    want = orc.attn(q, kc, vc, kv_dim, 0, pos + 1, nh, nkv, hd, 1.0 / 16)
+    G = 8
+    part = empty(lib, lib.L.g4_attn_part_bytes(nh, hd, G))
+    qd, kd, vd, od = dbuf(lib, q), dbuf(lib, kc), dbuf(lib, vc), empty(lib, 4 * nh * hd)
+    dpos = dbuf(lib, np.array([pos], np.int32))
+    q8 = empty(lib, lib.L.g4_q8K_bytes(nh * hd))
+    lib.g4_attn_decode_dev(qd.ptr, kd.ptr, vd.ptr, kv_dim, 0, dpos.ptr, 0, nh, nkv, hd, C.c_float(1.0 / 16), G, part.ptr,
+                           od.ptr, q8.ptr)
+    got = od.to_array(np.float32)
+    assert rel_err(got, want) < 1e-4
+    h = np.zeros(nh * hd // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), nh * hd)
+    assert h.tobytes() == orc.quantize_q8K(got).tobytes()
+
+
+# ---------------------------------------------------------------------------
+# embedding lookup, PLE, GELU gate, argmax
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+def test_emb_lookup_bitexact(lib, orc, qtype):
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(qtype)
+    rows, dim = 300, 2560
+    raw = synth.rand_kquant(rng, qtype, rows, dim)
+    w = upload_quant(lib, raw, qtype, dim, rows)
+    out = DBuf(lib, 4 * dim)
+    for tok in (0, 17, 299):
+        lib.g4_emb_lookup(out.ptr, w.ptr, qtype, rows, tok, dim)
+        want = np.empty(dim, np.float32)
+        assert orc.L.or_emb_lookup(P(want), P(raw), qtype, tok, dim) == 0
+        assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
+    assert lib.L.g4_emb_lookup(out.ptr, w.ptr, qtype, rows, rows, dim) == 1   # G4_ERR_ARG, id out of range
+
+
+def test_ple_finish(lib, orc):
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(5)
+    L, pd, vocab, dim = 42, 256, 64, 2560
+    raw = synth.rand_q6K(rng, vocab, pd * L)
+    ctx = (rng.standard_normal(pd * L) * 20).astype(np.float32)
+    norm = rng.uniform(0.8, 1.2, pd).astype(np.float32)
+    tok = 37
+    w = upload_quant(lib, raw, 14, pd * L, vocab)
+    ctxd, nd = dbuf(lib, ctx), dbuf(lib, norm)
+    out = DBuf(lib, 4 * pd * L)
+    st, sc, mix = np.float32(np.sqrt(np.float32(pd))), np.float32(1) / np.sqrt(np.float32(dim)), np.float32(1) / np.sqrt(np.float32(2))
+    lib.g4_ple_finish(out.ptr, ctxd.ptr, w.ptr, 14, vocab, nd.ptr, None, tok, pd, L, C.c_float(st), C.c_float(sc),
+                      C.c_float(mix), C.c_float(1e-6))
+    # oracle composition of build_ple (main.c:1751-1777)
+    row = np.empty(pd * L, np.float32)
+    orc.L.or_emb_lookup(P(row), P(raw), 14, tok, pd * L)
+    row = row * st
+    c = ctx * sc
+    want = np.empty_like(c)
+    for l in range(L):
+        want[l * pd:(l + 1) * pd] = orc.rmsnorm(c[l * pd:(l + 1) * pd], norm)
+    want = (row + want) * mix
+    assert rel_err(out.to_array(np.float32), want) < 2e-6
+
+
+def test_gelu_mul_quant(lib, orc):
+    rng = np.random.default_rng(8)
+    g = (rng.standard_normal(256) * 3).astype(np.float32)
+    ple = rng.standard_normal(256).astype(np.float32)
+    want = np.array([orc.L.or_gelu(float(v)) for v in g], np.float32) * ple
+    gd, pd_, q8 = dbuf(lib, g), dbuf(lib, ple), empty(lib, 292)
+    lib.g4_gelu_mul_quant(gd.ptr, pd_.ptr, 256, q8.ptr)
+    got = gd.to_array(np.float32)
+    assert np.allclose(got, want, rtol=2e-6, atol=1e-7)   # tanhf: device libm vs glibc
+    h = np.zeros(1, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), 256)
+    assert h.tobytes() == orc.quantize_q8K(got).tobytes()
+
+
+def test_argmax_first_index(lib):
+    rng = np.random.default_rng(12)
+    n = 262144
+    part = empty(lib, lib.L.g4_argmax_part_bytes(n))
+    out = empty(lib, 4)
+    for case in range(4):
+        v = rng.standard_normal(n).astype(np.float32)
+        if case == 1:
+            v[[100, 5000, 260000]] = 9.0            # tie: first index wins
+        if case == 2:
+            v[:] = -1.0
+            v[77777] = -0.0
+            v[99999] = 0.0                           # -0 == +0: first wins
+        if case == 3:
+            v[:] = -np.inf
+            v[n - 1] = -1e30
+        vd = dbuf(lib, v)
+        lib.g4_argmax(vd.ptr, n, out.ptr, part.ptr, None, None)
+        got = int(out.to_array(np.int32)[0])
+        best = 0
+        m = v[0]
+        for i in np.flatnonzero(v == v.max()):
+            best = int(i)
+            break
+        assert got == best, (case, got, best, m)
+
+
+def test_residual_norm(lib, orc):
+    rng = np.random.default_rng(13)
+    n = 2560
+    x = rng.standard_normal(n).astype(np.float32)
+    y = (rng.standard_normal(n) * 4).astype(np.float32)
+    wp = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    osc = np.array([0.9], np.float32)
+    xd, yd, wpd, wnd, od = dbuf(lib, x), dbuf(lib, y), dbuf(lib, wp), dbuf(lib, wn), dbuf(lib, osc)
+    xb2 = empty(lib, 4 * n)
+    q8 = empty(lib, lib.L.g4_q8K_bytes(n))
+    lib.g4_residual_norm(xd.ptr, yd.ptr, wpd.ptr, od.ptr, wnd.ptr, xb2.ptr, q8.ptr, 0, n, C.c_float(1e-6))
+    want_x = (x + orc.rmsnorm(y, wp)) * osc[0]
+    want_xb2 = orc.rmsnorm(want_x, wn)
+    gx, gxb2 = xd.to_array(np.float32), xb2.to_array(np.float32)
+    assert rel_err(gx, want_x) < 2e-6
+    assert rel_err(gxb2, want_xb2) < 4e-6
+    h = np.zeros(n // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(gxb2).tobytes()
+    # qsrc = 1: Q8_K of x itself, no y
+    xd2 = dbuf(lib, x)
+    lib.g4_residual_norm(xd2.ptr, None, None, None, None, None, q8.ptr, 1, n, C.c_float(1e-6))
+    lib.g4_download_q8K(q8.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(x).tobytes()
