@@ -44,6 +44,30 @@ __device__ __forceinline__ void rope_head_lds(float* seg, int hd, int n_rot, int
     }
 }
 
+// rotate with precomputed (cos, sin) of each pair (same values as the chain)
+__device__ __forceinline__ void rope_head_lds_tab(float* seg, int hd, int n_rot, const float2* __restrict__ tab) {
+    const int half = hd / 2;
+    for (int j = threadIdx.x; j < n_rot / 2; j += blockDim.x) {
+        const float2 cs = tab[j];
+        const float v0 = seg[j], v1 = seg[j + half];
+        seg[j] = v0 * cs.x - v1 * cs.y;
+        seg[j + half] = v0 * cs.y + v1 * cs.x;
+    }
+}
+
+// (cos, sin) of the n_rot/2 pair angles at position *dpos (or pos)
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ tab, const int* dpos, int pos, int npair,
+                                                         float ts, float fs, const float* __restrict__ ff) {
+    const int p = dpos ? *dpos : pos;
+    for (int j = threadIdx.x; j < npair; j += blockDim.x) {
+        float theta = (float)p;
+        for (int i = 0; i < j; i++) theta *= ts;
+        const float f = ff ? ff[j] : 1.0f;
+        const float angle = (fs * theta) / f;
+        tab[j] = make_float2(cosf(angle), sinf(angle));
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ vec, int hd, int n_rot, int pos, float ts,
                                                    float fs, const float* __restrict__ ff) {
     extern __shared__ __align__(16) float seg[];
@@ -66,6 +90,7 @@ struct QKVArgs {
     float* vc;
     const int* dpos;       // device position (nullptr: use pos)
     const float* ff;       // rope freq factors (nullptr = 1)
+    const float2* tab;     // (cos, sin) per pair at this position (nullptr: compute)
     int pos, n_heads, n_kv, hd, n_rot, kv_stride, ring;
     float ts, fs, eps;
 };
@@ -94,7 +119,8 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
     for (int i = threadIdx.x; i < hd; i += blockDim.x) seg[i] = w ? seg[i] * (s * w[i]) : seg[i] * s;
     __syncthreads();
     if (kind != 2) {
-        rope_head_lds(seg, hd, a.n_rot, pos, a.ts, a.fs, a.ff);
+        if (a.tab) rope_head_lds_tab(seg, hd, a.n_rot, a.tab);
+        else rope_head_lds(seg, hd, a.n_rot, pos, a.ts, a.fs, a.ff);
         __syncthreads();
     }
     float* dst;
@@ -108,12 +134,16 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
 }
 
 // ---- split-T decode attention --------------------------------------------
+// Workspace layout (g4_attn_part_bytes): 256 bytes of per-kv-head arrival
+// counters (zero at rest: the last workgroup of a kv head resets its counter),
+// then the partials [n_heads][G][hd+2] = (o[hd], max, sum).
 struct AttnArgs {
     const float* q;        // n_heads*hd
     const float* kc;       // slot 0 of the source layer's cache
     const float* vc;
     const int* dpos;       // device position (nullptr: t_start/nwin below)
-    float* part;           // [n_heads][G][hd+2] partials
+    float* part;           // partials
+    unsigned int* count;   // n_kv arrival counters
     float* out;            // n_heads*hd
     uint8_t* q8;           // optional Q8_K of out (n_heads*hd/256 blocks)
     int t_start, nwin;     // used when dpos == nullptr
@@ -124,12 +154,8 @@ struct AttnArgs {
 
 constexpr int kAttnThreads = 256;
 constexpr int kChunkMax = 1024;     // positions per workgroup
-
-// float offset of the (max, sum) pairs in the partial kernel's LDS
-__host__ __device__ inline int attn_ml_offset(int hd, int kvm) {
-    const int a = kvm * hd + kvm * kChunkMax, b = 4 * kvm * hd;
-    return a > b ? a : b;
-}
+constexpr int kAttnCounterBytes = 256;
+constexpr int kMaxChunks = 512;     // chunks (workgroups) per kv head
 
 __device__ __forceinline__ void attn_window(const AttnArgs& a, int& t0, int& nwin) {
     if (a.dpos) {
@@ -149,15 +175,29 @@ __device__ __forceinline__ float dot4(const float4 a, const float4 b, float acc)
     return __builtin_fmaf(a.w, b.w, acc);
 }
 
-// LDS: q [kvm][HD] | scores [kvm][kChunkMax], reused by the PV reduction as
-// [4 waves][kvm][HD]; the per-head (max, sum) pairs [2*kvm] sit after both
-// (attn_ml_offset), so the reduction cannot overwrite them.
+// LDS (floats): [0, R) work region: q [kvm][HD] + scores [kvm][kChunkMax] during
+// the scoring, then [4 waves][kvm][HD] for the PV reduction and the merge;
+// [R, R + 2*kvm) the chunk's (max, sum) per head.  R = attn_work_floats().
+__host__ __device__ inline int attn_work_floats(int hd, int kvm) {
+    const int a = kvm * hd + kvm * kChunkMax, b = 4 * kvm * hd;
+    return a > b ? a : b;
+}
+
+__device__ __forceinline__ int attn_slot(const AttnArgs& a, int t) { return a.ring > 0 ? t % a.ring : t; }
+
+// Workgroup (c, kvh) scores chunk c of the window for the kvm q heads of kv
+// head kvh (each K/V row read once for the group), keeps (o, max, sum) of its
+// chunk; the last workgroup of kv head kvh to finish merges the G chunks by
+// log-sum-exp, writes the heads' outputs and, if asked, their Q8_K blocks.
 template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
-    constexpr int KPL = HD / 64;          // float4 per 16-lane slice of a row
+    __shared__ int s_last;
+    constexpr int KPL = HD / 64;          // float4 per lane of a 16-lane row slice
+    constexpr int VPL = HD / 256;         // float4 per lane of a 64-lane row slice
     const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int kvm = a.n_heads / a.n_kv;
+    const int R = attn_work_floats(HD, kvm);
     int t0, nwin;
     attn_window(a, t0, nwin);
     const int cs = (nwin + a.G - 1) / a.G;
@@ -167,30 +207,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnArgs a) 
     const int cnt = min(kChunkMax, max(0, min(cb + cs, t0 + nwin) - cb));
     float* qs = sm;
     float* sc = sm + kvm * HD;
-    float* ml = sm + attn_ml_offset(HD, kvm);
+    float* ml = sm + R;
     const float* qsrc = a.q + (size_t)kvh * kvm * HD;
     for (int i = tid; i < kvm * HD; i += kAttnThreads) qs[i] = qsrc[i];
     __syncthreads();
 
-    // phase 1: scores, one position per 16-lane subgroup
+    // phase 1: scores; 16 subgroups of 16 lanes, two positions per subgroup in
+    // flight
     const int sub = tid >> 4, sl = tid & 15;
-    for (int t = sub; t < cnt; t += kAttnThreads / 16) {
-        const int tt = cb + t;
-        const int slot = a.ring > 0 ? tt % a.ring : tt;
-        const float4* kr = reinterpret_cast<const float4*>(a.kc + (size_t)slot * a.kv_stride + (size_t)kvh * HD);
-        float4 kv[KPL];
+    const float* kbase = a.kc + (size_t)kvh * HD;
+    for (int it = 0; it < cnt; it += 32) {
+        const int ta = it + sub, tb = it + 16 + sub;
+        float4 ka[KPL], kb[KPL];
+        const float4* ra = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(ta, cnt - 1)) * a.kv_stride);
+        const float4* rb = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(tb, cnt - 1)) * a.kv_stride);
 #pragma unroll
-        for (int k = 0; k < KPL; k++) kv[k] = kr[sl + 16 * k];
+        for (int k = 0; k < KPL; k++) ka[k] = ra[sl + 16 * k];
+#pragma unroll
+        for (int k = 0; k < KPL; k++) kb[k] = rb[sl + 16 * k];
         for (int h = 0; h < kvm; h++) {
             const float4* qh = reinterpret_cast<const float4*>(qs + h * HD);
-            float d = 0.0f;
+            float da = 0.0f, db = 0.0f;
 #pragma unroll
-            for (int k = 0; k < KPL; k++) d = dot4(kv[k], qh[sl + 16 * k], d);
-            d += __shfl_xor(d, 8, 64);
-            d += __shfl_xor(d, 4, 64);
-            d += __shfl_xor(d, 2, 64);
-            d += __shfl_xor(d, 1, 64);
-            if (sl == 0) sc[h * kChunkMax + t] = a.scale * d;
+            for (int k = 0; k < KPL; k++) {
+                const float4 qv = qh[sl + 16 * k];
+                da = dot4(ka[k], qv, da);
+                db = dot4(kb[k], qv, db);
+            }
+#pragma unroll
+            for (int m = 8; m >= 1; m >>= 1) {
+                da += __shfl_xor(da, m, 64);
+                db += __shfl_xor(db, m, 64);
+            }
+            if (sl == 0) {
+                if (ta < cnt) sc[h * kChunkMax + ta] = a.scale * da;
+                if (tb < cnt) sc[h * kChunkMax + tb] = a.scale * db;
+            }
         }
     }
     __syncthreads();
@@ -213,36 +265,45 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnArgs a) 
     }
     __syncthreads();
 
-    // phase 3: o[h] = sum_t p[h][t] V[t]; wave w takes t = w, w+4, ...
-    constexpr int VPL = HD / 256;        // float4 per lane of a row
+    // phase 3: o[h] = sum_t p[h][t] V[t]; wave w takes positions w, w+4, ...,
+    // four rows in flight per wave
     float4 acc[8][VPL];
 #pragma unroll
     for (int h = 0; h < 8; h++)
 #pragma unroll
         for (int k = 0; k < VPL; k++) acc[h][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t = wave; t < cnt; t += kAttnThreads / 64) {
-        const int tt = cb + t;
-        const int slot = a.ring > 0 ? tt % a.ring : tt;
-        const float4* vr = reinterpret_cast<const float4*>(a.vc + (size_t)slot * a.kv_stride + (size_t)kvh * HD);
-        float4 vv[VPL];
+    const float* vbase = a.vc + (size_t)kvh * HD;
+    for (int it = 0; it < cnt; it += 16) {
+        float4 vv[4][VPL];
 #pragma unroll
-        for (int k = 0; k < VPL; k++) vv[k] = vr[lane + 64 * k];
+        for (int u = 0; u < 4; u++) {
+            const int t = min(it + wave + 4 * u, cnt - 1);
+            const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)attn_slot(a, cb + t) * a.kv_stride);
 #pragma unroll
-        for (int h = 0; h < 8; h++) {
-            if (h < kvm) {
-                const float p = sc[h * kChunkMax + t];
+            for (int k = 0; k < VPL; k++) vv[u][k] = vr[lane + 64 * k];
+        }
 #pragma unroll
-                for (int k = 0; k < VPL; k++) {
-                    acc[h][k].x = __builtin_fmaf(p, vv[k].x, acc[h][k].x);
-                    acc[h][k].y = __builtin_fmaf(p, vv[k].y, acc[h][k].y);
-                    acc[h][k].z = __builtin_fmaf(p, vv[k].z, acc[h][k].z);
-                    acc[h][k].w = __builtin_fmaf(p, vv[k].w, acc[h][k].w);
+        for (int u = 0; u < 4; u++) {
+            const int t = it + wave + 4 * u;
+            if (t < cnt) {
+#pragma unroll
+                for (int h = 0; h < 8; h++) {
+                    if (h < kvm) {
+                        const float p = sc[h * kChunkMax + t];
+#pragma unroll
+                        for (int k = 0; k < VPL; k++) {
+                            acc[h][k].x = __builtin_fmaf(p, vv[u][k].x, acc[h][k].x);
+                            acc[h][k].y = __builtin_fmaf(p, vv[u][k].y, acc[h][k].y);
+                            acc[h][k].z = __builtin_fmaf(p, vv[u][k].z, acc[h][k].z);
+                            acc[h][k].w = __builtin_fmaf(p, vv[u][k].w, acc[h][k].w);
+                        }
+                    }
                 }
             }
         }
     }
-    __syncthreads();   // scores are dead; reuse q+scores for the cross-wave sum
-    float* rs = sm;    // [4][kvm][HD]
+    __syncthreads();   // scores are dead; the work region becomes [4][kvm][HD]
+    float* rs = sm;
 #pragma unroll
     for (int h = 0; h < 8; h++) {
         if (h < kvm) {
@@ -260,71 +321,94 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnArgs a) 
         p[dd] = o;
         if (dd == 0) { p[HD] = cnt > 0 ? ml[2 * h] : -INFINITY; p[HD + 1] = cnt > 0 ? ml[2 * h + 1] : 0.0f; }
     }
-}
 
-// one workgroup of HD threads per q head
-template <int HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
-    __shared__ __align__(16) float o[HD];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const float* p = a.part + (size_t)h * a.G * (HD + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < a.G; c++) M = fmaxf(M, p[(size_t)c * (HD + 2) + HD]);
-    float L = 0.0f, acc = 0.0f;
-    for (int c = 0; c < a.G; c++) {
-        const float* pc = p + (size_t)c * (HD + 2);
-        const float l = pc[HD + 1];
-        if (l > 0.0f) {
-            const float f = expf(pc[HD] - M);
+    // arrival: the last workgroup of this kv head merges (partials written by
+    // other workgroups are made visible by the release/acquire fences)
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned int prev = atomicAdd(&a.count[kvh], 1u);
+        s_last = prev == (unsigned int)(a.G - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // merge the G chunks of heads kvh*kvm .. kvh*kvm + kvm - 1:
+    // f[h][g] = exp(max_g - M_h) (0 for empty chunks), L_h = sum_g sum_g * f[h][g]
+    float* fw = ml + 2 * kvm;          // [kvm][G] chunk weights, then [kvm] L
+    float* Lh = fw + kvm * a.G;
+    const float* pk = a.part + (size_t)kvh * kvm * a.G * (HD + 2);
+    for (int h = wave; h < kvm; h += kAttnThreads / 64) {
+        const float* ph = pk + (size_t)h * a.G * (HD + 2);
+        float M = -INFINITY;
+        for (int g = lane; g < a.G; g += 64) M = fmaxf(M, ph[(size_t)g * (HD + 2) + HD]);
+        M = wave_max(M);
+        float L = 0.0f;
+        for (int g = lane; g < a.G; g += 64) {
+            const float l = ph[(size_t)g * (HD + 2) + HD + 1];
+            const float f = l > 0.0f ? expf(ph[(size_t)g * (HD + 2) + HD] - M) : 0.0f;
+            fw[h * a.G + g] = f;
             L += l * f;
-            acc = __builtin_fmaf(pc[tid], f, acc);
         }
+        L = wave_sum(L);
+        if (lane == 0) Lh[h] = L;
     }
-    const float r = L > 0.0f ? acc / L : 0.0f;
-    a.out[(size_t)h * HD + tid] = r;
+    __syncthreads();
+    float* mo = sm;    // [kvm][HD] merged outputs (for the Q8_K pass)
+    for (int i = tid; i < kvm * HD; i += kAttnThreads) {
+        const int h = i / HD, dd = i - h * HD;
+        const float* ph = pk + (size_t)h * a.G * (HD + 2) + dd;
+        const float* fh = fw + h * a.G;
+        float o = 0.0f;
+        for (int g = 0; g < a.G; g++) o = __builtin_fmaf(ph[(size_t)g * (HD + 2)], fh[g], o);
+        const float L = Lh[h];
+        const float r = L > 0.0f ? o / L : 0.0f;
+        a.out[(size_t)(kvh * kvm + h) * HD + dd] = r;
+        mo[i] = r;
+    }
     if (a.q8) {
-        o[tid] = r;
         __syncthreads();
-        const int wave = tid >> 6, lane = tid & 63;
-        if (wave < HD / 256) {
-            const float4 f = reinterpret_cast<const float4*>(o + wave * 256)[lane];
+        const int nb_total = a.n_heads * HD / 256;
+        for (int b = wave; b < kvm * HD / 256; b += kAttnThreads / 64) {
+            const float4 f = reinterpret_cast<const float4*>(mo + b * 256)[lane];
             const float v[4] = {f.x, f.y, f.z, f.w};
-            quantize_block_wave(v, lane, a.q8, a.n_heads * HD / 256, h * (HD / 256) + wave);
+            quantize_block_wave(v, lane, a.q8, nb_total, kvh * kvm * HD / 256 + b);
         }
     }
+    if (tid == 0) a.count[kvh] = 0u;   // ready for the next call
 }
 
-size_t attn_lds(int hd, int kvm) { return 4 * ((size_t)attn_ml_offset(hd, kvm) + 2 * (size_t)kvm); }
+// work region + (max, sum) pairs + merge weights [kvm][G] + [kvm] sums
+size_t attn_lds(int hd, int kvm, int G) {
+    return 4 * ((size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm + (size_t)kvm * G + (size_t)kvm);
+}
 
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
-    const dim3 g1(a.G, a.n_kv);
-    const size_t lds = attn_lds(a.hd, kvm);
-    if (a.hd == 256) {
-        hipLaunchKernelGGL(attn_partial_kernel<256>, g1, dim3(kAttnThreads), lds, g4_stream(), a);
-        hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads), dim3(256), 0, g4_stream(), a);
-    } else {
-        hipLaunchKernelGGL(attn_partial_kernel<512>, g1, dim3(kAttnThreads), lds, g4_stream(), a);
-        hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads), dim3(512), 0, g4_stream(), a);
-    }
-    return g4_check_launch("attn_partial_kernel/attn_merge_kernel");
+    const dim3 grid(a.G, a.n_kv);
+    const size_t lds = attn_lds(a.hd, kvm, a.G);
+    if (a.hd == 256) hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else hipLaunchKernelGGL(attn_decode_kernel<512>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    return g4_check_launch("attn_decode_kernel");
 }
 
-int check_attn_shape(const char* who, int n_heads, int n_kv, int hd) {
+int check_attn_shape(const char* who, int n_heads, int n_kv, int hd, int G) {
     if (hd != 256 && hd != 512) return g4_fail(G4_ERR_ARG, "%s: head_dim %d unsupported (256 or 512)", who, hd);
-    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8)
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8 || n_kv * 4 > kAttnCounterBytes)
         return g4_fail(G4_ERR_ARG, "%s: n_heads=%d n_kv=%d (need n_heads/n_kv in 1..8)", who, n_heads, n_kv);
-    if (attn_lds(hd, n_heads / n_kv) > 65536)
+    if (G < 1 || G > kMaxChunks) return g4_fail(G4_ERR_ARG, "%s: %d chunks (1..%d)", who, G, kMaxChunks);
+    if (attn_lds(hd, n_heads / n_kv, G) > 65536)
         return g4_fail(G4_ERR_ARG, "%s: %d q heads per kv head at head_dim %d exceed the LDS budget", who,
                        n_heads / n_kv, hd);
     return G4_OK;
 }
 
-// library-owned partials buffer for the host-position entry points
+// library-owned workspace for the host-position entry points
 void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
 
-int workspace(size_t bytes, float** p) {
+int workspace(size_t bytes, uint8_t** p) {
     if (bytes > g_ws_bytes) {
         if (g_ws) {
             G4_HIP(hipStreamSynchronize(g4_stream()));
@@ -333,16 +417,19 @@ int workspace(size_t bytes, float** p) {
             g_ws_bytes = 0;
         }
         if (hipMalloc(&g_ws, bytes) != hipSuccess) return g4_fail(G4_ERR_NOMEM, "attention workspace (%zu B)", bytes);
+        G4_HIP(hipMemset(g_ws, 0, kAttnCounterBytes));   // arrival counters start at zero
         g_ws_bytes = bytes;
     }
-    *p = (float*)g_ws;
+    *p = (uint8_t*)g_ws;
     return G4_OK;
 }
 
+// about 16 positions per workgroup, at most 64 chunks per kv head unless a
+// chunk would exceed kChunkMax positions
 int chunks_for(int nwin) {
-    int G = (nwin + 127) / 128;        // ~128 positions per workgroup
+    int G = (nwin + 15) / 16;
     if (G < 1) G = 1;
-    if (G > 512) G = 512;
+    if (G > 64) G = 64;
     while ((nwin + G - 1) / G > kChunkMax) G++;
     return G;
 }
@@ -365,9 +452,19 @@ extern "C" int g4_apply_rope_neox(float* vec, int n_heads, int head_dim, int n_r
     return g4_check_launch("rope_kernel");
 }
 
+extern "C" int g4_rope_table(float* tab, const int* dpos, int pos, int n_rot, float freq_base, float freq_scale,
+                             const float* freq_factors) {
+    G4_CHECK_ARG(tab && n_rot > 0 && n_rot % 2 == 0 && n_rot <= 2048, "g4_rope_table: bad arguments");
+    const float ts = powf(freq_base, -2.0f / (float)n_rot);
+    hipLaunchKernelGGL(rope_table_kernel, dim3(1), dim3(256), 0, g4_stream(), (float2*)tab, dpos, pos, n_rot / 2, ts,
+                       freq_scale, freq_factors);
+    return g4_check_launch("rope_table_kernel");
+}
+
 extern "C" int g4_qkv_post(float* q, const float* q_norm, const float* k, const float* v, const float* k_norm, float* kc,
-                float* vc, int kv_stride, int ring, const int* dpos, int pos, int n_heads, int n_kv, int hd,
-                int n_rot, float freq_base, float freq_scale, const float* ff, float eps) {
+                           float* vc, int kv_stride, int ring, const int* dpos, int pos, int n_heads, int n_kv, int hd,
+                           int n_rot, float freq_base, float freq_scale, const float* ff, float eps,
+                           const float* rope_tab) {
     G4_CHECK_ARG(q && q_norm && hd > 0 && hd <= 1024 && n_rot <= hd, "qkv_post: bad arguments");
     G4_CHECK_ARG(!k || (v && k_norm && kc && vc && kv_stride >= n_kv * hd), "qkv_post: bad K/V arguments");
     QKVArgs a;
@@ -376,6 +473,7 @@ extern "C" int g4_qkv_post(float* q, const float* q_norm, const float* k, const 
     a.kv_stride = kv_stride; a.ring = ring;
     a.ts = powf(freq_base, -2.0f / (float)n_rot);
     a.fs = freq_scale; a.eps = eps;
+    a.tab = (const float2*)rope_tab;
     const int grid = n_heads + (k ? 2 * n_kv : 0);
     hipLaunchKernelGGL(qkv_post_kernel, dim3(grid), dim3(256), (size_t)hd * 4, g4_stream(), a);
     return g4_check_launch("qkv_post_kernel");
@@ -392,19 +490,25 @@ extern "C" int g4_kv_append_rope(float* k, float* v, const float* k_norm, float*
     a.kv_stride = kv_stride; a.ring = ring;
     a.ts = powf(freq_base, -2.0f / (float)n_rot);
     a.fs = freq_scale; a.eps = eps;
+    a.tab = nullptr;
     hipLaunchKernelGGL(qkv_post_kernel, dim3(2 * n_kv), dim3(256), (size_t)hd * 4, g4_stream(), a);
     return g4_check_launch("qkv_post_kernel");
 }
 
+extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) {
+    return kAttnCounterBytes + (size_t)n_heads * G * (hd + 2) * 4;
+}
+
 static int attn_common(const char* who, AttnArgs& a) {
-    int rc = check_attn_shape(who, a.n_heads, a.n_kv, a.hd);
+    int rc = check_attn_shape(who, a.n_heads, a.n_kv, a.hd, a.G);
     if (rc) return rc;
     G4_CHECK_ARG(a.q && a.kc && a.vc && a.out, "%s: null pointer", who);
     G4_CHECK_ARG(a.kv_stride >= a.n_kv * a.hd, "%s: kv_stride %d < n_kv*hd", who, a.kv_stride);
-    float* ws = nullptr;
-    rc = workspace((size_t)a.n_heads * a.G * (a.hd + 2) * 4, &ws);
+    uint8_t* ws = nullptr;
+    rc = workspace(g4_attn_part_bytes(a.n_heads, a.hd, a.G), &ws);
     if (rc) return rc;
-    a.part = ws;
+    a.count = (unsigned int*)ws;
+    a.part = (float*)(ws + kAttnCounterBytes);
     return launch_attn(a);
 }
 
@@ -437,18 +541,20 @@ extern "C" int g4_attn_decode_ring(const float* q, const float* kc, const float*
 }
 
 // Engine form: position read from device memory, fixed chunk count G (so a
-// captured graph stays valid as pos advances), caller-owned partials buffer
-// of g4_attn_part_bytes(n_heads, hd, G) bytes, optional fused Q8_K output.
-extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) { return (size_t)n_heads * G * (hd + 2) * 4; }
-
-extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* vc, int kv_stride, int ring, const int* dpos,
-                       int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float* part, float* out,
-                       void* q8) {
-    int rc = check_attn_shape("attn_decode_dev", n_heads, n_kv, hd);
+// captured graph stays valid as pos advances; G * 1024 must cover the
+// window), caller-owned workspace of g4_attn_part_bytes(n_heads, hd, G) bytes
+// whose first 256 bytes are zero before the first call (they are left zero),
+// optional fused Q8_K output.
+extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* vc, int kv_stride, int ring,
+                                  const int* dpos, int window, int n_heads, int n_kv, int hd, float attn_scale, int G,
+                                  float* part, float* out, void* q8) {
+    int rc = check_attn_shape("attn_decode_dev", n_heads, n_kv, hd, G);
     if (rc) return rc;
-    G4_CHECK_ARG(q && kc && vc && dpos && part && out && G >= 1, "attn_decode_dev: bad arguments");
+    G4_CHECK_ARG(q && kc && vc && dpos && part && out && G >= 1 && G <= kMaxChunks, "attn_decode_dev: bad arguments");
     AttnArgs a = {};
-    a.q = q; a.kc = kc; a.vc = vc; a.dpos = dpos; a.part = part; a.out = out; a.q8 = (uint8_t*)q8;
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = dpos; a.out = out; a.q8 = (uint8_t*)q8;
+    a.count = (unsigned int*)part;
+    a.part = (float*)((uint8_t*)part + kAttnCounterBytes);
     a.window = window; a.kv_stride = kv_stride; a.ring = ring;
     a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
     return launch_attn(a);

@@ -2,24 +2,12 @@
 //
 // o[d] = W[d x n] . x   (W row-major, ne[0] = n; gemma4-4b/cpu-blas/main.c:1669)
 //
-// Work decomposition shared by all kernels: a 256-thread workgroup owns R
-// consecutive rows; its 32 groups of 8 lanes walk (row, block) tasks in
-// block-major order, so the groups of a wave read the same activation block
-// from LDS (broadcast) while each streams a different row's 16-byte weight
-// slices from HBM.  All weight loads of a group are issued before the
-// activation is staged into LDS, so HBM latency overlaps the staging.
-//
-// Q4_K / Q5_K x Q8_K: per-block integer sums are computed in the lane
-// partition of the reference's AVX2 dot (lane l = bytes 4l..4l+3 of every
-// 32-byte chunk, main.c:500-523) and parked in LDS; the fp32 combine then
-// replays main.c:476-529 (Q4_K) / 531-593 (Q5_K) exactly: eight FMA lanes
-// over the blocks in order, the min term (four FMA lanes, or one scalar for
-// Q5_K), and the fixed horizontal-add tree.  The result is bit-identical to
-// the reference for the same Q8_K input.
-//
-// Q6_K x fp32 (mm_quant_rows, main.c:1539-1556): weights are dequantized to
-// the reference's fp32 values ((d*sc)*q, main.c:226-229) and accumulated with
-// FMA in a parallel order (tolerance, not bit-exact).
+// Q4_K / Q5_K x Q8_K (mm_quant_dot_rows): one row per 8-lane group, bit-exact
+// with the reference's AVX2 dot (see gemv_q45_rows_kernel).
+// Q6_K x fp32 (mm_quant_rows): row slices per 8-lane group with x in LDS,
+// fp32 tolerance (see gemv_q6k_rows_kernel).
+// Q6_K x Q8_K (integer, no reference counterpart) and BF16 x fp32: 256-thread
+// workgroups of 32 row tasks.
 #include "g4_device.h"
 #include "g4_internal.h"
 
@@ -30,243 +18,6 @@ constexpr int kGroups = 32;   // 8-lane groups per workgroup
 
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int j) {
     return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
-}
-
-// ------------------------------------------------------------------------
-// Q4_K / Q5_K x Q8_K
-// ------------------------------------------------------------------------
-// LDS: [q8 copy: nb*292 B, padded to 16][S: Tmax*8 i32][P: Tmax*4 i32][D, DM: Tmax f32][res: 2R f32]
-template <int TPG, bool Q5, int NMAT, bool DBG>
-__global__ __launch_bounds__(kWG) void gemv_q45k_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
-                                                        const uint8_t* __restrict__ q8, float* __restrict__ out, int nb,
-                                                        int d, int R, int32_t* __restrict__ dbgS,
-                                                        int32_t* __restrict__ dbgM) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int Tmax = kGroups * TPG;
-    const int tid = threadIdx.x, l = tid & 7, g = tid >> 3;
-    const int r0 = blockIdx.x * R;
-    const int rows = min(R, d - r0);
-    const int per_mat = rows * nb;
-    const int T = NMAT * per_mat;
-    const size_t nblk = (size_t)d * nb;
-    const size_t hdr_off = Q5 ? q5k_planes(nblk).hdr : q4k_planes(nblk).hdr;
-    const size_t qh_off = q5k_planes(nblk).qh;
-
-    // ---- 1. issue every weight load of this group
-    uint4 wq[TPG], hd[TPG];
-    uint32_t qh[TPG];
-#pragma unroll
-    for (int i = 0; i < TPG; i++) {
-        const int t = g + kGroups * i;
-        wq[i] = make_uint4(0, 0, 0, 0);
-        hd[i] = make_uint4(0, 0, 0, 0);
-        qh[i] = 0;
-        if (t < T) {
-            const int m = NMAT == 2 ? t / per_mat : 0;
-            const int tt = t - m * per_mat;
-            const int b = tt / rows, rr = tt - b * rows;
-            const uint8_t* base = m ? w1 : w0;
-            const size_t blk = (size_t)(r0 + rr) * nb + b;
-            wq[i] = *reinterpret_cast<const uint4*>(base + blk * 128 + 16 * l);
-            hd[i] = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16);
-            if (Q5) qh[i] = *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32 + 4 * l);
-        }
-    }
-    // ---- 2. stage the Q8_K activation (qs | bsums | d) into LDS
-    const int q8w = nb * 73;   // 292 B per block
-    for (int k = tid; k < q8w; k += kWG) reinterpret_cast<uint32_t*>(smem)[k] = reinterpret_cast<const uint32_t*>(q8)[k];
-    const int q8bytes = (nb * 292 + 15) & ~15;
-    int32_t* S = reinterpret_cast<int32_t*>(smem + q8bytes);
-    int32_t* P = S + Tmax * 8;
-    float* D = reinterpret_cast<float*>(P + Tmax * 4);
-    float* DM = D + Tmax;
-    float* res = DM + Tmax;
-    const int16_t* bsums = reinterpret_cast<const int16_t*>(smem + q8k_bsums_off(nb));
-    const float* yd = reinterpret_cast<const float*>(smem + q8k_d_off(nb));
-    __syncthreads();
-
-    // ---- 3. exact per-block integer sums in the AVX2 lane partition
-#pragma unroll
-    for (int i = 0; i < TPG; i++) {
-        const int t = g + kGroups * i;
-        if (t < T) {
-            const int m = NMAT == 2 ? t / per_mat : 0;
-            const int tt = t - m * per_mat;
-            const int b = tt / rows;
-            uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
-            unpack_scales(hd[i].y, hd[i].z, hd[i].w, sc_lo, sc_hi, mn_lo, mn_hi);
-            const uint4 a0 = *reinterpret_cast<const uint4*>(smem + b * 256 + 32 * l);
-            const uint4 a1 = *reinterpret_cast<const uint4*>(smem + b * 256 + 32 * l + 16);
-            int32_t sumi = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t qw = word_of(wq[i], j);
-                uint32_t lo = qw & 0x0f0f0f0fu, hi = (qw >> 4) & 0x0f0f0f0fu;
-                if (Q5) {
-                    lo |= ((qh[i] >> (2 * j)) & 0x01010101u) << 4;
-                    hi |= ((qh[i] >> (2 * j + 1)) & 0x01010101u) << 4;
-                }
-                const int dl = __builtin_amdgcn_sdot4((int)lo, (int)word_of(a0, j), 0, false);
-                const int dh = __builtin_amdgcn_sdot4((int)hi, (int)word_of(a1, j), 0, false);
-                const uint32_t scw = j < 2 ? sc_lo : sc_hi;
-                sumi += byte_of(scw, 2 * (j & 1)) * dl + byte_of(scw, 2 * (j & 1) + 1) * dh;
-            }
-            const int k = l & 3;
-            const uint32_t mnw = k < 2 ? mn_lo : mn_hi;
-            const int16_t* bs = bsums + b * 16 + 4 * k;
-            const int32_t prod = byte_of(mnw, 2 * (k & 1)) * ((int)bs[0] + bs[1]) +
-                                 byte_of(mnw, 2 * (k & 1) + 1) * ((int)bs[2] + bs[3]);
-            if (DBG) {
-                int32_t s = sumi;
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
-                int32_t p = l < 4 ? prod : 0;
-                p += __shfl_xor(p, 1, 64);
-                p += __shfl_xor(p, 2, 64);
-                p += __shfl_xor(p, 4, 64);
-                if (l == 0) {
-                    const int rr = tt - b * rows;
-                    dbgS[(size_t)(r0 + rr) * nb + b] = s;
-                    dbgM[(size_t)(r0 + rr) * nb + b] = p;
-                }
-            }
-            S[t * 8 + l] = sumi;
-            if (l < 4) P[t * 4 + l] = prod;
-            if (l == 0) {
-                const float y = yd[b];
-                D[t] = y * f16_to_f32(hd[i].x & 0xffffu);
-                DM[t] = -y * f16_to_f32(hd[i].x >> 16);
-            }
-        }
-    }
-    __syncthreads();
-    if (DBG) return;
-
-    // ---- 4. per-row fp32 combine, in the reference's order
-    for (int ra = g; ra < NMAT * rows; ra += kGroups) {
-        const int m = NMAT == 2 ? ra / rows : 0;
-        const int rr = ra - m * rows;
-        float acc = 0.0f, accm = 0.0f, summs = 0.0f;
-        for (int b = 0; b < nb; b++) {
-            const int t = m * per_mat + b * rows + rr;
-            acc = __builtin_fmaf(D[t], (float)S[t * 8 + l], acc);
-            if (Q5) {
-                const int32_t pm = (P[t * 4 + 0] + P[t * 4 + 1]) + (P[t * 4 + 2] + P[t * 4 + 3]);
-                const float tm = DM[t] * (float)pm;
-                summs = summs + tm;
-            } else if (l < 4) {
-                accm = __builtin_fmaf(DM[t], (float)P[t * 4 + l], accm);
-            }
-        }
-        const float t1 = acc + __shfl_xor(acc, 4, 64);
-        const float t2 = t1 + __shfl_xor(t1, 2, 64);
-        const float h = t2 + __shfl_xor(t2, 1, 64);
-        float r;
-        if (Q5) {
-            r = h + summs;
-        } else {
-            const float v1 = accm + __shfl_xor(accm, 2, 64);
-            const float hm = v1 + __shfl_xor(v1, 1, 64);
-            r = h + hm;
-        }
-        if (l == 0) {
-            if (NMAT == 1) out[r0 + rr] = r;
-            else res[m * R + rr] = r;
-        }
-    }
-    if (NMAT == 2) {
-        __syncthreads();
-        for (int rr = tid; rr < rows; rr += kWG) out[r0 + rr] = gelu_ref(res[rr]) * res[R + rr];
-    }
-}
-
-// ------------------------------------------------------------------------
-// Q6_K x fp32 (reference semantics of mm_quant_rows)
-// ------------------------------------------------------------------------
-// LDS: [x: n floats][part: Tmax floats]
-template <int TPG, bool SOFTCAP>
-__global__ __launch_bounds__(kWG) void gemv_q6k_f32_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                           float* __restrict__ out, int nb, int d, int R, float cap) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
-    const int r0 = blockIdx.x * R;
-    const int rows = min(R, d - r0);
-    const int T = rows * nb;
-    const size_t nblk = (size_t)d * nb;
-    const Q6KPlanes p = q6k_planes(nblk);
-
-    uint4 qlv[TPG];
-    uint2 qhv[TPG], scv[TPG];
-    uint32_t dv[TPG];
-#pragma unroll
-    for (int i = 0; i < TPG; i++) {
-        const int t = g + kGroups * i;
-        qlv[i] = make_uint4(0, 0, 0, 0);
-        qhv[i] = make_uint2(0, 0);
-        scv[i] = make_uint2(0, 0);
-        dv[i] = 0;
-        if (t < T) {
-            const int b = t / rows, rr = t - b * rows;
-            const size_t blk = (size_t)(r0 + rr) * nb + b;
-            qlv[i] = *reinterpret_cast<const uint4*>(w + p.ql + blk * 128 + 16 * L);
-            qhv[i] = *reinterpret_cast<const uint2*>(w + p.qh + blk * 64 + 8 * L);
-            scv[i] = *reinterpret_cast<const uint2*>(w + p.sc + blk * 16 + 8 * h);
-            dv[i] = *reinterpret_cast<const uint16_t*>(w + p.d + blk * 2);
-        }
-    }
-    float* xs = reinterpret_cast<float*>(smem);
-    const int n4 = nb * 64;
-    for (int k = tid; k < n4; k += kWG) reinterpret_cast<float4*>(xs)[k] = reinterpret_cast<const float4*>(x)[k];
-    float* part = xs + nb * 256;
-    __syncthreads();
-
-#pragma unroll
-    for (int i = 0; i < TPG; i++) {
-        const int t = g + kGroups * i;
-        if (t < T) {
-            const int b = t / rows;
-            const float df = f16_to_f32(dv[i]);
-            float ds[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int sb = (u >> 1) + 2 * k;   // byte within the 8-byte half
-                const uint32_t sw = sb < 4 ? scv[i].x : scv[i].y;
-                ds[k] = df * (float)(int8_t)byte_of(sw, sb & 3);
-            }
-            const float* xb = xs + b * 256 + 128 * h + 8 * u;
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t qa = (k & 1) ? qlv[i].z : qlv[i].x;   // bytes 0..3 of the run
-                const uint32_t qb = (k & 1) ? qlv[i].w : qlv[i].y;   // bytes 4..7
-                const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * k);
-                const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * k + 4);
-                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint32_t qlb = byte_of(e < 4 ? qa : qb, e & 3);
-                    const uint32_t lo = k < 2 ? (qlb & 15u) : (qlb >> 4);
-                    const uint32_t hb = (byte_of(e < 4 ? qhv[i].x : qhv[i].y, e & 3) >> (2 * k)) & 3u;
-                    const int q = (int)(lo | (hb << 4)) - 32;
-                    const float wv = ds[k] * (float)q;
-                    acc = __builtin_fmaf(xv[e], wv, acc);
-                }
-            }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
-            if (L == 0) part[t] = acc;
-        }
-    }
-    __syncthreads();
-    const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
-    for (int rr = tid; rr < rows; rr += kWG) {
-        float s = 0.0f;
-        for (int b = 0; b < nb; b++) s += part[b * rows + rr];
-        if (SOFTCAP) s = cap * tanhf(s * inv);
-        out[r0 + rr] = s;
-    }
 }
 
 // ------------------------------------------------------------------------
@@ -399,6 +150,259 @@ __global__ __launch_bounds__(kWG) void gemv_bf16_kernel(const uint16_t* __restri
     }
 }
 
+// ------------------------------------------------------------------------
+// Q4_K / Q5_K x Q8_K (the decode path)
+// ------------------------------------------------------------------------
+// A row is owned by SPLIT 8-lane groups.  Lane l of a group takes bytes
+// 4l..4l+3 of every 32-byte qs chunk of a block (the AVX2 lane partition,
+// main.c:500-523) and computes that block's exact integer sums (sumi: the
+// scaled nibble dots, prod: the min products) and its fp32 scales
+// D = y.d * d and DM = -y.d * dmin.  Group g takes blocks g*NH .. g*NH+NH-1;
+// the other groups' values are gathered by lane shuffles into group 0, which
+// runs the reference's fp32 accumulation over the blocks in order (eight FMA
+// lanes plus four min lanes for Q4_K, one scalar min lane for Q5_K) and its
+// fixed horizontal-add tree -- bit-identical to main.c:476-529 / 531-593.
+// Splitting the integer work over two groups doubles the waves in flight;
+// 64-thread workgroups carry 8/SPLIT rows.  fp16 d/dmin are converted by
+// the hardware (exact, subnormals included).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+    _Float16 v;
+    const uint16_t b = (uint16_t)h;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT>
+__global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
+                                                           const uint8_t* __restrict__ w1,
+                                                           const uint8_t* __restrict__ q8, float* __restrict__ out,
+                                                           int nb_rt, int d, int32_t* __restrict__ dbgS,
+                                                           int32_t* __restrict__ dbgM) {
+    constexpr int GL = 8 * SPLIT;                               // lanes per row
+    constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
+    const int nb = NB > 0 ? NB : nb_rt;
+    const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
+    const int row = blockIdx.x * (64 / GL) + tid / GL;
+    if (row >= d) return;   // whole rows (groups of GL lanes) leave together
+    const uint32_t nblk = (uint32_t)d * (uint32_t)nb;
+    const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
+    const uint32_t qh_off = 128u * nblk;
+    const uint32_t rb = (uint32_t)row * (uint32_t)nb;            // first block of the row
+    const uint8_t* a_qs = q8 + 32 * l;
+    const uint8_t* a_bs = q8 + q8k_bsums_off(nb) + 8 * k;
+    const float* a_d = reinterpret_cast<const float*>(q8 + q8k_d_off(nb));
+
+    // one block's integer sums and scales for matrix m
+    auto block = [&](int m, int b, int32_t& S, int32_t& P, float& D, float& DM) {
+        const uint4 a0 = *reinterpret_cast<const uint4*>(a_qs + b * 256);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(a_qs + b * 256 + 16);
+        const uint2 bsw = *reinterpret_cast<const uint2*>(a_bs + b * 32);
+        const float yd = a_d[b];
+        const int bs_lo = (int)(int16_t)(bsw.x & 0xffffu) + (int)(int16_t)(bsw.x >> 16);
+        const int bs_hi = (int)(int16_t)(bsw.y & 0xffffu) + (int)(int16_t)(bsw.y >> 16);
+        const uint8_t* base = m ? w1 : w0;
+        const uint32_t blk = rb + (uint32_t)b;
+        const uint4 wq = *reinterpret_cast<const uint4*>(base + blk * 128u + 16 * l);
+        const uint4 hd = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16u);
+        const uint32_t qh = Q5 ? *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32u + 4 * l) : 0u;
+        uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
+        unpack_scales(hd.y, hd.z, hd.w, sc_lo, sc_hi, mn_lo, mn_hi);
+        int32_t sumi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t qw = word_of(wq, j);
+            uint32_t lo = qw & 0x0f0f0f0fu, hi = (qw >> 4) & 0x0f0f0f0fu;
+            if (Q5) {
+                lo |= ((qh >> (2 * j)) & 0x01010101u) << 4;
+                hi |= ((qh >> (2 * j + 1)) & 0x01010101u) << 4;
+            }
+            const int dl = __builtin_amdgcn_sdot4((int)lo, (int)word_of(a0, j), 0, false);
+            const int dh = __builtin_amdgcn_sdot4((int)hi, (int)word_of(a1, j), 0, false);
+            const uint32_t scw = j < 2 ? sc_lo : sc_hi;
+            // |dl|, |dh| <= 4*31*127 and scales <= 63: exact in 24-bit products
+            sumi += __mul24(byte_of(scw, 2 * (j & 1)), dl) + __mul24(byte_of(scw, 2 * (j & 1) + 1), dh);
+        }
+        const uint32_t mnw = k < 2 ? mn_lo : mn_hi;
+        S = sumi;
+        P = __mul24(byte_of(mnw, 2 * (k & 1)), bs_lo) + __mul24(byte_of(mnw, 2 * (k & 1) + 1), bs_hi);
+        D = yd * half_bits_to_f32(hd.x & 0xffffu);
+        DM = -yd * half_bits_to_f32(hd.x >> 16);
+        if (Q5) {
+            // the four min products summed exactly, on every lane of the group
+            int32_t pm = l < 4 ? P : 0;
+            pm += __shfl_xor(pm, 1, 64);
+            pm += __shfl_xor(pm, 2, 64);
+            P = __shfl(pm, tid & ~7, 64);
+        }
+        if (DBG) {
+            int32_t sS = sumi, sM = l < 4 ? P : 0;
+            if (Q5) sM = l == 0 ? P : 0;
+            sS += __shfl_xor(sS, 1, 64); sS += __shfl_xor(sS, 2, 64); sS += __shfl_xor(sS, 4, 64);
+            sM += __shfl_xor(sM, 1, 64); sM += __shfl_xor(sM, 2, 64); sM += __shfl_xor(sM, 4, 64);
+            if (l == 0) { dbgS[blk] = sS; dbgM[blk] = sM; }
+        }
+    };
+
+    float acc[NMAT], accm[NMAT], summs[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) { acc[m] = 0.0f; accm[m] = 0.0f; summs[m] = 0.0f; }
+    // the reference's per-block fp32 step
+    auto step = [&](int m, int32_t S, int32_t P, float D, float DM) {
+        acc[m] = __builtin_fmaf(D, (float)S, acc[m]);
+        if (Q5) {
+            const float tm = DM * (float)P;
+            summs[m] = summs[m] + tm;
+        } else if (l < 4) {
+            accm[m] = __builtin_fmaf(DM, (float)P, accm[m]);
+        }
+    };
+
+    if (NB > 0) {
+        int32_t S[NMAT][NH], P[NMAT][NH];
+        float D[NMAT][NH], DM[NMAT][NH];
+#pragma unroll
+        for (int i = 0; i < NH; i++) {
+            const int b = grp * NH + i;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                S[m][i] = 0; P[m][i] = 0; D[m][i] = 0.0f; DM[m][i] = 0.0f;
+                if (b < nb) block(m, b, S[m][i], P[m][i], D[m][i], DM[m][i]);
+            }
+        }
+        if (DBG) return;
+#pragma unroll
+        for (int gs = 0; gs < SPLIT; gs++) {
+#pragma unroll
+            for (int i = 0; i < NH; i++) {
+                if (gs * NH + i < nb) {
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        int32_t So = S[m][i], Po = P[m][i];
+                        float Do = D[m][i], DMo = DM[m][i];
+                        if (gs > 0) {   // group gs's values, seen from group 0 (lane ^ 8*gs)
+                            So = __shfl_xor(So, 8 * gs, 64);
+                            Po = __shfl_xor(Po, 8 * gs, 64);
+                            Do = __shfl_xor(Do, 8 * gs, 64);
+                            DMo = __shfl_xor(DMo, 8 * gs, 64);
+                        }
+                        step(m, So, Po, Do, DMo);
+                    }
+                }
+            }
+        }
+    } else {
+        for (int b = 0; b < nb; b++) {
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                int32_t S, P;
+                float D, DM;
+                block(m, b, S, P, D, DM);
+                if (!DBG) step(m, S, P, D, DM);
+            }
+        }
+        if (DBG) return;
+    }
+    float r[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        const float t1 = acc[m] + __shfl_xor(acc[m], 4, 64);
+        const float t2 = t1 + __shfl_xor(t1, 2, 64);
+        const float h = t2 + __shfl_xor(t2, 1, 64);
+        if (Q5) {
+            r[m] = h + summs[m];
+        } else {
+            const float v1 = accm[m] + __shfl_xor(accm[m], 2, 64);
+            const float hm = v1 + __shfl_xor(v1, 1, 64);
+            r[m] = h + hm;
+        }
+    }
+    if (l == 0 && grp == 0) out[row] = NMAT == 2 ? gelu_ref(r[0]) * r[NMAT - 1] : r[0];
+}
+
+// ------------------------------------------------------------------------
+// Q6_K x fp32 (mm_quant_rows semantics), one row slice per 8-lane group
+// ------------------------------------------------------------------------
+// A 256-thread workgroup stages x in LDS once and sweeps row groups of
+// 32/KS rows; each row is split over KS groups (ks takes blocks ks, ks+KS,
+// ...) whose partial sums are added in LDS.  Lane L = 4h+u of a group owns
+// the 32 weights 128h + 32k + 8u + e (k < 4, e < 8) of each block: their
+// 6-bit codes are assembled four at a time into bytes of (q - 32), converted
+// to float and multiplied by x; each run of 8 is scaled once by d*sc (the
+// reference scales every weight, (d*sc)*(q-32); results agree to fp32
+// tolerance, not bit for bit).
+template <int KS, bool SOFTCAP>
+__global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                            float* __restrict__ out, int nb, int d, float cap) {
+    extern __shared__ __align__(16) float xs[];   // n floats, then [32] partials
+    constexpr int RPW = 32 / KS;
+    const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
+    const int rr = g % RPW, ks = g / RPW;
+    const size_t nblk = (size_t)d * nb;
+    const Q6KPlanes P = q6k_planes(nblk);
+    const int n4 = nb * 64;
+    for (int i = tid; i < n4; i += 256) reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+    float* part = xs + nb * 256;
+    __syncthreads();
+    const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
+    const int ngroups = (d + RPW - 1) / RPW;
+    for (int rg = blockIdx.x; rg < ngroups; rg += gridDim.x) {
+        const int row = rg * RPW + rr;
+        float acc = 0.0f;
+        if (row < d) {
+            for (int b = ks; b < nb; b += KS) {
+                const size_t blk = (size_t)row * nb + b;
+                const uint4 ql = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
+                const uint2 qh = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
+                const uint2 sc = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+                const float df = f16_to_f32(*reinterpret_cast<const uint16_t*>(w + P.d + blk * 2));
+                const float* xb = xs + b * 256 + 128 * h + 8 * u;
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
+                    const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
+                    const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+                    const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+                    const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);
+                    const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
+                    // bytes q in [0,63] -> (q - 32) as int8, per byte without borrows
+                    const uint32_t sa = ((ca | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                    const uint32_t sb = ((cb | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                    const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
+                    const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
+                    float dot = x0.x * (float)(int8_t)(sa & 0xff);
+                    dot = __builtin_fmaf(x0.y, (float)(int8_t)((sa >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(x0.z, (float)(int8_t)((sa >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(x0.w, (float)(int8_t)(sa >> 24), dot);
+                    dot = __builtin_fmaf(x1.x, (float)(int8_t)(sb & 0xff), dot);
+                    dot = __builtin_fmaf(x1.y, (float)(int8_t)((sb >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(x1.z, (float)(int8_t)((sb >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(x1.w, (float)(int8_t)(sb >> 24), dot);
+                    const int sbi = (u >> 1) + 2 * kk;
+                    const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
+                    acc = __builtin_fmaf(df * (float)s8, dot, acc);
+                }
+            }
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        if (KS > 1) {
+            if (L == 0) part[g] = acc;
+            __syncthreads();
+            if (tid < RPW) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KS; j++) s += part[j * RPW + tid];
+                const int r = rg * RPW + tid;
+                if (r < d) out[r] = SOFTCAP ? cap * tanhf(s * inv) : s;
+            }
+            __syncthreads();
+        } else if (L == 0 && row < d) {
+            out[row] = SOFTCAP ? cap * tanhf(acc * inv) : acc;
+        }
+    }
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -429,40 +433,46 @@ bool pick_tiling(int nb, int d, int nmat, int* tpg, int* R) {
     return false;
 }
 
-size_t q45_lds(int nb, int tpg, int R) {
-    return (size_t)((nb * 292 + 15) & ~15) + (size_t)kGroups * tpg * 56 + (size_t)2 * R * 4;
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT>
+void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M) {
+    constexpr int rows_per_wg = 8 / SPLIT;
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT>), dim3((d + rows_per_wg - 1) / rows_per_wg),
+                       dim3(64), 0, g4_stream(), (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)q8, o, nb, d,
+                       S, M);
 }
 
 template <bool Q5, int NMAT, bool DBG>
 int launch_q45(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M) {
-    int tpg = 1, R = 1;
-    if (!pick_tiling(nb, d, NMAT, &tpg, &R)) return g4_fail(G4_ERR_ARG, "GEMV: row length %d blocks too long", nb);
-    const dim3 grid((d + R - 1) / R);
-    const size_t lds = q45_lds(nb, tpg, R);
-    const uint8_t *a = (const uint8_t*)w0, *b = (const uint8_t*)w1, *q = (const uint8_t*)q8;
-    switch (tpg) {
-    case 8: hipLaunchKernelGGL((gemv_q45k_kernel<8, Q5, NMAT, DBG>), grid, dim3(kWG), lds, g4_stream(), a, b, q, o, nb, d, R, S, M); break;
-    case 4: hipLaunchKernelGGL((gemv_q45k_kernel<4, Q5, NMAT, DBG>), grid, dim3(kWG), lds, g4_stream(), a, b, q, o, nb, d, R, S, M); break;
-    case 2: hipLaunchKernelGGL((gemv_q45k_kernel<2, Q5, NMAT, DBG>), grid, dim3(kWG), lds, g4_stream(), a, b, q, o, nb, d, R, S, M); break;
-    default: hipLaunchKernelGGL((gemv_q45k_kernel<1, Q5, NMAT, DBG>), grid, dim3(kWG), lds, g4_stream(), a, b, q, o, nb, d, R, S, M); break;
+    switch (nb) {   // unrolled for the row lengths of the model (256, 2048, 2560, 4096)
+    case 1: launch_q45_nb<Q5, NMAT, DBG, 1, 1>(w0, w1, q8, o, nb, d, S, M); break;
+    case 8: launch_q45_nb<Q5, NMAT, DBG, 8, 2>(w0, w1, q8, o, nb, d, S, M); break;
+    case 10: launch_q45_nb<Q5, NMAT, DBG, 10, 2>(w0, w1, q8, o, nb, d, S, M); break;
+    case 16: launch_q45_nb<Q5, NMAT, DBG, 16, 2>(w0, w1, q8, o, nb, d, S, M); break;
+    default: launch_q45_nb<Q5, NMAT, DBG, 0, 1>(w0, w1, q8, o, nb, d, S, M); break;
     }
-    return g4_check_launch("gemv_q45k_kernel");
+    return g4_check_launch("gemv_q45_rows_kernel");
+}
+
+// rows per workgroup pass = 32/KS; pick the smallest split that still gives
+// at least two workgroups per CU
+template <bool SOFTCAP, int KS>
+void launch_q6_ks(const void* w, const float* x, float* o, int nb, int d, float cap) {
+    const int ngroups = (d + 32 / KS - 1) / (32 / KS);
+    int grid = 4 * g4_num_cus();
+    if (grid > ngroups) grid = ngroups;
+    const size_t lds = (size_t)nb * 1024 + 32 * 4;
+    hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP>), dim3(grid), dim3(256), lds, g4_stream(),
+                       (const uint8_t*)w, x, o, nb, d, cap);
 }
 
 template <bool SOFTCAP>
 int launch_q6_f32(const void* w, const float* x, float* o, int nb, int d, float cap) {
-    int tpg = 1, R = 1;
-    if (!pick_tiling(nb, d, 1, &tpg, &R)) return g4_fail(G4_ERR_ARG, "GEMV: row length %d blocks too long", nb);
-    const dim3 grid((d + R - 1) / R);
-    const size_t lds = (size_t)nb * 1024 + (size_t)kGroups * tpg * 4;
-    const uint8_t* a = (const uint8_t*)w;
-    switch (tpg) {
-    case 8: hipLaunchKernelGGL((gemv_q6k_f32_kernel<8, SOFTCAP>), grid, dim3(kWG), lds, g4_stream(), a, x, o, nb, d, R, cap); break;
-    case 4: hipLaunchKernelGGL((gemv_q6k_f32_kernel<4, SOFTCAP>), grid, dim3(kWG), lds, g4_stream(), a, x, o, nb, d, R, cap); break;
-    case 2: hipLaunchKernelGGL((gemv_q6k_f32_kernel<2, SOFTCAP>), grid, dim3(kWG), lds, g4_stream(), a, x, o, nb, d, R, cap); break;
-    default: hipLaunchKernelGGL((gemv_q6k_f32_kernel<1, SOFTCAP>), grid, dim3(kWG), lds, g4_stream(), a, x, o, nb, d, R, cap); break;
-    }
-    return g4_check_launch("gemv_q6k_f32_kernel");
+    const int target = 2 * g4_num_cus();
+    if ((d + 31) / 32 >= target) launch_q6_ks<SOFTCAP, 1>(w, x, o, nb, d, cap);
+    else if ((d + 15) / 16 >= target) launch_q6_ks<SOFTCAP, 2>(w, x, o, nb, d, cap);
+    else if ((d + 7) / 8 >= target) launch_q6_ks<SOFTCAP, 4>(w, x, o, nb, d, cap);
+    else launch_q6_ks<SOFTCAP, 8>(w, x, o, nb, d, cap);
+    return g4_check_launch("gemv_q6k_rows_kernel");
 }
 
 int launch_q6_q8(const void* w, const void* q8, float* o, int nb, int d) {

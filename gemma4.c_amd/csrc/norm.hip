@@ -63,37 +63,65 @@ struct ResidualArgs {
     float eps;
 };
 
+// EPT elements per thread (n <= EPT * kNormThreads); every global load is
+// issued at entry, so the kernel pays one memory round trip.
+template <int EPT>
 __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArgs a) {
     extern __shared__ __align__(16) float buf[];   // n floats: the vector to quantize
     __shared__ float red[16];
-    const int n = a.n;
-    float* x = a.x;
+    const int n = a.n, tid = threadIdx.x;
+    float xv[EPT], yv[EPT], wp[EPT], wn[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int i = tid + k * kNormThreads;
+        const bool ok = i < n;
+        xv[k] = ok ? a.x[i] : 0.0f;
+        yv[k] = (ok && a.y) ? a.y[i] : 0.0f;
+        wp[k] = (ok && a.y) ? a.w_post[i] : 0.0f;
+        wn[k] = (ok && a.w_next) ? a.w_next[i] : 0.0f;
+    }
+    const float sc = a.oscale ? a.oscale[0] : 1.0f;
     if (a.y) {
-        const float sy = rms_scale(a.y, n, a.eps, red);
-        const float sc = a.oscale ? a.oscale[0] : 1.0f;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            float v = x[i] + (a.y[i] * sy) * a.w_post[i];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) ss += yv[k] * yv[k];
+        ss = block_sum(ss, red);
+        const float sy = 1.0f / sqrtf(ss / (float)n + a.eps);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * kNormThreads;
+            float v = xv[k] + (yv[k] * sy) * wp[k];
             if (a.oscale) v = v * sc;
-            x[i] = v;
-            buf[i] = v;
+            xv[k] = v;
+            if (i < n) a.x[i] = v;
+        }
+    }
+    if (a.w_next) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) ss += xv[k] * xv[k];
+        ss = block_sum(ss, red);
+        const float sx = 1.0f / sqrtf(ss / (float)n + a.eps);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * kNormThreads;
+            const float t = (xv[k] * sx) * wn[k];
+            if (i < n) {
+                if (a.xb2) a.xb2[i] = t;
+                buf[i] = a.qsrc == 0 ? t : xv[k];
+            }
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = x[i];
-    }
-    __syncthreads();
-    if (a.w_next) {
-        const float sx = rms_scale(buf, n, a.eps, red);
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const float v = (buf[i] * sx) * a.w_next[i];
-            if (a.xb2) a.xb2[i] = v;
-            if (a.qsrc == 0) buf[i] = v;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * kNormThreads;
+            if (i < n) buf[i] = xv[k];
         }
-        __syncthreads();
     }
     if (a.q8) {
-        const int nb = n / 256, lane = threadIdx.x & 63;
-        for (int b = threadIdx.x >> 6; b < nb; b += blockDim.x >> 6) {
+        __syncthreads();
+        const int nb = n / 256, lane = tid & 63;
+        for (int b = tid >> 6; b < nb; b += kNormThreads / 64) {
             const float4 f = reinterpret_cast<const float4*>(buf + (size_t)b * 256)[lane];
             const float v[4] = {f.x, f.y, f.z, f.w};
             quantize_block_wave(v, lane, a.q8, nb, b);
@@ -112,7 +140,11 @@ extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, c
     G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm: n=%d not a multiple of 256 for Q8_K", n);
     G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm: quantizing xb2 needs w_next");
     ResidualArgs a{x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
-    hipLaunchKernelGGL(residual_norm_kernel, dim3(1), dim3(kNormThreads), (size_t)n * 4, g4_stream(), a);
+    const dim3 g(1), b(kNormThreads);
+    const size_t lds = (size_t)n * 4;
+    if (n <= 1 * kNormThreads) hipLaunchKernelGGL(residual_norm_kernel<1>, g, b, lds, g4_stream(), a);
+    else if (n <= 4 * kNormThreads) hipLaunchKernelGGL(residual_norm_kernel<4>, g, b, lds, g4_stream(), a);
+    else hipLaunchKernelGGL(residual_norm_kernel<16>, g, b, lds, g4_stream(), a);
     return g4_check_launch("residual_norm_kernel");
 }
 

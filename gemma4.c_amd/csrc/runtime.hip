@@ -109,6 +109,13 @@ extern "C" int g4_memcpy_d2h_async(void* dst, const void* src, size_t bytes) {
     G4_CHECK_ARG(dst && src, "g4_memcpy_d2h_async: null pointer");
     return g4_hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
 }
+// synchronous fill of device memory (set-up only; never inside a captured graph)
+extern "C" int g4_memset(void* p, int value, size_t bytes) {
+    G4_CHECK_ARG(p || !bytes, "g4_memset: null pointer");
+    if (!bytes) return G4_OK;
+    G4_HIP(hipMemsetAsync(p, value, bytes, g_stream));
+    return g4_hip_status(hipStreamSynchronize(g_stream));
+}
 extern "C" int g4_host_alloc(void** p, size_t bytes) {
     G4_CHECK_ARG(p && bytes, "g4_host_alloc: bad arguments");
     return g4_hip_status(hipHostMalloc(p, bytes, hipHostMallocDefault));

@@ -69,13 +69,15 @@ _SIGS = {
     "g4_argmax_part_bytes": (SZ, [I]),
     "g4_argmax": (I, [VP, I, VP, VP, VP, VP]),
     "g4_residual_norm": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, F]),
-    "g4_qkv_post": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, F, F, VP, F]),
+    "g4_qkv_post": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, F, F, VP, F, VP]),
+    "g4_rope_table": (I, [VP, VP, I, I, F, F, VP]),
     "g4_attn_part_bytes": (SZ, [I, I, I]),
     "g4_attn_decode_dev": (I, [VP, VP, VP, I, I, VP, I, I, I, I, F, I, VP, VP, VP]),
     "g4_emb_lookup_dev": (I, [VP, VP, I, I, VP, I, F]),
     "g4_ple_finish": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
     "g4_gelu_mul_quant": (I, [VP, VP, I, VP]),
     "g4_store_i32x2": (I, [VP, I, I]),
+    "g4_memset": (I, [VP, I, SZ]),
     "g4_memcpy_h2d_async": (I, [VP, VP, SZ]),
     "g4_memcpy_d2h_async": (I, [VP, VP, SZ]),
     "g4_host_alloc": (I, [C.POINTER(VP), SZ]),

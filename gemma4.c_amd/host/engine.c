@@ -82,6 +82,7 @@ struct g4e_model {
     float *kc[E_N_LAYER_KV], *vc[E_N_LAYER_KV];
     int kv_ring[E_N_LAYER_KV];
     float *attn_part;
+    float *rope_tab;         /* (cos, sin) per pair: [rot_swa/2] then [rot_full/2] */
     int G_swa, G_full;
     int *dstep;              /* [0] token, [1] pos, [2] argmax result */
     void *argmax_part;
@@ -411,6 +412,17 @@ int g4e_check_image(const void *data, size_t size, int max_seq, int out[9]) {
     return rc;
 }
 
+/* time chunks of the decode attention for a window capacity: about 16
+ * positions per workgroup at full capacity, 1..64 chunks (more only if a chunk
+ * would exceed 1024 positions) */
+static int attn_chunks(int cap) {
+    int G = (cap + 15) / 16;
+    if (G < 1) G = 1;
+    if (G > 64) G = 64;
+    while ((cap + G - 1) / G > 1024) G++;
+    return G;
+}
+
 /* load_weights (upload to HBM) + alloc_state (main.c:1328-1423) */
 static int load(g4e_model *m, const Image *im) {
     const Config *c = &m->c;
@@ -497,14 +509,14 @@ static int load(g4e_model *m, const Image *im) {
     /* attention partials: chunk counts fixed from capacity (<= 1024 positions
      * per chunk) so that one captured graph serves every position */
     const int cap_swa = c->window > 0 && c->window < c->max_seq ? c->window : c->max_seq;
-    m->G_swa = (cap_swa + 127) / 128;
-    m->G_full = (c->max_seq + 127) / 128;
-    if (m->G_full > 256) m->G_full = 256;
-    while ((c->max_seq + m->G_full - 1) / m->G_full > 1024) m->G_full++;
-    while ((cap_swa + m->G_swa - 1) / m->G_swa > 1024) m->G_swa++;
+    m->G_swa = attn_chunks(cap_swa);
+    m->G_full = attn_chunks(c->max_seq);
     const int Gmax = m->G_full > m->G_swa ? m->G_full : m->G_swa;
     DA(m->attn_part, g4_attn_part_bytes(c->n_heads, hdmax, Gmax));
 #undef DA
+    CK(g4_memset(m->attn_part, 0, 256));      /* attention arrival counters */
+    if ((rc = dalloc(m, &p, (size_t)(c->rot_swa / 2 + c->rot_full / 2) * 8))) return rc;
+    m->rope_tab = p;
     CK(g4_host_alloc((void **)&m->hstep, 64));
     memset(m->hstep, 0, 64);
     return 0;
@@ -588,6 +600,10 @@ static int enqueue_step(g4e_model *m, int lm_mode, int capture_pos_host) {
     CK(g4_mm(m->ple_ctx, m->x, m->ple_proj.p, m->ple_proj.n, m->ple_proj.d, m->ple_proj.type, m->q8, 0));
     CK(g4_ple_finish(m->ple, m->ple_ctx, m->ple_tok.p, m->ple_tok.type, m->ple_tok.d, m->ple_proj_norm, dtok, 0, pd, L,
                      sqrtf((float)pd), 1.0f / sqrtf((float)dim), 1.0f / sqrtf(2.0f), c->eps));
+    /* RoPE angles of this position for both layer types (main.c:1725-1742) */
+    float *tab_swa = m->rope_tab, *tab_full = m->rope_tab + c->rot_swa;
+    CK(g4_rope_table(tab_swa, dpos, 0, c->rot_swa, c->theta_swa, 1.0f, NULL));
+    CK(g4_rope_table(tab_full, dpos, 0, c->rot_full, c->theta, 1.0f, m->rope_freqs));
     if (m->trace) CK(g4_memcpy_d2h(m->layer_x, m->x, (size_t)dim * 4));
     /* layer 0's attn_norm + Q8_K (later layers get it fused into the previous tail) */
     CK(g4_residual_norm(m->x, NULL, NULL, NULL, m->attn_norm[0], m->xb2, is_q8_type(m->wq[0].type) ? m->q8 : NULL, 0,
@@ -608,10 +624,11 @@ static int enqueue_step(g4e_model *m, int lm_mode, int capture_pos_host) {
             if ((rc = mm(m, m->k, m->xb2, &m->wk[l], 1))) return rc;
             if ((rc = mm(m, m->v, m->xb2, &m->wv[l], 1))) return rc;
             CK(g4_qkv_post(m->q, m->q_norm[l], m->k, m->v, m->k_norm[l], m->kc[l], m->vc[l], c->n_kv * hd, m->kv_ring[l],
-                           dpos, capture_pos_host, c->n_heads, c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps));
+                           dpos, capture_pos_host, c->n_heads, c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps,
+                           swa ? tab_swa : tab_full));
         } else {
             CK(g4_qkv_post(m->q, m->q_norm[l], NULL, NULL, NULL, NULL, NULL, 0, 0, dpos, capture_pos_host, c->n_heads,
-                           c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps));
+                           c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps, swa ? tab_swa : tab_full));
         }
         /* attention over the source layer's cache (main.c:1909-1950), attn_scale 1.0 */
         const int o_q8 = is_q8_type(m->wo[l].type);

@@ -181,13 +181,20 @@ int g4_residual_norm(float *x, const float *y, const float *w_post, const float 
                      float *xb2, void *q8, int qsrc, int n, float eps);
 /* main.c:1886-1904: q heads q_norm + RoPE in place; if k: k heads k_norm +
  * RoPE and v heads unweighted norm, stored at slot (ring ? pos%ring : pos);
- * pos = *dpos if dpos else pos. */
+ * pos = *dpos if dpos else pos; rope_tab (nullable): g4_rope_table output for
+ * this position and layer type. */
 int g4_qkv_post(float *q, const float *q_norm, const float *k, const float *v, const float *k_norm, float *kc,
                 float *vc, int kv_stride, int ring, const int *dpos, int pos, int n_heads, int n_kv, int hd, int n_rot,
-                float freq_base, float freq_scale, const float *ff, float eps);
+                float freq_base, float freq_scale, const float *ff, float eps, const float *rope_tab);
+/* (cos, sin) of the n_rot/2 RoPE pair angles at pos = *dpos (or pos), the
+ * angle chain of main.c:1727-1742; rope_tab argument of g4_qkv_post. */
+int g4_rope_table(float *tab, const int *dpos, int pos, int n_rot, float freq_base, float freq_scale,
+                  const float *freq_factors);
 /* attention block with pos = *dpos, t_start = max(0, pos+1-window) (window 0:
- * 0), G time chunks (fixed; <= 1024 positions each), partials buffer of
- * g4_attn_part_bytes(n_heads, hd, G) bytes, optional Q8_K of the output. */
+ * 0), G time chunks (fixed, 1..512; <= 1024 positions each), workspace of
+ * g4_attn_part_bytes(n_heads, hd, G) bytes whose first 256 bytes (arrival
+ * counters) are zero before the first call and are left zero, optional Q8_K of
+ * the output. */
 size_t g4_attn_part_bytes(int n_heads, int hd, int G);
 int    g4_attn_decode_dev(const float *q, const float *kc, const float *vc, int kv_stride, int ring, const int *dpos,
                           int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float *part, float *out,
@@ -207,6 +214,8 @@ int g4_store_i32x2(int *dst, int a, int b);
 /* ---------------------------------------------------------------------------
  * Streams, graphs, copies
  * ------------------------------------------------------------------------- */
+/* synchronous fill (set-up only, not for captured graphs) */
+int g4_memset(void *p, int value, size_t bytes);
 int g4_memcpy_h2d_async(void *dst, const void *src, size_t bytes);
 int g4_memcpy_d2h_async(void *dst, const void *src, size_t bytes);
 int g4_host_alloc(void **p, size_t bytes);   /* pinned host memory */
