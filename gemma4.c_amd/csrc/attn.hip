@@ -134,16 +134,14 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
 }
 
 // ---- split-T decode attention --------------------------------------------
-// Workspace layout (g4_attn_part_bytes): 256 bytes of per-kv-head arrival
-// counters (zero at rest: the last workgroup of a kv head resets its counter),
-// then the partials [n_heads][G][hd+2] = (o[hd], max, sum).
+// Workspace (g4_attn_part_bytes): the partials [n_heads][G][hd+2] =
+// (o[hd], max, sum) of every chunk.
 struct AttnArgs {
     const float* q;        // n_heads*hd
     const float* kc;       // slot 0 of the source layer's cache
     const float* vc;
     const int* dpos;       // device position (nullptr: t_start/nwin below)
     float* part;           // partials
-    unsigned int* count;   // n_kv arrival counters
     float* out;            // n_heads*hd
     uint8_t* q8;           // optional Q8_K of out (n_heads*hd/256 blocks)
     int t_start, nwin;     // used when dpos == nullptr
@@ -154,7 +152,6 @@ struct AttnArgs {
 
 constexpr int kAttnThreads = 256;
 constexpr int kChunkMax = 1024;     // positions per workgroup
-constexpr int kAttnCounterBytes = 256;
 constexpr int kMaxChunks = 512;     // chunks (workgroups) per kv head
 
 __device__ __forceinline__ void attn_window(const AttnArgs& a, int& t0, int& nwin) {
@@ -186,13 +183,11 @@ __host__ __device__ inline int attn_work_floats(int hd, int kvm) {
 __device__ __forceinline__ int attn_slot(const AttnArgs& a, int t) { return a.ring > 0 ? t % a.ring : t; }
 
 // Workgroup (c, kvh) scores chunk c of the window for the kvm q heads of kv
-// head kvh (each K/V row read once for the group), keeps (o, max, sum) of its
-// chunk; the last workgroup of kv head kvh to finish merges the G chunks by
-// log-sum-exp, writes the heads' outputs and, if asked, their Q8_K blocks.
+// head kvh (each K/V row read once for the group) and keeps (o, max, sum) of
+// its chunk; attn_merge_kernel combines the chunks by log-sum-exp.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
-    __shared__ int s_last;
     constexpr int KPL = HD / 64;          // float4 per lane of a 16-lane row slice
     constexpr int VPL = HD / 256;         // float4 per lane of a 64-lane row slice
     const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
@@ -322,83 +317,83 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         if (dd == 0) { p[HD] = cnt > 0 ? ml[2 * h] : -INFINITY; p[HD + 1] = cnt > 0 ? ml[2 * h + 1] : 0.0f; }
     }
 
-    // arrival: the last workgroup of this kv head merges (partials written by
-    // other workgroups are made visible by the release/acquire fences)
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned int prev = atomicAdd(&a.count[kvh], 1u);
-        s_last = prev == (unsigned int)(a.G - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
-    // merge the G chunks of heads kvh*kvm .. kvh*kvm + kvm - 1:
-    // f[h][g] = exp(max_g - M_h) (0 for empty chunks), L_h = sum_g sum_g * f[h][g]
-    float* fw = ml + 2 * kvm;          // [kvm][G] chunk weights, then [kvm] L
-    float* Lh = fw + kvm * a.G;
-    const float* pk = a.part + (size_t)kvh * kvm * a.G * (HD + 2);
-    for (int h = wave; h < kvm; h += kAttnThreads / 64) {
-        const float* ph = pk + (size_t)h * a.G * (HD + 2);
-        float M = -INFINITY;
-        for (int g = lane; g < a.G; g += 64) M = fmaxf(M, ph[(size_t)g * (HD + 2) + HD]);
-        M = wave_max(M);
-        float L = 0.0f;
-        for (int g = lane; g < a.G; g += 64) {
-            const float l = ph[(size_t)g * (HD + 2) + HD + 1];
-            const float f = l > 0.0f ? expf(ph[(size_t)g * (HD + 2) + HD] - M) : 0.0f;
-            fw[h * a.G + g] = f;
-            L += l * f;
-        }
-        L = wave_sum(L);
-        if (lane == 0) Lh[h] = L;
-    }
+// Merge of the G chunk partials of one q head: workgroup (h, slice) owns
+// 256 output dims.  Chunk weights f_g = exp(max_g - M) and the total
+// L = sum_g sum_g f_g are computed once in LDS; each thread then reduces its
+// dim over the chunks (eight loads in flight) and, if asked, the workgroup
+// quantizes its 256 outputs as one Q8_K block.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float fw[kMaxChunks];
+    __shared__ float red[16];
+    __shared__ __align__(16) float mo[256];
+    const int h = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x;
+    const int G = a.G;
+    const float* ph = a.part + (size_t)h * G * (HD + 2);
+    float M = -INFINITY;
+    for (int g = tid; g < G; g += 256) M = fmaxf(M, ph[(size_t)g * (HD + 2) + HD]);
+    M = wave_max(M);
+    if ((tid & 63) == 0) red[tid >> 6] = M;
     __syncthreads();
-    float* mo = sm;    // [kvm][HD] merged outputs (for the Q8_K pass)
-    for (int i = tid; i < kvm * HD; i += kAttnThreads) {
-        const int h = i / HD, dd = i - h * HD;
-        const float* ph = pk + (size_t)h * a.G * (HD + 2) + dd;
-        const float* fh = fw + h * a.G;
-        float o = 0.0f;
-        for (int g = 0; g < a.G; g++) o = __builtin_fmaf(ph[(size_t)g * (HD + 2)], fh[g], o);
-        const float L = Lh[h];
-        const float r = L > 0.0f ? o / L : 0.0f;
-        a.out[(size_t)(kvh * kvm + h) * HD + dd] = r;
-        mo[i] = r;
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float L = 0.0f;
+    for (int g = tid; g < G; g += 256) {
+        const float l = ph[(size_t)g * (HD + 2) + HD + 1];
+        const float f = l > 0.0f ? expf(ph[(size_t)g * (HD + 2) + HD] - M) : 0.0f;
+        fw[g] = f;
+        L += l * f;
     }
+    L = block_sum(L, red + 4);
+    const int dd = slice * 256 + tid;
+    const float* pd = ph + dd;
+    float o = 0.0f;
+    int g = 0;
+    for (; g + 8 <= G; g += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = pd[(size_t)(g + u) * (HD + 2)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) o = __builtin_fmaf(v[u], fw[g + u], o);
+    }
+    for (; g < G; g++) o = __builtin_fmaf(pd[(size_t)g * (HD + 2)], fw[g], o);
+    const float r = L > 0.0f ? o / L : 0.0f;
+    a.out[(size_t)h * HD + dd] = r;
     if (a.q8) {
+        mo[tid] = r;
         __syncthreads();
-        const int nb_total = a.n_heads * HD / 256;
-        for (int b = wave; b < kvm * HD / 256; b += kAttnThreads / 64) {
-            const float4 f = reinterpret_cast<const float4*>(mo + b * 256)[lane];
-            const float v[4] = {f.x, f.y, f.z, f.w};
-            quantize_block_wave(v, lane, a.q8, nb_total, kvh * kvm * HD / 256 + b);
+        if (tid < 64) {
+            const float4 f4 = reinterpret_cast<const float4*>(mo)[tid];
+            const float v[4] = {f4.x, f4.y, f4.z, f4.w};
+            quantize_block_wave(v, tid, a.q8, a.n_heads * HD / 256, h * (HD / 256) + slice);
         }
     }
-    if (tid == 0) a.count[kvh] = 0u;   // ready for the next call
 }
 
-// work region + (max, sum) pairs + merge weights [kvm][G] + [kvm] sums
-size_t attn_lds(int hd, int kvm, int G) {
-    return 4 * ((size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm + (size_t)kvm * G + (size_t)kvm);
-}
+// partial kernel LDS: work region + (max, sum) pairs
+size_t attn_lds(int hd, int kvm) { return 4 * ((size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm); }
 
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
     const dim3 grid(a.G, a.n_kv);
-    const size_t lds = attn_lds(a.hd, kvm, a.G);
-    if (a.hd == 256) hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
-    else hipLaunchKernelGGL(attn_decode_kernel<512>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
-    return g4_check_launch("attn_decode_kernel");
+    const size_t lds = attn_lds(a.hd, kvm);
+    if (a.hd == 256) {
+        hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1), dim3(256), 0, g4_stream(), a);
+    } else {
+        hipLaunchKernelGGL(attn_decode_kernel<512>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2), dim3(256), 0, g4_stream(), a);
+    }
+    return g4_check_launch("attn_decode_kernel/attn_merge_kernel");
 }
 
 int check_attn_shape(const char* who, int n_heads, int n_kv, int hd, int G) {
     if (hd != 256 && hd != 512) return g4_fail(G4_ERR_ARG, "%s: head_dim %d unsupported (256 or 512)", who, hd);
-    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8 || n_kv * 4 > kAttnCounterBytes)
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8)
         return g4_fail(G4_ERR_ARG, "%s: n_heads=%d n_kv=%d (need n_heads/n_kv in 1..8)", who, n_heads, n_kv);
     if (G < 1 || G > kMaxChunks) return g4_fail(G4_ERR_ARG, "%s: %d chunks (1..%d)", who, G, kMaxChunks);
-    if (attn_lds(hd, n_heads / n_kv, G) > 65536)
+    if (attn_lds(hd, n_heads / n_kv) > 65536)
         return g4_fail(G4_ERR_ARG, "%s: %d q heads per kv head at head_dim %d exceed the LDS budget", who,
                        n_heads / n_kv, hd);
     return G4_OK;
@@ -417,7 +412,6 @@ int workspace(size_t bytes, uint8_t** p) {
             g_ws_bytes = 0;
         }
         if (hipMalloc(&g_ws, bytes) != hipSuccess) return g4_fail(G4_ERR_NOMEM, "attention workspace (%zu B)", bytes);
-        G4_HIP(hipMemset(g_ws, 0, kAttnCounterBytes));   // arrival counters start at zero
         g_ws_bytes = bytes;
     }
     *p = (uint8_t*)g_ws;
@@ -427,9 +421,9 @@ int workspace(size_t bytes, uint8_t** p) {
 // about 16 positions per workgroup, at most 64 chunks per kv head unless a
 // chunk would exceed kChunkMax positions
 int chunks_for(int nwin) {
-    int G = (nwin + 15) / 16;
+    int G = (nwin + 31) / 32;          // about 32 positions per workgroup, 1..128 chunks
     if (G < 1) G = 1;
-    if (G > 64) G = 64;
+    if (G > 128) G = 128;
     while ((nwin + G - 1) / G > kChunkMax) G++;
     return G;
 }
@@ -495,9 +489,7 @@ extern "C" int g4_kv_append_rope(float* k, float* v, const float* k_norm, float*
     return g4_check_launch("qkv_post_kernel");
 }
 
-extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) {
-    return kAttnCounterBytes + (size_t)n_heads * G * (hd + 2) * 4;
-}
+extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) { return (size_t)n_heads * G * (hd + 2) * 4; }
 
 static int attn_common(const char* who, AttnArgs& a) {
     int rc = check_attn_shape(who, a.n_heads, a.n_kv, a.hd, a.G);
@@ -507,8 +499,7 @@ static int attn_common(const char* who, AttnArgs& a) {
     uint8_t* ws = nullptr;
     rc = workspace(g4_attn_part_bytes(a.n_heads, a.hd, a.G), &ws);
     if (rc) return rc;
-    a.count = (unsigned int*)ws;
-    a.part = (float*)(ws + kAttnCounterBytes);
+    a.part = (float*)ws;
     return launch_attn(a);
 }
 
@@ -542,8 +533,7 @@ extern "C" int g4_attn_decode_ring(const float* q, const float* kc, const float*
 
 // Engine form: position read from device memory, fixed chunk count G (so a
 // captured graph stays valid as pos advances; G * 1024 must cover the
-// window), caller-owned workspace of g4_attn_part_bytes(n_heads, hd, G) bytes
-// whose first 256 bytes are zero before the first call (they are left zero),
+// window), caller-owned workspace of g4_attn_part_bytes(n_heads, hd, G) bytes,
 // optional fused Q8_K output.
 extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* vc, int kv_stride, int ring,
                                   const int* dpos, int window, int n_heads, int n_kv, int hd, float attn_scale, int G,
@@ -553,8 +543,7 @@ extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* 
     G4_CHECK_ARG(q && kc && vc && dpos && part && out && G >= 1 && G <= kMaxChunks, "attn_decode_dev: bad arguments");
     AttnArgs a = {};
     a.q = q; a.kc = kc; a.vc = vc; a.dpos = dpos; a.out = out; a.q8 = (uint8_t*)q8;
-    a.count = (unsigned int*)part;
-    a.part = (float*)((uint8_t*)part + kAttnCounterBytes);
+    a.part = part;
     a.window = window; a.kv_stride = kv_stride; a.ring = ring;
     a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
     return launch_attn(a);

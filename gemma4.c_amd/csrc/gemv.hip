@@ -172,17 +172,33 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
     return (float)v;
 }
 
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT>
+// QIN (single-block rows only): the workgroup quantizes the fp32 input xin
+// itself (the one Q8_K block, exactly as quantize_row_q8_K) into LDS, and
+// workgroup 0 also stores it to q8 -- the reference's mm() side effect.
+// aux (nullable, NMAT == 1): epilogue out = gelu(r) * aux[row]
+// (main.c:1989-1993).
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN>
 __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
-                                                           const uint8_t* __restrict__ q8, float* __restrict__ out,
+                                                           const uint8_t* q8, float* __restrict__ out,
                                                            int nb_rt, int d, int32_t* __restrict__ dbgS,
-                                                           int32_t* __restrict__ dbgM) {
+                                                           int32_t* __restrict__ dbgM, const float* __restrict__ xin,
+                                                           uint8_t* __restrict__ q8_store,
+                                                           const float* __restrict__ aux) {
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
     const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
     const int row = blockIdx.x * (64 / GL) + tid / GL;
+    if (QIN) {
+        __shared__ __align__(16) uint8_t q8s[292];
+        const float4 f = reinterpret_cast<const float4*>(xin)[tid];
+        const float v[4] = {f.x, f.y, f.z, f.w};
+        quantize_block_wave(v, tid, q8s, 1, 0);
+        if (blockIdx.x == 0 && q8_store) quantize_block_wave(v, tid, q8_store, 1, 0);
+        __syncthreads();
+        q8 = q8s;
+    }
     if (row >= d) return;   // whole rows (groups of GL lanes) leave together
     const uint32_t nblk = (uint32_t)d * (uint32_t)nb;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
@@ -316,7 +332,10 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
             r[m] = h + hm;
         }
     }
-    if (l == 0 && grp == 0) out[row] = NMAT == 2 ? gelu_ref(r[0]) * r[NMAT - 1] : r[0];
+    if (l == 0 && grp == 0) {
+        if (NMAT == 2) out[row] = gelu_ref(r[0]) * r[NMAT - 1];
+        else out[row] = aux ? gelu_ref(r[0]) * aux[row] : r[0];
+    }
 }
 
 // ------------------------------------------------------------------------
@@ -433,22 +452,27 @@ bool pick_tiling(int nb, int d, int nmat, int* tpg, int* R) {
     return false;
 }
 
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT>
-void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M) {
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN = false>
+void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M,
+                   const float* xin = nullptr, void* q8_store = nullptr, const float* aux = nullptr) {
     constexpr int rows_per_wg = 8 / SPLIT;
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT>), dim3((d + rows_per_wg - 1) / rows_per_wg),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT, QIN>), dim3((d + rows_per_wg - 1) / rows_per_wg),
                        dim3(64), 0, g4_stream(), (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)q8, o, nb, d,
-                       S, M);
+                       S, M, xin, (uint8_t*)q8_store, aux);
 }
 
+// rows of nb blocks; the split of a row over lane groups grows with the work
+// per lane (the fused gate|up pair does twice the integer work per block)
 template <bool Q5, int NMAT, bool DBG>
-int launch_q45(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M) {
+int launch_q45(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M,
+               const float* aux = nullptr) {
+    constexpr int SP = NMAT == 2 ? 4 : 2;
     switch (nb) {   // unrolled for the row lengths of the model (256, 2048, 2560, 4096)
-    case 1: launch_q45_nb<Q5, NMAT, DBG, 1, 1>(w0, w1, q8, o, nb, d, S, M); break;
-    case 8: launch_q45_nb<Q5, NMAT, DBG, 8, 2>(w0, w1, q8, o, nb, d, S, M); break;
-    case 10: launch_q45_nb<Q5, NMAT, DBG, 10, 2>(w0, w1, q8, o, nb, d, S, M); break;
-    case 16: launch_q45_nb<Q5, NMAT, DBG, 16, 2>(w0, w1, q8, o, nb, d, S, M); break;
-    default: launch_q45_nb<Q5, NMAT, DBG, 0, 1>(w0, w1, q8, o, nb, d, S, M); break;
+    case 1: launch_q45_nb<Q5, NMAT, DBG, 1, 1>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
+    case 8: launch_q45_nb<Q5, NMAT, DBG, 8, SP>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
+    case 10: launch_q45_nb<Q5, NMAT, DBG, 10, SP>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
+    case 16: launch_q45_nb<Q5, NMAT, DBG, 16, SP>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
+    default: launch_q45_nb<Q5, NMAT, DBG, 0, 1>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
     }
     return g4_check_launch("gemv_q45_rows_kernel");
 }
@@ -564,6 +588,15 @@ extern "C" int g4_mm(float* o, const float* x, const void* w, int n, int d, int 
     case G4_Q4_K:
     case G4_Q5_K: {
         if (n % 256) return g4_fail(G4_ERR_ARG, "mm: n=%d not multiple of QK_K", n);
+        if (!q8_ready && n == 256) {
+            // one Q8_K block: every workgroup quantizes x itself (no separate launch)
+            int rc = check_gemv("mm", o, w, x, n, d);
+            if (rc) return rc;
+            G4_CHECK_ARG(q8, "mm: null q8");
+            if (type == G4_Q4_K) launch_q45_nb<false, 1, false, 1, 1, true>(w, nullptr, nullptr, o, 1, d, nullptr, nullptr, x, q8);
+            else launch_q45_nb<true, 1, false, 1, 1, true>(w, nullptr, nullptr, o, 1, d, nullptr, nullptr, x, q8);
+            return g4_check_launch("gemv_q45_rows_kernel");
+        }
         if (!q8_ready) {
             int rc = g4_quantize_row_q8_K(x, q8, n);
             if (rc) return rc;
@@ -574,6 +607,17 @@ extern "C" int g4_mm(float* o, const float* x, const void* w, int n, int d, int 
     case G4_BF16: return g4_mm_bf16(o, x, w, n, d);
     default: return g4_fail(G4_ERR_TYPE, "Unsupported tensor type %d in matmul", type);
     }
+}
+
+extern "C" int g4_mm_quant_dot_rows_gelu_mul(float* o, const void* w, int n, int d, int type, const void* q8,
+                                             const float* mul) {
+    int rc = check_gemv("g4_mm_quant_dot_rows_gelu_mul", o, w, q8, n, d);
+    if (rc) return rc;
+    if (!mul) return g4_fail(G4_ERR_ARG, "g4_mm_quant_dot_rows_gelu_mul: null mul");
+    const int nb = n / 256;
+    if (type == G4_Q4_K) return launch_q45<false, 1, false>(w, nullptr, q8, o, nb, d, nullptr, nullptr, mul);
+    if (type == G4_Q5_K) return launch_q45<true, 1, false>(w, nullptr, q8, o, nb, d, nullptr, nullptr, mul);
+    return g4_fail(G4_ERR_TYPE, "g4_mm_quant_dot_rows_gelu_mul: type %d not supported", type);
 }
 
 extern "C" int g4_mm_gate_up_gelu(float* hb, const void* gate, const void* up, int n, int d, int type, const void* q8) {

@@ -55,6 +55,7 @@ _SIGS = {
     "g4_mm_bf16": (I, [VP, VP, VP, I, I]),
     "g4_mm": (I, [VP, VP, VP, I, I, I, VP, I]),
     "g4_mm_gate_up_gelu": (I, [VP, VP, VP, I, I, I, VP]),
+    "g4_mm_quant_dot_rows_gelu_mul": (I, [VP, VP, I, I, I, VP, VP]),
     "g4_debug_block_sums": (I, [VP, I, I, I, VP, VP, VP]),
     "g4_set_gemv_occupancy": (I, [I]),
     "g4_rmsnorm": (I, [VP, VP, VP, I, F]),

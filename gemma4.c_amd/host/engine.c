@@ -412,13 +412,13 @@ int g4e_check_image(const void *data, size_t size, int max_seq, int out[9]) {
     return rc;
 }
 
-/* time chunks of the decode attention for a window capacity: about 16
- * positions per workgroup at full capacity, 1..64 chunks (more only if a chunk
- * would exceed 1024 positions) */
+/* time chunks of the decode attention for a window capacity: about 32
+ * positions per workgroup at full capacity, 1..128 chunks (more only if a
+ * chunk would exceed 1024 positions) */
 static int attn_chunks(int cap) {
-    int G = (cap + 15) / 16;
+    int G = (cap + 31) / 32;
     if (G < 1) G = 1;
-    if (G > 64) G = 64;
+    if (G > 128) G = 128;
     while ((cap + G - 1) / G > 1024) G++;
     return G;
 }
@@ -514,7 +514,6 @@ static int load(g4e_model *m, const Image *im) {
     const int Gmax = m->G_full > m->G_swa ? m->G_full : m->G_swa;
     DA(m->attn_part, g4_attn_part_bytes(c->n_heads, hdmax, Gmax));
 #undef DA
-    CK(g4_memset(m->attn_part, 0, 256));      /* attention arrival counters */
     if ((rc = dalloc(m, &p, (size_t)(c->rot_swa / 2 + c->rot_full / 2) * 8))) return rc;
     m->rope_tab = p;
     CK(g4_host_alloc((void **)&m->hstep, 64));
@@ -646,11 +645,16 @@ static int enqueue_step(g4e_model *m, int lm_mode, int capture_pos_host) {
         /* post_ffw_norm + residual; Q8_K of x for inp_gate (main.c:1982-1988) */
         const int q8_ig = is_q8_type(m->inp_gate[l].type);
         CK(g4_residual_norm(m->x, m->xb2, m->post_ffw_norm[l], NULL, NULL, NULL, q8_ig ? m->q8 : NULL, 1, dim, c->eps));
-        if ((rc = mm(m, m->ple_gate, m->x, &m->inp_gate[l], q8_ig))) return rc;
-        /* gelu * ple[l], then Q8_K for proj (main.c:1989-1994) */
-        const int q8_pj = is_q8_type(m->proj[l].type);
-        CK(g4_gelu_mul_quant(m->ple_gate, m->ple + (size_t)l * pd, pd, q8_pj ? m->q8 : NULL));
-        if ((rc = mm(m, m->xb2, m->ple_gate, &m->proj[l], q8_pj))) return rc;
+        /* inp_gate GEMV with gelu * ple[l] in its epilogue (main.c:1988-1993) */
+        if (q8_ig) {
+            CK(g4_mm_quant_dot_rows_gelu_mul(m->ple_gate, m->inp_gate[l].p, dim, pd, m->inp_gate[l].type, m->q8,
+                                             m->ple + (size_t)l * pd));
+        } else {
+            if ((rc = mm(m, m->ple_gate, m->x, &m->inp_gate[l], 0))) return rc;
+            CK(g4_gelu_mul_quant(m->ple_gate, m->ple + (size_t)l * pd, pd, NULL));
+        }
+        /* proj (main.c:1994): mm() quantizes its 256-wide input inside the GEMV */
+        if ((rc = mm(m, m->xb2, m->ple_gate, &m->proj[l], 0))) return rc;
         /* post_norm + residual, out_scale (main.c:1995-2003), fused with the next
          * layer's attn_norm + Q8_K, or with the final norm (main.c:2021) */
         if (l + 1 < L) {

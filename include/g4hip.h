@@ -112,6 +112,8 @@ int g4_mm_bf16(float *o, const float *x, const void *w, int n, int d);
  * q8 unless q8_ready, then integer dots; Q6_K -> mm_quant_rows; BF16 ->
  * mm_bf16; other types -> G4_ERR_TYPE. */
 int g4_mm(float *o, const float *x, const void *w, int n, int d, int type, void *q8, int q8_ready);
+/* PLE gate (main.c:1988-1993): o[i] = gelu(W_i . q8) * mul[i], W Q4_K/Q5_K. */
+int g4_mm_quant_dot_rows_gelu_mul(float *o, const void *w, int n, int d, int type, const void *q8, const float *mul);
 /* Fused FFN up-projection: hb[i] = gelu(gate_i . x) * (up_i . x) for
  * i < d, both Q4_K/Q5_K against one Q8_K vector (main.c:1974-1980). */
 int g4_mm_gate_up_gelu(float *hb, const void *gate, const void *up, int n, int d, int type, const void *q8);
@@ -192,9 +194,7 @@ int g4_rope_table(float *tab, const int *dpos, int pos, int n_rot, float freq_ba
                   const float *freq_factors);
 /* attention block with pos = *dpos, t_start = max(0, pos+1-window) (window 0:
  * 0), G time chunks (fixed, 1..512; <= 1024 positions each), workspace of
- * g4_attn_part_bytes(n_heads, hd, G) bytes whose first 256 bytes (arrival
- * counters) are zero before the first call and are left zero, optional Q8_K of
- * the output. */
+ * g4_attn_part_bytes(n_heads, hd, G) bytes, optional Q8_K of the output. */
 size_t g4_attn_part_bytes(int n_heads, int hd, int G);
 int    g4_attn_decode_dev(const float *q, const float *kc, const float *vc, int kv_stride, int ring, const int *dpos,
                           int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float *part, float *out,

@@ -250,3 +250,40 @@ def test_mm_dispatch(lib, orc):
     lib.g4_mm(out.ptr, xd.ptr, w.ptr, n, d, 12, q8.ptr, 0)
     want = orc.mm_quant_dot_rows(raw, n, d, 12, orc.quantize_q8K(x))
     assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_gelu_mul_epilogue(lib, orc, qtype):
+    """PLE gate: gelu(W.q8) * mul (main.c:1988-1993) in the GEMV epilogue."""
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 256
+    rng = np.random.default_rng(51 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    mul = rng.standard_normal(d).astype(np.float32)
+    w = upload_quant(lib, raw, qtype, n, d)
+    _, q8 = gpu_q8(lib, x)
+    md, out = dbuf(lib, mul), DBuf(lib, 4 * d)
+    lib.g4_mm_quant_dot_rows_gelu_mul(out.ptr, w.ptr, n, d, qtype, q8.ptr, md.ptr)
+    g = orc.mm_quant_dot_rows(raw, n, d, qtype, orc.quantize_q8K(x))
+    want = np.array([orc.L.or_gelu(float(v)) for v in g], np.float32) * mul
+    # the GEMV is bit-exact; tanhf (device libm vs glibc) may differ by ulps
+    assert np.allclose(out.to_array(np.float32), want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_single_block_quantizes_inside(lib, orc, qtype):
+    """mm() on a 256-wide input quantizes inside the GEMV; the output and the
+    q8 side effect equal the reference's quantize_row_q8_K + dot."""
+    from g4 import DBuf, upload_quant
+    n, d = 256, 2560
+    rng = np.random.default_rng(61 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = upload_quant(lib, raw, qtype, n, d)
+    xd, q8, out = dbuf(lib, x), DBuf(lib, lib.L.g4_q8K_bytes(n)), DBuf(lib, 4 * d)
+    lib.g4_mm(out.ptr, xd.ptr, w.ptr, n, d, qtype, q8.ptr, 0)
+    q8h = orc.quantize_q8K(x)
+    want = orc.mm_quant_dot_rows(raw, n, d, qtype, q8h)
+    assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
+    assert download_q8(lib, q8, n).tobytes() == q8h.tobytes()
