@@ -65,10 +65,22 @@ class Timer:
         return ms.value
 
 
-def roofline(bytes_per_launch: float, sec_per_launch: float) -> dict:
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE KiB per dispatch, each
+    scaled by what the counter reads for a plain copy of known size)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        t = json.load(open(path))[kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return round(1024 * (t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]))
+
+
+def roofline(bytes_per_launch: float, sec_per_launch: float, kernel: str = "") -> dict:
     gbs = bytes_per_launch / sec_per_launch / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel)}
 
 
 # ---------------------------------------------------------------------------
@@ -104,7 +116,8 @@ def bench_gemv(lib, g4, synth, args):
         "ms_per_step": ms / args.steps, "dtype": "int8xu4->int32, fp32 combine",
         "config": {"workload": "Q4_K x Q8_K GEMV 10240x2560 (seed 0), batch 1", "rows": d, "n": n,
                    "weight_copies_rotated": ncp},
-        "roofline": dict(roofline(algo, per_launch), kernel="gemv_q45k_kernel", bytes_per_launch=algo),
+        "roofline": dict(roofline(algo, per_launch, "gemv_q45k_kernel"), kernel="gemv_q45k_kernel",
+                         bytes_per_launch=algo),
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_gemv_baseline(raw, x, n, d, algo)
@@ -170,6 +183,25 @@ def bench_lmhead(lib, g4, synth, args):
     return res
 
 
+def bench_copy(lib, g4, synth, args):
+    """Plain device-to-device copy of 64 MiB (read + write): the practical HBM
+    ceiling, and the reference kernel for scaling rocprof byte counters."""
+    nbytes = 64 << 20
+    ncp = 4
+    srcs = [g4.DBuf(lib, nbytes) for _ in range(ncp)]
+    dst = g4.DBuf(lib, nbytes)
+    L = lib.L
+
+    def step(i):
+        L.g4_memcpy_d2d_async(dst.ptr, srcs[i % ncp].ptr, nbytes)
+
+    ms = _time_steps(lib, step, args)
+    per = ms / 1e3 / args.steps
+    return {"value": round(2 * nbytes / per / 1e9, 1), "unit": "GB/s (read+write)", "higher_is_better": True,
+            "ms_per_step": ms / args.steps, "dtype": "u8", "config": {"workload": "device copy 64 MiB"},
+            "roofline": dict(roofline(2 * nbytes, per), kernel="copy", bytes_per_launch=2 * nbytes)}
+
+
 def _gguf_e4b(synth, seed: int = 4) -> str:
     """The synthetic E4B-shape GGUF (about 5.4 GB), written once per machine."""
     d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
@@ -206,12 +238,21 @@ def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):
     ms = _time_steps(lib, step, A)
     per = ms / 1e3 / n_launch
     algo = 2 * g_raw.nbytes + lib.L.g4_q8K_bytes(n) + 4 * d
-    return dict(roofline(algo, per), kernel="gemv_q45k_kernel<gate|up, GELU> 2x10240x2560 Q4_K",
-                bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
+    name = "gemv_q45_rows_kernel<gate|up, GELU> 2x10240x2560 Q4_K"
+    return dict(roofline(algo, per, name), kernel=name, bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
 
 
 def _log(msg: str) -> None:
     print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def bench_gateup(lib, g4, synth, args):
+    """The dominant decode kernel alone: fused gate|up GELU GEMV at its decode
+    shape (Q4_K 2 x 10240x2560), weight copies rotated through >= 512 MB."""
+    r = _gate_up_roofline(lib, g4, synth, n_launch=args.steps)
+    return {"value": r["achieved"], "unit": "GB/s", "higher_is_better": True,
+            "ms_per_step": r["us_per_launch"] / 1e3, "dtype": "int8xu4->int32, fp32 combine",
+            "config": {"workload": "fused gate|up GELU GEMV, Q4_K 2 x 10240x2560, batch 1 (seed 1)"}, "roofline": r}
 
 
 def bench_decode(lib, g4, synth, args):
@@ -291,7 +332,8 @@ def _time_steps(lib, step, args) -> float:
     return ms
 
 
-WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "lmhead": bench_lmhead}
+WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
+             "copy": bench_copy}
 
 
 def main() -> int:

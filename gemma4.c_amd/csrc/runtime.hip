@@ -109,6 +109,11 @@ extern "C" int g4_memcpy_d2h_async(void* dst, const void* src, size_t bytes) {
     G4_CHECK_ARG(dst && src, "g4_memcpy_d2h_async: null pointer");
     return g4_hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
 }
+extern "C" int g4_memcpy_d2d_async(void* dst, const void* src, size_t bytes) {
+    G4_CHECK_ARG(dst && src, "g4_memcpy_d2d_async: null pointer");
+    return g4_hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+}
+
 // synchronous fill of device memory (set-up only; never inside a captured graph)
 extern "C" int g4_memset(void* p, int value, size_t bytes) {
     G4_CHECK_ARG(p || !bytes, "g4_memset: null pointer");

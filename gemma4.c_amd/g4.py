@@ -81,6 +81,7 @@ _SIGS = {
     "g4_memset": (I, [VP, I, SZ]),
     "g4_memcpy_h2d_async": (I, [VP, VP, SZ]),
     "g4_memcpy_d2h_async": (I, [VP, VP, SZ]),
+    "g4_memcpy_d2d_async": (I, [VP, VP, SZ]),
     "g4_host_alloc": (I, [C.POINTER(VP), SZ]),
     "g4_host_free": (I, [VP]),
     "g4_stream_create": (I, [C.POINTER(VP)]),

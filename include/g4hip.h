@@ -218,6 +218,7 @@ int g4_store_i32x2(int *dst, int a, int b);
 int g4_memset(void *p, int value, size_t bytes);
 int g4_memcpy_h2d_async(void *dst, const void *src, size_t bytes);
 int g4_memcpy_d2h_async(void *dst, const void *src, size_t bytes);
+int g4_memcpy_d2d_async(void *dst, const void *src, size_t bytes);
 int g4_host_alloc(void **p, size_t bytes);   /* pinned host memory */
 int g4_host_free(void *p);
 int g4_stream_create(void **stream);
