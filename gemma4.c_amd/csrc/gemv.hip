@@ -208,19 +208,33 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
     const uint8_t* a_bs = q8 + q8k_bsums_off(nb) + 8 * k;
     const float* a_d = reinterpret_cast<const float*>(q8 + q8k_d_off(nb));
 
-    // one block's integer sums and scales for matrix m
-    auto block = [&](int m, int b, int32_t& S, int32_t& P, float& D, float& DM) {
-        const uint4 a0 = *reinterpret_cast<const uint4*>(a_qs + b * 256);
-        const uint4 a1 = *reinterpret_cast<const uint4*>(a_qs + b * 256 + 16);
-        const uint2 bsw = *reinterpret_cast<const uint2*>(a_bs + b * 32);
-        const float yd = a_d[b];
-        const int bs_lo = (int)(int16_t)(bsw.x & 0xffffu) + (int)(int16_t)(bsw.x >> 16);
-        const int bs_hi = (int)(int16_t)(bsw.y & 0xffffu) + (int)(int16_t)(bsw.y >> 16);
-        const uint8_t* base = m ? w1 : w0;
+    // raw operands of one block (both matrices share the activation block)
+    struct Raw {
+        uint4 a0, a1, wq[NMAT], hd[NMAT];
+        uint2 bsw;
+        uint32_t qh[NMAT];
+        float yd;
+    };
+    auto load = [&](int b, Raw& r) {
+        r.a0 = *reinterpret_cast<const uint4*>(a_qs + b * 256);
+        r.a1 = *reinterpret_cast<const uint4*>(a_qs + b * 256 + 16);
+        r.bsw = *reinterpret_cast<const uint2*>(a_bs + b * 32);
+        r.yd = a_d[b];
         const uint32_t blk = rb + (uint32_t)b;
-        const uint4 wq = *reinterpret_cast<const uint4*>(base + blk * 128u + 16 * l);
-        const uint4 hd = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16u);
-        const uint32_t qh = Q5 ? *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32u + 4 * l) : 0u;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const uint8_t* base = m ? w1 : w0;
+            r.wq[m] = *reinterpret_cast<const uint4*>(base + blk * 128u + 16 * l);
+            r.hd[m] = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16u);
+            r.qh[m] = Q5 ? *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32u + 4 * l) : 0u;
+        }
+    };
+    // one block's integer sums and fp32 scales for matrix m
+    auto block = [&](int m, int b, const Raw& r, int32_t& S, int32_t& P, float& D, float& DM) {
+        const int bs_lo = (int)(int16_t)(r.bsw.x & 0xffffu) + (int)(int16_t)(r.bsw.x >> 16);
+        const int bs_hi = (int)(int16_t)(r.bsw.y & 0xffffu) + (int)(int16_t)(r.bsw.y >> 16);
+        const uint4 wq = r.wq[m], hd = r.hd[m];
+        const uint32_t qh = r.qh[m];
         uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
         unpack_scales(hd.y, hd.z, hd.w, sc_lo, sc_hi, mn_lo, mn_hi);
         int32_t sumi = 0;
@@ -232,8 +246,8 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
                 lo |= ((qh >> (2 * j)) & 0x01010101u) << 4;
                 hi |= ((qh >> (2 * j + 1)) & 0x01010101u) << 4;
             }
-            const int dl = __builtin_amdgcn_sdot4((int)lo, (int)word_of(a0, j), 0, false);
-            const int dh = __builtin_amdgcn_sdot4((int)hi, (int)word_of(a1, j), 0, false);
+            const int dl = __builtin_amdgcn_sdot4((int)lo, (int)word_of(r.a0, j), 0, false);
+            const int dh = __builtin_amdgcn_sdot4((int)hi, (int)word_of(r.a1, j), 0, false);
             const uint32_t scw = j < 2 ? sc_lo : sc_hi;
             // |dl|, |dh| <= 4*31*127 and scales <= 63: exact in 24-bit products
             sumi += __mul24(byte_of(scw, 2 * (j & 1)), dl) + __mul24(byte_of(scw, 2 * (j & 1) + 1), dh);
@@ -241,8 +255,8 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
         const uint32_t mnw = k < 2 ? mn_lo : mn_hi;
         S = sumi;
         P = __mul24(byte_of(mnw, 2 * (k & 1)), bs_lo) + __mul24(byte_of(mnw, 2 * (k & 1) + 1), bs_hi);
-        D = yd * half_bits_to_f32(hd.x & 0xffffu);
-        DM = -yd * half_bits_to_f32(hd.x >> 16);
+        D = r.yd * half_bits_to_f32(hd.x & 0xffffu);
+        DM = -r.yd * half_bits_to_f32(hd.x >> 16);
         if (Q5) {
             // the four min products summed exactly, on every lane of the group
             int32_t pm = l < 4 ? P : 0;
@@ -255,7 +269,7 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
             if (Q5) sM = l == 0 ? P : 0;
             sS += __shfl_xor(sS, 1, 64); sS += __shfl_xor(sS, 2, 64); sS += __shfl_xor(sS, 4, 64);
             sM += __shfl_xor(sM, 1, 64); sM += __shfl_xor(sM, 2, 64); sM += __shfl_xor(sM, 4, 64);
-            if (l == 0) { dbgS[blk] = sS; dbgM[blk] = sM; }
+            if (l == 0) { dbgS[rb + (uint32_t)b] = sS; dbgM[rb + (uint32_t)b] = sM; }
         }
     };
 
@@ -274,6 +288,13 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
     };
 
     if (NB > 0) {
+        // every load of this group's blocks first, then the integer work
+        Raw raw[NH];
+#pragma unroll
+        for (int i = 0; i < NH; i++) {
+            const int b = grp * NH + i;
+            if (b < nb) load(b, raw[i]);
+        }
         int32_t S[NMAT][NH], P[NMAT][NH];
         float D[NMAT][NH], DM[NMAT][NH];
 #pragma unroll
@@ -282,7 +303,7 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 S[m][i] = 0; P[m][i] = 0; D[m][i] = 0.0f; DM[m][i] = 0.0f;
-                if (b < nb) block(m, b, S[m][i], P[m][i], D[m][i], DM[m][i]);
+                if (b < nb) block(m, b, raw[i], S[m][i], P[m][i], D[m][i], DM[m][i]);
             }
         }
         if (DBG) return;
@@ -308,11 +329,13 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
         }
     } else {
         for (int b = 0; b < nb; b++) {
+            Raw r;
+            load(b, r);
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 int32_t S, P;
                 float D, DM;
-                block(m, b, S, P, D, DM);
+                block(m, b, r, S, P, D, DM);
                 if (!DBG) step(m, S, P, D, DM);
             }
         }
@@ -368,37 +391,58 @@ __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __res
         const int row = rg * RPW + rr;
         float acc = 0.0f;
         if (row < d) {
-            for (int b = ks; b < nb; b += KS) {
-                const size_t blk = (size_t)row * nb + b;
-                const uint4 ql = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
-                const uint2 qh = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
-                const uint2 sc = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
-                const float df = f16_to_f32(*reinterpret_cast<const uint16_t*>(w + P.d + blk * 2));
-                const float* xb = xs + b * 256 + 128 * h + 8 * u;
+            // this lane's blocks ks, ks+KS, ... in batches of QB: all loads of a
+            // batch are issued before any of its arithmetic
+            constexpr int QB = 5;
+            for (int b0 = ks; b0 < nb; b0 += QB * KS) {
+                uint4 qlv[QB];
+                uint2 qhv[QB], scv[QB];
+                uint32_t dv[QB];
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
-                    const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
-                    const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
-                    const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
-                    const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);
-                    const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
-                    // bytes q in [0,63] -> (q - 32) as int8, per byte without borrows
-                    const uint32_t sa = ((ca | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                    const uint32_t sb = ((cb | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                    const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
-                    const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
-                    float dot = x0.x * (float)(int8_t)(sa & 0xff);
-                    dot = __builtin_fmaf(x0.y, (float)(int8_t)((sa >> 8) & 0xff), dot);
-                    dot = __builtin_fmaf(x0.z, (float)(int8_t)((sa >> 16) & 0xff), dot);
-                    dot = __builtin_fmaf(x0.w, (float)(int8_t)(sa >> 24), dot);
-                    dot = __builtin_fmaf(x1.x, (float)(int8_t)(sb & 0xff), dot);
-                    dot = __builtin_fmaf(x1.y, (float)(int8_t)((sb >> 8) & 0xff), dot);
-                    dot = __builtin_fmaf(x1.z, (float)(int8_t)((sb >> 16) & 0xff), dot);
-                    dot = __builtin_fmaf(x1.w, (float)(int8_t)(sb >> 24), dot);
-                    const int sbi = (u >> 1) + 2 * kk;
-                    const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
-                    acc = __builtin_fmaf(df * (float)s8, dot, acc);
+                for (int i = 0; i < QB; i++) {
+                    const int b = b0 + i * KS;
+                    if (b < nb) {
+                        const size_t blk = (size_t)row * nb + b;
+                        qlv[i] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
+                        qhv[i] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
+                        scv[i] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+                        dv[i] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < QB; i++) {
+                    const int b = b0 + i * KS;
+                    if (b < nb) {
+                        const uint4 ql = qlv[i];
+                        const uint2 qh = qhv[i], sc = scv[i];
+                        const float df = half_bits_to_f32(dv[i]);
+                        const float* xb = xs + b * 256 + 128 * h + 8 * u;
+#pragma unroll
+                        for (int kk = 0; kk < 4; kk++) {
+                            const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
+                            const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
+                            const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+                            const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+                            const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);
+                            const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
+                            // bytes q in [0,63] -> (q - 32) as int8, per byte without borrows
+                            const uint32_t sa = ((ca | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                            const uint32_t sb = ((cb | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+                            const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
+                            const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
+                            float dot = x0.x * (float)(int8_t)(sa & 0xff);
+                            dot = __builtin_fmaf(x0.y, (float)(int8_t)((sa >> 8) & 0xff), dot);
+                            dot = __builtin_fmaf(x0.z, (float)(int8_t)((sa >> 16) & 0xff), dot);
+                            dot = __builtin_fmaf(x0.w, (float)(int8_t)(sa >> 24), dot);
+                            dot = __builtin_fmaf(x1.x, (float)(int8_t)(sb & 0xff), dot);
+                            dot = __builtin_fmaf(x1.y, (float)(int8_t)((sb >> 8) & 0xff), dot);
+                            dot = __builtin_fmaf(x1.z, (float)(int8_t)((sb >> 16) & 0xff), dot);
+                            dot = __builtin_fmaf(x1.w, (float)(int8_t)(sb >> 24), dot);
+                            const int sbi = (u >> 1) + 2 * kk;
+                            const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
+                            acc = __builtin_fmaf(df * (float)s8, dot, acc);
+                        }
+                    }
                 }
             }
         }
