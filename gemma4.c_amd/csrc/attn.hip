@@ -203,23 +203,43 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     float* qs = sm;
     float* sc = sm + kvm * HD;
     float* ml = sm + R;
-    const float* qsrc = a.q + (size_t)kvh * kvm * HD;
-    for (int i = tid; i < kvm * HD; i += kAttnThreads) qs[i] = qsrc[i];
-    __syncthreads();
-
-    // phase 1: scores; 16 subgroups of 16 lanes, two positions per subgroup in
-    // flight
     const int sub = tid >> 4, sl = tid & 15;
+    const int wave = tid >> 6, lane = tid & 63;
     const float* kbase = a.kc + (size_t)kvh * HD;
-    for (int it = 0; it < cnt; it += 32) {
-        const int ta = it + sub, tb = it + 16 + sub;
-        float4 ka[KPL], kb[KPL];
-        const float4* ra = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(ta, cnt - 1)) * a.kv_stride);
-        const float4* rb = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(tb, cnt - 1)) * a.kv_stride);
+    const float* vbase = a.vc + (size_t)kvh * HD;
+    // K rows of positions it+sub, it+16+sub (phase 1) and V rows of positions
+    // it+wave+4u (phase 3); the first ones are issued before q is staged
+    float4 ka[KPL], kb[KPL];
+    auto load_k = [&](int it) {
+        const float4* ra = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(it + sub, cnt - 1)) * a.kv_stride);
+        const float4* rb = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(it + 16 + sub, cnt - 1)) * a.kv_stride);
 #pragma unroll
         for (int k = 0; k < KPL; k++) ka[k] = ra[sl + 16 * k];
 #pragma unroll
         for (int k = 0; k < KPL; k++) kb[k] = rb[sl + 16 * k];
+    };
+    float4 vv[4][VPL];
+    auto load_v = [&](int it) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = min(it + wave + 4 * u, cnt - 1);
+            const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)attn_slot(a, cb + t) * a.kv_stride);
+#pragma unroll
+            for (int k = 0; k < VPL; k++) vv[u][k] = vr[lane + 64 * k];
+        }
+    };
+    if (cnt > 0) {
+        load_k(0);
+        load_v(0);
+    }
+    const float* qsrc = a.q + (size_t)kvh * kvm * HD;
+    for (int i = tid; i < kvm * HD; i += kAttnThreads) qs[i] = qsrc[i];
+    __syncthreads();
+
+    // phase 1: scores; 16 subgroups of 16 lanes, two positions per subgroup
+    for (int it = 0; it < cnt; it += 32) {
+        if (it > 0) load_k(it);
+        const int ta = it + sub, tb = it + 16 + sub;
         for (int h = 0; h < kvm; h++) {
             const float4* qh = reinterpret_cast<const float4*>(qs + h * HD);
             float da = 0.0f, db = 0.0f;
@@ -243,7 +263,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
 
     // phase 2: chunk max / exp / sum per head (one wave per head)
-    const int wave = tid >> 6, lane = tid & 63;
     for (int h = wave; h < kvm; h += kAttnThreads / 64) {
         float* s = sc + h * kChunkMax;
         float m = -INFINITY;
@@ -267,16 +286,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     for (int h = 0; h < 8; h++)
 #pragma unroll
         for (int k = 0; k < VPL; k++) acc[h][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float* vbase = a.vc + (size_t)kvh * HD;
     for (int it = 0; it < cnt; it += 16) {
-        float4 vv[4][VPL];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int t = min(it + wave + 4 * u, cnt - 1);
-            const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)attn_slot(a, cb + t) * a.kv_stride);
-#pragma unroll
-            for (int k = 0; k < VPL; k++) vv[u][k] = vr[lane + 64 * k];
-        }
+        if (it > 0) load_v(it);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int t = it + wave + 4 * u;
