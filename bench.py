@@ -12,6 +12,8 @@ Workloads (synthetic inputs, generated from fixed seeds on the host):
   lmhead  tied LM head, Q6_K 262144x2560 times an fp32 hidden vector, with the
           30*tanh(l/30) soft-cap (seed 2)
   attn    ISWA decode attention over an fp32 KV cache (seed 3)
+  prefill batched prefill GEMM: 512 tokens through one E4B layer's Q4_K
+          matrices on the matrix cores (seed 1)
 
 Prints ONE JSON line.  `value` is whole-job throughput with inputs resident
 in HBM; `roofline` is the dominant kernel's algorithmic bytes over its average
@@ -155,6 +157,100 @@ def cpu_gemv_baseline(raw, x, n, d, algo):
     return {"value": round(algo / med / 1e9, 2), "unit": "GB/s", "cores": thr, "kind": kind,
             "sample": f"quantize_row_q8_K + mm_quant_dot_rows (Q4_K 10240x2560), median of {len(ts)} runs "
                       f"after 3 warm-ups, OpenMP {thr} threads"}
+
+
+FP16_MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 matrix peak (the instruction the prefill GEMM issues)
+
+# one E4B sliding-window layer's Q4_K matrices (rows d, inputs n): Q, K, O,
+# gate, up, PLE inp_gate, PLE proj
+PREFILL_MATS = [("q", 2048, 2560), ("k", 512, 2560), ("o", 2560, 2048), ("gate", 10240, 2560),
+                ("up", 10240, 2560), ("inp_gate", 256, 2560), ("proj", 2560, 256)]
+
+
+def bench_prefill(lib, g4, synth, args):
+    """Batched prefill GEMM: 512 prompt tokens through one E4B layer's Q4_K
+    matrices (Q, K, O, gate, up, inp_gate, proj) with pre-quantized Q8_K
+    activations; a step is the seven launches.  Reports matrix-core
+    throughput (2 * tokens * rows * n algorithmic ops) against the fp16 dense
+    peak, and the dominant launch (gate, 10240x2560) alone."""
+    m = 512
+    rng = np.random.default_rng(1)
+    mats = []
+    for name, d, n in PREFILL_MATS:
+        raw = synth.rand_q4K(rng, d, n)
+        w = g4.upload_quant(lib, raw, g4.Q4_K, n, d)
+        x = g4.DBuf.from_array(lib, rng.standard_normal((m, n)).astype(np.float32))
+        q8 = g4.DBuf(lib, lib.L.g4_q8K_row_stride(n) * m)
+        lib.g4_quantize_rows_q8_K(x.ptr, q8.ptr, n, m)
+        out = g4.DBuf(lib, 4 * m * d)
+        mats.append((name, d, n, raw, w, q8, out))
+    L = lib.L
+
+    def step(i):
+        for _, d, n, _, w, q8, out in mats:
+            L.g4_mm_batch_q8(out.ptr, w.ptr, q8.ptr, n, d, m, g4.Q4_K)
+
+    ms = _time_steps(lib, step, args)
+    per_step = ms / 1e3 / args.steps
+    ops = sum(2.0 * m * d * n for _, d, n, *_ in mats)
+    # the dominant launch alone
+    _, d, n, _, w, q8, out = mats[3]
+
+    def one(i):
+        L.g4_mm_batch_q8(out.ptr, w.ptr, q8.ptr, n, d, m, g4.Q4_K)
+    ms1 = _time_steps(lib, one, args)
+    per1 = ms1 / 1e3 / args.steps
+    ops1 = 2.0 * m * d * n
+    tf1 = ops1 / per1 / 1e12
+    name = "mm_batch_kq_kernel<Q4_K> 10240x2560, 512 tokens"
+    res = {
+        "value": round(m / per_step, 1), "unit": "tok/s (one layer's Q4_K GEMMs)", "higher_is_better": True,
+        "ms_per_step": ms / args.steps, "dtype": "u4 x int8 -> exact fp16 matrix products, fp32 combine",
+        "config": {"workload": "batched prefill GEMM: 512 tokens x one E4B SWA layer's Q4_K matrices "
+                               "(Q 2048, K 512, O 2560<-2048, gate/up 10240, PLE 256/2560) (seed 1)",
+                   "tokens": m, "layer_tflops": round(ops / per_step / 1e12, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tf1, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf1 / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(name),
+                     "kernel": name, "us_per_launch": round(per1 * 1e6, 2)},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_prefill_baseline(mats[3][3], mats[3][2], mats[3][1])
+    return res
+
+
+def cpu_prefill_baseline(raw, n, d, tokens: int = 4):
+    """The reference's prefill of this matrix: quantize_row_q8_K +
+    mm_quant_dot_rows once per token (forward() per prompt token)."""
+    import oracle as orc_mod
+    thr = cpu_threads()
+    rng = np.random.default_rng(7)
+    xs = rng.standard_normal((tokens, n)).astype(np.float32)
+    o = np.empty(d, np.float32)
+    q8 = np.zeros(n // 256, orc_mod.Q8K_DTYPE)
+    if orc_mod.Ref.available():
+        ref, kind = orc_mod.Ref(), "reference"
+
+        def run():
+            for t in range(tokens):
+                ref.L.ref_quantize_row_q8_K(xs[t].ctypes.data, q8.ctypes.data, n)
+                ref.L.ref_mm_quant_dot_rows(o.ctypes.data, raw.ctypes.data, n, d, 12, q8.ctypes.data)
+    else:
+        orc, kind = orc_mod.Oracle(), "port"
+
+        def run():
+            for t in range(tokens):
+                orc.mm_quant_dot_rows(raw, n, d, 12, orc.quantize_q8K(xs[t]))
+    run()
+    ts = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end or len(ts) < 5:
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(2.0 * tokens * d * n / med / 1e12, 4), "unit": "TFLOP/s", "cores": thr, "kind": kind,
+            "sample": f"{tokens} tokens of quantize_row_q8_K + mm_quant_dot_rows (Q4_K {d}x{n}), median of "
+                      f"{len(ts)} runs, OpenMP {thr} threads"}
 
 
 def bench_lmhead(lib, g4, synth, args):
@@ -333,7 +429,7 @@ def _time_steps(lib, step, args) -> float:
 
 
 WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
-             "copy": bench_copy}
+             "copy": bench_copy, "prefill": bench_prefill}
 
 
 def main() -> int:

@@ -126,6 +126,28 @@ int g4_mm_quant_rows_softcap(float *o, const float *x, const void *w, int n, int
 int g4_set_gemv_occupancy(int wg_per_cu);
 
 /* ---------------------------------------------------------------------------
+ * Batched prefill GEMM.  The reference has none: generate() runs forward()
+ * once per prompt token (main.c:2366-2384), so for m tokens it performs m
+ * times quantize_row_q8_K(x_t) (main.c:282) + mm_quant_dot_rows (main.c:1558).
+ * These entry points do the same m products in one launch on the matrix
+ * cores; every output equals the per-token result bit for bit.
+ * ------------------------------------------------------------------------- */
+/* Bytes between consecutive Q8_K rows of a batch: g4_q8K_bytes(k) rounded
+ * up to 64 (0 if k is not a positive multiple of 256). */
+size_t g4_q8K_row_stride(int k);
+/* m rows of k floats (row stride k) -> m Q8_K rows at g4_q8K_row_stride(k)
+ * bytes apart: quantize_row_q8_K (main.c:282) per row. */
+int g4_quantize_rows_q8_K(const float *x, void *y, int k, int m);
+/* o[t*d + r] = mm_quant_dot_rows row r on Q8_K row t (main.c:1558-1566,
+ * vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K main.c:476-593), t < m, r < d.
+ * Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
+int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m, int type);
+/* m tokens through mm(o_t, x_t, w, n, d, type, q8, 0) (main.c:1669): Q4_K /
+ * Q5_K quantize all rows into q8 (m * g4_q8K_bytes(n) bytes) and take the
+ * batched GEMM; Q6_K and BF16 run the per-token GEMV m times. */
+int g4_mm_batch(float *o, const float *x, const void *w, int n, int d, int m, int type, void *q8);
+
+/* ---------------------------------------------------------------------------
  * Norms, RoPE, attention (main.c:1451-1488, 1725-1745, 1886-1950)
  * ------------------------------------------------------------------------- */
 /* rmsnorm(float *o, const float *x, const float *w, int n, float eps), main.c:1451 */
