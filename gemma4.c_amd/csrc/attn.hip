@@ -148,6 +148,21 @@ struct AttnArgs {
     int window;            // used with dpos: 0 = full attention
     int kv_stride, ring, n_heads, n_kv, hd, G;
     float scale;
+    // fused per-head norms, RoPE and KV append (main.c:1886-1904), all
+    // optional: q_norm non-null means q is the raw Q projection; kraw
+    // non-null means this layer stores K/V: the raw K/V projections of this
+    // position are normalised (K also rotated) and written to slot pos of
+    // kstore/vstore, and the workgroup whose chunk holds pos uses them
+    // directly for that position
+    const float* q_norm;
+    const float* kraw;
+    const float* vraw;
+    const float* k_norm;
+    float* kstore;
+    float* vstore;
+    const float2* tab;     // (cos, sin) of each RoPE pair at this position
+    int n_rot;
+    float eps;
 };
 
 constexpr int kAttnThreads = 256;
@@ -180,6 +195,9 @@ __host__ __device__ inline int attn_work_floats(int hd, int kvm) {
     return a > b ? a : b;
 }
 
+// start of the fused path's K/V staging (16-byte aligned, after (max, sum))
+__host__ __device__ inline int attn_new_kv_off(int hd, int kvm) { return (attn_work_floats(hd, kvm) + 2 * kvm + 3) & ~3; }
+
 __device__ __forceinline__ int attn_slot(const AttnArgs& a, int t) { return a.ring > 0 ? t % a.ring : t; }
 
 // Workgroup (c, kvh) scores chunk c of the window for the kvm q heads of kv
@@ -203,10 +221,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     float* qs = sm;
     float* sc = sm + kvm * HD;
     float* ml = sm + R;
+    float* kn = sm + attn_new_kv_off(HD, kvm);   // this position's K, V (fused append)
+    float* vn = kn + HD;
     const int sub = tid >> 4, sl = tid & 15;
     const int wave = tid >> 6, lane = tid & 63;
     const float* kbase = a.kc + (size_t)kvh * HD;
     const float* vbase = a.vc + (size_t)kvh * HD;
+    const int pos = t0 + nwin - 1;
+    const int tl = pos - cb;                              // pos inside this chunk
+    const bool owner = a.kraw != nullptr && cnt > 0 && tl >= 0 && tl < cnt;
     // K rows of positions it+sub, it+16+sub (phase 1) and V rows of positions
     // it+wave+4u (phase 3); the first ones are issued before q is staged
     float4 ka[KPL], kb[KPL];
@@ -218,10 +241,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < KPL; k++) kb[k] = rb[sl + 16 * k];
     };
-    float4 vv[4][VPL];
+    constexpr int VU = 8;                 // V rows in flight per wave
+    float4 vv[VU][VPL];
     auto load_v = [&](int it) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < VU; u++) {
             const int t = min(it + wave + 4 * u, cnt - 1);
             const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)attn_slot(a, cb + t) * a.kv_stride);
 #pragma unroll
@@ -232,14 +256,84 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         load_k(0);
         load_v(0);
     }
+    // norm weights of this lane's elements and the RoPE pair of this thread,
+    // also issued before anything waits (np = n_rot/2 divides 256)
+    const bool fuse = a.q_norm != nullptr;
+    const int np = fuse ? a.n_rot / 2 : 1, per = kAttnThreads / np;
+    float wq[HD / 64], wk[HD / 64];
+    float2 cs2 = make_float2(1.0f, 0.0f);
+    if (fuse) {
+#pragma unroll
+        for (int e = 0; e < HD / 64; e++) {
+            wq[e] = a.q_norm[lane + 64 * e];
+            wk[e] = owner ? a.k_norm[lane + 64 * e] : 0.0f;
+        }
+        if (tid < per * np) cs2 = a.tab[tid % np];
+    }
     const float* qsrc = a.q + (size_t)kvh * kvm * HD;
     for (int i = tid; i < kvm * HD; i += kAttnThreads) qs[i] = qsrc[i];
+    if (owner) {
+        for (int i = tid; i < HD; i += kAttnThreads) {
+            kn[i] = a.kraw[(size_t)kvh * HD + i];
+            vn[i] = a.vraw[(size_t)kvh * HD + i];
+        }
+    }
     __syncthreads();
+    if (fuse) {
+        // rmsnorm_head_inplace (q: q_norm, k: k_norm) / _noweight (v), one
+        // wave per head vector: seg *= s * w with s = 1/sqrt(mean(seg^2)+eps)
+        const int nvec = kvm + (owner ? 2 : 0);
+        for (int vi = wave; vi < nvec; vi += kAttnThreads / 64) {
+            float* seg = vi < kvm ? qs + vi * HD : (vi == kvm ? kn : vn);
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < HD / 64; e++) {
+                const float t = seg[lane + 64 * e];
+                ss += t * t;
+            }
+            ss = wave_sum(ss);
+            const float sf = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int e = 0; e < HD / 64; e++) {
+                const int i = lane + 64 * e;
+                seg[i] = vi < kvm ? seg[i] * (sf * wq[e]) : vi == kvm ? seg[i] * (sf * wk[e]) : seg[i] * sf;
+            }
+        }
+        __syncthreads();
+        // RoPE (apply_rope_neox) of the q heads and k: pair j = tid % np of
+        // vectors tid / np, + per, ...
+        if (tid < per * np) {
+            const int j = tid % np, nv = kvm + (owner ? 1 : 0);
+            for (int vi = tid / np; vi < nv; vi += per) {
+                float* seg = vi < kvm ? qs + vi * HD : kn;
+                const float v0 = seg[j], v1 = seg[j + HD / 2];
+                seg[j] = v0 * cs2.x - v1 * cs2.y;
+                seg[j + HD / 2] = v0 * cs2.y + v1 * cs2.x;
+            }
+        }
+        __syncthreads();
+    }
+    if (owner) {
+        const size_t off = (size_t)attn_slot(a, pos) * a.kv_stride + (size_t)kvh * HD;
+        for (int i = tid; i < HD; i += kAttnThreads) {
+            a.kstore[off + i] = kn[i];
+            a.vstore[off + i] = vn[i];
+        }
+    }
 
     // phase 1: scores; 16 subgroups of 16 lanes, two positions per subgroup
     for (int it = 0; it < cnt; it += 32) {
         if (it > 0) load_k(it);
         const int ta = it + sub, tb = it + 16 + sub;
+        if (owner && (ta == tl || tb == tl)) {
+            // this position's K is not in the cache yet: take it from LDS
+            const float4* kr = reinterpret_cast<const float4*>(kn);
+#pragma unroll
+            for (int k = 0; k < KPL; k++) {
+                if (ta == tl) ka[k] = kr[sl + 16 * k];
+                else kb[k] = kr[sl + 16 * k];
+            }
+        }
         for (int h = 0; h < kvm; h++) {
             const float4* qh = reinterpret_cast<const float4*>(qs + h * HD);
             float da = 0.0f, db = 0.0f;
@@ -249,11 +343,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
                 da = dot4(ka[k], qv, da);
                 db = dot4(kb[k], qv, db);
             }
-#pragma unroll
-            for (int m = 8; m >= 1; m >>= 1) {
-                da += __shfl_xor(da, m, 64);
-                db += __shfl_xor(db, m, 64);
-            }
+            // sum over the 16 lanes of the row (DPP; the xor-8..1 butterfly's bits)
+            da += dpp_f<kDppXor1>(da);
+            db += dpp_f<kDppXor1>(db);
+            da += dpp_f<kDppXor2>(da);
+            db += dpp_f<kDppXor2>(db);
+            da += dpp_f<kDppHalfMirror>(da);
+            db += dpp_f<kDppHalfMirror>(db);
+            da += dpp_f<kDppMirror>(da);
+            db += dpp_f<kDppMirror>(db);
             if (sl == 0) {
                 if (ta < cnt) sc[h * kChunkMax + ta] = a.scale * da;
                 if (tb < cnt) sc[h * kChunkMax + tb] = a.scale * db;
@@ -280,16 +378,25 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
 
     // phase 3: o[h] = sum_t p[h][t] V[t]; wave w takes positions w, w+4, ...,
-    // four rows in flight per wave
+    // VU rows in flight per wave
     float4 acc[8][VPL];
 #pragma unroll
     for (int h = 0; h < 8; h++)
 #pragma unroll
         for (int k = 0; k < VPL; k++) acc[h][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int it = 0; it < cnt; it += 16) {
+    for (int it = 0; it < cnt; it += 4 * VU) {
         if (it > 0) load_v(it);
+        if (owner) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < VU; u++) {
+                if (it + wave + 4 * u == tl) {
+#pragma unroll
+                    for (int k = 0; k < VPL; k++) vv[u][k] = reinterpret_cast<const float4*>(vn)[lane + 64 * k];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
             const int t = it + wave + 4 * u;
             if (t < cnt) {
 #pragma unroll
@@ -382,13 +489,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
-// partial kernel LDS: work region + (max, sum) pairs
-size_t attn_lds(int hd, int kvm) { return 4 * ((size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm); }
+// partial kernel LDS: work region + (max, sum) pairs [+ this position's K, V]
+size_t attn_lds(int hd, int kvm, bool fused) {
+    return 4 * (fused ? (size_t)attn_new_kv_off(hd, kvm) + 2 * (size_t)hd
+                      : (size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm);
+}
 
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
     const dim3 grid(a.G, a.n_kv);
-    const size_t lds = attn_lds(a.hd, kvm);
+    const size_t lds = attn_lds(a.hd, kvm, a.q_norm != nullptr);
     if (a.hd == 256) {
         hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
         hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1), dim3(256), 0, g4_stream(), a);
@@ -399,12 +509,12 @@ int launch_attn(const AttnArgs& a) {
     return g4_check_launch("attn_decode_kernel/attn_merge_kernel");
 }
 
-int check_attn_shape(const char* who, int n_heads, int n_kv, int hd, int G) {
+int check_attn_shape(const char* who, int n_heads, int n_kv, int hd, int G, bool fused = false) {
     if (hd != 256 && hd != 512) return g4_fail(G4_ERR_ARG, "%s: head_dim %d unsupported (256 or 512)", who, hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || n_heads / n_kv > 8)
         return g4_fail(G4_ERR_ARG, "%s: n_heads=%d n_kv=%d (need n_heads/n_kv in 1..8)", who, n_heads, n_kv);
     if (G < 1 || G > kMaxChunks) return g4_fail(G4_ERR_ARG, "%s: %d chunks (1..%d)", who, G, kMaxChunks);
-    if (attn_lds(hd, n_heads / n_kv) > 65536)
+    if (attn_lds(hd, n_heads / n_kv, fused) > 65536)
         return g4_fail(G4_ERR_ARG, "%s: %d q heads per kv head at head_dim %d exceed the LDS budget", who,
                        n_heads / n_kv, hd);
     return G4_OK;
@@ -557,5 +667,31 @@ extern "C" int g4_attn_decode_dev(const float* q, const float* kc, const float* 
     a.part = part;
     a.window = window; a.kv_stride = kv_stride; a.ring = ring;
     a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
+    return launch_attn(a);
+}
+
+// qkv_post + attention in one pass (main.c:1886-1950): q_raw is the raw Q
+// projection (left unchanged); k_raw/v_raw (null on shared-KV layers) are
+// this position's raw K/V projections, stored normalised (K rotated) at slot
+// pos of kstore/vstore.  Otherwise as g4_attn_decode_dev.
+extern "C" int g4_attn_decode_fused(const float* q_raw, const float* q_norm, const float* k_raw, const float* v_raw,
+                                    const float* k_norm, float* kstore, float* vstore, const float* kc, const float* vc,
+                                    int kv_stride, int ring, const int* dpos, int window, int n_heads, int n_kv, int hd,
+                                    int n_rot, const float* rope_tab, float eps, float attn_scale, int G, float* part,
+                                    float* out, void* q8) {
+    int rc = check_attn_shape("attn_decode_fused", n_heads, n_kv, hd, G, true);
+    if (rc) return rc;
+    G4_CHECK_ARG(q_raw && q_norm && rope_tab && kc && vc && dpos && part && out, "attn_decode_fused: null pointer");
+    G4_CHECK_ARG(n_rot > 0 && n_rot % 2 == 0 && n_rot <= hd && (2 * kAttnThreads) % n_rot == 0,
+                 "attn_decode_fused: n_rot=%d (hd %d; n_rot/2 must divide %d)", n_rot, hd, kAttnThreads);
+    G4_CHECK_ARG(!k_raw || (v_raw && k_norm && kstore && vstore), "attn_decode_fused: incomplete K/V append arguments");
+    G4_CHECK_ARG(kv_stride >= n_kv * hd, "attn_decode_fused: kv_stride %d < n_kv*hd", kv_stride);
+    AttnArgs a = {};
+    a.q = q_raw; a.kc = kc; a.vc = vc; a.dpos = dpos; a.out = out; a.q8 = (uint8_t*)q8;
+    a.part = part;
+    a.window = window; a.kv_stride = kv_stride; a.ring = ring;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
+    a.q_norm = q_norm; a.kraw = k_raw; a.vraw = v_raw; a.k_norm = k_norm; a.kstore = kstore; a.vstore = vstore;
+    a.tab = (const float2*)rope_tab; a.n_rot = n_rot; a.eps = eps;
     return launch_attn(a);
 }

@@ -82,13 +82,40 @@ __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Wave-wide reductions on DPP lane moves inside each 16-lane row (xor 1,
+// xor 2 by quad permutes; then the mirrors, which pair a lane with one that
+// holds the same partial value as its xor-4 / xor-8 partner) and four
+// readlanes across the rows: (r0 + r1) + (r2 + r3).  The result is the same,
+// bit for bit, as the xor butterfly v += shfl_xor(v, 1), (2), ..., (32), in
+// every lane.  All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm(1,0,3,2)
+constexpr int kDppXor2 = 0x4E;         // quad_perm(2,3,0,1)
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15-i within 16
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    v += dpp_f<kDppMirror>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Sum over the whole workgroup (blockDim.x a multiple of 64, <= 1024); every
@@ -116,22 +143,20 @@ __device__ __forceinline__ float gelu_ref(float x) {
 // layout (qs permuted, bsums, d).  Every lane of the wave must call it.
 __device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, uint8_t* __restrict__ y,
                                                     int nb, int b) {
-    // local first max of |x| over this lane's 4 elements
-    float amax = 0.0f, maxv = 0.0f;
-    int idx = 0x7fffffff;
+    // amax = max |x|; maxv = the element of smallest index with |x| == amax
+    // (lane l owns elements 4l..4l+3, so the first such lane holds it)
+    float al = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float a = fabsf(v[e]);
-        if (a > amax) { amax = a; maxv = v[e]; idx = 4 * lane + e; }
-    }
-    // wave argmax: larger |x|, ties to the smaller index (total order)
+    for (int e = 0; e < 4; e++) al = fmaxf(al, fabsf(v[e]));
+    const float amax = wave_max(al);
+    float cand = v[3];
+    bool hit = fabsf(v[3]) == amax;
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float oa = __shfl_xor(amax, m, 64);
-        const float ov = __shfl_xor(maxv, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; maxv = ov; idx = oi; }
+    for (int e = 2; e >= 0; e--) {
+        if (fabsf(v[e]) == amax) { cand = v[e]; hit = true; }
     }
+    const unsigned long long hits = __ballot(hit);
+    const float maxv = hits ? lane_f(cand, (int)__builtin_ctzll(hits)) : 0.0f;
     int8_t q[4];
     float dval = 0.0f;
     if (amax == 0.0f) {
@@ -150,8 +175,8 @@ __device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, 
     reinterpret_cast<uint32_t*>(y + (size_t)b * 256)[q8k_word_dev(lane)] = word;
     // bsums: 16 elements = 4 lanes
     int s = (int)q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += dpp_i<kDppXor1>(s);
+    s += dpp_i<kDppXor2>(s);
     if ((lane & 3) == 0) reinterpret_cast<int16_t*>(y + q8k_bsums_off(nb))[b * 16 + (lane >> 2)] = (int16_t)s;
     if (lane == 0) reinterpret_cast<float*>(y + q8k_d_off(nb))[b] = dval;
 }

@@ -69,11 +69,11 @@ template <int EPT>
 __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArgs a) {
     extern __shared__ __align__(16) float buf[];   // n floats: the vector to quantize
     __shared__ float red[16];
-    const int n = a.n, tid = threadIdx.x;
+    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
     float xv[EPT], yv[EPT], wp[EPT], wn[EPT];
 #pragma unroll
     for (int k = 0; k < EPT; k++) {
-        const int i = tid + k * kNormThreads;
+        const int i = tid + k * nt;
         const bool ok = i < n;
         xv[k] = ok ? a.x[i] : 0.0f;
         yv[k] = (ok && a.y) ? a.y[i] : 0.0f;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArg
         const float sy = 1.0f / sqrtf(ss / (float)n + a.eps);
 #pragma unroll
         for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * kNormThreads;
+            const int i = tid + k * nt;
             float v = xv[k] + (yv[k] * sy) * wp[k];
             if (a.oscale) v = v * sc;
             xv[k] = v;
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArg
         const float sx = 1.0f / sqrtf(ss / (float)n + a.eps);
 #pragma unroll
         for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * kNormThreads;
+            const int i = tid + k * nt;
             const float t = (xv[k] * sx) * wn[k];
             if (i < n) {
                 if (a.xb2) a.xb2[i] = t;
@@ -114,14 +114,14 @@ __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArg
     } else {
 #pragma unroll
         for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * kNormThreads;
+            const int i = tid + k * nt;
             if (i < n) buf[i] = xv[k];
         }
     }
     if (a.q8) {
         __syncthreads();
         const int nb = n / 256, lane = tid & 63;
-        for (int b = tid >> 6; b < nb; b += kNormThreads / 64) {
+        for (int b = tid >> 6; b < nb; b += nt / 64) {
             const float4 f = reinterpret_cast<const float4*>(buf + (size_t)b * 256)[lane];
             const float v[4] = {f.x, f.y, f.z, f.w};
             quantize_block_wave(v, lane, a.q8, nb, b);
@@ -140,10 +140,14 @@ extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, c
     G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm: n=%d not a multiple of 256 for Q8_K", n);
     G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm: quantizing xb2 needs w_next");
     ResidualArgs a{x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
-    const dim3 g(1), b(kNormThreads);
+    // EPT elements per thread, as few waves as cover n (n = 2560: 640 threads,
+    // one wave per Q8_K block)
+    const int ept = n <= kNormThreads ? 1 : n <= 4 * kNormThreads ? 4 : 16;
+    const int nt = ((n + ept - 1) / ept + 63) / 64 * 64;
+    const dim3 g(1), b(nt);
     const size_t lds = (size_t)n * 4;
-    if (n <= 1 * kNormThreads) hipLaunchKernelGGL(residual_norm_kernel<1>, g, b, lds, g4_stream(), a);
-    else if (n <= 4 * kNormThreads) hipLaunchKernelGGL(residual_norm_kernel<4>, g, b, lds, g4_stream(), a);
+    if (ept == 1) hipLaunchKernelGGL(residual_norm_kernel<1>, g, b, lds, g4_stream(), a);
+    else if (ept == 4) hipLaunchKernelGGL(residual_norm_kernel<4>, g, b, lds, g4_stream(), a);
     else hipLaunchKernelGGL(residual_norm_kernel<16>, g, b, lds, g4_stream(), a);
     return g4_check_launch("residual_norm_kernel");
 }

@@ -317,7 +317,7 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_batch_kq_kernel(const uint8_t
 // waves, 1..4 tiles at E4B shapes and 512 tokens): 4 row waves x 1 token
 // wave x 2 tiles = 64 rows x 32 tokens per 256-thread workgroup
 constexpr int kRW = 4, kTW = 1, kNT = 2;
-constexpr int kPfRows = 16 * kRW, kPfToks = 16 * kNT * kTW;
+constexpr int kPfToks = 16 * kNT * kTW;
 
 template <bool Q5, int RW, int TW, int NT>
 void launch_mm_batch(const uint8_t* w, const uint8_t* q8, float* o, int nb, int d, int m) {

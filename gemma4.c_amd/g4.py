@@ -78,6 +78,7 @@ _SIGS = {
     "g4_rope_table": (I, [VP, VP, I, I, F, F, VP]),
     "g4_attn_part_bytes": (SZ, [I, I, I]),
     "g4_attn_decode_dev": (I, [VP, VP, VP, I, I, VP, I, I, I, I, F, I, VP, VP, VP]),
+    "g4_attn_decode_fused": (I, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, VP, F, F, I, VP, VP, VP]),
     "g4_emb_lookup_dev": (I, [VP, VP, I, I, VP, I, F]),
     "g4_ple_finish": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
     "g4_gelu_mul_quant": (I, [VP, VP, I, VP]),

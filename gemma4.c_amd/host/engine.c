@@ -590,7 +590,7 @@ static int mm(g4e_model *m, float *o, const float *x, const Tensor *w, int q8_re
 
 /* Enqueue one forward step; token and position are read from m->dstep, so the
  * same sequence of launches is valid for every position (graph capture). */
-static int enqueue_step(g4e_model *m, int lm_mode, int capture_pos_host) {
+static int enqueue_step(g4e_model *m, int lm_mode) {
     const Config *c = &m->c;
     const int dim = c->dim, L = c->n_layers, pd = c->ple_dim;
     const int *dtok = m->dstep, *dpos = m->dstep + 1;
@@ -610,30 +610,26 @@ static int enqueue_step(g4e_model *m, int lm_mode, int capture_pos_host) {
     for (int l = 0; l < L; l++) {
         const int hd = layer_hd(c, l), swa = is_swa(c, l);
         const int n_rot = swa ? c->rot_swa : c->rot_full;
-        const float base = swa ? c->theta_swa : c->theta;
-        const float *ff = swa ? NULL : m->rope_freqs;
         const int q8_att = is_q8_type(m->wq[l].type);
         /* Q, K, V share one Q8_K of xb2 (main.c:1883-1892) */
         int rc = mm(m, m->q, m->xb2, &m->wq[l], q8_att);
         if (rc) return rc;
-        const int src = kv_source(c, l);
-        if (layer_has_kv(l)) {
+        const int src = kv_source(c, l), has_kv = layer_has_kv(l);
+        if (has_kv) {
             if (is_q8_type(m->wk[l].type) != q8_att && is_q8_type(m->wk[l].type))
                 CK(g4_quantize_row_q8_K(m->xb2, m->q8, dim));
             if ((rc = mm(m, m->k, m->xb2, &m->wk[l], 1))) return rc;
             if ((rc = mm(m, m->v, m->xb2, &m->wv[l], 1))) return rc;
-            CK(g4_qkv_post(m->q, m->q_norm[l], m->k, m->v, m->k_norm[l], m->kc[l], m->vc[l], c->n_kv * hd, m->kv_ring[l],
-                           dpos, capture_pos_host, c->n_heads, c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps,
-                           swa ? tab_swa : tab_full));
-        } else {
-            CK(g4_qkv_post(m->q, m->q_norm[l], NULL, NULL, NULL, NULL, NULL, 0, 0, dpos, capture_pos_host, c->n_heads,
-                           c->n_kv, hd, n_rot, base, 1.0f, ff, c->eps, swa ? tab_swa : tab_full));
         }
-        /* attention over the source layer's cache (main.c:1909-1950), attn_scale 1.0 */
+        /* q_norm + RoPE, K/V norm + RoPE + append (main.c:1886-1904) and the
+         * attention over the source layer's cache (main.c:1909-1950, attn_scale
+         * 1.0) in one launch pair */
         const int o_q8 = is_q8_type(m->wo[l].type);
-        CK(g4_attn_decode_dev(m->q, m->kc[src], m->vc[src], c->n_kv * layer_hd(c, src), m->kv_ring[src], dpos,
-                              swa ? c->window : 0, c->n_heads, c->n_kv, hd, 1.0f, swa ? m->G_swa : m->G_full,
-                              m->attn_part, m->q_out, o_q8 ? m->q8 : NULL));
+        CK(g4_attn_decode_fused(m->q, m->q_norm[l], has_kv ? m->k : NULL, has_kv ? m->v : NULL,
+                                has_kv ? m->k_norm[l] : NULL, has_kv ? m->kc[l] : NULL, has_kv ? m->vc[l] : NULL,
+                                m->kc[src], m->vc[src], c->n_kv * layer_hd(c, src), m->kv_ring[src], dpos,
+                                swa ? c->window : 0, c->n_heads, c->n_kv, hd, n_rot, swa ? tab_swa : tab_full, c->eps,
+                                1.0f, swa ? m->G_swa : m->G_full, m->attn_part, m->q_out, o_q8 ? m->q8 : NULL));
         if ((rc = mm(m, m->xb2, m->q_out, &m->wo[l], o_q8))) return rc;
         /* post_attention_norm + residual, then ffn_norm + Q8_K (main.c:1960-1975) */
         const int q8_ffn = is_q8_type(m->gate[l].type);
@@ -688,7 +684,7 @@ int g4e_forward(g4e_model *m, int token, int pos, int lm_mode) {
     g4_set_stream(m->stream);
     int rc = set_step(m, token, pos);
     if (rc) return rc;
-    rc = enqueue_step(m, lm_mode, pos);
+    rc = enqueue_step(m, lm_mode);
     if (rc) return rc;
     CK(g4_sync());
     return 0;
@@ -727,7 +723,7 @@ const float *g4e_layer_x(const g4e_model *m) { return m->layer_x; }
 /* One greedy decode step as launches: forward with logits, then argmax,
  * which also stores the token as the next input and advances the position. */
 static int enqueue_greedy_step(g4e_model *m) {
-    int rc = enqueue_step(m, 1, 0);
+    int rc = enqueue_step(m, 1);
     if (rc) return rc;
     CK(g4_argmax(m->logits, m->c.vocab, m->dstep + 2, m->argmax_part, m->dstep, m->dstep + 1));
     return 0;
@@ -784,7 +780,7 @@ int g4e_generate_greedy(g4e_model *m, const int *prompt, int n_prompt, int max_n
     /* prefill: token-serial, lm_mode 0 except for the last prompt token (main.c:2366-2384) */
     for (int pos = 0; pos < n_prompt - 1; pos++) {
         if (pos >= m->c.max_seq) return gen;
-        if ((rc = set_step(m, prompt[pos], pos)) || (rc = enqueue_step(m, 0, pos))) return -rc;
+        if ((rc = set_step(m, prompt[pos], pos)) || (rc = enqueue_step(m, 0))) return -rc;
     }
     const int last = n_prompt - 1;
     if (last >= m->c.max_seq) return gen;

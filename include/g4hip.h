@@ -221,6 +221,19 @@ size_t g4_attn_part_bytes(int n_heads, int hd, int G);
 int    g4_attn_decode_dev(const float *q, const float *kc, const float *vc, int kv_stride, int ring, const int *dpos,
                           int window, int n_heads, int n_kv, int hd, float attn_scale, int G, float *part, float *out,
                           void *q8);
+/* qkv_post + attention in one launch pair (main.c:1886-1950): per-head
+ * rmsnorm of the raw Q projection q_raw with q_norm and RoPE from rope_tab
+ * (g4_rope_table at this position; q_raw itself is not modified); if k_raw
+ * is non-null (a layer that stores KV), k_raw/v_raw are normalised (K with
+ * k_norm and rotated, V without weight) and stored at slot pos (pos % ring
+ * when ring > 0) of kstore/vstore, and the attention over kc/vc (the cache
+ * read: this layer's own, or the donor's on shared-KV layers) uses them for
+ * position pos.  n_rot/2 must divide 256.  Otherwise as g4_attn_decode_dev. */
+int    g4_attn_decode_fused(const float *q_raw, const float *q_norm, const float *k_raw, const float *v_raw,
+                            const float *k_norm, float *kstore, float *vstore, const float *kc, const float *vc,
+                            int kv_stride, int ring, const int *dpos, int window, int n_heads, int n_kv, int hd,
+                            int n_rot, const float *rope_tab, float eps, float attn_scale, int G, float *part,
+                            float *out, void *q8);
 /* x = emb_lookup(w, *dtok) * scale (main.c:1849-1854) */
 int g4_emb_lookup_dev(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale);
 /* build_ple after its projection (main.c:1751-1777): ple[l*pd+i] =

@@ -213,6 +213,75 @@ def test_attn_dev_fused_quant(lib, orc):
     assert h.tobytes() == orc.quantize_q8K(got).tobytes()
 
 
+@pytest.mark.parametrize("hd,window,pos,G,store", [(256, 512, 700, 16, True), (256, 512, 100, 4, True),
+                                                   (256, 512, 511, 16, True), (512, 0, 300, 10, True),
+                                                   (512, 0, 37, 1, True), (256, 512, 900, 16, False),
+                                                   (512, 0, 640, 20, False)])
+def test_attn_decode_fused(lib, orc, hd, window, pos, G, store):
+    """qkv_post + attention in one pass (main.c:1886-1950): raw Q/K/V of
+    position pos, per-head norms, RoPE from the position's table, K/V append
+    into the (ring or flat) cache, attention over the window -- against the
+    oracle's norms, RoPE and attention over a flat cache.  store=False is a
+    shared-KV layer: nothing is appended and the cache already holds pos."""
+    rng = np.random.default_rng(hd + pos + G)
+    nh, nkv, eps = 8, 2, 1e-6
+    kv_dim = nkv * hd
+    base = 1e4 if window else 1e6
+    ff = None if window else rng.uniform(1.0, 4.0, hd // 2).astype(np.float32)
+    q_norm = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    k_norm = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    flat_k = rng.standard_normal((pos + 1, kv_dim)).astype(np.float32)
+    flat_v = rng.standard_normal((pos + 1, kv_dim)).astype(np.float32)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(kv_dim).astype(np.float32)
+    v = rng.standard_normal(kv_dim).astype(np.float32)
+    qn = q.copy()
+    orc.L.or_rmsnorm_head_inplace(P(qn), P(q_norm), nh, hd, C.c_float(eps))
+    qn = orc.rope(qn, nh, hd, hd, pos, base, ff)
+    if store:
+        kk = k.copy()
+        orc.L.or_rmsnorm_head_inplace(P(kk), P(k_norm), nkv, hd, C.c_float(eps))
+        flat_k[pos] = orc.rope(kk, nkv, hd, hd, pos, base, ff)
+        vv = v.copy()
+        orc.L.or_rmsnorm_head_noweight_inplace(P(vv), nkv, hd, C.c_float(eps))
+        flat_v[pos] = vv
+    t_start = max(0, pos + 1 - window) if window else 0
+    want = orc.attn(qn, flat_k, flat_v, kv_dim, t_start, pos + 1 - t_start, nh, nkv, hd, 1.0)
+    # device cache: a ring of `window` slots or flat; slot pos holds garbage
+    # when the kernel is to append it
+    slots = window if window else pos + 1
+    cache_k = np.full((slots, kv_dim), 7.0, np.float32)
+    cache_v = np.full((slots, kv_dim), -7.0, np.float32)
+    for t in range(t_start, pos + (0 if store else 1)):
+        cache_k[t % slots], cache_v[t % slots] = flat_k[t], flat_v[t]
+    kc, vc = dbuf(lib, cache_k), dbuf(lib, cache_v)
+    dpos = dbuf(lib, np.array([pos], np.int32))
+    tab = empty(lib, 4 * hd)
+    ffd = dbuf(lib, ff) if ff is not None else None
+    lib.g4_rope_table(tab.ptr, dpos.ptr, 0, hd, C.c_float(base), C.c_float(1.0), ffd.ptr if ffd else None)
+    qd, kd, vd = dbuf(lib, q), dbuf(lib, k), dbuf(lib, v)
+    qnd, knd = dbuf(lib, q_norm), dbuf(lib, k_norm)
+    part = empty(lib, lib.L.g4_attn_part_bytes(nh, hd, G))
+    od = empty(lib, 4 * nh * hd)
+    q8 = empty(lib, lib.L.g4_q8K_bytes(nh * hd))
+    lib.g4_attn_decode_fused(qd.ptr, qnd.ptr, kd.ptr if store else None, vd.ptr if store else None,
+                             knd.ptr if store else None, kc.ptr if store else None, vc.ptr if store else None,
+                             kc.ptr, vc.ptr, kv_dim, window, dpos.ptr, window, nh, nkv, hd, hd, tab.ptr,
+                             C.c_float(eps), C.c_float(1.0), G, part.ptr, od.ptr, q8.ptr)
+    got = od.to_array(np.float32)
+    assert rel_err(got, want) < 1e-4
+    assert np.array_equal(qd.to_array(np.float32), q)          # q_raw is left as it was
+    ck = kc.to_array(np.float32).reshape(slots, kv_dim)
+    cv = vc.to_array(np.float32).reshape(slots, kv_dim)
+    s = pos % slots
+    assert np.max(np.abs(ck[s] - flat_k[pos])) < 1e-5 and np.max(np.abs(cv[s] - flat_v[pos])) < 1e-5
+    others = [t % slots for t in range(t_start, pos)]
+    assert np.array_equal(ck[others], cache_k[others]) and np.array_equal(cv[others], cache_v[others])
+    h = np.zeros(nh * hd // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), nh * hd)
+    assert h.tobytes() == orc.quantize_q8K(got).tobytes()
+
+
 # ---------------------------------------------------------------------------
 # embedding lookup, PLE, GELU gate, argmax
 # ---------------------------------------------------------------------------
