@@ -181,4 +181,118 @@ __device__ __forceinline__ void quantize_block_wave(const float v[4], int lane, 
     if (lane == 0) reinterpret_cast<float*>(y + q8k_d_off(nb))[b] = dval;
 }
 
+
+// ---- residual step + next norm + Q8_K (one workgroup) ----------------------
+//   if y:       x'[i] = x[i] + (y[i] * s_y) * w_post[i]       (main.c:1960-1962,
+//               1982-1984, 1995-1997: post-norm then residual add)
+//   if oscale:  x'[i] = x'[i] * oscale[0]                     (main.c:1999-2003)
+//   if w_next:  xb2[i] = (x'[i] * s_x) * w_next[i]            (main.c:1878, 1973)
+//   q8 = quantize_row_q8_K(qsrc == 0 ? xb2 : x')              (main.c:1884, 1975)
+// s_v = 1/sqrtf(sum(v^2)/n + eps) (main.c:1451-1456; the sum is a tree).
+struct ResidualArgs {
+    const float* x;        // residual stream in
+    float* x_out;          // residual stream out (may be x; nullptr: not stored)
+    const float* y;        // sub-layer output (nullptr: no residual step)
+    const float* w_post;
+    const float* oscale;
+    const float* w_next;   // nullptr: no second norm (the vector is x')
+    float* xb2;            // nullable
+    uint8_t* q8;           // nullable (global Q8_K of the vector)
+    int qsrc;
+    int n;
+    float eps;
+};
+
+// The whole workgroup (n <= EPT * blockDim.x).  residual_load issues every
+// global load of the step; residual_finish leaves the vector to quantize in
+// buf (n floats of LDS) and, if store, writes x_out and xb2.  A caller may
+// issue other loads between the two (they then overlap the norm's latency).
+// red: 16 floats of LDS.
+template <int EPT>
+struct ResidualRegs {
+    float xv[EPT], yv[EPT], wp[EPT], wn[EPT];
+};
+
+template <int EPT>
+__device__ __forceinline__ void residual_load(const ResidualArgs& a, ResidualRegs<EPT>& r) {
+    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int i = tid + k * nt;
+        const bool ok = i < n;
+        r.xv[k] = ok ? a.x[i] : 0.0f;
+        r.yv[k] = (ok && a.y) ? a.y[i] : 0.0f;
+        r.wp[k] = (ok && a.y) ? a.w_post[i] : 0.0f;
+        r.wn[k] = (ok && a.w_next) ? a.w_next[i] : 0.0f;
+    }
+}
+
+template <int EPT>
+__device__ __forceinline__ void residual_finish(const ResidualArgs& a, ResidualRegs<EPT>& r, float* buf, float* red,
+                                                bool store) {
+    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
+    float* xv = r.xv;
+    const float sc = a.oscale ? a.oscale[0] : 1.0f;
+    if (a.y) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) ss += r.yv[k] * r.yv[k];
+        ss = block_sum(ss, red);
+        const float sy = 1.0f / sqrtf(ss / (float)n + a.eps);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            float v = xv[k] + (r.yv[k] * sy) * r.wp[k];
+            if (a.oscale) v = v * sc;
+            xv[k] = v;
+        }
+    }
+    if (store && a.x_out && (a.y || a.x_out != a.x)) {
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * nt;
+            if (i < n) a.x_out[i] = xv[k];
+        }
+    }
+    if (a.w_next) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < EPT; k++) ss += xv[k] * xv[k];
+        ss = block_sum(ss, red);
+        const float sx = 1.0f / sqrtf(ss / (float)n + a.eps);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * nt;
+            const float t = (xv[k] * sx) * r.wn[k];
+            if (i < n) {
+                if (store && a.xb2) a.xb2[i] = t;
+                buf[i] = a.qsrc == 0 ? t : xv[k];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int i = tid + k * nt;
+            if (i < n) buf[i] = xv[k];
+        }
+    }
+}
+
+template <int EPT>
+__device__ __forceinline__ void residual_core(const ResidualArgs& a, float* buf, float* red, bool store) {
+    ResidualRegs<EPT> r;
+    residual_load<EPT>(a, r);
+    residual_finish<EPT>(a, r, buf, red, store);
+}
+
+// Q8_K of the nb blocks in buf (LDS) into y (global or LDS, device layout),
+// one wave per block
+__device__ __forceinline__ void quantize_blocks_wg(const float* buf, uint8_t* y, int nb) {
+    const int lane = threadIdx.x & 63;
+    for (int b = threadIdx.x >> 6; b < nb; b += blockDim.x >> 6) {
+        const float4 f = reinterpret_cast<const float4*>(buf + (size_t)b * 256)[lane];
+        const float v[4] = {f.x, f.y, f.z, f.w};
+        quantize_block_wave(v, lane, y, nb, b);
+    }
+}
+
 }  // namespace g4

@@ -177,19 +177,24 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
 // workgroup 0 also stores it to q8 -- the reference's mm() side effect.
 // aux (nullable, NMAT == 1): epilogue out = gelu(r) * aux[row]
 // (main.c:1989-1993).
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN>
-__global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, bool PRO = false>
+__global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
                                                            const uint8_t* q8, float* __restrict__ out,
                                                            int nb_rt, int d, int32_t* __restrict__ dbgS,
                                                            int32_t* __restrict__ dbgM, const float* __restrict__ xin,
                                                            uint8_t* __restrict__ q8_store,
-                                                           const float* __restrict__ aux) {
+                                                           const float* __restrict__ aux, const ResidualArgs ra) {
+    static_assert(!QIN || WG == 64, "the single-block input path runs one wave");
+    static_assert(!PRO || (WG == 256 && NB > 0 && !DBG), "the prologue needs 256 threads and a fixed row length");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
     const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
-    const int row = blockIdx.x * (64 / GL) + tid / GL;
+    const int row_ = blockIdx.x * (WG / GL) + tid / GL;
+    // with the prologue every thread stays for its barriers; rows past d
+    // compute row d-1 and do not store
+    const int row = PRO ? min(row_, d - 1) : row_;
     if (QIN) {
         __shared__ __align__(16) uint8_t q8s[292];
         const float4 f = reinterpret_cast<const float4*>(xin)[tid];
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
         __syncthreads();
         q8 = q8s;
     }
-    if (row >= d) return;   // whole rows (groups of GL lanes) leave together
+    if (!PRO && row >= d) return;   // whole rows (groups of GL lanes) leave together
     const uint32_t nblk = (uint32_t)d * (uint32_t)nb;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
     const uint32_t qh_off = 128u * nblk;
@@ -215,11 +220,13 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
         uint32_t qh[NMAT];
         float yd;
     };
-    auto load = [&](int b, Raw& r) {
+    auto load_a = [&](int b, Raw& r) {
         r.a0 = *reinterpret_cast<const uint4*>(a_qs + b * 256);
         r.a1 = *reinterpret_cast<const uint4*>(a_qs + b * 256 + 16);
         r.bsw = *reinterpret_cast<const uint2*>(a_bs + b * 32);
         r.yd = a_d[b];
+    };
+    auto load_w = [&](int b, Raw& r) {
         const uint32_t blk = rb + (uint32_t)b;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
@@ -228,6 +235,10 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
             r.hd[m] = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16u);
             r.qh[m] = Q5 ? *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32u + 4 * l) : 0u;
         }
+    };
+    auto load = [&](int b, Raw& r) {
+        load_a(b, r);
+        load_w(b, r);
     };
     // one block's integer sums and fp32 scales for matrix m
     auto block = [&](int m, int b, const Raw& r, int32_t& S, int32_t& P, float& D, float& DM) {
@@ -290,10 +301,46 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
     if (NB > 0) {
         // every load of this group's blocks first, then the integer work
         Raw raw[NH];
+        if constexpr (PRO) {
+            // the activations are produced here: residual step, norm and Q8_K
+            // by the whole workgroup into LDS (workgroup 0 also stores x_out,
+            // xb2 and q8), then read from LDS.  The step's small loads go
+            // first, the weight loads behind them, so the norm's arithmetic
+            // waits only for the former
+            ResidualRegs<NB> rr;
+            residual_load<NB>(ra, rr);
 #pragma unroll
-        for (int i = 0; i < NH; i++) {
-            const int b = grp * NH + i;
-            if (b < nb) load(b, raw[i]);
+            for (int i = 0; i < NH; i++) {
+                const int b = grp * NH + i;
+                if (b < nb) load_w(b, raw[i]);
+            }
+            extern __shared__ __align__(16) float pbuf[];   // NB*256 floats, then the Q8_K blocks
+            __shared__ float red[16];
+            uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf + NB * 256);
+            residual_finish<NB>(ra, rr, pbuf, red, blockIdx.x == 0);
+            __syncthreads();
+            quantize_blocks_wg(pbuf, q8l, NB);
+            if (blockIdx.x == 0 && ra.q8) quantize_blocks_wg(pbuf, ra.q8, NB);
+            __syncthreads();
+            const uint8_t* a_qs_l = q8l + 32 * l;
+            const uint8_t* a_bs_l = q8l + q8k_bsums_off(NB) + 8 * k;
+            const float* a_d_l = reinterpret_cast<const float*>(q8l + q8k_d_off(NB));
+#pragma unroll
+            for (int i = 0; i < NH; i++) {
+                const int b = grp * NH + i;
+                if (b < nb) {
+                    raw[i].a0 = *reinterpret_cast<const uint4*>(a_qs_l + b * 256);
+                    raw[i].a1 = *reinterpret_cast<const uint4*>(a_qs_l + b * 256 + 16);
+                    raw[i].bsw = *reinterpret_cast<const uint2*>(a_bs_l + b * 32);
+                    raw[i].yd = a_d_l[b];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NH; i++) {
+                const int b = grp * NH + i;
+                if (b < nb) load(b, raw[i]);
+            }
         }
         int32_t S[NMAT][NH], P[NMAT][NH];
         float D[NMAT][NH], DM[NMAT][NH];
@@ -355,7 +402,7 @@ __global__ __launch_bounds__(64) void gemv_q45_rows_kernel(const uint8_t* __rest
             r[m] = h + hm;
         }
     }
-    if (l == 0 && grp == 0) {
+    if (l == 0 && grp == 0 && row_ < d) {
         if (NMAT == 2) out[row] = gelu_ref(r[0]) * r[NMAT - 1];
         else out[row] = aux ? gelu_ref(r[0]) * aux[row] : r[0];
     }
@@ -502,7 +549,18 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
     constexpr int rows_per_wg = 8 / SPLIT;
     hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT, QIN>), dim3((d + rows_per_wg - 1) / rows_per_wg),
                        dim3(64), 0, g4_stream(), (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)q8, o, nb, d,
-                       S, M, xin, (uint8_t*)q8_store, aux);
+                       S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{});
+}
+
+// residual step + norm + Q8_K as the prologue of every workgroup (256
+// threads: four waves of 8/SPLIT rows each)
+template <bool Q5, int NB, int SPLIT>
+void launch_q45_pro(const void* w, float* o, int d, const float* aux, const ResidualArgs& ra) {
+    constexpr int rows_per_wg = 4 * 8 / SPLIT;
+    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15);
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, 1, false, NB, SPLIT, false, 256, true>),
+                       dim3((d + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, g4_stream(), (const uint8_t*)w,
+                       nullptr, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra);
 }
 
 // rows of nb blocks; the split of a row over lane groups grows with the work
@@ -682,4 +740,30 @@ extern "C" int g4_debug_block_sums(const void* w, int n, int d, int type, const 
     if (type == G4_Q4_K) return launch_q45<false, 1, true>(w, nullptr, q8, nullptr, nb, d, S, M);
     if (type == G4_Q5_K) return launch_q45<true, 1, true>(w, nullptr, q8, nullptr, nb, d, S, M);
     return g4_fail(G4_ERR_TYPE, "g4_debug_block_sums: type %d not supported", type);
+}
+
+// g4_residual_norm (with the residual stream read from x and written to
+// x_out) followed by mm_quant_dot_rows on its Q8_K, in one launch: every
+// workgroup computes the norm and the Q8_K itself (into LDS) while its weight
+// loads are in flight; workgroup 0 stores x_out, xb2 and q8.
+extern "C" int g4_mm_residual_q8(float* o, const void* w, int n, int d, int type, const float* mul, const float* x,
+                                 float* x_out, const float* y, const float* w_post, const float* oscale,
+                                 const float* w_next, float* xb2, void* q8, int qsrc, float eps) {
+    int rc = check_gemv("g4_mm_residual_q8", o, w, x, n, d);
+    if (rc) return rc;
+    G4_CHECK_ARG(!y || w_post, "g4_mm_residual_q8: y without w_post");
+    G4_CHECK_ARG(qsrc == 1 || w_next, "g4_mm_residual_q8: quantizing the normed vector needs w_next");
+    G4_CHECK_ARG(!(y && x_out == x), "g4_mm_residual_q8: x_out must not alias x when y is given");
+    G4_CHECK_ARG(!q8 || aligned16(q8), "g4_mm_residual_q8: q8 must be 16-byte aligned");
+    ResidualArgs ra{x, x_out, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    const int nb = n / 256;
+    const bool q5 = type == G4_Q5_K;
+    if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "g4_mm_residual_q8: type %d not supported", type);
+    switch (nb) {
+    case 8: q5 ? launch_q45_pro<true, 8, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 8, 2>(w, o, d, mul, ra); break;
+    case 10: q5 ? launch_q45_pro<true, 10, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 10, 2>(w, o, d, mul, ra); break;
+    case 16: q5 ? launch_q45_pro<true, 16, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 16, 2>(w, o, d, mul, ra); break;
+    default: return g4_fail(G4_ERR_ARG, "g4_mm_residual_q8: n=%d (2048, 2560 or 4096)", n);
+    }
+    return g4_check_launch("gemv_q45_rows_kernel<prologue>");
 }

@@ -50,82 +50,15 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict__ 
 // ---------------------------------------------------------------------------
 constexpr int kResidualMax = 16384;
 
-struct ResidualArgs {
-    float* x;
-    const float* y;
-    const float* w_post;
-    const float* oscale;
-    const float* w_next;
-    float* xb2;
-    uint8_t* q8;
-    int qsrc;
-    int n;
-    float eps;
-};
-
-// EPT elements per thread (n <= EPT * kNormThreads); every global load is
-// issued at entry, so the kernel pays one memory round trip.
+// EPT elements per thread (n <= EPT * blockDim.x)
 template <int EPT>
 __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArgs a) {
     extern __shared__ __align__(16) float buf[];   // n floats: the vector to quantize
     __shared__ float red[16];
-    const int n = a.n, tid = threadIdx.x, nt = blockDim.x;
-    float xv[EPT], yv[EPT], wp[EPT], wn[EPT];
-#pragma unroll
-    for (int k = 0; k < EPT; k++) {
-        const int i = tid + k * nt;
-        const bool ok = i < n;
-        xv[k] = ok ? a.x[i] : 0.0f;
-        yv[k] = (ok && a.y) ? a.y[i] : 0.0f;
-        wp[k] = (ok && a.y) ? a.w_post[i] : 0.0f;
-        wn[k] = (ok && a.w_next) ? a.w_next[i] : 0.0f;
-    }
-    const float sc = a.oscale ? a.oscale[0] : 1.0f;
-    if (a.y) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int k = 0; k < EPT; k++) ss += yv[k] * yv[k];
-        ss = block_sum(ss, red);
-        const float sy = 1.0f / sqrtf(ss / (float)n + a.eps);
-#pragma unroll
-        for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * nt;
-            float v = xv[k] + (yv[k] * sy) * wp[k];
-            if (a.oscale) v = v * sc;
-            xv[k] = v;
-            if (i < n) a.x[i] = v;
-        }
-    }
-    if (a.w_next) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int k = 0; k < EPT; k++) ss += xv[k] * xv[k];
-        ss = block_sum(ss, red);
-        const float sx = 1.0f / sqrtf(ss / (float)n + a.eps);
-#pragma unroll
-        for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * nt;
-            const float t = (xv[k] * sx) * wn[k];
-            if (i < n) {
-                if (a.xb2) a.xb2[i] = t;
-                buf[i] = a.qsrc == 0 ? t : xv[k];
-            }
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < EPT; k++) {
-            const int i = tid + k * nt;
-            if (i < n) buf[i] = xv[k];
-        }
-    }
+    residual_core<EPT>(a, buf, red, true);
     if (a.q8) {
         __syncthreads();
-        const int nb = n / 256, lane = tid & 63;
-        for (int b = tid >> 6; b < nb; b += nt / 64) {
-            const float4 f = reinterpret_cast<const float4*>(buf + (size_t)b * 256)[lane];
-            const float v[4] = {f.x, f.y, f.z, f.w};
-            quantize_block_wave(v, lane, a.q8, nb, b);
-        }
+        quantize_blocks_wg(buf, a.q8, a.n / 256);
     }
 }
 
@@ -139,7 +72,7 @@ extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, c
     G4_CHECK_ARG(!y || w_post, "residual_norm: y without w_post");
     G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm: n=%d not a multiple of 256 for Q8_K", n);
     G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm: quantizing xb2 needs w_next");
-    ResidualArgs a{x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    ResidualArgs a{x, x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
     // EPT elements per thread, as few waves as cover n (n = 2560: 640 threads,
     // one wave per Q8_K block)
     const int ept = n <= kNormThreads ? 1 : n <= 4 * kNormThreads ? 4 : 16;

@@ -78,6 +78,9 @@ struct g4e_model {
     Tensor inp_gate[E_MAX_LAYERS], proj[E_MAX_LAYERS];
     /* state (HBM) */
     float *x, *xb2, *hb, *q, *k, *v, *q_out, *ple, *ple_ctx, *ple_gate, *logits;
+    float *x_alt;            /* second residual-stream buffer (fused prologues write the other one) */
+    float *ybuf;             /* PLE projection output, read by the next residual step */
+    float *x_last;           /* buffer holding the residual stream after the last step */
     void *q8;
     float *kc[E_N_LAYER_KV], *vc[E_N_LAYER_KV];
     int kv_ring[E_N_LAYER_KV];
@@ -483,6 +486,9 @@ static int load(g4e_model *m, const Image *im) {
     void *p;
 #define DA(field, bytes) if ((rc = dalloc(m, &p, (size_t)(bytes)))) return rc; field = p;
     DA(m->x, (size_t)c->dim * 4);
+    DA(m->x_alt, (size_t)c->dim * 4);
+    DA(m->ybuf, (size_t)c->dim * 4);
+    m->x_last = m->x;
     DA(m->xb2, (size_t)c->dim * 4);
     DA(m->hb, (size_t)c->hidden * 4);
     DA(m->q, (size_t)qmax * 4);
@@ -590,30 +596,52 @@ static int mm(g4e_model *m, float *o, const float *x, const Tensor *w, int q8_re
 
 /* Enqueue one forward step; token and position are read from m->dstep, so the
  * same sequence of launches is valid for every position (graph capture). */
+/* a Q4_K/Q5_K GEMV that can take the residual step + norm + Q8_K as its
+ * prologue (g4_mm_residual_q8) */
+static int pro_ok(const Config *c, const Tensor *w) {
+    const int nb = c->dim / 256;
+    return is_q8_type(w->type) && c->dim % 256 == 0 && (nb == 8 || nb == 10 || nb == 16);
+}
+
+/* Enqueue one forward step; token and position are read from m->dstep, so the
+ * same sequence of launches is valid for every position (graph capture).
+ * The residual stream lives in two buffers: a GEMV whose prologue performs
+ * a residual step reads one and writes the other (its workgroups run
+ * concurrently); single-workgroup steps update it in place. */
 static int enqueue_step(g4e_model *m, int lm_mode) {
     const Config *c = &m->c;
     const int dim = c->dim, L = c->n_layers, pd = c->ple_dim;
     const int *dtok = m->dstep, *dpos = m->dstep + 1;
+    float *x = m->x, *xo = m->x_alt;
     /* emb_lookup * sqrt(dim) (main.c:1849-1854) and build_ple (main.c:1747-1778) */
-    CK(g4_emb_lookup_dev(m->x, m->embd.p, m->embd.type, m->embd.d, dtok, dim, sqrtf((float)dim)));
-    CK(g4_mm(m->ple_ctx, m->x, m->ple_proj.p, m->ple_proj.n, m->ple_proj.d, m->ple_proj.type, m->q8, 0));
+    CK(g4_emb_lookup_dev(x, m->embd.p, m->embd.type, m->embd.d, dtok, dim, sqrtf((float)dim)));
+    CK(g4_mm(m->ple_ctx, x, m->ple_proj.p, m->ple_proj.n, m->ple_proj.d, m->ple_proj.type, m->q8, 0));
     CK(g4_ple_finish(m->ple, m->ple_ctx, m->ple_tok.p, m->ple_tok.type, m->ple_tok.d, m->ple_proj_norm, dtok, 0, pd, L,
                      sqrtf((float)pd), 1.0f / sqrtf((float)dim), 1.0f / sqrtf(2.0f), c->eps));
     /* RoPE angles of this position for both layer types (main.c:1725-1742) */
     float *tab_swa = m->rope_tab, *tab_full = m->rope_tab + c->rot_swa;
     CK(g4_rope_table(tab_swa, dpos, 0, c->rot_swa, c->theta_swa, 1.0f, NULL));
     CK(g4_rope_table(tab_full, dpos, 0, c->rot_full, c->theta, 1.0f, m->rope_freqs));
-    if (m->trace) CK(g4_memcpy_d2h(m->layer_x, m->x, (size_t)dim * 4));
-    /* layer 0's attn_norm + Q8_K (later layers get it fused into the previous tail) */
-    CK(g4_residual_norm(m->x, NULL, NULL, NULL, m->attn_norm[0], m->xb2, is_q8_type(m->wq[0].type) ? m->q8 : NULL, 0,
-                        dim, c->eps));
+    if (m->trace) CK(g4_memcpy_d2h(m->layer_x, x, (size_t)dim * 4));
     for (int l = 0; l < L; l++) {
         const int hd = layer_hd(c, l), swa = is_swa(c, l);
         const int n_rot = swa ? c->rot_swa : c->rot_full;
         const int q8_att = is_q8_type(m->wq[l].type);
-        /* Q, K, V share one Q8_K of xb2 (main.c:1883-1892) */
-        int rc = mm(m, m->q, m->xb2, &m->wq[l], q8_att);
-        if (rc) return rc;
+        /* the previous layer's post_norm + residual + out_scale (main.c:1995-2003;
+         * none before layer 0), this layer's attn_norm + Q8_K (main.c:1878-1884),
+         * then Q, K, V on that one Q8_K of xb2 (main.c:1883-1892) */
+        const float *y = l ? m->ybuf : NULL, *w_post = l ? m->post_norm[l - 1] : NULL;
+        const float *osc = l ? m->out_scale[l - 1] : NULL;
+        int rc;
+        if (pro_ok(c, &m->wq[l])) {
+            CK(g4_mm_residual_q8(m->q, m->wq[l].p, m->wq[l].n, m->wq[l].d, m->wq[l].type, NULL, x, y ? xo : x, y,
+                                 w_post, osc, m->attn_norm[l], m->xb2, m->q8, 0, c->eps));
+            if (y) { float *t = x; x = xo; xo = t; }
+        } else {
+            CK(g4_residual_norm(x, y, w_post, osc, m->attn_norm[l], m->xb2, q8_att ? m->q8 : NULL, 0, dim, c->eps));
+            if ((rc = mm(m, m->q, m->xb2, &m->wq[l], q8_att))) return rc;
+        }
+        if (m->trace && l > 0) CK(g4_memcpy_d2h(m->layer_x + (size_t)l * dim, x, (size_t)dim * 4));
         const int src = kv_source(c, l), has_kv = layer_has_kv(l);
         if (has_kv) {
             if (is_q8_type(m->wk[l].type) != q8_att && is_q8_type(m->wk[l].type))
@@ -633,40 +661,41 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
         if ((rc = mm(m, m->xb2, m->q_out, &m->wo[l], o_q8))) return rc;
         /* post_attention_norm + residual, then ffn_norm + Q8_K (main.c:1960-1975) */
         const int q8_ffn = is_q8_type(m->gate[l].type);
-        CK(g4_residual_norm(m->x, m->xb2, m->post_attn_norm[l], NULL, m->ffn_norm[l], m->xb2, q8_ffn ? m->q8 : NULL, 0,
-                            dim, c->eps));
+        CK(g4_residual_norm(x, m->xb2, m->post_attn_norm[l], NULL, m->ffn_norm[l], m->xb2, q8_ffn ? m->q8 : NULL, 0, dim,
+                            c->eps));
         /* gelu(gate) * up (main.c:1976-1980), down (main.c:1981) */
         CK(g4_mm_gate_up_gelu(m->hb, m->gate[l].p, m->up[l].p, dim, c->hidden, m->gate[l].type, m->q8));
         if ((rc = mm(m, m->xb2, m->hb, &m->down[l], 0))) return rc;
-        /* post_ffw_norm + residual; Q8_K of x for inp_gate (main.c:1982-1988) */
-        const int q8_ig = is_q8_type(m->inp_gate[l].type);
-        CK(g4_residual_norm(m->x, m->xb2, m->post_ffw_norm[l], NULL, NULL, NULL, q8_ig ? m->q8 : NULL, 1, dim, c->eps));
-        /* inp_gate GEMV with gelu * ple[l] in its epilogue (main.c:1988-1993) */
-        if (q8_ig) {
-            CK(g4_mm_quant_dot_rows_gelu_mul(m->ple_gate, m->inp_gate[l].p, dim, pd, m->inp_gate[l].type, m->q8,
-                                             m->ple + (size_t)l * pd));
+        /* post_ffw_norm + residual, Q8_K of x (main.c:1982-1988) and the
+         * inp_gate GEMV with gelu * ple[l] in its epilogue (main.c:1988-1993) */
+        if (pro_ok(c, &m->inp_gate[l])) {
+            CK(g4_mm_residual_q8(m->ple_gate, m->inp_gate[l].p, dim, pd, m->inp_gate[l].type, m->ple + (size_t)l * pd, x,
+                                 xo, m->xb2, m->post_ffw_norm[l], NULL, NULL, NULL, NULL, 1, c->eps));
+            float *t = x; x = xo; xo = t;
         } else {
-            if ((rc = mm(m, m->ple_gate, m->x, &m->inp_gate[l], 0))) return rc;
-            CK(g4_gelu_mul_quant(m->ple_gate, m->ple + (size_t)l * pd, pd, NULL));
+            const int q8_ig = is_q8_type(m->inp_gate[l].type);
+            CK(g4_residual_norm(x, m->xb2, m->post_ffw_norm[l], NULL, NULL, NULL, q8_ig ? m->q8 : NULL, 1, dim, c->eps));
+            if (q8_ig) {
+                CK(g4_mm_quant_dot_rows_gelu_mul(m->ple_gate, m->inp_gate[l].p, dim, pd, m->inp_gate[l].type, m->q8,
+                                                 m->ple + (size_t)l * pd));
+            } else {
+                if ((rc = mm(m, m->ple_gate, x, &m->inp_gate[l], 0))) return rc;
+                CK(g4_gelu_mul_quant(m->ple_gate, m->ple + (size_t)l * pd, pd, NULL));
+            }
         }
-        /* proj (main.c:1994): mm() quantizes its 256-wide input inside the GEMV */
-        if ((rc = mm(m, m->xb2, m->ple_gate, &m->proj[l], 0))) return rc;
-        /* post_norm + residual, out_scale (main.c:1995-2003), fused with the next
-         * layer's attn_norm + Q8_K, or with the final norm (main.c:2021) */
-        if (l + 1 < L) {
-            CK(g4_residual_norm(m->x, m->xb2, m->post_norm[l], m->out_scale[l], m->attn_norm[l + 1], m->xb2,
-                                is_q8_type(m->wq[l + 1].type) ? m->q8 : NULL, 0, dim, c->eps));
-        } else {
-            CK(g4_residual_norm(m->x, m->xb2, m->post_norm[l], m->out_scale[l], lm_mode ? m->norm_out : NULL,
-                                lm_mode ? m->xb2 : NULL, NULL, 0, dim, c->eps));
-        }
-        if (m->trace) {
-            CK(g4_memcpy_d2h(m->layer_x + (size_t)(l + 1) * dim, m->x, (size_t)dim * 4));
-        }
+        /* proj (main.c:1994): mm() quantizes its 256-wide input inside the GEMV;
+         * its residual step runs in the next layer's Q launch */
+        if ((rc = mm(m, m->ybuf, m->ple_gate, &m->proj[l], 0))) return rc;
     }
+    /* the last layer's post_norm + residual + out_scale and the final norm
+     * (main.c:1995-2003, 2021) */
+    CK(g4_residual_norm(x, m->ybuf, m->post_norm[L - 1], m->out_scale[L - 1], lm_mode ? m->norm_out : NULL,
+                        lm_mode ? m->xb2 : NULL, NULL, 0, dim, c->eps));
+    if (m->trace) CK(g4_memcpy_d2h(m->layer_x + (size_t)L * dim, x, (size_t)dim * 4));
+    m->x_last = x;
     if (lm_mode == 0) return 0;
     /* logits_tied (main.c:1780-1796): Q6_K rows times the final-normed hidden
-     * (kept in xb2; x keeps the last layer's output), soft-cap */
+     * (kept in xb2), soft-cap */
     CK(g4_mm_quant_rows_softcap(m->logits, m->xb2, m->embd.p, dim, c->vocab, m->embd.type, c->softcap));
     return 0;
 }
@@ -698,7 +727,7 @@ int g4e_read_logits(g4e_model *m, float *host) {
 
 int g4e_read_x(g4e_model *m, float *host) {
     g4_set_stream(m->stream);
-    CK(g4_memcpy_d2h(host, m->x, (size_t)m->c.dim * 4));
+    CK(g4_memcpy_d2h(host, m->x_last, (size_t)m->c.dim * 4));
     return 0;
 }
 

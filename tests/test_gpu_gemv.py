@@ -5,6 +5,8 @@ Bars: Q8_K bytes, per-block int32 sums, and the Q4_K/Q5_K fp32 outputs are
 bit-exact; fp32-activation GEMVs are within 1e-5 of the result, normalised by
 sum |w * x| (the reference sums sequentially, the GPU in a tree).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -287,3 +289,73 @@ def test_mm_single_block_quantizes_inside(lib, orc, qtype):
     want = orc.mm_quant_dot_rows(raw, n, d, qtype, q8h)
     assert np.array_equal(out.to_array(np.float32).view(np.uint32), want.view(np.uint32))
     assert download_q8(lib, q8, n).tobytes() == q8h.tobytes()
+
+
+def rel_err(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+@pytest.mark.parametrize("qtype,n,d,mode", [(12, 2560, 2048, "attn"), (12, 2560, 256, "ple"), (13, 2560, 200, "attn"),
+                                            (12, 2048, 96, "first"), (12, 4096, 520, "attn"), (13, 2560, 256, "ple")])
+def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
+    """Residual step + norm + Q8_K as the GEMV's prologue (g4_mm_residual_q8):
+    x_out and xb2 to the residual_norm bars against the oracle's rmsnorm; the
+    stored Q8_K equal to quantize_row_q8_K of the stored vector; every output
+    row equal, bit for bit, to mm_quant_dot_rows on that stored Q8_K (each
+    workgroup quantizes for itself, so this also checks that they agree)."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(n + d + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = (rng.standard_normal(n) * 4).astype(np.float32)
+    wp = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    osc = np.array([0.9], np.float32)
+    mul = rng.standard_normal(d).astype(np.float32)
+    xd, yd, wpd, wnd, od = (DBuf.from_array(lib, a) for a in (x, y, wp, wn, osc))
+    xo, xb2, out = DBuf(lib, 4 * n), DBuf(lib, 4 * n), DBuf(lib, 4 * d)
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(n))
+    muld = DBuf.from_array(lib, mul)
+    eps = C.c_float(1e-6)
+    if mode == "attn":       # post_norm + residual + out_scale, next attn_norm, Q8_K of xb2
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, None, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, od.ptr, wnd.ptr,
+                              xb2.ptr, q8.ptr, 0, eps)
+        want_x = (x + orc.rmsnorm(y, wp)) * osc[0]
+        want_v = orc.rmsnorm(want_x, wn)
+        got_v = xb2.to_array(np.float32)
+        assert rel_err(got_v, want_v) < 4e-6
+    elif mode == "ple":      # post_ffw_norm + residual, Q8_K of x, gelu * mul epilogue
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, muld.ptr, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None, None, None,
+                              q8.ptr, 1, eps)
+        want_x = x + orc.rmsnorm(y, wp)
+        got_v = xo.to_array(np.float32)
+    else:                    # layer 0: attn_norm only, the stream is not rewritten
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, None, xd.ptr, xd.ptr, None, None, None, wnd.ptr, xb2.ptr,
+                              q8.ptr, 0, eps)
+        want_x = x
+        got_v = xb2.to_array(np.float32)
+        assert rel_err(got_v, orc.rmsnorm(x, wn)) < 4e-6
+    gx = xo.to_array(np.float32) if mode != "first" else xd.to_array(np.float32)
+    assert rel_err(gx, want_x) < 2e-6
+    if mode == "first":
+        assert np.array_equal(gx, x)
+    h = np.zeros(n // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(got_v).tobytes()
+    ref = DBuf(lib, 4 * d)
+    if mode == "ple":
+        lib.g4_mm_quant_dot_rows_gelu_mul(ref.ptr, w.ptr, n, d, qtype, q8.ptr, muld.ptr)
+    else:
+        lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
+    g, r = out.to_array(np.float32), ref.to_array(np.float32)
+    assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), np.flatnonzero(g != r)[:8]
+
+
+def test_mm_residual_q8_rejects_alias(lib):
+    from g4 import DBuf, G4Error
+    b = DBuf(lib, 4 * 4096)
+    with pytest.raises(G4Error):
+        lib.g4_mm_residual_q8(b.ptr, b.ptr, 2560, 8, 12, None, b.ptr, b.ptr, b.ptr, b.ptr, None, None, None, None, 1,
+                              C.c_float(1e-6))
