@@ -554,13 +554,20 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
 
 // residual step + norm + Q8_K as the prologue of every workgroup (256
 // threads: four waves of 8/SPLIT rows each)
-template <bool Q5, int NB, int SPLIT>
-void launch_q45_pro(const void* w, float* o, int d, const float* aux, const ResidualArgs& ra) {
+template <bool Q5, int NMAT, int NB>
+void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra) {
+    constexpr int SPLIT = NMAT == 2 ? 4 : 2;
     constexpr int rows_per_wg = 4 * 8 / SPLIT;
     const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15);
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, 1, false, NB, SPLIT, false, 256, true>),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, 256, true>),
                        dim3((d + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, g4_stream(), (const uint8_t*)w,
-                       nullptr, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra);
+                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra);
+}
+
+template <bool Q5, int NB>
+void launch_q45_pro_nm(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra) {
+    if (w2) launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra);
+    else launch_q45_pro<Q5, 1, NB>(w, nullptr, o, d, aux, ra);
 }
 
 // rows of nb blocks; the split of a row over lane groups grows with the work
@@ -745,24 +752,27 @@ extern "C" int g4_debug_block_sums(const void* w, int n, int d, int type, const 
 // g4_residual_norm (with the residual stream read from x and written to
 // x_out) followed by mm_quant_dot_rows on its Q8_K, in one launch: every
 // workgroup computes the norm and the Q8_K itself (into LDS) while its weight
-// loads are in flight; workgroup 0 stores x_out, xb2 and q8.
-extern "C" int g4_mm_residual_q8(float* o, const void* w, int n, int d, int type, const float* mul, const float* x,
-                                 float* x_out, const float* y, const float* w_post, const float* oscale,
-                                 const float* w_next, float* xb2, void* q8, int qsrc, float eps) {
+// loads are in flight; workgroup 0 stores x_out, xb2 and q8.  With w2 the
+// GEMV is the fused gate|up pair: o = gelu(W.x) * (W2.x).
+extern "C" int g4_mm_residual_q8(float* o, const void* w, const void* w2, int n, int d, int type, const float* mul,
+                                 const float* x, float* x_out, const float* y, const float* w_post,
+                                 const float* oscale, const float* w_next, float* xb2, void* q8, int qsrc, float eps) {
     int rc = check_gemv("g4_mm_residual_q8", o, w, x, n, d);
     if (rc) return rc;
+    G4_CHECK_ARG(!w2 || (aligned16(w2) && !mul), "g4_mm_residual_q8: bad w2 (16-byte aligned, no mul)");
     G4_CHECK_ARG(!y || w_post, "g4_mm_residual_q8: y without w_post");
     G4_CHECK_ARG(qsrc == 1 || w_next, "g4_mm_residual_q8: quantizing the normed vector needs w_next");
     G4_CHECK_ARG(!(y && x_out == x), "g4_mm_residual_q8: x_out must not alias x when y is given");
+    G4_CHECK_ARG(!(y && xb2 == y), "g4_mm_residual_q8: xb2 must not alias y");
     G4_CHECK_ARG(!q8 || aligned16(q8), "g4_mm_residual_q8: q8 must be 16-byte aligned");
     ResidualArgs ra{x, x_out, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
     const int nb = n / 256;
     const bool q5 = type == G4_Q5_K;
     if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "g4_mm_residual_q8: type %d not supported", type);
     switch (nb) {
-    case 8: q5 ? launch_q45_pro<true, 8, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 8, 2>(w, o, d, mul, ra); break;
-    case 10: q5 ? launch_q45_pro<true, 10, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 10, 2>(w, o, d, mul, ra); break;
-    case 16: q5 ? launch_q45_pro<true, 16, 2>(w, o, d, mul, ra) : launch_q45_pro<false, 16, 2>(w, o, d, mul, ra); break;
+    case 8: q5 ? launch_q45_pro_nm<true, 8>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 8>(w, w2, o, d, mul, ra); break;
+    case 10: q5 ? launch_q45_pro_nm<true, 10>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 10>(w, w2, o, d, mul, ra); break;
+    case 16: q5 ? launch_q45_pro_nm<true, 16>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 16>(w, w2, o, d, mul, ra); break;
     default: return g4_fail(G4_ERR_ARG, "g4_mm_residual_q8: n=%d (2048, 2560 or 4096)", n);
     }
     return g4_check_launch("gemv_q45_rows_kernel<prologue>");

@@ -634,7 +634,7 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
         const float *osc = l ? m->out_scale[l - 1] : NULL;
         int rc;
         if (pro_ok(c, &m->wq[l])) {
-            CK(g4_mm_residual_q8(m->q, m->wq[l].p, m->wq[l].n, m->wq[l].d, m->wq[l].type, NULL, x, y ? xo : x, y,
+            CK(g4_mm_residual_q8(m->q, m->wq[l].p, NULL, m->wq[l].n, m->wq[l].d, m->wq[l].type, NULL, x, y ? xo : x, y,
                                  w_post, osc, m->attn_norm[l], m->xb2, m->q8, 0, c->eps));
             if (y) { float *t = x; x = xo; xo = t; }
         } else {
@@ -659,17 +659,21 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
                                 swa ? c->window : 0, c->n_heads, c->n_kv, hd, n_rot, swa ? tab_swa : tab_full, c->eps,
                                 1.0f, swa ? m->G_swa : m->G_full, m->attn_part, m->q_out, o_q8 ? m->q8 : NULL));
         if ((rc = mm(m, m->xb2, m->q_out, &m->wo[l], o_q8))) return rc;
-        /* post_attention_norm + residual, then ffn_norm + Q8_K (main.c:1960-1975) */
+        /* post_attention_norm + residual, then ffn_norm + Q8_K (main.c:1960-1975),
+         * in place (one workgroup); as a prologue of the 20480-row gate|up GEMV
+         * it would run in every one of its workgroups and costs more than the
+         * launch it saves */
         const int q8_ffn = is_q8_type(m->gate[l].type);
         CK(g4_residual_norm(x, m->xb2, m->post_attn_norm[l], NULL, m->ffn_norm[l], m->xb2, q8_ffn ? m->q8 : NULL, 0, dim,
                             c->eps));
-        /* gelu(gate) * up (main.c:1976-1980), down (main.c:1981) */
+        /* gelu(gate) * up (main.c:1976-1980) */
         CK(g4_mm_gate_up_gelu(m->hb, m->gate[l].p, m->up[l].p, dim, c->hidden, m->gate[l].type, m->q8));
+        /* down (main.c:1981) */
         if ((rc = mm(m, m->xb2, m->hb, &m->down[l], 0))) return rc;
         /* post_ffw_norm + residual, Q8_K of x (main.c:1982-1988) and the
          * inp_gate GEMV with gelu * ple[l] in its epilogue (main.c:1988-1993) */
         if (pro_ok(c, &m->inp_gate[l])) {
-            CK(g4_mm_residual_q8(m->ple_gate, m->inp_gate[l].p, dim, pd, m->inp_gate[l].type, m->ple + (size_t)l * pd, x,
+            CK(g4_mm_residual_q8(m->ple_gate, m->inp_gate[l].p, NULL, dim, pd, m->inp_gate[l].type, m->ple + (size_t)l * pd, x,
                                  xo, m->xb2, m->post_ffw_norm[l], NULL, NULL, NULL, NULL, 1, c->eps));
             float *t = x; x = xo; xo = t;
         } else {

@@ -125,16 +125,17 @@ int g4_mm_quant_rows_softcap(float *o, const float *x, const void *w, int n, int
 /* tiling knob of the K-quant GEMVs (workgroups per CU targeted; default 4) */
 int g4_set_gemv_occupancy(int wg_per_cu);
 /* g4_residual_norm followed by g4_mm_quant_dot_rows (or, with mul,
- * g4_mm_quant_dot_rows_gelu_mul) on the Q8_K it produces, in one launch:
- * the residual step of main.c:1960-1962 / 1982-1984 / 1995-2003 reads the
- * stream from x and writes it to x_out (which must differ from x when y is
- * given; with y == NULL it is x copied, or nothing if x_out == x), the next
- * norm (main.c:1878, 1973) goes to xb2 and Q8_K(qsrc == 0 ? xb2 : x_out) to
- * q8 (each optional), and o = W . Q8_K.  W is Q4_K/Q5_K with n in {2048,
- * 2560, 4096}. */
-int g4_mm_residual_q8(float *o, const void *w, int n, int d, int type, const float *mul, const float *x, float *x_out,
-                      const float *y, const float *w_post, const float *oscale, const float *w_next, float *xb2,
-                      void *q8, int qsrc, float eps);
+ * g4_mm_quant_dot_rows_gelu_mul; or, with w2, g4_mm_gate_up_gelu with gate
+ * w and up w2) on the Q8_K it produces, in one launch: the residual step of
+ * main.c:1960-1962 / 1982-1984 / 1995-2003 reads the stream from x and
+ * writes it to x_out (which must differ from x when y is given; with
+ * y == NULL it is x copied, or nothing if x_out == x), the next norm
+ * (main.c:1878, 1973) goes to xb2 (must differ from y) and
+ * Q8_K(qsrc == 0 ? normed : x_out) to q8 (each optional), and o = W . Q8_K.
+ * W is Q4_K/Q5_K with n in {2048, 2560, 4096}. */
+int g4_mm_residual_q8(float *o, const void *w, const void *w2, int n, int d, int type, const float *mul,
+                      const float *x, float *x_out, const float *y, const float *w_post, const float *oscale,
+                      const float *w_next, float *xb2, void *q8, int qsrc, float eps);
 
 /* ---------------------------------------------------------------------------
  * Batched prefill GEMM.  The reference has none: generate() runs forward()

@@ -297,7 +297,8 @@ def rel_err(got, want):
 
 
 @pytest.mark.parametrize("qtype,n,d,mode", [(12, 2560, 2048, "attn"), (12, 2560, 256, "ple"), (13, 2560, 200, "attn"),
-                                            (12, 2048, 96, "first"), (12, 4096, 520, "attn"), (13, 2560, 256, "ple")])
+                                            (12, 2048, 96, "first"), (12, 4096, 520, "attn"), (13, 2560, 256, "ple"),
+                                            (12, 2560, 10240, "ffn"), (13, 2560, 1000, "ffn")])
 def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
     """Residual step + norm + Q8_K as the GEMV's prologue (g4_mm_residual_q8):
     x_out and xb2 to the residual_norm bars against the oracle's rmsnorm; the
@@ -319,20 +320,29 @@ def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
     q8 = DBuf(lib, lib.L.g4_q8K_bytes(n))
     muld = DBuf.from_array(lib, mul)
     eps = C.c_float(1e-6)
-    if mode == "attn":       # post_norm + residual + out_scale, next attn_norm, Q8_K of xb2
-        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, None, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, od.ptr, wnd.ptr,
+    up_raw = synth.rand_kquant(rng, qtype, d, n) if mode == "ffn" else None
+    up = upload_quant(lib, up_raw, qtype, n, d) if mode == "ffn" else None
+    if mode == "ffn":        # post_attention_norm + residual, ffn_norm, Q8_K; gelu(gate) * up
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, up.ptr, n, d, qtype, None, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None, wnd.ptr,
+                              xb2.ptr, q8.ptr, 0, eps)
+        want_x = x + orc.rmsnorm(y, wp)
+        want_v = orc.rmsnorm(want_x, wn)
+        got_v = xb2.to_array(np.float32)
+        assert rel_err(got_v, want_v) < 4e-6
+    elif mode == "attn":     # post_norm + residual + out_scale, next attn_norm, Q8_K of xb2
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, None, n, d, qtype, None, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, od.ptr, wnd.ptr,
                               xb2.ptr, q8.ptr, 0, eps)
         want_x = (x + orc.rmsnorm(y, wp)) * osc[0]
         want_v = orc.rmsnorm(want_x, wn)
         got_v = xb2.to_array(np.float32)
         assert rel_err(got_v, want_v) < 4e-6
     elif mode == "ple":      # post_ffw_norm + residual, Q8_K of x, gelu * mul epilogue
-        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, muld.ptr, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None, None, None,
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, None, n, d, qtype, muld.ptr, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None, None, None,
                               q8.ptr, 1, eps)
         want_x = x + orc.rmsnorm(y, wp)
         got_v = xo.to_array(np.float32)
     else:                    # layer 0: attn_norm only, the stream is not rewritten
-        lib.g4_mm_residual_q8(out.ptr, w.ptr, n, d, qtype, None, xd.ptr, xd.ptr, None, None, None, wnd.ptr, xb2.ptr,
+        lib.g4_mm_residual_q8(out.ptr, w.ptr, None, n, d, qtype, None, xd.ptr, xd.ptr, None, None, None, wnd.ptr, xb2.ptr,
                               q8.ptr, 0, eps)
         want_x = x
         got_v = xb2.to_array(np.float32)
@@ -345,7 +355,9 @@ def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
     lib.g4_download_q8K(q8.ptr, P(h), n)
     assert h.tobytes() == orc.quantize_q8K(got_v).tobytes()
     ref = DBuf(lib, 4 * d)
-    if mode == "ple":
+    if mode == "ffn":
+        lib.g4_mm_gate_up_gelu(ref.ptr, w.ptr, up.ptr, n, d, qtype, q8.ptr)
+    elif mode == "ple":
         lib.g4_mm_quant_dot_rows_gelu_mul(ref.ptr, w.ptr, n, d, qtype, q8.ptr, muld.ptr)
     else:
         lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
@@ -357,5 +369,5 @@ def test_mm_residual_q8_rejects_alias(lib):
     from g4 import DBuf, G4Error
     b = DBuf(lib, 4 * 4096)
     with pytest.raises(G4Error):
-        lib.g4_mm_residual_q8(b.ptr, b.ptr, 2560, 8, 12, None, b.ptr, b.ptr, b.ptr, b.ptr, None, None, None, None, 1,
+        lib.g4_mm_residual_q8(b.ptr, b.ptr, None, 2560, 8, 12, None, b.ptr, b.ptr, b.ptr, b.ptr, None, None, None, None, 1,
                               C.c_float(1e-6))
