@@ -415,76 +415,97 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
 // 32/KS rows; each row is split over KS groups (ks takes blocks ks, ks+KS,
 // ...) whose partial sums are added in LDS.  Lane L = 4h+u of a group owns
 // the 32 weights 128h + 32k + 8u + e (k < 4, e < 8) of each block: their
-// 6-bit codes are assembled four at a time into bytes of (q - 32), converted
-// to float and multiplied by x; each run of 8 is scaled once by d*sc (the
+// 6-bit codes q are assembled four at a time into bytes, converted to float
+// and multiplied by x; a run of 8 contributes sum x*q - 32 * sum x (the run
+// sums of x are computed once per workgroup) scaled once by d*sc (the
 // reference scales every weight, (d*sc)*(q-32); results agree to fp32
-// tolerance, not bit for bit).
+// tolerance, not bit for bit).  The first batch of weight loads is issued
+// before x is staged.
 template <int KS, bool SOFTCAP>
 __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                             float* __restrict__ out, int nb, int d, float cap) {
-    extern __shared__ __align__(16) float xs[];   // n floats, then [32] partials
+    // LDS: x (n floats), the sums of its runs of 8 (n/8 floats), [32] partials
+    extern __shared__ __align__(16) float xs[];
     constexpr int RPW = 32 / KS;
+    constexpr int QB = 5;                  // blocks per load batch
     const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
     const int rr = g % RPW, ks = g / RPW;
     const size_t nblk = (size_t)d * nb;
     const Q6KPlanes P = q6k_planes(nblk);
-    const int n4 = nb * 64;
-    for (int i = tid; i < n4; i += 256) reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
-    float* part = xs + nb * 256;
-    __syncthreads();
+    float* x8 = xs + nb * 256;
+    float* part = x8 + nb * 32;
     const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
     const int ngroups = (d + RPW - 1) / RPW;
-    for (int rg = blockIdx.x; rg < ngroups; rg += gridDim.x) {
+
+    struct Batch {
+        uint4 ql[QB];
+        uint2 qh[QB], sc[QB];
+        uint32_t dv[QB];
+    };
+    // this lane's blocks b0, b0+KS, ... (QB of them) of `row`
+    auto load = [&](int row, int b0, Batch& bt) {
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            const int b = b0 + i * KS;
+            if (b < nb) {
+                const size_t blk = (size_t)row * nb + b;
+                bt.ql[i] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
+                bt.qh[i] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
+                bt.sc[i] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+                bt.dv[i] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+            }
+        }
+    };
+    // the first batch of the first row group is in flight before x is staged
+    Batch bt;
+    int rg = blockIdx.x;
+    bool pre = rg < ngroups && rg * RPW + rr < d && ks < nb;
+    if (pre) load(rg * RPW + rr, ks, bt);
+    for (int i = tid; i < nb * 64; i += 256) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i];
+        reinterpret_cast<float4*>(xs)[i] = v;
+        // i covers elements 4i..4i+3; pairs of float4 make one run of 8
+        const float s4 = (v.x + v.y) + (v.z + v.w);
+        const float o4 = __shfl_xor(s4, 1, 64);
+        if ((i & 1) == 0) x8[i >> 1] = s4 + o4;
+    }
+    __syncthreads();
+    for (; rg < ngroups; rg += gridDim.x) {
         const int row = rg * RPW + rr;
         float acc = 0.0f;
         if (row < d) {
-            // this lane's blocks ks, ks+KS, ... in batches of QB: all loads of a
-            // batch are issued before any of its arithmetic
-            constexpr int QB = 5;
             for (int b0 = ks; b0 < nb; b0 += QB * KS) {
-                uint4 qlv[QB];
-                uint2 qhv[QB], scv[QB];
-                uint32_t dv[QB];
+                if (!pre) load(row, b0, bt);
+                pre = false;
 #pragma unroll
                 for (int i = 0; i < QB; i++) {
                     const int b = b0 + i * KS;
                     if (b < nb) {
-                        const size_t blk = (size_t)row * nb + b;
-                        qlv[i] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
-                        qhv[i] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
-                        scv[i] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
-                        dv[i] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < QB; i++) {
-                    const int b = b0 + i * KS;
-                    if (b < nb) {
-                        const uint4 ql = qlv[i];
-                        const uint2 qh = qhv[i], sc = scv[i];
-                        const float df = half_bits_to_f32(dv[i]);
+                        const uint4 ql = bt.ql[i];
+                        const uint2 qh = bt.qh[i], sc = bt.sc[i];
+                        const float df = half_bits_to_f32(bt.dv[i]);
                         const float* xb = xs + b * 256 + 128 * h + 8 * u;
+                        const float* sb8 = x8 + b * 32 + 16 * h + u;
 #pragma unroll
                         for (int kk = 0; kk < 4; kk++) {
                             const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
                             const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
                             const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
                             const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
-                            const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);
+                            const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);   // q in [0, 63]
                             const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
-                            // bytes q in [0,63] -> (q - 32) as int8, per byte without borrows
-                            const uint32_t sa = ((ca | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                            const uint32_t sb = ((cb | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
                             const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
                             const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
-                            float dot = x0.x * (float)(int8_t)(sa & 0xff);
-                            dot = __builtin_fmaf(x0.y, (float)(int8_t)((sa >> 8) & 0xff), dot);
-                            dot = __builtin_fmaf(x0.z, (float)(int8_t)((sa >> 16) & 0xff), dot);
-                            dot = __builtin_fmaf(x0.w, (float)(int8_t)(sa >> 24), dot);
-                            dot = __builtin_fmaf(x1.x, (float)(int8_t)(sb & 0xff), dot);
-                            dot = __builtin_fmaf(x1.y, (float)(int8_t)((sb >> 8) & 0xff), dot);
-                            dot = __builtin_fmaf(x1.z, (float)(int8_t)((sb >> 16) & 0xff), dot);
-                            dot = __builtin_fmaf(x1.w, (float)(int8_t)(sb >> 24), dot);
+                            // sum_e x_e (q_e - 32) = sum_e x_e q_e - 32 * sum_e x_e
+                            float dot = x0.x * (float)(ca & 0xff);
+                            dot = __builtin_fmaf(x0.y, (float)((ca >> 8) & 0xff), dot);
+                            dot = __builtin_fmaf(x0.z, (float)((ca >> 16) & 0xff), dot);
+                            dot = __builtin_fmaf(x0.w, (float)(ca >> 24), dot);
+                            dot = __builtin_fmaf(x1.x, (float)(cb & 0xff), dot);
+                            dot = __builtin_fmaf(x1.y, (float)((cb >> 8) & 0xff), dot);
+                            dot = __builtin_fmaf(x1.z, (float)((cb >> 16) & 0xff), dot);
+                            dot = __builtin_fmaf(x1.w, (float)(cb >> 24), dot);
+                            dot = __builtin_fmaf(-32.0f, sb8[4 * kk], dot);
                             const int sbi = (u >> 1) + 2 * kk;
                             const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
                             acc = __builtin_fmaf(df * (float)s8, dot, acc);
@@ -593,7 +614,7 @@ void launch_q6_ks(const void* w, const float* x, float* o, int nb, int d, float 
     const int ngroups = (d + 32 / KS - 1) / (32 / KS);
     int grid = 4 * g4_num_cus();
     if (grid > ngroups) grid = ngroups;
-    const size_t lds = (size_t)nb * 1024 + 32 * 4;
+    const size_t lds = (size_t)nb * 1024 + (size_t)nb * 128 + 32 * 4;
     hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP>), dim3(grid), dim3(256), lds, g4_stream(),
                        (const uint8_t*)w, x, o, nb, d, cap);
 }
