@@ -177,6 +177,13 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
 // workgroup 0 also stores it to q8 -- the reference's mm() side effect.
 // aux (nullable, NMAT == 1): epilogue out = gelu(r) * aux[row]
 // (main.c:1989-1993).
+// a second tensor stacked under the first (same type and n, own output)
+struct Stack2 {
+    const uint8_t* w;
+    float* out;
+    int d;
+};
+
 template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, bool PRO = false>
 __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
@@ -184,7 +191,8 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                                                            int nb_rt, int d, int32_t* __restrict__ dbgS,
                                                            int32_t* __restrict__ dbgM, const float* __restrict__ xin,
                                                            uint8_t* __restrict__ q8_store,
-                                                           const float* __restrict__ aux, const ResidualArgs ra) {
+                                                           const float* __restrict__ aux, const ResidualArgs ra,
+                                                           const Stack2 st) {
     static_assert(!QIN || WG == 64, "the single-block input path runs one wave");
     static_assert(!PRO || (WG == 256 && NB > 0 && !DBG), "the prologue needs 256 threads and a fixed row length");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
@@ -192,9 +200,15 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
     const int nb = NB > 0 ? NB : nb_rt;
     const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
     const int row_ = blockIdx.x * (WG / GL) + tid / GL;
-    // with the prologue every thread stays for its barriers; rows past d
-    // compute row d-1 and do not store
-    const int row = PRO ? min(row_, d - 1) : row_;
+    // with the prologue every thread stays for its barriers; rows past the
+    // end compute the last row and do not store.  Rows d.. d+st.d-1 (PRO
+    // only) belong to the stacked second tensor.
+    const int dtot = d + (PRO ? st.d : 0);
+    const int row = PRO ? min(row_, dtot - 1) : row_;
+    const bool sec = PRO && row >= d;
+    const int dl = sec ? st.d : d, rl = sec ? row - d : row;
+    const uint8_t* const wa = sec ? st.w : w0;
+    float* const outp = sec ? st.out : out;
     if (QIN) {
         __shared__ __align__(16) uint8_t q8s[292];
         const float4 f = reinterpret_cast<const float4*>(xin)[tid];
@@ -205,10 +219,10 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
         q8 = q8s;
     }
     if (!PRO && row >= d) return;   // whole rows (groups of GL lanes) leave together
-    const uint32_t nblk = (uint32_t)d * (uint32_t)nb;
+    const uint32_t nblk = (uint32_t)dl * (uint32_t)nb;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
     const uint32_t qh_off = 128u * nblk;
-    const uint32_t rb = (uint32_t)row * (uint32_t)nb;            // first block of the row
+    const uint32_t rb = (uint32_t)rl * (uint32_t)nb;             // first block of the row
     const uint8_t* a_qs = q8 + 32 * l;
     const uint8_t* a_bs = q8 + q8k_bsums_off(nb) + 8 * k;
     const float* a_d = reinterpret_cast<const float*>(q8 + q8k_d_off(nb));
@@ -230,7 +244,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
         const uint32_t blk = rb + (uint32_t)b;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const uint8_t* base = m ? w1 : w0;
+            const uint8_t* base = m ? w1 : wa;
             r.wq[m] = *reinterpret_cast<const uint4*>(base + blk * 128u + 16 * l);
             r.hd[m] = *reinterpret_cast<const uint4*>(base + hdr_off + blk * 16u);
             r.qh[m] = Q5 ? *reinterpret_cast<const uint32_t*>(base + qh_off + blk * 32u + 4 * l) : 0u;
@@ -402,9 +416,9 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             r[m] = h + hm;
         }
     }
-    if (l == 0 && grp == 0 && row_ < d) {
-        if (NMAT == 2) out[row] = gelu_ref(r[0]) * r[NMAT - 1];
-        else out[row] = aux ? gelu_ref(r[0]) * aux[row] : r[0];
+    if (l == 0 && grp == 0 && row_ < dtot) {
+        if (NMAT == 2) outp[rl] = gelu_ref(r[0]) * r[NMAT - 1];
+        else outp[rl] = aux ? gelu_ref(r[0]) * aux[rl] : r[0];
     }
 }
 
@@ -570,25 +584,28 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
     constexpr int rows_per_wg = 8 / SPLIT;
     hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT, QIN>), dim3((d + rows_per_wg - 1) / rows_per_wg),
                        dim3(64), 0, g4_stream(), (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)q8, o, nb, d,
-                       S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{});
+                       S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{}, Stack2{});
 }
 
 // residual step + norm + Q8_K as the prologue of every workgroup (256
 // threads: four waves of 8/SPLIT rows each)
 template <bool Q5, int NMAT, int NB>
-void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra) {
+void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
+                    const Stack2& st) {
     constexpr int SPLIT = NMAT == 2 ? 4 : 2;
     constexpr int rows_per_wg = 4 * 8 / SPLIT;
+    const int rows = d + st.d;
     const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15);
     hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, 256, true>),
-                       dim3((d + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, g4_stream(), (const uint8_t*)w,
-                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra);
+                       dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, g4_stream(), (const uint8_t*)w,
+                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st);
 }
 
 template <bool Q5, int NB>
-void launch_q45_pro_nm(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra) {
-    if (w2) launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra);
-    else launch_q45_pro<Q5, 1, NB>(w, nullptr, o, d, aux, ra);
+void launch_q45_pro_nm(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
+                       const Stack2& st) {
+    if (w2) launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra, st);
+    else launch_q45_pro<Q5, 1, NB>(w, nullptr, o, d, aux, ra, st);
 }
 
 // rows of nb blocks; the split of a row over lane groups grows with the work
@@ -770,6 +787,31 @@ extern "C" int g4_debug_block_sums(const void* w, int n, int d, int type, const 
     return g4_fail(G4_ERR_TYPE, "g4_debug_block_sums: type %d not supported", type);
 }
 
+static int mm_residual(const char* who, float* o, const void* w, const void* w2, int n, int d, int type,
+                       const float* mul, const Stack2& st, const float* x, float* x_out, const float* y,
+                       const float* w_post, const float* oscale, const float* w_next, float* xb2, void* q8, int qsrc,
+                       float eps) {
+    int rc = check_gemv(who, o, w, x, n, d);
+    if (rc) return rc;
+    G4_CHECK_ARG(!w2 || (aligned16(w2) && !mul), "%s: bad w2 (16-byte aligned, no mul)", who);
+    G4_CHECK_ARG(!y || w_post, "%s: y without w_post", who);
+    G4_CHECK_ARG(qsrc == 1 || w_next, "%s: quantizing the normed vector needs w_next", who);
+    G4_CHECK_ARG(!(y && x_out == x), "%s: x_out must not alias x when y is given", who);
+    G4_CHECK_ARG(!(y && xb2 == y), "%s: xb2 must not alias y", who);
+    G4_CHECK_ARG(!q8 || aligned16(q8), "%s: q8 must be 16-byte aligned", who);
+    ResidualArgs ra{x, x_out, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    const int nb = n / 256;
+    const bool q5 = type == G4_Q5_K;
+    if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "%s: type %d not supported", who, type);
+    switch (nb) {
+    case 8: q5 ? launch_q45_pro_nm<true, 8>(w, w2, o, d, mul, ra, st) : launch_q45_pro_nm<false, 8>(w, w2, o, d, mul, ra, st); break;
+    case 10: q5 ? launch_q45_pro_nm<true, 10>(w, w2, o, d, mul, ra, st) : launch_q45_pro_nm<false, 10>(w, w2, o, d, mul, ra, st); break;
+    case 16: q5 ? launch_q45_pro_nm<true, 16>(w, w2, o, d, mul, ra, st) : launch_q45_pro_nm<false, 16>(w, w2, o, d, mul, ra, st); break;
+    default: return g4_fail(G4_ERR_ARG, "%s: n=%d (2048, 2560 or 4096)", who, n);
+    }
+    return g4_check_launch("gemv_q45_rows_kernel<prologue>");
+}
+
 // g4_residual_norm (with the residual stream read from x and written to
 // x_out) followed by mm_quant_dot_rows on its Q8_K, in one launch: every
 // workgroup computes the norm and the Q8_K itself (into LDS) while its weight
@@ -778,23 +820,18 @@ extern "C" int g4_debug_block_sums(const void* w, int n, int d, int type, const 
 extern "C" int g4_mm_residual_q8(float* o, const void* w, const void* w2, int n, int d, int type, const float* mul,
                                  const float* x, float* x_out, const float* y, const float* w_post,
                                  const float* oscale, const float* w_next, float* xb2, void* q8, int qsrc, float eps) {
-    int rc = check_gemv("g4_mm_residual_q8", o, w, x, n, d);
-    if (rc) return rc;
-    G4_CHECK_ARG(!w2 || (aligned16(w2) && !mul), "g4_mm_residual_q8: bad w2 (16-byte aligned, no mul)");
-    G4_CHECK_ARG(!y || w_post, "g4_mm_residual_q8: y without w_post");
-    G4_CHECK_ARG(qsrc == 1 || w_next, "g4_mm_residual_q8: quantizing the normed vector needs w_next");
-    G4_CHECK_ARG(!(y && x_out == x), "g4_mm_residual_q8: x_out must not alias x when y is given");
-    G4_CHECK_ARG(!(y && xb2 == y), "g4_mm_residual_q8: xb2 must not alias y");
-    G4_CHECK_ARG(!q8 || aligned16(q8), "g4_mm_residual_q8: q8 must be 16-byte aligned");
-    ResidualArgs ra{x, x_out, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
-    const int nb = n / 256;
-    const bool q5 = type == G4_Q5_K;
-    if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "g4_mm_residual_q8: type %d not supported", type);
-    switch (nb) {
-    case 8: q5 ? launch_q45_pro_nm<true, 8>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 8>(w, w2, o, d, mul, ra); break;
-    case 10: q5 ? launch_q45_pro_nm<true, 10>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 10>(w, w2, o, d, mul, ra); break;
-    case 16: q5 ? launch_q45_pro_nm<true, 16>(w, w2, o, d, mul, ra) : launch_q45_pro_nm<false, 16>(w, w2, o, d, mul, ra); break;
-    default: return g4_fail(G4_ERR_ARG, "g4_mm_residual_q8: n=%d (2048, 2560 or 4096)", n);
-    }
-    return g4_check_launch("gemv_q45_rows_kernel<prologue>");
+    return mm_residual("g4_mm_residual_q8", o, w, w2, n, d, type, mul, Stack2{}, x, x_out, y, w_post, oscale, w_next,
+                       xb2, q8, qsrc, eps);
+}
+
+// The same with a second, independent GEMV of the same type and n on the
+// same Q8_K in the same launch (e.g. the Q and K projections): o1 = W1.q8
+// (d1 rows), o2 = W2.q8 (d2 rows).
+extern "C" int g4_mm_residual_q8_pair(float* o1, const void* w1, int d1, float* o2, const void* w2, int d2, int n,
+                                      int type, const float* x, float* x_out, const float* y, const float* w_post,
+                                      const float* oscale, const float* w_next, float* xb2, void* q8, int qsrc,
+                                      float eps) {
+    G4_CHECK_ARG(o2 && w2 && aligned16(w2) && d2 > 0, "g4_mm_residual_q8_pair: bad second tensor");
+    return mm_residual("g4_mm_residual_q8_pair", o1, w1, nullptr, n, d1, type, nullptr,
+                       Stack2{(const uint8_t*)w2, o2, d2}, x, x_out, y, w_post, oscale, w_next, xb2, q8, qsrc, eps);
 }

@@ -633,7 +633,15 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
         const float *y = l ? m->ybuf : NULL, *w_post = l ? m->post_norm[l - 1] : NULL;
         const float *osc = l ? m->out_scale[l - 1] : NULL;
         int rc;
-        if (pro_ok(c, &m->wq[l])) {
+        const int src = kv_source(c, l), has_kv = layer_has_kv(l);
+        /* K rides in the Q launch when it has Q's type */
+        const int k_pair = has_kv && pro_ok(c, &m->wq[l]) && m->wk[l].type == m->wq[l].type;
+        if (k_pair) {
+            CK(g4_mm_residual_q8_pair(m->q, m->wq[l].p, m->wq[l].d, m->k, m->wk[l].p, m->wk[l].d, m->wq[l].n,
+                                      m->wq[l].type, x, y ? xo : x, y, w_post, osc, m->attn_norm[l], m->xb2, m->q8, 0,
+                                      c->eps));
+            if (y) { float *t = x; x = xo; xo = t; }
+        } else if (pro_ok(c, &m->wq[l])) {
             CK(g4_mm_residual_q8(m->q, m->wq[l].p, NULL, m->wq[l].n, m->wq[l].d, m->wq[l].type, NULL, x, y ? xo : x, y,
                                  w_post, osc, m->attn_norm[l], m->xb2, m->q8, 0, c->eps));
             if (y) { float *t = x; x = xo; xo = t; }
@@ -642,11 +650,10 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
             if ((rc = mm(m, m->q, m->xb2, &m->wq[l], q8_att))) return rc;
         }
         if (m->trace && l > 0) CK(g4_memcpy_d2h(m->layer_x + (size_t)l * dim, x, (size_t)dim * 4));
-        const int src = kv_source(c, l), has_kv = layer_has_kv(l);
         if (has_kv) {
             if (is_q8_type(m->wk[l].type) != q8_att && is_q8_type(m->wk[l].type))
                 CK(g4_quantize_row_q8_K(m->xb2, m->q8, dim));
-            if ((rc = mm(m, m->k, m->xb2, &m->wk[l], 1))) return rc;
+            if (!k_pair && (rc = mm(m, m->k, m->xb2, &m->wk[l], 1))) return rc;
             if ((rc = mm(m, m->v, m->xb2, &m->wv[l], 1))) return rc;
         }
         /* q_norm + RoPE, K/V norm + RoPE + append (main.c:1886-1904) and the

@@ -136,6 +136,12 @@ int g4_set_gemv_occupancy(int wg_per_cu);
 int g4_mm_residual_q8(float *o, const void *w, const void *w2, int n, int d, int type, const float *mul,
                       const float *x, float *x_out, const float *y, const float *w_post, const float *oscale,
                       const float *w_next, float *xb2, void *q8, int qsrc, float eps);
+/* g4_mm_residual_q8 with two independent GEMVs of the same type and n on
+ * the one Q8_K (e.g. the Q and K projections of a layer, main.c:1883-1891):
+ * o1 = W1 . Q8_K (d1 rows), o2 = W2 . Q8_K (d2 rows), one launch. */
+int g4_mm_residual_q8_pair(float *o1, const void *w1, int d1, float *o2, const void *w2, int d2, int n, int type,
+                           const float *x, float *x_out, const float *y, const float *w_post, const float *oscale,
+                           const float *w_next, float *xb2, void *q8, int qsrc, float eps);
 
 /* ---------------------------------------------------------------------------
  * Batched prefill GEMM.  The reference has none: generate() runs forward()

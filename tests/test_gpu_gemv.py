@@ -371,3 +371,29 @@ def test_mm_residual_q8_rejects_alias(lib):
     with pytest.raises(G4Error):
         lib.g4_mm_residual_q8(b.ptr, b.ptr, None, 2560, 8, 12, None, b.ptr, b.ptr, b.ptr, b.ptr, None, None, None, None, 1,
                               C.c_float(1e-6))
+
+
+@pytest.mark.parametrize("qtype,d1,d2", [(12, 2048, 512), (13, 200, 70), (12, 4096, 1024)])
+def test_mm_residual_q8_pair(lib, orc, qtype, d1, d2):
+    """Two GEMVs stacked in one prologue launch (Q and K): each output equal,
+    bit for bit, to mm_quant_dot_rows on the stored Q8_K."""
+    from g4 import DBuf, upload_quant
+    n = 2560
+    rng = np.random.default_rng(d1 + d2 + qtype)
+    r1, r2 = synth.rand_kquant(rng, qtype, d1, n), synth.rand_kquant(rng, qtype, d2, n)
+    w1, w2 = upload_quant(lib, r1, qtype, n, d1), upload_quant(lib, r2, qtype, n, d2)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = (rng.standard_normal(n) * 4).astype(np.float32)
+    wp = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    xd, yd, wpd, wnd = (DBuf.from_array(lib, a) for a in (x, y, wp, wn))
+    xo, xb2, o1, o2 = DBuf(lib, 4 * n), DBuf(lib, 4 * n), DBuf(lib, 4 * d1), DBuf(lib, 4 * d2)
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(n))
+    lib.g4_mm_residual_q8_pair(o1.ptr, w1.ptr, d1, o2.ptr, w2.ptr, d2, n, qtype, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None,
+                               wnd.ptr, xb2.ptr, q8.ptr, 0, C.c_float(1e-6))
+    assert rel_err(xo.to_array(np.float32), x + orc.rmsnorm(y, wp)) < 2e-6
+    for o, w, d in ((o1, w1, d1), (o2, w2, d2)):
+        ref = DBuf(lib, 4 * d)
+        lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
+        g, r = o.to_array(np.float32), ref.to_array(np.float32)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (d, np.flatnonzero(g != r)[:8])
