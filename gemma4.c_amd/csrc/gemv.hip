@@ -177,12 +177,105 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
 // workgroup 0 also stores it to q8 -- the reference's mm() side effect.
 // aux (nullable, NMAT == 1): epilogue out = gelu(r) * aux[row]
 // (main.c:1989-1993).
-// a second tensor stacked under the first (same type and n, own output)
+// a second tensor stacked under the first (same type and n, own output),
+// and (prologue kernels) a Q6_K tensor taking the fp32 normed vector the
+// prologue leaves in LDS, as mm_quant_rows does (main.c:1539-1556)
 struct Stack2 {
     const uint8_t* w;
     float* out;
     int d;
+    const uint8_t* w6;
+    float* out6;
+    int d6;
 };
+constexpr int kKs6 = 2;                 // Q6_K row split inside a prologue kernel
+constexpr int kRows6 = 32 / kKs6;       // Q6_K rows per 256-thread workgroup
+
+// Q6_K rows of a prologue kernel's workgroup vb: 256 threads, kRows6 rows x
+// kKs6 slices, x = the fp32 vector the prologue leaves in pbuf; same lane
+// mapping and arithmetic as gemv_q6k_rows_kernel (below).  The weight loads
+// are issued before the prologue's arithmetic.
+template <int NB>
+__device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, const ResidualArgs& ra,
+                                                  ResidualRegs<NB>& rr, float* pbuf, float* red) {
+    constexpr int QB = (NB + kKs6 - 1) / kKs6;
+    const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
+    const int rr6 = g % kRows6, ks = g / kRows6;
+    const int row_ = vb * kRows6 + rr6, row = min(row_, st.d6 - 1);
+    const Q6KPlanes P = q6k_planes((size_t)st.d6 * NB);
+    uint4 qlv[QB];
+    uint2 qhv[QB], scv[QB];
+    uint32_t dv[QB];
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+        const int b = ks + i * kKs6;
+        if (b < NB) {
+            const size_t blk = (size_t)row * NB + b;
+            qlv[i] = *reinterpret_cast<const uint4*>(st.w6 + P.ql + blk * 128 + 16 * L);
+            qhv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.qh + blk * 64 + 8 * L);
+            scv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.sc + blk * 16 + 8 * h);
+            dv[i] = *reinterpret_cast<const uint16_t*>(st.w6 + P.d + blk * 2);
+        }
+    }
+    residual_finish<NB>(ra, rr, pbuf, red, false);
+    __syncthreads();
+    // sums of the runs of 8 of x
+    float* x8 = pbuf + NB * 256 + ((NB * 292 + 15) & ~15) / 4;
+    for (int i = tid; i < NB * 32; i += blockDim.x) {
+        const float4 a = reinterpret_cast<const float4*>(pbuf)[2 * i];
+        const float4 b = reinterpret_cast<const float4*>(pbuf)[2 * i + 1];
+        x8[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+        const int b = ks + i * kKs6;
+        if (b < NB) {
+            const uint4 ql = qlv[i];
+            const uint2 qh = qhv[i], sc = scv[i];
+            const float df = half_bits_to_f32(dv[i]);
+            const float* xb = pbuf + b * 256 + 128 * h + 8 * u;
+            const float* sb8 = x8 + b * 32 + 16 * h + u;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const uint32_t qa = (kk & 1) ? ql.z : ql.x;
+                const uint32_t qb = (kk & 1) ? ql.w : ql.y;
+                const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+                const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+                const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);
+                const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
+                const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
+                const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
+                float dot = x0.x * (float)(ca & 0xff);
+                dot = __builtin_fmaf(x0.y, (float)((ca >> 8) & 0xff), dot);
+                dot = __builtin_fmaf(x0.z, (float)((ca >> 16) & 0xff), dot);
+                dot = __builtin_fmaf(x0.w, (float)(ca >> 24), dot);
+                dot = __builtin_fmaf(x1.x, (float)(cb & 0xff), dot);
+                dot = __builtin_fmaf(x1.y, (float)((cb >> 8) & 0xff), dot);
+                dot = __builtin_fmaf(x1.z, (float)((cb >> 16) & 0xff), dot);
+                dot = __builtin_fmaf(x1.w, (float)(cb >> 24), dot);
+                dot = __builtin_fmaf(-32.0f, sb8[4 * kk], dot);
+                const int sbi = (u >> 1) + 2 * kk;
+                const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
+                acc = __builtin_fmaf(df * (float)s8, dot, acc);
+            }
+        }
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 4, 64);
+    float* part = x8 + NB * 32;
+    if (L == 0) part[g] = acc;
+    __syncthreads();
+    if (tid < kRows6) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kKs6; j++) s += part[j * kRows6 + tid];
+        if (vb * kRows6 + tid < st.d6) st.out6[vb * kRows6 + tid] = s;
+    }
+    (void)row_;
+}
 
 template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, bool PRO = false>
 __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
@@ -320,17 +413,27 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             // by the whole workgroup into LDS (workgroup 0 also stores x_out,
             // xb2 and q8), then read from LDS.  The step's small loads go
             // first, the weight loads behind them, so the norm's arithmetic
-            // waits only for the former
+            // waits only for the former.  Workgroups past the K-quant rows
+            // take the Q6_K tensor (st.w6) on the fp32 normed vector.
+            constexpr int rpw = WG / GL;
+            const int qk_wgs = (dtot + rpw - 1) / rpw;
+            const bool vwg = st.w6 != nullptr && (int)blockIdx.x >= qk_wgs;
             ResidualRegs<NB> rr;
             residual_load<NB>(ra, rr);
+            if (!vwg) {
 #pragma unroll
-            for (int i = 0; i < NH; i++) {
-                const int b = grp * NH + i;
-                if (b < nb) load_w(b, raw[i]);
+                for (int i = 0; i < NH; i++) {
+                    const int b = grp * NH + i;
+                    if (b < nb) load_w(b, raw[i]);
+                }
             }
-            extern __shared__ __align__(16) float pbuf[];   // NB*256 floats, then the Q8_K blocks
+            extern __shared__ __align__(16) float pbuf[];   // NB*256 floats, the Q8_K blocks, [Q6_K: run sums]
             __shared__ float red[16];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf + NB * 256);
+            if (vwg) {
+                q6k_prologue_rows<NB>(st, blockIdx.x - qk_wgs, ra, rr, pbuf, red);
+                return;
+            }
             residual_finish<NB>(ra, rr, pbuf, red, blockIdx.x == 0);
             __syncthreads();
             quantize_blocks_wg(pbuf, q8l, NB);
@@ -595,9 +698,11 @@ void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float*
     constexpr int SPLIT = NMAT == 2 ? 4 : 2;
     constexpr int rows_per_wg = 4 * 8 / SPLIT;
     const int rows = d + st.d;
-    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15);
+    // x, Q8_K, and for a Q6_K tensor the run sums of x and 32 partials
+    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15) + (size_t)NB * 32 * 4 + 32 * 4;
+    const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + kRows6 - 1) / kRows6 : 0);
     hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, 256, true>),
-                       dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(256), lds, g4_stream(), (const uint8_t*)w,
+                       dim3(wgs), dim3(256), lds, g4_stream(), (const uint8_t*)w,
                        (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st);
 }
 
@@ -833,5 +938,20 @@ extern "C" int g4_mm_residual_q8_pair(float* o1, const void* w1, int d1, float* 
                                       float eps) {
     G4_CHECK_ARG(o2 && w2 && aligned16(w2) && d2 > 0, "g4_mm_residual_q8_pair: bad second tensor");
     return mm_residual("g4_mm_residual_q8_pair", o1, w1, nullptr, n, d1, type, nullptr,
-                       Stack2{(const uint8_t*)w2, o2, d2}, x, x_out, y, w_post, oscale, w_next, xb2, q8, qsrc, eps);
+                       Stack2{(const uint8_t*)w2, o2, d2, nullptr, nullptr, 0}, x, x_out, y, w_post, oscale, w_next,
+                       xb2, q8, qsrc, eps);
+}
+
+// ... and a third, Q6_K GEMV on the fp32 normed vector (mm_quant_rows,
+// main.c:1539-1556): the Q, K and V projections of a layer in one launch.
+extern "C" int g4_mm_residual_q8_qkv(float* o1, const void* w1, int d1, float* o2, const void* w2, int d2, float* o3,
+                                     const void* w3, int d3, int type3, int n, int type, const float* x, float* x_out,
+                                     const float* y, const float* w_post, const float* oscale, const float* w_next,
+                                     float* xb2, void* q8, float eps) {
+    G4_CHECK_ARG(o2 && w2 && aligned16(w2) && d2 > 0, "g4_mm_residual_q8_qkv: bad second tensor");
+    G4_CHECK_ARG(o3 && w3 && aligned16(w3) && d3 > 0, "g4_mm_residual_q8_qkv: bad third tensor");
+    if (type3 != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_residual_q8_qkv: third tensor type %d (Q6_K only)", type3);
+    return mm_residual("g4_mm_residual_q8_qkv", o1, w1, nullptr, n, d1, type, nullptr,
+                       Stack2{(const uint8_t*)w2, o2, d2, (const uint8_t*)w3, o3, d3}, x, x_out, y, w_post, oscale,
+                       w_next, xb2, q8, 0, eps);
 }

@@ -60,6 +60,7 @@ _SIGS = {
     "g4_set_gemv_occupancy": (I, [I]),
     "g4_mm_residual_q8": (I, [VP, VP, VP, I, I, I, VP, VP, VP, VP, VP, VP, VP, VP, VP, I, F]),
     "g4_mm_residual_q8_pair": (I, [VP, VP, I, VP, VP, I, I, I, VP, VP, VP, VP, VP, VP, VP, VP, I, F]),
+    "g4_mm_residual_q8_qkv": (I, [VP, VP, I, VP, VP, I, VP, VP, I, I, I, I, VP, VP, VP, VP, VP, VP, VP, VP, F]),
     "g4_q8K_row_stride": (SZ, [I]),
     "g4_quantize_rows_q8_K": (I, [VP, VP, I, I]),
     "g4_mm_batch_q8": (I, [VP, VP, VP, I, I, I, I]),

@@ -634,9 +634,16 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
         const float *osc = l ? m->out_scale[l - 1] : NULL;
         int rc;
         const int src = kv_source(c, l), has_kv = layer_has_kv(l);
-        /* K rides in the Q launch when it has Q's type */
+        /* K rides in the Q launch when it has Q's type, and V with them when it
+         * is Q6_K (fp32 path on the normed vector) */
         const int k_pair = has_kv && pro_ok(c, &m->wq[l]) && m->wk[l].type == m->wq[l].type;
-        if (k_pair) {
+        const int v_too = k_pair && m->wv[l].type == G4_Q6_K;
+        if (v_too) {
+            CK(g4_mm_residual_q8_qkv(m->q, m->wq[l].p, m->wq[l].d, m->k, m->wk[l].p, m->wk[l].d, m->v, m->wv[l].p,
+                                     m->wv[l].d, m->wv[l].type, m->wq[l].n, m->wq[l].type, x, y ? xo : x, y, w_post, osc,
+                                     m->attn_norm[l], m->xb2, m->q8, c->eps));
+            if (y) { float *t = x; x = xo; xo = t; }
+        } else if (k_pair) {
             CK(g4_mm_residual_q8_pair(m->q, m->wq[l].p, m->wq[l].d, m->k, m->wk[l].p, m->wk[l].d, m->wq[l].n,
                                       m->wq[l].type, x, y ? xo : x, y, w_post, osc, m->attn_norm[l], m->xb2, m->q8, 0,
                                       c->eps));
@@ -654,7 +661,7 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
             if (is_q8_type(m->wk[l].type) != q8_att && is_q8_type(m->wk[l].type))
                 CK(g4_quantize_row_q8_K(m->xb2, m->q8, dim));
             if (!k_pair && (rc = mm(m, m->k, m->xb2, &m->wk[l], 1))) return rc;
-            if ((rc = mm(m, m->v, m->xb2, &m->wv[l], 1))) return rc;
+            if (!v_too && (rc = mm(m, m->v, m->xb2, &m->wv[l], 1))) return rc;
         }
         /* q_norm + RoPE, K/V norm + RoPE + append (main.c:1886-1904) and the
          * attention over the source layer's cache (main.c:1909-1950, attn_scale

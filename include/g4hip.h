@@ -142,6 +142,14 @@ int g4_mm_residual_q8(float *o, const void *w, const void *w2, int n, int d, int
 int g4_mm_residual_q8_pair(float *o1, const void *w1, int d1, float *o2, const void *w2, int d2, int n, int type,
                            const float *x, float *x_out, const float *y, const float *w_post, const float *oscale,
                            const float *w_next, float *xb2, void *q8, int qsrc, float eps);
+/* ... plus a third tensor of type Q6_K (w3, d3 rows) on the fp32 normed
+ * vector (xb2), as mm routes Q6_K to mm_quant_rows (main.c:1687-1689): the
+ * Q, K and V projections of a layer (main.c:1883-1892) in one launch.
+ * Requires w_next (the vector is the normed one). */
+int g4_mm_residual_q8_qkv(float *o1, const void *w1, int d1, float *o2, const void *w2, int d2, float *o3,
+                          const void *w3, int d3, int type3, int n, int type, const float *x, float *x_out,
+                          const float *y, const float *w_post, const float *oscale, const float *w_next, float *xb2,
+                          void *q8, float eps);
 
 /* ---------------------------------------------------------------------------
  * Batched prefill GEMM.  The reference has none: generate() runs forward()

@@ -397,3 +397,42 @@ def test_mm_residual_q8_pair(lib, orc, qtype, d1, d2):
         lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
         g, r = o.to_array(np.float32), ref.to_array(np.float32)
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (d, np.flatnonzero(g != r)[:8])
+
+
+@pytest.mark.parametrize("qtype,d1,d2,d3", [(12, 2048, 512, 512), (13, 200, 70, 90), (12, 4096, 1024, 1024)])
+def test_mm_residual_q8_qkv(lib, orc, qtype, d1, d2, d3):
+    """Q, K (K-quant, stacked) and V (Q6_K on the fp32 normed vector) in one
+    prologue launch: Q and K bit-exact against mm_quant_dot_rows on the stored
+    Q8_K; V against the oracle's mm_quant_rows on the stored normed vector
+    to 1e-5 of sum |w*x|."""
+    from g4 import DBuf, upload_quant
+    n = 2560
+    rng = np.random.default_rng(d1 + d2 + d3 + qtype)
+    r1, r2 = synth.rand_kquant(rng, qtype, d1, n), synth.rand_kquant(rng, qtype, d2, n)
+    r3 = synth.rand_q6K(rng, d3, n)
+    w1, w2, w3 = upload_quant(lib, r1, qtype, n, d1), upload_quant(lib, r2, qtype, n, d2), upload_quant(lib, r3, 14, n, d3)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = (rng.standard_normal(n) * 4).astype(np.float32)
+    wp = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    osc = np.array([0.9], np.float32)
+    xd, yd, wpd, wnd, od = (DBuf.from_array(lib, a) for a in (x, y, wp, wn, osc))
+    xo, xb2 = DBuf(lib, 4 * n), DBuf(lib, 4 * n)
+    o1, o2, o3 = DBuf(lib, 4 * d1), DBuf(lib, 4 * d2), DBuf(lib, 4 * d3)
+    q8 = DBuf(lib, lib.L.g4_q8K_bytes(n))
+    lib.g4_mm_residual_q8_qkv(o1.ptr, w1.ptr, d1, o2.ptr, w2.ptr, d2, o3.ptr, w3.ptr, d3, 14, n, qtype, xd.ptr, xo.ptr,
+                              yd.ptr, wpd.ptr, od.ptr, wnd.ptr, xb2.ptr, q8.ptr, C.c_float(1e-6))
+    want_x = (x + orc.rmsnorm(y, wp)) * osc[0]
+    assert rel_err(xo.to_array(np.float32), want_x) < 2e-6
+    xb = xb2.to_array(np.float32)
+    assert rel_err(xb, orc.rmsnorm(want_x, wn)) < 4e-6
+    for o, w, d in ((o1, w1, d1), (o2, w2, d2)):
+        ref = DBuf(lib, 4 * d)
+        lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
+        g, r = o.to_array(np.float32), ref.to_array(np.float32)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (d, np.flatnonzero(g != r)[:8])
+    want = orc.mm_quant_rows(xb, r3, n, d3, 14)
+    W = np.abs(kq.dequant_f64(r3.reshape(-1, 210), 14).reshape(d3, n))
+    mag = W @ np.abs(xb.astype(np.float64))
+    err = np.abs(o3.to_array(np.float32).astype(np.float64) - want) / mag
+    assert err.max() <= 1e-5, err.max()
