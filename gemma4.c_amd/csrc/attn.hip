@@ -230,12 +230,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const int pos = t0 + nwin - 1;
     const int tl = pos - cb;                              // pos inside this chunk
     const bool owner = a.kraw != nullptr && cnt > 0 && tl >= 0 && tl < cnt;
+    // cache slot of chunk position i (one modulo per workgroup: the chunk is
+    // shorter than the ring, so it wraps at most once)
+    const int s0 = attn_slot(a, cb);
+    auto slot_of = [&](int i) {
+        const int sl_ = s0 + i;
+        return (a.ring > 0 && sl_ >= a.ring) ? sl_ - a.ring : sl_;
+    };
     // K rows of positions it+sub, it+16+sub (phase 1) and V rows of positions
     // it+wave+4u (phase 3); the first ones are issued before q is staged
     float4 ka[KPL], kb[KPL];
     auto load_k = [&](int it) {
-        const float4* ra = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(it + sub, cnt - 1)) * a.kv_stride);
-        const float4* rb = reinterpret_cast<const float4*>(kbase + (size_t)attn_slot(a, cb + min(it + 16 + sub, cnt - 1)) * a.kv_stride);
+        const float4* ra = reinterpret_cast<const float4*>(kbase + (size_t)slot_of(min(it + sub, cnt - 1)) * a.kv_stride);
+        const float4* rb = reinterpret_cast<const float4*>(kbase + (size_t)slot_of(min(it + 16 + sub, cnt - 1)) * a.kv_stride);
 #pragma unroll
         for (int k = 0; k < KPL; k++) ka[k] = ra[sl + 16 * k];
 #pragma unroll
@@ -247,7 +254,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < VU; u++) {
             const int t = min(it + wave + 4 * u, cnt - 1);
-            const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)attn_slot(a, cb + t) * a.kv_stride);
+            const float4* vr = reinterpret_cast<const float4*>(vbase + (size_t)slot_of(t) * a.kv_stride);
 #pragma unroll
             for (int k = 0; k < VPL; k++) vv[u][k] = vr[lane + 64 * k];
         }
