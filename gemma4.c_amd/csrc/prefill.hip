@@ -75,9 +75,12 @@ __device__ __forceinline__ float hbits_to_f32(uint32_t h) {
     return (float)v;
 }
 
-// RW row waves x TW token waves; each wave owns 16 rows x NT 16-token tiles
-template <bool Q5, int RW, int TW, int NT>
-__global__ __launch_bounds__(64 * RW * TW) void mm_batch_kq_kernel(const uint8_t* __restrict__ w,
+// RW row waves x TW token waves; each wave owns 16 rows x NT 16-token tiles.
+// At least WPE waves per SIMD caps the VGPRs at 512 / WPE: at 256 or fewer the
+// compiler writes the matrix-core results straight to VGPRs instead of going
+// through accumulation registers (a v_accvgpr_read per result element).
+template <bool Q5, int RW, int TW, int NT, int WPE = 2>
+__global__ __launch_bounds__(64 * RW * TW) __attribute__((amdgpu_waves_per_eu(WPE))) void mm_batch_kq_kernel(const uint8_t* __restrict__ w,
                                                                     const uint8_t* __restrict__ q8,
                                                                     float* __restrict__ out, int nb, int d, int m) {
     constexpr int NTHR = 64 * RW * TW;
@@ -319,11 +322,11 @@ __global__ __launch_bounds__(64 * RW * TW) void mm_batch_kq_kernel(const uint8_t
 constexpr int kRW = 4, kTW = 1, kNT = 2;
 constexpr int kPfToks = 16 * kNT * kTW;
 
-template <bool Q5, int RW, int TW, int NT>
+template <bool Q5, int RW, int TW, int NT, int WPE = 2>
 void launch_mm_batch(const uint8_t* w, const uint8_t* q8, float* o, int nb, int d, int m) {
     const dim3 grid((d + 16 * RW - 1) / (16 * RW), (m + 16 * NT * TW - 1) / (16 * NT * TW));
-    hipLaunchKernelGGL((mm_batch_kq_kernel<Q5, RW, TW, NT>), grid, dim3(64 * RW * TW), 0, g4_stream(), w, q8, o, nb,
-                       d, m);
+    hipLaunchKernelGGL((mm_batch_kq_kernel<Q5, RW, TW, NT, WPE>), grid, dim3(64 * RW * TW), 0, g4_stream(), w, q8, o,
+                       nb, d, m);
 }
 
 // m rows of k floats -> m consecutive device Q8_K rows of k/256 blocks
