@@ -334,7 +334,7 @@ def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):
     ms = _time_steps(lib, step, A)
     per = ms / 1e3 / n_launch
     algo = 2 * g_raw.nbytes + lib.L.g4_q8K_bytes(n) + 4 * d
-    name = "gemv_q45_rows_kernel<gate|up, GELU> 2x10240x2560 Q4_K"
+    name = "gemv_q45_stream_kernel<gate|up, GELU> 2x10240x2560 Q4_K"
     return dict(roofline(algo, per, name), kernel=name, bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
 
 

@@ -526,6 +526,169 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
 }
 
 // ------------------------------------------------------------------------
+// Q4_K / Q5_K x Q8_K, streaming form (rows of 8, 10 or 16 blocks)
+// ------------------------------------------------------------------------
+// One wave per workgroup; an 8-lane group owns one row of one matrix and
+// runs all NB blocks of it in order, so no lane shuffles are needed between
+// blocks.  With two matrices (gate|up) lanes 0..31 take four gate rows and
+// lanes 32..63 the same four up rows; with one matrix the wave has eight
+// rows.  The wave issues, in this order, its loads of the Q8_K vector and of
+// its rows' 16-byte block headers (both staged in LDS: every lane of a group
+// needs the whole header, and every group the whole vector) and then every
+// weight load of its rows (NB x 16 bytes per lane), so the weight stream is
+// in flight before anything waits.  Per block the lane's integer sums are
+// those of gemv_q45_rows_kernel, formed with fewer instructions: each pair
+// of nibble dots (dl, dh) is packed as two int16 (|dl|, |dh| <= 4*31*127)
+// and multiplied by its two sub-block scales in one v_dot2, and the min
+// lane's product m_a*(bs0+bs1) + m_b*(bs2+bs3) is two v_dot2 over the raw
+// int16 bsums.  The fp32 steps and the horizontal adds are the reference's
+// (main.c:476-529, 531-593), so outputs are bit-identical to the rows
+// kernel.
+typedef short s2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2_t, a), __builtin_bit_cast(s2_t, b), c, false);
+}
+
+template <bool Q5, int NB, int NMAT>
+__global__ __launch_bounds__(64) void gemv_q45_stream_kernel(const uint8_t* __restrict__ w0,
+                                                             const uint8_t* __restrict__ w1,
+                                                             const uint8_t* __restrict__ q8, float* __restrict__ out,
+                                                             int d, const float* __restrict__ aux) {
+    constexpr int RPW = 8 / NMAT;                 // rows per wave
+    constexpr int Q8B = NB * 292;                 // device Q8_K bytes
+    constexpr int Q8C = Q8B / 16, Q8T = (Q8B - Q8C * 16) / 4;
+    constexpr int HC = RPW * NB;                  // header chunks per matrix
+    constexpr int QPL = (Q8C + 63) / 64, HPL = (HC + 63) / 64;
+    __shared__ __align__(16) uint8_t sq[Q8B + 16];
+    __shared__ __align__(16) uint8_t sh[NMAT][HC * 16];
+    const int lane = threadIdx.x, l = lane & 7, k = l & 3, grp = (lane >> 3) & (RPW - 1);
+    const int m = NMAT == 2 ? lane >> 5 : 0;
+    const int r0 = blockIdx.x * RPW;
+    const int row = min(r0 + grp, d - 1);
+    const uint32_t nblk = (uint32_t)d * NB;
+    const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk, qh_off = 128u * nblk;   // q4k_planes / q5k_planes
+
+    uint4 qv[QPL], hv[NMAT][HPL];
+    uint32_t tv = 0u;
+#pragma unroll
+    for (int j = 0; j < QPL; j++) {
+        const int c = lane + 64 * j;
+        qv[j] = make_uint4(0u, 0u, 0u, 0u);
+        if (c < Q8C) qv[j] = reinterpret_cast<const uint4*>(q8)[c];
+    }
+    if (lane < Q8T) tv = reinterpret_cast<const uint32_t*>(q8 + Q8C * 16)[lane];
+#pragma unroll
+    for (int j = 0; j < HPL; j++) {
+        const int c = lane + 64 * j;
+        const uint32_t blk = (uint32_t)min(r0 + c / NB, d - 1) * NB + (uint32_t)(c % NB);
+#pragma unroll
+        for (int mm = 0; mm < NMAT; mm++) {
+            hv[mm][j] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < HC) hv[mm][j] = *reinterpret_cast<const uint4*>((mm ? w1 : w0) + hdr_off + blk * 16u);
+        }
+    }
+    const uint8_t* const wm = m ? w1 : w0;
+    const uint32_t rb = (uint32_t)row * NB;
+    uint4 wq[NB];
+    uint32_t qh[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        wq[b] = *reinterpret_cast<const uint4*>(wm + (rb + b) * 128u + 16 * l);
+        qh[b] = Q5 ? *reinterpret_cast<const uint32_t*>(wm + qh_off + (rb + b) * 32u + 4 * l) : 0u;
+    }
+    __builtin_amdgcn_sched_barrier(0);   // all loads issued before the LDS stores wait for the first ones
+#pragma unroll
+    for (int j = 0; j < QPL; j++) {
+        const int c = lane + 64 * j;
+        if (c < Q8C) reinterpret_cast<uint4*>(sq)[c] = qv[j];
+    }
+    if (lane < Q8T) reinterpret_cast<uint32_t*>(sq + Q8C * 16)[lane] = tv;
+#pragma unroll
+    for (int j = 0; j < HPL; j++) {
+        const int c = lane + 64 * j;
+#pragma unroll
+        for (int mm = 0; mm < NMAT; mm++)
+            if (c < HC) reinterpret_cast<uint4*>(sh[mm])[c] = hv[mm][j];
+    }
+    __syncthreads();
+
+    // byte selectors of the two mins (m_2k, m_2k+1 of min lane k), as int16 pairs
+    const uint32_t selA = (k & 1) ? 0x0c020c02u : 0x0c000c00u;
+    const uint32_t selB = (k & 1) ? 0x0c030c03u : 0x0c010c01u;
+    // min lanes 0, 1 use mins 0..3, lanes 2, 3 mins 4..7; a mask rather than
+    // a conditional, which the compiler turns into a branch per block and
+    // then hoists every block's LDS reads above it (198 VGPRs instead of 74)
+    const uint32_t kmask = k < 2 ? 0xffffffffu : 0u;
+    float acc = 0.0f, accm = 0.0f, summs = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const uint8_t* a_qs = sq + 32 * l + b * 256;
+        const uint4 a0 = *reinterpret_cast<const uint4*>(a_qs);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(a_qs + 16);
+        const uint2 bsw = *reinterpret_cast<const uint2*>(sq + q8k_bsums_off(NB) + b * 32 + 8 * k);
+        const float yd = reinterpret_cast<const float*>(sq + q8k_d_off(NB))[b];
+        const uint4 hd = *reinterpret_cast<const uint4*>(sh[m] + (grp * NB + b) * 16);
+        // the 6-bit scales (sub-blocks 0..3, 4..7) and this min lane's two mins
+        const uint32_t sc_lo = hd.y & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = hd.z & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((hd.w >> 4) & 0x0f0f0f0fu) | (((hd.z >> 6) & 0x03030303u) << 4);
+        const uint32_t mnw = (mn_lo & kmask) | (mn_hi & ~kmask);
+        int32_t sumi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t qw = word_of(wq[b], j);
+            uint32_t lo = qw & 0x0f0f0f0fu, hi = (qw >> 4) & 0x0f0f0f0fu;
+            if (Q5) {
+                lo |= ((qh[b] >> (2 * j)) & 0x01010101u) << 4;
+                hi |= ((qh[b] >> (2 * j + 1)) & 0x01010101u) << 4;
+            }
+            const int dl = __builtin_amdgcn_sdot4((int)lo, (int)word_of(a0, j), 0, false);
+            const int dh = __builtin_amdgcn_sdot4((int)hi, (int)word_of(a1, j), 0, false);
+            const uint32_t pk = __builtin_amdgcn_perm((uint32_t)dh, (uint32_t)dl, 0x05040100u);
+            const uint32_t scp = __builtin_amdgcn_perm(0u, j < 2 ? sc_lo : sc_hi, (j & 1) ? 0x0c030c02u : 0x0c010c00u);
+            sumi = dot2_i16(pk, scp, sumi);
+        }
+        int32_t P = dot2_i16(bsw.x, __builtin_amdgcn_perm(0u, mnw, selA),
+                             dot2_i16(bsw.y, __builtin_amdgcn_perm(0u, mnw, selB), 0));
+        const float D = yd * half_bits_to_f32(hd.x & 0xffffu);
+        const float DM = -yd * half_bits_to_f32(hd.x >> 16);
+        if (Q5) {
+            // the four min products summed exactly, on every lane of the group
+            int32_t pm = l < 4 ? P : 0;
+            pm += __shfl_xor(pm, 1, 64);
+            pm += __shfl_xor(pm, 2, 64);
+            P = __shfl(pm, lane & ~7, 64);
+        }
+        acc = __builtin_fmaf(D, (float)sumi, acc);
+        if (Q5) {
+            const float tm = DM * (float)P;
+            summs = summs + tm;
+        } else if (l < 4) {
+            accm = __builtin_fmaf(DM, (float)P, accm);
+        }
+    }
+    const float t1 = acc + __shfl_xor(acc, 4, 64);
+    const float t2 = t1 + __shfl_xor(t1, 2, 64);
+    const float h = t2 + __shfl_xor(t2, 1, 64);
+    float r;
+    if (Q5) {
+        r = h + summs;
+    } else {
+        const float v1 = accm + __shfl_xor(accm, 2, 64);
+        const float hm = v1 + __shfl_xor(v1, 1, 64);
+        r = h + hm;
+    }
+    const int ro = r0 + grp;
+    if (NMAT == 2) {
+        const float up = __shfl_xor(r, 32, 64);
+        if (l == 0 && m == 0 && ro < d) out[ro] = gelu_ref(r) * up;
+    } else if (l == 0 && ro < d) {
+        out[ro] = aux ? gelu_ref(r) * aux[ro] : r;
+    }
+}
+
+// ------------------------------------------------------------------------
 // Q6_K x fp32 (mm_quant_rows semantics), one row slice per 8-lane group
 // ------------------------------------------------------------------------
 // A 256-thread workgroup stages x in LDS once and sweeps row groups of
@@ -719,6 +882,15 @@ template <bool Q5, int NMAT, bool DBG>
 int launch_q45(const void* w0, const void* w1, const void* q8, float* o, int nb, int d, int32_t* S, int32_t* M,
                const float* aux = nullptr) {
     constexpr int SP = NMAT == 2 ? 4 : 2;
+    if (!DBG && (nb == 8 || nb == 10 || nb == 16)) {
+        const dim3 grid((d + 8 / NMAT - 1) / (8 / NMAT));
+        const uint8_t* a = (const uint8_t*)w0;
+        const uint8_t* b = (const uint8_t*)w1;
+        if (nb == 8) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 8, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
+        else if (nb == 10) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 10, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
+        else hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 16, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
+        return g4_check_launch("gemv_q45_stream_kernel");
+    }
     switch (nb) {   // unrolled for the row lengths of the model (256, 2048, 2560, 4096)
     case 1: launch_q45_nb<Q5, NMAT, DBG, 1, 1>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
     case 8: launch_q45_nb<Q5, NMAT, DBG, 8, SP>(w0, w1, q8, o, nb, d, S, M, nullptr, nullptr, aux); break;
