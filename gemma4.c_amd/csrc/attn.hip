@@ -444,6 +444,327 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 
 }
 
+// ---- register-resident chunk kernel ---------------------------------------
+// Same partials as attn_decode_kernel, computed without LDS round trips
+// between the phases.  Every wave holds its vectors in the layout lane l ->
+// elements 4l..4l+3 (+256 e for head_dim 512), so K and V rows are float4
+// loads of 1 KB per wave instruction, and
+//  - each wave loads and normalises all KVM q heads itself (a wave sum per
+//    head) and rotates them in registers: pair (j, j + hd/2) sits in lanes l
+//    and l + 32 at head_dim 256 (one lane exchange per element) and in the
+//    same lane at head_dim 512;
+//  - a round gives each wave PPW positions; its PPW x KVM partial dot
+//    products are summed over the wave by a transposed butterfly (each
+//    exchange step halves the number of values a lane carries), after which
+//    lane L holds the score of pair j = L >> (6 - log2(PPW*KVM)) = h*PPW + p,
+//    so head h's scores fill an aligned group of 64/KVM lanes;
+//  - the chunk's online softmax (max, exp, sum) runs on those groups, and
+//    o_h += p * V_p takes each p by a readlane (an SGPR operand of the FMA);
+//  - the four waves' (max, sum, o) are combined once through LDS.
+// The fused K/V append is computed by every wave of the owner workgroup;
+// the wave whose round holds position pos uses it in place of the (stale)
+// cache row, and wave 0 stores it.
+template <int M>
+__device__ __forceinline__ float lane_xchg(float x) {   // partner lane across lane bit M
+    if constexpr (M >= 16) return __shfl_xor(x, M, 64);
+    else if constexpr (M == 8) return dpp_f<kDppMirror>(x);
+    else if constexpr (M == 4) return dpp_f<kDppHalfMirror>(x);
+    else if constexpr (M == 2) return dpp_f<kDppXor2>(x);
+    else return dpp_f<kDppXor1>(x);
+}
+
+// one exchange step over bit M on N values, then the rest
+template <int M, int N>
+__device__ __forceinline__ float xpose_sum_step(float (&v)[32], int lane) {
+    if constexpr (N == 1) {
+        float x = v[0];
+        if constexpr (M >= 1) {
+            x += lane_xchg<M>(x);
+            v[0] = x;
+            return xpose_sum_step<M / 2, 1>(v, lane);
+        }
+        return x;
+    } else {
+        const bool up = (lane & M) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; i++) {
+            const float a = v[i], b = v[i + N / 2];
+            v[i] = (up ? b : a) + lane_xchg<M>(up ? a : b);
+        }
+        return xpose_sum_step<M / 2, N / 2>(v, lane);
+    }
+}
+
+// max / sum over aligned groups of W lanes
+template <int W>
+__device__ __forceinline__ float group_max(float x) {
+    if constexpr (W >= 64) x = fmaxf(x, lane_xchg<32>(x));
+    if constexpr (W >= 32) x = fmaxf(x, lane_xchg<16>(x));
+    if constexpr (W >= 16) x = fmaxf(x, lane_xchg<8>(x));
+    if constexpr (W >= 8) x = fmaxf(x, lane_xchg<4>(x));
+    if constexpr (W >= 4) x = fmaxf(x, lane_xchg<2>(x));
+    if constexpr (W >= 2) x = fmaxf(x, lane_xchg<1>(x));
+    return x;
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (W >= 64) x += lane_xchg<32>(x);
+    if constexpr (W >= 32) x += lane_xchg<16>(x);
+    if constexpr (W >= 16) x += lane_xchg<8>(x);
+    if constexpr (W >= 8) x += lane_xchg<4>(x);
+    if constexpr (W >= 4) x += lane_xchg<2>(x);
+    if constexpr (W >= 2) x += lane_xchg<1>(x);
+    return x;
+}
+
+__device__ __forceinline__ float4 f4_scale(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+__device__ __forceinline__ float f4_sq(float4 a, float acc) { return dot4(a, a, acc); }
+
+// rms-normalise a head vector held as NV float4 per lane (w: weight or null)
+template <int NV, int HD>
+__device__ __forceinline__ void norm_vec(float4 (&v)[NV], const float4 (&w)[NV], bool weighted, float eps) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NV; e++) ss = f4_sq(v[e], ss);
+    ss = wave_sum(ss);
+    const float s = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int e = 0; e < NV; e++) {
+        if (weighted) {
+            v[e].x = v[e].x * (s * w[e].x);
+            v[e].y = v[e].y * (s * w[e].y);
+            v[e].z = v[e].z * (s * w[e].z);
+            v[e].w = v[e].w * (s * w[e].w);
+        } else {
+            v[e] = f4_scale(v[e], s);
+        }
+    }
+}
+
+// Neox rotation of pairs (j, j + HD/2), j < n_rot/2, in the float4 layout;
+// cs[c]: (cos, sin) of this lane's pair of element c
+template <int NV, int HD>
+__device__ __forceinline__ void rope_vec(float4 (&v)[NV], const float2 (&cs)[4], int lane, int n_rot) {
+    if constexpr (HD == 256) {
+        float* f = reinterpret_cast<float*>(&v[0]);
+        const bool second = lane >= 32;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int j = 4 * (lane & 31) + c;
+            const float o = __shfl_xor(f[c], 32, 64);
+            const float v0 = second ? o : f[c], v1 = second ? f[c] : o;
+            if (j < n_rot / 2) f[c] = second ? v0 * cs[c].y + v1 * cs[c].x : v0 * cs[c].x - v1 * cs[c].y;
+        }
+    } else {
+        float* f0 = reinterpret_cast<float*>(&v[0]);
+        float* f1 = reinterpret_cast<float*>(&v[1]);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int j = 4 * lane + c;
+            if (j < n_rot / 2) {
+                const float v0 = f0[c], v1 = f1[c];
+                f0[c] = v0 * cs[c].x - v1 * cs[c].y;
+                f1[c] = v0 * cs[c].y + v1 * cs[c].x;
+            }
+        }
+    }
+}
+
+template <int HD, int KVM>
+__host__ __device__ constexpr int chunk_ppw() {   // positions per wave per round
+    return (HD == 256 ? 8 : 4) < 32 / KVM ? (HD == 256 ? 8 : 4) : 32 / KVM;
+}
+
+__host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2) {
+    return (size_t)4 * kvm_pow2 * (hd + 2) * 4;
+}
+
+template <int HD, int KVM>
+__global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
+    constexpr int NV = HD / 256;                  // float4 per lane per vector
+    constexpr int NW = kAttnThreads / 64;
+    constexpr int PPW = chunk_ppw<HD, KVM>();
+    constexpr int V = PPW * KVM;                  // score values per wave and round
+    constexpr int LV = V == 32 ? 5 : V == 16 ? 4 : V == 8 ? 3 : V == 4 ? 2 : V == 2 ? 1 : 0;
+    constexpr int HG = 64 / KVM;                  // lanes per head group after the reduction
+    static_assert(V <= 32 && (1 << LV) == V, "score values per round");
+    extern __shared__ __align__(16) float sm[];   // [NW][KVM][HD] o, then [NW][KVM] (max, sum)
+    const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvm = a.n_heads / a.n_kv;
+    int t0, nwin;
+    attn_window(a, t0, nwin);
+    const int cs = (nwin + a.G - 1) / a.G;
+    const int cb = t0 + c * cs;
+    const int cnt = min(kChunkMax, max(0, min(cb + cs, t0 + nwin) - cb));
+    const int pos = t0 + nwin - 1;
+    const int tl = pos - cb;
+    const bool owner = a.kraw != nullptr && cnt > 0 && tl >= 0 && tl < cnt;
+    const int s0 = attn_slot(a, cb);
+    auto slot_of = [&](int i) {
+        const int s = s0 + i;
+        return (a.ring > 0 && s >= a.ring) ? s - a.ring : s;
+    };
+    const float* kbase = a.kc + (size_t)kvh * HD;
+    const float* vbase = a.vc + (size_t)kvh * HD;
+
+    float4 kr[PPW][NV], vr[PPW][NV];
+    auto load_kv = [&](int r) {
+#pragma unroll
+        for (int p = 0; p < PPW; p++) {
+            const int i = min(r * NW * PPW + wave * PPW + p, cnt - 1);
+            const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)slot_of(i) * a.kv_stride);
+            const float4* vp = reinterpret_cast<const float4*>(vbase + (size_t)slot_of(i) * a.kv_stride);
+#pragma unroll
+            for (int e = 0; e < NV; e++) {
+                kr[p][e] = kp[lane + 64 * e];
+                vr[p][e] = vp[lane + 64 * e];
+            }
+        }
+    };
+    if (cnt > 0) load_kv(0);
+
+    // q heads of this kv head (heads past kvm repeat the last one; unused)
+    const bool fuse = a.q_norm != nullptr;
+    float4 q[KVM][NV];
+#pragma unroll
+    for (int h = 0; h < KVM; h++) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * kvm + min(h, kvm - 1)) * HD);
+#pragma unroll
+        for (int e = 0; e < NV; e++) q[h][e] = qp[lane + 64 * e];
+    }
+    float4 wq[NV], wk[NV], kn[NV], vn[NV];
+    float2 rc[4];
+    if (fuse) {
+#pragma unroll
+        for (int e = 0; e < NV; e++) wq[e] = reinterpret_cast<const float4*>(a.q_norm)[lane + 64 * e];
+        // (cos, sin) of this lane's pairs: j = 4*(lane % 32) + c (head_dim 256) or 4*lane + c (512)
+        const int jb = HD == 256 ? 4 * (lane & 31) : 4 * lane;
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) rc[cc] = jb + cc < a.n_rot / 2 ? a.tab[jb + cc] : make_float2(1.0f, 0.0f);
+        if (owner) {
+#pragma unroll
+            for (int e = 0; e < NV; e++) {
+                wk[e] = reinterpret_cast<const float4*>(a.k_norm)[lane + 64 * e];
+                kn[e] = reinterpret_cast<const float4*>(a.kraw + (size_t)kvh * HD)[lane + 64 * e];
+                vn[e] = reinterpret_cast<const float4*>(a.vraw + (size_t)kvh * HD)[lane + 64 * e];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < KVM; h++) {
+            norm_vec<NV, HD>(q[h], wq, true, a.eps);
+            rope_vec<NV, HD>(q[h], rc, lane, a.n_rot);
+        }
+        if (owner) {
+            norm_vec<NV, HD>(kn, wk, true, a.eps);
+            rope_vec<NV, HD>(kn, rc, lane, a.n_rot);
+            norm_vec<NV, HD>(vn, wk, false, a.eps);
+            if (wave == 0) {
+                const size_t off = (size_t)attn_slot(a, pos) * a.kv_stride + (size_t)kvh * HD;
+#pragma unroll
+                for (int e = 0; e < NV; e++) {
+                    reinterpret_cast<float4*>(a.kstore + off)[lane + 64 * e] = kn[e];
+                    reinterpret_cast<float4*>(a.vstore + off)[lane + 64 * e] = vn[e];
+                }
+            }
+        }
+    }
+
+    // per-head online softmax state of this wave (m, l uniform in the head's
+    // lane group; o in every lane)
+    float m = -INFINITY, l = 0.0f;
+    float4 o[KVM][NV];
+#pragma unroll
+    for (int h = 0; h < KVM; h++)
+#pragma unroll
+        for (int e = 0; e < NV; e++) o[h][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int nrounds = (cnt + NW * PPW - 1) / (NW * PPW);
+    const int jl = lane >> (6 - LV);             // score pair this lane ends with
+    const int hl = jl / PPW, pl = jl - hl * PPW;
+    for (int r = 0; r < nrounds; r++) {
+        if (r > 0) load_kv(r);
+        const int base = r * NW * PPW + wave * PPW;
+        if (owner && tl >= base && tl < base + PPW) {
+#pragma unroll
+            for (int p = 0; p < PPW; p++)
+                if (base + p == tl) {
+#pragma unroll
+                    for (int e = 0; e < NV; e++) { kr[p][e] = kn[e]; vr[p][e] = vn[e]; }
+                }
+        }
+        float sv[32];
+#pragma unroll
+        for (int h = 0; h < KVM; h++)
+#pragma unroll
+            for (int p = 0; p < PPW; p++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < NV; e++) d = dot4(kr[p][e], q[h][e], d);
+                sv[h * PPW + p] = d;
+            }
+        const float sraw = xpose_sum_step<32, V>(sv, lane);
+        const bool valid = base + pl < cnt && hl < kvm;
+        const float s = valid ? a.scale * sraw : -INFINITY;
+        const float mr = group_max<HG>(s);
+        const float mn = fmaxf(m, mr);
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+        const float pv = valid ? expf(s - mn) : 0.0f;
+        // each score sits in 64/V adjacent lanes: count it once
+        l = l * alpha + group_sum<HG>((lane & (64 / V - 1)) == 0 ? pv : 0.0f);
+        m = mn;
+#pragma unroll
+        for (int h = 0; h < KVM; h++) {
+            const float ah = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), h * HG));
+#pragma unroll
+            for (int e = 0; e < NV; e++) o[h][e] = f4_scale(o[h][e], ah);
+#pragma unroll
+            for (int p = 0; p < PPW; p++) {
+                const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), (h * PPW + p) << (6 - LV)));
+#pragma unroll
+                for (int e = 0; e < NV; e++) {
+                    o[h][e].x = __builtin_fmaf(ph, vr[p][e].x, o[h][e].x);
+                    o[h][e].y = __builtin_fmaf(ph, vr[p][e].y, o[h][e].y);
+                    o[h][e].z = __builtin_fmaf(ph, vr[p][e].z, o[h][e].z);
+                    o[h][e].w = __builtin_fmaf(ph, vr[p][e].w, o[h][e].w);
+                }
+            }
+        }
+    }
+
+    // combine the waves: LDS [NW][KVM][HD] o and [NW][KVM] (max, sum)
+    float* so = sm;
+    float* sml = sm + NW * KVM * HD;
+#pragma unroll
+    for (int h = 0; h < KVM; h++) {
+#pragma unroll
+        for (int e = 0; e < NV; e++) reinterpret_cast<float4*>(so + (size_t)(wave * KVM + h) * HD)[lane + 64 * e] = o[h][e];
+        if (lane == h * HG) {
+            sml[2 * (wave * KVM + h)] = m;
+            sml[2 * (wave * KVM + h) + 1] = l;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < kvm * HD; i += kAttnThreads) {
+        const int h = i / HD, dd = i - h * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sml[2 * (w * KVM + h)]);
+        float acc = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = sml[2 * (w * KVM + h)];
+            const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
+            acc = __builtin_fmaf(f, so[(size_t)(w * KVM + h) * HD + dd], acc);
+            L = __builtin_fmaf(f, sml[2 * (w * KVM + h) + 1], L);
+        }
+        float* pp = a.part + ((size_t)(kvh * kvm + h) * a.G + c) * (HD + 2);
+        pp[dd] = acc;
+        if (dd == 0) {
+            pp[HD] = M;
+            pp[HD + 1] = L;
+        }
+    }
+}
+
 // Merge of the G chunk partials of one q head: workgroup (h, slice) owns
 // 256 output dims.  Chunk weights f_g = exp(max_g - M) and the total
 // L = sum_g sum_g f_g are computed once in LDS; each thread then reduces its
@@ -502,9 +823,31 @@ size_t attn_lds(int hd, int kvm, bool fused) {
                       : (size_t)attn_work_floats(hd, kvm) + 2 * (size_t)kvm);
 }
 
+template <int HD>
+void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
+    const size_t lds = attn_chunk_lds(HD, kp);
+    if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else if (kp == 2) hipLaunchKernelGGL((attn_chunk_kernel<HD, 2>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else if (kp == 4) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+}
+
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
     const dim3 grid(a.G, a.n_kv);
+    // q heads per kv head rounded up to a power of two (the register kernel's
+    // template); its LDS must fit the default 64 KB
+    const int kp = kvm <= 1 ? 1 : kvm <= 2 ? 2 : kvm <= 4 ? 4 : 8;
+    if (attn_chunk_lds(a.hd, kp) <= 65536) {
+        if (a.hd == 256) {
+            launch_chunk<256>(a, kp, grid);
+            hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1), dim3(256), 0, g4_stream(), a);
+        } else {
+            launch_chunk<512>(a, kp, grid);
+            hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2), dim3(256), 0, g4_stream(), a);
+        }
+        return g4_check_launch("attn_chunk_kernel/attn_merge_kernel");
+    }
     const size_t lds = attn_lds(a.hd, kvm, a.q_norm != nullptr);
     if (a.hd == 256) {
         hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);

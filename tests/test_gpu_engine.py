@@ -11,8 +11,13 @@ A Q8_K rounding that lands on the other side of .5 because its input moved by
 one ulp changes one quantized activation by one step, which at this model's
 width (256) moves a GEMV output by up to ~(amax/127)/(rms*sqrt(256)), a few
 1e-3; such layers are rare, so the bars are on the median, the 90th
-percentile and the maximum.  Logits are computed from the engine's final
-hidden state on both sides and must agree to 1e-5.
+percentile, the share of layers with such a flip (under 5 %) and the
+maximum.  Which layers flip depends on the GPU's summation order: two
+attention kernels with the same error against the oracle (median 2e-7,
+max 1.5e-5 over 40 random cases each) gave worst layers of 5.6e-3 and
+1.6e-2 on this model, so the maximum allows a few flips (3e-2).  Logits are
+computed from the engine's final hidden state on both sides and must agree
+to 1e-5.
 """
 import numpy as np
 import pytest
@@ -23,7 +28,9 @@ pytestmark = pytest.mark.gpu
 
 MEDIAN_TOL = 2e-6      # per-layer relative error (max |diff| / max |ref|)
 P90_TOL = 2e-5
-MAX_TOL = 1e-2         # one Q8_K rounding flip at width 256
+FLIP_TOL = 1e-3        # a layer above this has had a Q8_K rounding flip
+FLIP_SHARE = 0.05      # ... and such layers are rare
+MAX_TOL = 3e-2         # a few flips at width 256
 LOGIT_TOL = 1e-5
 
 
@@ -77,6 +84,7 @@ def test_layerwise_teacher_forced(pair):
           f"max {errs.max():.2e}; logits max {max(lerr):.2e}")
     assert np.median(errs) < MEDIAN_TOL
     assert np.percentile(errs, 90) < P90_TOL
+    assert np.mean(errs > FLIP_TOL) < FLIP_SHARE
     assert errs.max() < MAX_TOL
     assert max(lerr) < LOGIT_TOL
 
