@@ -446,24 +446,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 
 // ---- register-resident chunk kernel ---------------------------------------
 // Same partials as attn_decode_kernel, computed without LDS round trips
-// between the phases.  Every wave holds its vectors in the layout lane l ->
-// elements 4l..4l+3 (+256 e for head_dim 512), so K and V rows are float4
-// loads of 1 KB per wave instruction, and
+// between the phases.  Every wave holds its vectors in the HVec layout (lane
+// l: elements W*l .. W*l+W-1 and their RoPE partners HD/2 further), so
 //  - each wave loads and normalises all KVM q heads itself (a wave sum per
-//    head) and rotates them in registers: pair (j, j + hd/2) sits in lanes l
-//    and l + 32 at head_dim 256 (one lane exchange per element) and in the
-//    same lane at head_dim 512;
+//    head) and rotates them in registers, with no lane exchanges;
 //  - a round gives each wave PPW positions; its PPW x KVM partial dot
-//    products are summed over the wave by a transposed butterfly (each
-//    exchange step halves the number of values a lane carries), after which
-//    lane L holds the score of pair j = L >> (6 - log2(PPW*KVM)) = h*PPW + p,
-//    so head h's scores fill an aligned group of 64/KVM lanes;
-//  - the chunk's online softmax (max, exp, sum) runs on those groups, and
-//    o_h += p * V_p takes each p by a readlane (an SGPR operand of the FMA);
+//    products are summed over the wave by a transposed butterfly: each
+//    exchange step over a lane bit halves the number of values a lane
+//    carries (in-row DPP steps first, while there are many values, the two
+//    cross-row steps last), so that score j = h*PPW + p ends in the lanes
+//    whose bits 3, 2, 1, 0, 4 (in that order, most significant first) spell
+//    j, and head h's scores fill the lanes whose leading bits spell h;
+//  - the chunk's online softmax (max, exp, sum) reduces over those lanes,
+//    and o_h += p * V_p takes each p by a readlane (an SGPR operand);
 //  - the four waves' (max, sum, o) are combined once through LDS.
 // The fused K/V append is computed by every wave of the owner workgroup;
 // the wave whose round holds position pos uses it in place of the (stale)
 // cache row, and wave 0 stores it.
+// On a sliding-window layer whose ring holds exactly the window, chunk c
+// takes fixed ring slots, so its K/V loads do not wait for the position:
+// the softmax does not depend on the order of the positions, and a slot is
+// valid once the ring is full (pos >= ring-1) or if it does not exceed pos.
 template <int M>
 __device__ __forceinline__ float lane_xchg(float x) {   // partner lane across lane bit M
     if constexpr (M >= 16) return __shfl_xor(x, M, 64);
@@ -473,99 +476,118 @@ __device__ __forceinline__ float lane_xchg(float x) {   // partner lane across l
     else return dpp_f<kDppXor1>(x);
 }
 
-// one exchange step over bit M on N values, then the rest
-template <int M, int N>
+// lane bits in the order the transposed butterfly consumes them
+__host__ __device__ constexpr int xbit(int k) { return k == 0 ? 8 : k == 1 ? 4 : k == 2 ? 2 : k == 3 ? 1 : k == 4 ? 16 : 32; }
+
+// lane holding score j of an nb-bit index (free bits zero)
+__host__ __device__ constexpr int xlane(int j, int nb) {
+    int l = 0;
+    for (int k = 0; k < nb; k++) l |= ((j >> (nb - 1 - k)) & 1) ? xbit(k) : 0;
+    return l;
+}
+__host__ __device__ constexpr int xfree(int nb) {   // lane bits not part of the index
+    int m = 0;
+    for (int k = nb; k < 6; k++) m |= xbit(k);
+    return m;
+}
+
+// step K of the butterfly on N values (N == 1: plain all-reduce steps)
+template <int K, int N>
 __device__ __forceinline__ float xpose_sum_step(float (&v)[32], int lane) {
-    if constexpr (N == 1) {
-        float x = v[0];
-        if constexpr (M >= 1) {
-            x += lane_xchg<M>(x);
-            v[0] = x;
-            return xpose_sum_step<M / 2, 1>(v, lane);
-        }
-        return x;
+    if constexpr (K >= 6) {
+        return v[0];
+    } else if constexpr (N == 1) {
+        v[0] += lane_xchg<xbit(K)>(v[0]);
+        return xpose_sum_step<K + 1, 1>(v, lane);
     } else {
-        const bool up = (lane & M) != 0;
+        const bool up = (lane & xbit(K)) != 0;
 #pragma unroll
         for (int i = 0; i < N / 2; i++) {
             const float a = v[i], b = v[i + N / 2];
-            v[i] = (up ? b : a) + lane_xchg<M>(up ? a : b);
+            v[i] = (up ? b : a) + lane_xchg<xbit(K)>(up ? a : b);
         }
-        return xpose_sum_step<M / 2, N / 2>(v, lane);
+        return xpose_sum_step<K + 1, N / 2>(v, lane);
     }
 }
 
-// max / sum over aligned groups of W lanes
-template <int W>
+// max / sum over the lanes that share index bits 0..K0-1 (steps K0..5)
+template <int K>
 __device__ __forceinline__ float group_max(float x) {
-    if constexpr (W >= 64) x = fmaxf(x, lane_xchg<32>(x));
-    if constexpr (W >= 32) x = fmaxf(x, lane_xchg<16>(x));
-    if constexpr (W >= 16) x = fmaxf(x, lane_xchg<8>(x));
-    if constexpr (W >= 8) x = fmaxf(x, lane_xchg<4>(x));
-    if constexpr (W >= 4) x = fmaxf(x, lane_xchg<2>(x));
-    if constexpr (W >= 2) x = fmaxf(x, lane_xchg<1>(x));
-    return x;
+    if constexpr (K < 6) return group_max<K + 1>(fmaxf(x, lane_xchg<xbit(K)>(x)));
+    else return x;
 }
-template <int W>
+template <int K>
 __device__ __forceinline__ float group_sum(float x) {
-    if constexpr (W >= 64) x += lane_xchg<32>(x);
-    if constexpr (W >= 32) x += lane_xchg<16>(x);
-    if constexpr (W >= 16) x += lane_xchg<8>(x);
-    if constexpr (W >= 8) x += lane_xchg<4>(x);
-    if constexpr (W >= 4) x += lane_xchg<2>(x);
-    if constexpr (W >= 2) x += lane_xchg<1>(x);
-    return x;
+    if constexpr (K < 6) return group_sum<K + 1>(x + lane_xchg<xbit(K)>(x));
+    else return x;
 }
 
-__device__ __forceinline__ float4 f4_scale(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
-__device__ __forceinline__ float f4_sq(float4 a, float acc) { return dot4(a, a, acc); }
-
-// rms-normalise a head vector held as NV float4 per lane (w: weight or null)
-template <int NV, int HD>
-__device__ __forceinline__ void norm_vec(float4 (&v)[NV], const float4 (&w)[NV], bool weighted, float eps) {
-    float ss = 0.0f;
+// A head vector as one lane holds it: elements W*l .. W*l+W-1 and, HD/2
+// further, their RoPE partners (W = HD/128: a float2 or float4 load per
+// half, 512 B or 1 KB per wave instruction).
+template <int HD>
+struct HVec {
+    static constexpr int W = HD / 128;
+    float v[2][W];
+    __device__ __forceinline__ void load(const float* __restrict__ p, int lane) {
 #pragma unroll
-    for (int e = 0; e < NV; e++) ss = f4_sq(v[e], ss);
+        for (int k = 0; k < 2; k++) {
+            if constexpr (W == 2) {
+                const float2 t = reinterpret_cast<const float2*>(p)[64 * k + lane];
+                v[k][0] = t.x; v[k][1] = t.y;
+            } else {
+                const float4 t = reinterpret_cast<const float4*>(p)[64 * k + lane];
+                v[k][0] = t.x; v[k][1] = t.y; v[k][2] = t.z; v[k][3] = t.w;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* p, int lane) const {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            if constexpr (W == 2) reinterpret_cast<float2*>(p)[64 * k + lane] = make_float2(v[k][0], v[k][1]);
+            else reinterpret_cast<float4*>(p)[64 * k + lane] = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+        }
+    }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int w = 0; w < W; w++) v[k][w] = 0.0f;
+    }
+};
+
+template <int HD>
+__device__ __forceinline__ float hdot(const HVec<HD>& a, const HVec<HD>& b, float acc) {
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int w = 0; w < HD / 128; w++) acc = __builtin_fmaf(a.v[k][w], b.v[k][w], acc);
+    return acc;
+}
+
+// rmsnorm_head_inplace (w) / rmsnorm_head_noweight_inplace (w == null) of
+// one head vector: x * (s * w) or x * s, s = 1/sqrt(mean(x^2) + eps)
+template <int HD>
+__device__ __forceinline__ void norm_vec(HVec<HD>& x, const HVec<HD>* w, float eps) {
+    float ss = hdot(x, x, 0.0f);
     ss = wave_sum(ss);
     const float s = 1.0f / sqrtf(ss / (float)HD + eps);
 #pragma unroll
-    for (int e = 0; e < NV; e++) {
-        if (weighted) {
-            v[e].x = v[e].x * (s * w[e].x);
-            v[e].y = v[e].y * (s * w[e].y);
-            v[e].z = v[e].z * (s * w[e].z);
-            v[e].w = v[e].w * (s * w[e].w);
-        } else {
-            v[e] = f4_scale(v[e], s);
-        }
-    }
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int i = 0; i < HD / 128; i++) x.v[k][i] = w ? x.v[k][i] * (s * w->v[k][i]) : x.v[k][i] * s;
 }
 
-// Neox rotation of pairs (j, j + HD/2), j < n_rot/2, in the float4 layout;
-// cs[c]: (cos, sin) of this lane's pair of element c
-template <int NV, int HD>
-__device__ __forceinline__ void rope_vec(float4 (&v)[NV], const float2 (&cs)[4], int lane, int n_rot) {
-    if constexpr (HD == 256) {
-        float* f = reinterpret_cast<float*>(&v[0]);
-        const bool second = lane >= 32;
+// Neox rotation of pairs (j, j + HD/2), j = W*lane + i < n_rot/2, both in
+// this lane; cs[i] = (cos, sin) of pair j
+template <int HD>
+__device__ __forceinline__ void rope_vec(HVec<HD>& x, const float2 (&cs)[HD / 128], int lane, int n_rot) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int j = 4 * (lane & 31) + c;
-            const float o = __shfl_xor(f[c], 32, 64);
-            const float v0 = second ? o : f[c], v1 = second ? f[c] : o;
-            if (j < n_rot / 2) f[c] = second ? v0 * cs[c].y + v1 * cs[c].x : v0 * cs[c].x - v1 * cs[c].y;
-        }
-    } else {
-        float* f0 = reinterpret_cast<float*>(&v[0]);
-        float* f1 = reinterpret_cast<float*>(&v[1]);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int j = 4 * lane + c;
-            if (j < n_rot / 2) {
-                const float v0 = f0[c], v1 = f1[c];
-                f0[c] = v0 * cs[c].x - v1 * cs[c].y;
-                f1[c] = v0 * cs[c].y + v1 * cs[c].x;
-            }
+    for (int i = 0; i < HD / 128; i++) {
+        if ((HD / 128) * lane + i < n_rot / 2) {
+            const float v0 = x.v[0][i], v1 = x.v[1][i];
+            x.v[0][i] = v0 * cs[i].x - v1 * cs[i].y;
+            x.v[1][i] = v0 * cs[i].y + v1 * cs[i].x;
         }
     }
 }
@@ -581,105 +603,120 @@ __host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2) {
 
 template <int HD, int KVM>
 __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
-    constexpr int NV = HD / 256;                  // float4 per lane per vector
+    constexpr int W = HD / 128;
     constexpr int NW = kAttnThreads / 64;
     constexpr int PPW = chunk_ppw<HD, KVM>();
     constexpr int V = PPW * KVM;                  // score values per wave and round
     constexpr int LV = V == 32 ? 5 : V == 16 ? 4 : V == 8 ? 3 : V == 4 ? 2 : V == 2 ? 1 : 0;
-    constexpr int HG = 64 / KVM;                  // lanes per head group after the reduction
+    constexpr int LK = KVM == 8 ? 3 : KVM == 4 ? 2 : KVM == 2 ? 1 : 0;
     static_assert(V <= 32 && (1 << LV) == V, "score values per round");
     extern __shared__ __align__(16) float sm[];   // [NW][KVM][HD] o, then [NW][KVM] (max, sum)
     const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvm = a.n_heads / a.n_kv;
-    int t0, nwin;
-    attn_window(a, t0, nwin);
-    const int cs = (nwin + a.G - 1) / a.G;
-    const int cb = t0 + c * cs;
-    const int cnt = min(kChunkMax, max(0, min(cb + cs, t0 + nwin) - cb));
-    const int pos = t0 + nwin - 1;
-    const int tl = pos - cb;
-    const bool owner = a.kraw != nullptr && cnt > 0 && tl >= 0 && tl < cnt;
-    const int s0 = attn_slot(a, cb);
+    const bool fuse = a.q_norm != nullptr;
+    const bool append = fuse && a.kraw != nullptr;
+
+    // q heads of this kv head (heads past kvm repeat the last one; unused),
+    // the norm weights, the RoPE pairs and the raw K/V of this position:
+    // issued first, so their arithmetic waits only for them
+    HVec<HD> q[KVM];
+#pragma unroll
+    for (int h = 0; h < KVM; h++) q[h].load(a.q + (size_t)(kvh * kvm + min(h, kvm - 1)) * HD, lane);
+    HVec<HD> wq, wk, kn, vn;
+    float2 rc[W];
+    if (fuse) {
+        wq.load(a.q_norm, lane);
+#pragma unroll
+        for (int i = 0; i < W; i++) rc[i] = W * lane + i < a.n_rot / 2 ? a.tab[W * lane + i] : make_float2(1.0f, 0.0f);
+        if (append) {
+            wk.load(a.k_norm, lane);
+            kn.load(a.kraw + (size_t)kvh * HD, lane);
+            vn.load(a.vraw + (size_t)kvh * HD, lane);
+        }
+    }
+
+    // the chunk: cnt cache slots from slot s0 (wrapping once at the ring end)
+    const bool slotm = a.dpos != nullptr && a.ring > 0 && a.window == a.ring;
+    int cnt, s0, t0 = 0, nwin = 0, cb = 0;
+    if (slotm) {
+        const int css = (a.ring + a.G - 1) / a.G;
+        s0 = c * css;
+        cnt = max(0, min(css, a.ring - s0));
+    } else {
+        attn_window(a, t0, nwin);
+        const int cs = (nwin + a.G - 1) / a.G;
+        cb = t0 + c * cs;
+        // the launcher sizes G so that a chunk fits kChunkMax; the clamp only
+        // keeps the loads in bounds
+        cnt = min(kChunkMax, max(0, min(cb + cs, t0 + nwin) - cb));
+        s0 = attn_slot(a, cb);
+    }
     auto slot_of = [&](int i) {
-        const int s = s0 + i;
-        return (a.ring > 0 && s >= a.ring) ? s - a.ring : s;
+        const int sl = s0 + i;
+        return (a.ring > 0 && sl >= a.ring) ? sl - a.ring : sl;
     };
     const float* kbase = a.kc + (size_t)kvh * HD;
     const float* vbase = a.vc + (size_t)kvh * HD;
-
-    float4 kr[PPW][NV], vr[PPW][NV];
+    HVec<HD> kr[PPW], vr[PPW];
     auto load_kv = [&](int r) {
 #pragma unroll
         for (int p = 0; p < PPW; p++) {
             const int i = min(r * NW * PPW + wave * PPW + p, cnt - 1);
-            const float4* kp = reinterpret_cast<const float4*>(kbase + (size_t)slot_of(i) * a.kv_stride);
-            const float4* vp = reinterpret_cast<const float4*>(vbase + (size_t)slot_of(i) * a.kv_stride);
-#pragma unroll
-            for (int e = 0; e < NV; e++) {
-                kr[p][e] = kp[lane + 64 * e];
-                vr[p][e] = vp[lane + 64 * e];
-            }
+            kr[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
+            vr[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
         }
     };
     if (cnt > 0) load_kv(0);
+    // the position (slot mode: not needed by the loads above)
+    const int dpv = slotm ? *a.dpos : 0;
+    __builtin_amdgcn_sched_barrier(0);   // the loads are in flight before anything waits
 
-    // q heads of this kv head (heads past kvm repeat the last one; unused)
-    const bool fuse = a.q_norm != nullptr;
-    float4 q[KVM][NV];
-#pragma unroll
-    for (int h = 0; h < KVM; h++) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * kvm + min(h, kvm - 1)) * HD);
-#pragma unroll
-        for (int e = 0; e < NV; e++) q[h][e] = qp[lane + 64 * e];
-    }
-    float4 wq[NV], wk[NV], kn[NV], vn[NV];
-    float2 rc[4];
+    // per-head norms and RoPE (q; this position's K and V, whichever
+    // workgroup turns out to own the position)
     if (fuse) {
 #pragma unroll
-        for (int e = 0; e < NV; e++) wq[e] = reinterpret_cast<const float4*>(a.q_norm)[lane + 64 * e];
-        // (cos, sin) of this lane's pairs: j = 4*(lane % 32) + c (head_dim 256) or 4*lane + c (512)
-        const int jb = HD == 256 ? 4 * (lane & 31) : 4 * lane;
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++) rc[cc] = jb + cc < a.n_rot / 2 ? a.tab[jb + cc] : make_float2(1.0f, 0.0f);
-        if (owner) {
-#pragma unroll
-            for (int e = 0; e < NV; e++) {
-                wk[e] = reinterpret_cast<const float4*>(a.k_norm)[lane + 64 * e];
-                kn[e] = reinterpret_cast<const float4*>(a.kraw + (size_t)kvh * HD)[lane + 64 * e];
-                vn[e] = reinterpret_cast<const float4*>(a.vraw + (size_t)kvh * HD)[lane + 64 * e];
-            }
-        }
-#pragma unroll
         for (int h = 0; h < KVM; h++) {
-            norm_vec<NV, HD>(q[h], wq, true, a.eps);
-            rope_vec<NV, HD>(q[h], rc, lane, a.n_rot);
+            norm_vec<HD>(q[h], &wq, a.eps);
+            rope_vec<HD>(q[h], rc, lane, a.n_rot);
         }
-        if (owner) {
-            norm_vec<NV, HD>(kn, wk, true, a.eps);
-            rope_vec<NV, HD>(kn, rc, lane, a.n_rot);
-            norm_vec<NV, HD>(vn, wk, false, a.eps);
-            if (wave == 0) {
-                const size_t off = (size_t)attn_slot(a, pos) * a.kv_stride + (size_t)kvh * HD;
-#pragma unroll
-                for (int e = 0; e < NV; e++) {
-                    reinterpret_cast<float4*>(a.kstore + off)[lane + 64 * e] = kn[e];
-                    reinterpret_cast<float4*>(a.vstore + off)[lane + 64 * e] = vn[e];
-                }
-            }
+        if (append) {
+            norm_vec<HD>(kn, &wk, a.eps);
+            rope_vec<HD>(kn, rc, lane, a.n_rot);
+            norm_vec<HD>(vn, nullptr, a.eps);
         }
     }
 
-    // per-head online softmax state of this wave (m, l uniform in the head's
-    // lane group; o in every lane)
+    // valid positions: a prefix of nvalid chunk entries; tl = this
+    // position's entry
+    int nvalid, tl, pos;
+    if (slotm) {
+        pos = dpv;
+        nvalid = pos >= a.ring - 1 ? cnt : min(cnt, max(0, pos + 1 - s0));
+        tl = pos % a.ring - s0;
+    } else {
+        nvalid = cnt;
+        pos = t0 + nwin - 1;
+        tl = pos - cb;
+    }
+    const bool owner = append && tl >= 0 && tl < nvalid;
+    if (owner && wave == 0) {
+        const size_t off = (size_t)attn_slot(a, pos) * a.kv_stride + (size_t)kvh * HD;
+        kn.store(a.kstore + off, lane);
+        vn.store(a.vstore + off, lane);
+    }
+
+    // per-head online softmax state of this wave (m, l uniform over the
+    // head's lanes; o in every lane)
     float m = -INFINITY, l = 0.0f;
-    float4 o[KVM][NV];
+    HVec<HD> o[KVM];
 #pragma unroll
-    for (int h = 0; h < KVM; h++)
+    for (int h = 0; h < KVM; h++) o[h].zero();
+    const int nrounds = (nvalid + NW * PPW - 1) / (NW * PPW);
+    int jl = 0;                                   // score index this lane ends with
 #pragma unroll
-        for (int e = 0; e < NV; e++) o[h][e] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int nrounds = (cnt + NW * PPW - 1) / (NW * PPW);
-    const int jl = lane >> (6 - LV);             // score pair this lane ends with
+    for (int k = 0; k < LV; k++) jl |= ((lane & xbit(k)) ? 1 : 0) << (LV - 1 - k);
     const int hl = jl / PPW, pl = jl - hl * PPW;
+    const bool counted = (lane & xfree(LV)) == 0;   // one lane of each score's copies
     for (int r = 0; r < nrounds; r++) {
         if (r > 0) load_kv(r);
         const int base = r * NW * PPW + wave * PPW;
@@ -687,45 +724,37 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
             for (int p = 0; p < PPW; p++)
                 if (base + p == tl) {
-#pragma unroll
-                    for (int e = 0; e < NV; e++) { kr[p][e] = kn[e]; vr[p][e] = vn[e]; }
+                    kr[p] = kn;
+                    vr[p] = vn;
                 }
         }
         float sv[32];
 #pragma unroll
         for (int h = 0; h < KVM; h++)
 #pragma unroll
-            for (int p = 0; p < PPW; p++) {
-                float d = 0.0f;
-#pragma unroll
-                for (int e = 0; e < NV; e++) d = dot4(kr[p][e], q[h][e], d);
-                sv[h * PPW + p] = d;
-            }
-        const float sraw = xpose_sum_step<32, V>(sv, lane);
-        const bool valid = base + pl < cnt && hl < kvm;
-        const float s = valid ? a.scale * sraw : -INFINITY;
-        const float mr = group_max<HG>(s);
-        const float mn = fmaxf(m, mr);
+            for (int p = 0; p < PPW; p++) sv[h * PPW + p] = hdot(kr[p], q[h], 0.0f);
+        const float sraw = xpose_sum_step<0, V>(sv, lane);
+        const bool valid = base + pl < nvalid && hl < kvm;
+        const float sc = valid ? a.scale * sraw : -INFINITY;
+        const float mn = fmaxf(m, group_max<LK>(sc));
         const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
-        const float pv = valid ? expf(s - mn) : 0.0f;
-        // each score sits in 64/V adjacent lanes: count it once
-        l = l * alpha + group_sum<HG>((lane & (64 / V - 1)) == 0 ? pv : 0.0f);
+        const float pv = valid ? expf(sc - mn) : 0.0f;
+        l = l * alpha + group_sum<LK>(counted ? pv : 0.0f);
         m = mn;
 #pragma unroll
         for (int h = 0; h < KVM; h++) {
-            const float ah = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), h * HG));
+            const float ah = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), xlane(h, LK)));
 #pragma unroll
-            for (int e = 0; e < NV; e++) o[h][e] = f4_scale(o[h][e], ah);
+            for (int k = 0; k < 2; k++)
+#pragma unroll
+                for (int i = 0; i < W; i++) o[h].v[k][i] *= ah;
 #pragma unroll
             for (int p = 0; p < PPW; p++) {
-                const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), (h * PPW + p) << (6 - LV)));
+                const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), xlane(h * PPW + p, LV)));
 #pragma unroll
-                for (int e = 0; e < NV; e++) {
-                    o[h][e].x = __builtin_fmaf(ph, vr[p][e].x, o[h][e].x);
-                    o[h][e].y = __builtin_fmaf(ph, vr[p][e].y, o[h][e].y);
-                    o[h][e].z = __builtin_fmaf(ph, vr[p][e].z, o[h][e].z);
-                    o[h][e].w = __builtin_fmaf(ph, vr[p][e].w, o[h][e].w);
-                }
+                for (int k = 0; k < 2; k++)
+#pragma unroll
+                    for (int i = 0; i < W; i++) o[h].v[k][i] = __builtin_fmaf(ph, vr[p].v[k][i], o[h].v[k][i]);
             }
         }
     }
@@ -735,30 +764,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     float* sml = sm + NW * KVM * HD;
 #pragma unroll
     for (int h = 0; h < KVM; h++) {
-#pragma unroll
-        for (int e = 0; e < NV; e++) reinterpret_cast<float4*>(so + (size_t)(wave * KVM + h) * HD)[lane + 64 * e] = o[h][e];
-        if (lane == h * HG) {
+        o[h].store(so + (size_t)(wave * KVM + h) * HD, lane);
+        if (lane == xlane(h, LK)) {
             sml[2 * (wave * KVM + h)] = m;
             sml[2 * (wave * KVM + h) + 1] = l;
         }
     }
     __syncthreads();
-    for (int i = tid; i < kvm * HD; i += kAttnThreads) {
-        const int h = i / HD, dd = i - h * HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sml[2 * (w * KVM + h)]);
-        float acc = 0.0f, L = 0.0f;
+    // a thread per (head, 4 dims): the waves' weights exp(m_w - M) once,
+    // then its dims (the partial rows are 8-byte aligned: float2 stores)
+    constexpr int Q4 = HD / 4;
+    for (int i = tid; i < kvm * Q4; i += kAttnThreads) {
+        const int h = i / Q4, d4 = i - h * Q4;
+        float mw[NW], M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float mw = sml[2 * (w * KVM + h)];
-            const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
-            acc = __builtin_fmaf(f, so[(size_t)(w * KVM + h) * HD + dd], acc);
+            mw[w] = sml[2 * (w * KVM + h)];
+            M = fmaxf(M, mw[w]);
+        }
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - M);
+            const float4 ow = reinterpret_cast<const float4*>(so + (size_t)(w * KVM + h) * HD)[d4];
+            acc.x = __builtin_fmaf(f, ow.x, acc.x);
+            acc.y = __builtin_fmaf(f, ow.y, acc.y);
+            acc.z = __builtin_fmaf(f, ow.z, acc.z);
+            acc.w = __builtin_fmaf(f, ow.w, acc.w);
             L = __builtin_fmaf(f, sml[2 * (w * KVM + h) + 1], L);
         }
         float* pp = a.part + ((size_t)(kvh * kvm + h) * a.G + c) * (HD + 2);
-        pp[dd] = acc;
-        if (dd == 0) {
+        reinterpret_cast<float2*>(pp)[2 * d4] = make_float2(acc.x, acc.y);
+        reinterpret_cast<float2*>(pp)[2 * d4 + 1] = make_float2(acc.z, acc.w);
+        if (d4 == 0) {
             pp[HD] = M;
             pp[HD + 1] = L;
         }
@@ -766,10 +805,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
 }
 
 // Merge of the G chunk partials of one q head: workgroup (h, slice) owns
-// 256 output dims.  Chunk weights f_g = exp(max_g - M) and the total
-// L = sum_g sum_g f_g are computed once in LDS; each thread then reduces its
-// dim over the chunks (eight loads in flight) and, if asked, the workgroup
-// quantizes its 256 outputs as one Q8_K block.
+// 256 output dims.  Every load is issued first: each thread's dim of the
+// first kMergeReg chunks and the (max, sum) of the chunks it reduces; then
+// the chunk weights f_g = exp(max_g - M) and the total L = sum_g sum_g f_g
+// (through LDS), the thread's dim over the chunks (the rest of them, if G
+// is larger, streamed eight at a time) and, if asked, the Q8_K block of the
+// workgroup's 256 outputs.
+constexpr int kMergeReg = 32;
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     __shared__ float fw[kMaxChunks];
@@ -778,30 +821,47 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const int h = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x;
     const int G = a.G;
     const float* ph = a.part + (size_t)h * G * (HD + 2);
+    const int dd = slice * 256 + tid;
+    const float* pd = ph + dd;
+    float v[kMergeReg];
+#pragma unroll
+    for (int u = 0; u < kMergeReg; u++) v[u] = u < G ? pd[(size_t)u * (HD + 2)] : 0.0f;
+    float mg[kMaxChunks / 256], lg[kMaxChunks / 256];
+#pragma unroll
+    for (int k = 0; k < kMaxChunks / 256; k++) {
+        const int g = tid + 256 * k;
+        mg[k] = g < G ? ph[(size_t)g * (HD + 2) + HD] : -INFINITY;
+        lg[k] = g < G ? ph[(size_t)g * (HD + 2) + HD + 1] : 0.0f;
+    }
     float M = -INFINITY;
-    for (int g = tid; g < G; g += 256) M = fmaxf(M, ph[(size_t)g * (HD + 2) + HD]);
+#pragma unroll
+    for (int k = 0; k < kMaxChunks / 256; k++) M = fmaxf(M, mg[k]);
     M = wave_max(M);
     if ((tid & 63) == 0) red[tid >> 6] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f;
-    for (int g = tid; g < G; g += 256) {
-        const float l = ph[(size_t)g * (HD + 2) + HD + 1];
-        const float f = l > 0.0f ? expf(ph[(size_t)g * (HD + 2) + HD] - M) : 0.0f;
-        fw[g] = f;
-        L += l * f;
+#pragma unroll
+    for (int k = 0; k < kMaxChunks / 256; k++) {
+        const int g = tid + 256 * k;
+        if (g < G) {
+            const float f = lg[k] > 0.0f ? expf(mg[k] - M) : 0.0f;
+            fw[g] = f;
+            L += lg[k] * f;
+        }
     }
-    L = block_sum(L, red + 4);
-    const int dd = slice * 256 + tid;
-    const float* pd = ph + dd;
+    L = block_sum(L, red + 4);   // its barrier also publishes fw
     float o = 0.0f;
-    int g = 0;
+#pragma unroll
+    for (int u = 0; u < kMergeReg; u++)
+        if (u < G) o = __builtin_fmaf(v[u], fw[u], o);
+    int g = kMergeReg;
     for (; g + 8 <= G; g += 8) {
-        float v[8];
+        float w8[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = pd[(size_t)(g + u) * (HD + 2)];
+        for (int u = 0; u < 8; u++) w8[u] = pd[(size_t)(g + u) * (HD + 2)];
 #pragma unroll
-        for (int u = 0; u < 8; u++) o = __builtin_fmaf(v[u], fw[g + u], o);
+        for (int u = 0; u < 8; u++) o = __builtin_fmaf(w8[u], fw[g + u], o);
     }
     for (; g < G; g++) o = __builtin_fmaf(pd[(size_t)g * (HD + 2)], fw[g], o);
     const float r = L > 0.0f ? o / L : 0.0f;
@@ -811,8 +871,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
         __syncthreads();
         if (tid < 64) {
             const float4 f4 = reinterpret_cast<const float4*>(mo)[tid];
-            const float v[4] = {f4.x, f4.y, f4.z, f4.w};
-            quantize_block_wave(v, tid, a.q8, a.n_heads * HD / 256, h * (HD / 256) + slice);
+            const float v4[4] = {f4.x, f4.y, f4.z, f4.w};
+            quantize_block_wave(v4, tid, a.q8, a.n_heads * HD / 256, h * (HD / 256) + slice);
         }
     }
 }

@@ -736,19 +736,35 @@ __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __res
             }
         }
     };
-    // the first batch of the first row group is in flight before x is staged
+    // x (kQ6Xpt float4 per thread, the rest in a loop) and then the first
+    // batch of the first row group are in flight before anything waits: a
+    // load-then-store loop would wait for every earlier load on each of its
+    // iterations
+    constexpr int kQ6Xpt = 4;
+    const int n4 = nb * 64;                // float4 of x; a multiple of 64, so a wave's lanes agree
+    float4 xv[kQ6Xpt];
+#pragma unroll
+    for (int j = 0; j < kQ6Xpt; j++) {
+        const int i = tid + 256 * j;
+        xv[j] = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     Batch bt;
     int rg = blockIdx.x;
     bool pre = rg < ngroups && rg * RPW + rr < d && ks < nb;
     if (pre) load(rg * RPW + rr, ks, bt);
-    for (int i = tid; i < nb * 64; i += 256) {
-        const float4 v = reinterpret_cast<const float4*>(x)[i];
+    // i covers elements 4i..4i+3; pairs of float4 make one run of 8
+    auto stage = [&](int i, const float4& v) {
         reinterpret_cast<float4*>(xs)[i] = v;
-        // i covers elements 4i..4i+3; pairs of float4 make one run of 8
         const float s4 = (v.x + v.y) + (v.z + v.w);
         const float o4 = __shfl_xor(s4, 1, 64);
         if ((i & 1) == 0) x8[i >> 1] = s4 + o4;
+    };
+#pragma unroll
+    for (int j = 0; j < kQ6Xpt; j++) {
+        const int i = tid + 256 * j;
+        if (i < n4) stage(i, xv[j]);
     }
+    for (int i = tid + 256 * kQ6Xpt; i < n4; i += 256) stage(i, reinterpret_cast<const float4*>(x)[i]);
     __syncthreads();
     for (; rg < ngroups; rg += gridDim.x) {
         const int row = rg * RPW + rr;
@@ -820,6 +836,101 @@ using namespace g4;
 
 // ------------------------------------------------------------------------
 // host side
+// ------------------------------------------------------------------------
+// Q6_K x fp32, one K slice per 8-lane group (rows of up to 64 blocks)
+// ------------------------------------------------------------------------
+// Group g of a workgroup of 8*nb threads owns block g of every row, so the
+// 32 elements of x its lanes use (lane L = 4h+u: 128h + 32k + 8u + e, the
+// mapping of gemv_q6k_rows_kernel) and their run sums stay in registers:
+// no staging of x through LDS and no LDS reads in the loop.  A workgroup
+// runs R consecutive rows and issues every weight load of them before it
+// waits (up to 84 KB per workgroup at the FFN-down shape, one workgroup per
+// CU).  Per row the group's partial dot is summed over its 8 lanes, and the
+// nb block partials of each row are added once through LDS.  Same
+// arithmetic per block as gemv_q6k_rows_kernel; the blocks are summed as a
+// tree (fp32 tolerance of the reference's sequential sum).
+namespace g4 {
+
+constexpr int kQ6SliceRows = 10;
+constexpr int kQ6SliceMaxNb = 64;
+
+template <int R>
+__global__ __launch_bounds__(8 * kQ6SliceMaxNb) void gemv_q6k_kslice_kernel(const uint8_t* __restrict__ w,
+                                                                          const float* __restrict__ x,
+                                                                          float* __restrict__ out, int nb, int d) {
+    __shared__ float part[R][kQ6SliceMaxNb];
+    const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
+    const int r0 = blockIdx.x * R;
+    const Q6KPlanes P = q6k_planes((size_t)d * nb);
+    uint4 ql[R];
+    uint2 qh[R], sc[R];
+    uint32_t dv[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const size_t blk = (size_t)min(r0 + r, d - 1) * nb + g;
+        ql[r] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
+        qh[r] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
+        sc[r] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+        dv[r] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+    }
+    // x of this lane: runs k = 0..3 of 8 elements at g*256 + 128h + 32k + 8u
+    float4 xa[4], xb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)g * 256 + 128 * h + 32 * k + 8 * u);
+        xa[k] = xp[0];
+        xb[k] = xp[1];
+    }
+    float s8[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) s8[k] = ((xa[k].x + xa[k].y) + (xa[k].z + xa[k].w)) + ((xb[k].x + xb[k].y) + (xb[k].z + xb[k].w));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float df = half_bits_to_f32(dv[r]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t qa = (kk & 1) ? ql[r].z : ql[r].x;      // codes e = 0..3
+            const uint32_t qb = (kk & 1) ? ql[r].w : ql[r].y;      // codes e = 4..7
+            const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+            const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+            const uint32_t ca = la | (((qh[r].x >> (2 * kk)) & 0x03030303u) << 4);   // q in [0, 63]
+            const uint32_t cb = lb | (((qh[r].y >> (2 * kk)) & 0x03030303u) << 4);
+            // sum_e x_e (q_e - 32) = sum_e x_e q_e - 32 * sum_e x_e
+            float dot = xa[kk].x * (float)(ca & 0xff);
+            dot = __builtin_fmaf(xa[kk].y, (float)((ca >> 8) & 0xff), dot);
+            dot = __builtin_fmaf(xa[kk].z, (float)((ca >> 16) & 0xff), dot);
+            dot = __builtin_fmaf(xa[kk].w, (float)(ca >> 24), dot);
+            dot = __builtin_fmaf(xb[kk].x, (float)(cb & 0xff), dot);
+            dot = __builtin_fmaf(xb[kk].y, (float)((cb >> 8) & 0xff), dot);
+            dot = __builtin_fmaf(xb[kk].z, (float)((cb >> 16) & 0xff), dot);
+            dot = __builtin_fmaf(xb[kk].w, (float)(cb >> 24), dot);
+            dot = __builtin_fmaf(-32.0f, s8[kk], dot);
+            const int sbi = (u >> 1) + 2 * kk;
+            const int8_t s8i = (int8_t)byte_of(sbi < 4 ? sc[r].x : sc[r].y, sbi & 3);
+            acc = __builtin_fmaf(df * (float)s8i, dot, acc);
+        }
+        // the group's 8 lanes (quad xor 1, 2, then the two quads)
+        acc += dpp_f<kDppXor1>(acc);
+        acc += dpp_f<kDppXor2>(acc);
+        acc += dpp_f<kDppHalfMirror>(acc);
+        if (L == 0) part[r][g] = acc;
+    }
+    __syncthreads();
+    // row r: 8 lanes add nb/8 block partials each, then the 8 lanes
+    for (int t = tid; t < R * 8; t += blockDim.x) {
+        const int r = t >> 3, j = t & 7;
+        float s = 0.0f;
+        for (int b = j; b < nb; b += 8) s += part[r][b];
+        s += dpp_f<kDppXor1>(s);
+        s += dpp_f<kDppXor2>(s);
+        s += dpp_f<kDppHalfMirror>(s);
+        if (j == 0 && r0 + r < d) out[r0 + r] = s;
+    }
+}
+
+}  // namespace g4
+
 // ------------------------------------------------------------------------
 namespace {
 
@@ -915,6 +1026,11 @@ void launch_q6_ks(const void* w, const float* x, float* o, int nb, int d, float 
 
 template <bool SOFTCAP>
 int launch_q6_f32(const void* w, const float* x, float* o, int nb, int d, float cap) {
+    if (!SOFTCAP && nb <= kQ6SliceMaxNb && nb % 8 == 0) {
+        hipLaunchKernelGGL((gemv_q6k_kslice_kernel<kQ6SliceRows>), dim3((d + kQ6SliceRows - 1) / kQ6SliceRows),
+                           dim3(8 * nb), 0, g4_stream(), (const uint8_t*)w, x, o, nb, d);
+        return g4_check_launch("gemv_q6k_kslice_kernel");
+    }
     const int target = 2 * g4_num_cus();
     if ((d + 31) / 32 >= target) launch_q6_ks<SOFTCAP, 1>(w, x, o, nb, d, cap);
     else if ((d + 15) / 16 >= target) launch_q6_ks<SOFTCAP, 2>(w, x, o, nb, d, cap);
