@@ -844,14 +844,14 @@ using namespace g4;
 // mapping of gemv_q6k_rows_kernel) and their run sums stay in registers:
 // no staging of x through LDS and no LDS reads in the loop.  A workgroup
 // runs R consecutive rows and issues every weight load of them before it
-// waits (up to 84 KB per workgroup at the FFN-down shape, one workgroup per
-// CU).  Per row the group's partial dot is summed over its 8 lanes, and the
+// waits (42 KB per workgroup at the FFN-down shape, two workgroups per CU;
+// a sweep of R = 3..10 there: 5 fastest, 7.6 us against 8.9 us at 10).  Per row the group's partial dot is summed over its 8 lanes, and the
 // nb block partials of each row are added once through LDS.  Same
 // arithmetic per block as gemv_q6k_rows_kernel; the blocks are summed as a
 // tree (fp32 tolerance of the reference's sequential sum).
 namespace g4 {
 
-constexpr int kQ6SliceRows = 10;
+constexpr int kQ6SliceRows = 5;       // 512 workgroups at the FFN-down shape: two per CU
 constexpr int kQ6SliceMaxNb = 64;
 
 template <int R>
