@@ -549,26 +549,38 @@ __device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2_t, a), __builtin_bit_cast(s2_t, b), c, false);
 }
 
-template <bool Q5, int NB, int NMAT>
-__global__ __launch_bounds__(64) void gemv_q45_stream_kernel(const uint8_t* __restrict__ w0,
-                                                             const uint8_t* __restrict__ w1,
-                                                             const uint8_t* __restrict__ q8, float* __restrict__ out,
-                                                             int d, const float* __restrict__ aux) {
+// PRO: a 256-thread workgroup of four such waves whose Q8_K vector is made
+// by the workgroup itself: the residual step, norm and Q8_K of ResidualArgs
+// (its loads issued first, then every wave's header and weight loads, so the
+// norm's arithmetic runs while the weights stream in), into LDS; workgroup 0
+// also stores the residual stream, xb2 and the Q8_K when asked.
+template <bool Q5, int NB, int NMAT, bool PRO = false>
+__global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const uint8_t* __restrict__ w0,
+                                                                         const uint8_t* __restrict__ w1,
+                                                                         const uint8_t* __restrict__ q8,
+                                                                         float* __restrict__ out, int d,
+                                                                         const float* __restrict__ aux,
+                                                                         const ResidualArgs ra) {
     constexpr int RPW = 8 / NMAT;                 // rows per wave
+    constexpr int NWV = PRO ? 4 : 1;              // waves per workgroup
     constexpr int Q8B = NB * 292;                 // device Q8_K bytes
     constexpr int Q8C = Q8B / 16, Q8T = (Q8B - Q8C * 16) / 4;
-    constexpr int HC = RPW * NB;                  // header chunks per matrix
-    constexpr int QPL = (Q8C + 63) / 64, HPL = (HC + 63) / 64;
+    constexpr int HC = RPW * NB;                  // header chunks per matrix and wave
+    constexpr int QPL = PRO ? 0 : (Q8C + 63) / 64, HPL = (HC + 63) / 64;
     __shared__ __align__(16) uint8_t sq[Q8B + 16];
-    __shared__ __align__(16) uint8_t sh[NMAT][HC * 16];
-    const int lane = threadIdx.x, l = lane & 7, k = l & 3, grp = (lane >> 3) & (RPW - 1);
+    __shared__ __align__(16) uint8_t shw[NWV][NMAT][HC * 16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l = lane & 7, k = l & 3;
+    const int grp = (lane >> 3) & (RPW - 1);
     const int m = NMAT == 2 ? lane >> 5 : 0;
-    const int r0 = blockIdx.x * RPW;
+    const int r0 = (blockIdx.x * NWV + wv) * RPW;
     const int row = min(r0 + grp, d - 1);
     const uint32_t nblk = (uint32_t)d * NB;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk, qh_off = 128u * nblk;   // q4k_planes / q5k_planes
+    uint8_t (&sh)[NMAT][HC * 16] = shw[wv];
 
-    uint4 qv[QPL], hv[NMAT][HPL];
+    [[maybe_unused]] ResidualRegs<NB> rr;
+    if constexpr (PRO) residual_load<NB>(ra, rr);
+    uint4 qv[QPL > 0 ? QPL : 1], hv[NMAT][HPL];
     uint32_t tv = 0u;
 #pragma unroll
     for (int j = 0; j < QPL; j++) {
@@ -576,7 +588,7 @@ __global__ __launch_bounds__(64) void gemv_q45_stream_kernel(const uint8_t* __re
         qv[j] = make_uint4(0u, 0u, 0u, 0u);
         if (c < Q8C) qv[j] = reinterpret_cast<const uint4*>(q8)[c];
     }
-    if (lane < Q8T) tv = reinterpret_cast<const uint32_t*>(q8 + Q8C * 16)[lane];
+    if (!PRO && lane < Q8T) tv = reinterpret_cast<const uint32_t*>(q8 + Q8C * 16)[lane];
 #pragma unroll
     for (int j = 0; j < HPL; j++) {
         const int c = lane + 64 * j;
@@ -597,12 +609,21 @@ __global__ __launch_bounds__(64) void gemv_q45_stream_kernel(const uint8_t* __re
         qh[b] = Q5 ? *reinterpret_cast<const uint32_t*>(wm + qh_off + (rb + b) * 32u + 4 * l) : 0u;
     }
     __builtin_amdgcn_sched_barrier(0);   // all loads issued before the LDS stores wait for the first ones
+    if constexpr (PRO) {
+        __shared__ __align__(16) float pbuf[NB * 256];
+        __shared__ float red[16];
+        residual_finish<NB>(ra, rr, pbuf, red, blockIdx.x == 0);
+        __syncthreads();
+        quantize_blocks_wg(pbuf, sq, NB);
+        if (blockIdx.x == 0 && ra.q8) quantize_blocks_wg(pbuf, ra.q8, NB);
+    } else {
 #pragma unroll
-    for (int j = 0; j < QPL; j++) {
-        const int c = lane + 64 * j;
-        if (c < Q8C) reinterpret_cast<uint4*>(sq)[c] = qv[j];
+        for (int j = 0; j < QPL; j++) {
+            const int c = lane + 64 * j;
+            if (c < Q8C) reinterpret_cast<uint4*>(sq)[c] = qv[j];
+        }
+        if (lane < Q8T) reinterpret_cast<uint32_t*>(sq + Q8C * 16)[lane] = tv;
     }
-    if (lane < Q8T) reinterpret_cast<uint32_t*>(sq + Q8C * 16)[lane] = tv;
 #pragma unroll
     for (int j = 0; j < HPL; j++) {
         const int c = lane + 64 * j;
@@ -983,8 +1004,15 @@ void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float*
 template <bool Q5, int NB>
 void launch_q45_pro_nm(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                        const Stack2& st) {
-    if (w2) launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra, st);
-    else launch_q45_pro<Q5, 1, NB>(w, nullptr, o, d, aux, ra, st);
+    if (w2 && !st.w && !st.w6) {
+        // gate|up: the streaming kernel, four waves of 4 rows x {gate, up}
+        hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, NB, 2, true>), dim3((d + 15) / 16), dim3(256), 0, g4_stream(),
+                           (const uint8_t*)w, (const uint8_t*)w2, nullptr, o, d, nullptr, ra);
+    } else if (w2) {
+        launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra, st);
+    } else {
+        launch_q45_pro<Q5, 1, NB>(w, nullptr, o, d, aux, ra, st);
+    }
 }
 
 // rows of nb blocks; the split of a row over lane groups grows with the work
@@ -997,9 +1025,10 @@ int launch_q45(const void* w0, const void* w1, const void* q8, float* o, int nb,
         const dim3 grid((d + 8 / NMAT - 1) / (8 / NMAT));
         const uint8_t* a = (const uint8_t*)w0;
         const uint8_t* b = (const uint8_t*)w1;
-        if (nb == 8) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 8, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
-        else if (nb == 10) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 10, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
-        else hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 16, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux);
+        const ResidualArgs none{};
+        if (nb == 8) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 8, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux, none);
+        else if (nb == 10) hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 10, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux, none);
+        else hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, 16, NMAT>), grid, dim3(64), 0, g4_stream(), a, b, (const uint8_t*)q8, o, d, aux, none);
         return g4_check_launch("gemv_q45_stream_kernel");
     }
     switch (nb) {   // unrolled for the row lengths of the model (256, 2048, 2560, 4096)

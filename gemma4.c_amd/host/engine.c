@@ -674,13 +674,13 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
                                 1.0f, swa ? m->G_swa : m->G_full, m->attn_part, m->q_out, o_q8 ? m->q8 : NULL));
         if ((rc = mm(m, m->xb2, m->q_out, &m->wo[l], o_q8))) return rc;
         /* post_attention_norm + residual, then ffn_norm + Q8_K (main.c:1960-1975),
-         * in place (one workgroup); as a prologue of the 20480-row gate|up GEMV
-         * it would run in every one of its workgroups and costs more than the
-         * launch it saves */
+         * in place (one workgroup), then gelu(gate) * up (main.c:1976-1980).  As
+         * the prologue of every workgroup of the gate|up GEMV (g4_mm_residual_q8
+         * with both matrices) the step costs as much as this launch: 14.5 us
+         * against 5.0 + 9.5 us at the E4B shape */
         const int q8_ffn = is_q8_type(m->gate[l].type);
         CK(g4_residual_norm(x, m->xb2, m->post_attn_norm[l], NULL, m->ffn_norm[l], m->xb2, q8_ffn ? m->q8 : NULL, 0, dim,
                             c->eps));
-        /* gelu(gate) * up (main.c:1976-1980) */
         CK(g4_mm_gate_up_gelu(m->hb, m->gate[l].p, m->up[l].p, dim, c->hidden, m->gate[l].type, m->q8));
         /* down (main.c:1981) */
         if ((rc = mm(m, m->xb2, m->hb, &m->down[l], 0))) return rc;
