@@ -68,6 +68,20 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ ta
     }
 }
 
+// rows: position pos0 + blockIdx.x -> tab + blockIdx.x * npair
+__global__ __launch_bounds__(256) void rope_table_rows_kernel(float2* __restrict__ tab, int pos0, int npair, float ts,
+                                                              float fs, const float* __restrict__ ff) {
+    const int p = pos0 + blockIdx.x;
+    float2* t = tab + (size_t)blockIdx.x * npair;
+    for (int j = threadIdx.x; j < npair; j += blockDim.x) {
+        float theta = (float)p;
+        for (int i = 0; i < j; i++) theta *= ts;
+        const float f = ff ? ff[j] : 1.0f;
+        const float angle = (fs * theta) / f;
+        t[j] = make_float2(cosf(angle), sinf(angle));
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ vec, int hd, int n_rot, int pos, float ts,
                                                    float fs, const float* __restrict__ ff) {
     extern __shared__ __align__(16) float seg[];
@@ -95,10 +109,8 @@ struct QKVArgs {
     float ts, fs, eps;
 };
 
-__global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
-    extern __shared__ __align__(16) float seg[];
-    __shared__ float red[16];
-    const int b = blockIdx.x, hd = a.hd;
+__device__ __forceinline__ void qkv_post_body(const QKVArgs& a, int b, float* seg, float* red) {
+    const int hd = a.hd;
     const int pos = a.dpos ? *a.dpos : a.pos;
     const float* src;
     const float* w;
@@ -133,6 +145,43 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
     for (int i = threadIdx.x; i < hd; i += blockDim.x) dst[i] = seg[i];
 }
 
+__global__ __launch_bounds__(256) void qkv_post_kernel(QKVArgs a) {
+    extern __shared__ __align__(16) float seg[];
+    __shared__ float red[16];
+    qkv_post_body(a, blockIdx.x, seg, red);
+}
+
+// token z = blockIdx.y of a prompt chunk: q, k, v rows (n_heads*hd, n_kv*hd
+// floats apart), K/V stored to row z of the chunk buffers kc/vc (stride
+// kv_stride), RoPE pairs from row z of the position table
+__global__ __launch_bounds__(256) void qkv_post_rows_kernel(QKVArgs a) {
+    extern __shared__ __align__(16) float seg[];
+    __shared__ float red[16];
+    const size_t z = blockIdx.y;
+    a.q += z * (size_t)a.n_heads * a.hd;
+    if (a.k) {
+        a.k += z * (size_t)a.n_kv * a.hd;
+        a.v += z * (size_t)a.n_kv * a.hd;
+        a.kc += z * (size_t)a.kv_stride;
+        a.vc += z * (size_t)a.kv_stride;
+    }
+    a.tab += z * (size_t)(a.n_rot / 2);
+    qkv_post_body(a, blockIdx.x, seg, red);
+}
+
+// rows z of the chunk buffers -> cache slots of positions pos0 + z (a ring
+// keeps the last `ring` of them)
+__global__ __launch_bounds__(256) void kv_store_rows_kernel(float* __restrict__ kc, float* __restrict__ vc,
+                                                            const float* __restrict__ kin, const float* __restrict__ vin,
+                                                            int kv_stride, int ring, int pos0, int kvd) {
+    const int z = blockIdx.x, pos = pos0 + z;
+    const size_t slot = ring > 0 ? pos % ring : pos;
+    for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
+        kc[slot * kv_stride + i] = kin[(size_t)z * kv_stride + i];
+        vc[slot * kv_stride + i] = vin[(size_t)z * kv_stride + i];
+    }
+}
+
 // ---- split-T decode attention --------------------------------------------
 // Workspace (g4_attn_part_bytes): the partials [n_heads][G][hd+2] =
 // (o[hd], max, sum) of every chunk.
@@ -163,7 +212,31 @@ struct AttnArgs {
     const float2* tab;     // (cos, sin) of each RoPE pair at this position
     int n_rot;
     float eps;
+    // query rows of a prompt chunk (qrows > 0, register kernel only): query
+    // z = blockIdx.z sits at position p0 + z and sees its own window; K/V of
+    // positions >= p0 come from row t - p0 of kchunk/vchunk (stride
+    // kv_stride), earlier ones from the cache; q and out rows n_heads*hd
+    // apart, partials part_z floats apart, Q8_K rows q8_row bytes apart
+    int qrows, p0;
+    const float* kchunk;
+    const float* vchunk;
+    size_t part_z, q8_row;
 };
+
+// the query row of this workgroup (qrows > 0): pointers and window
+__device__ __forceinline__ void attn_query_row(AttnArgs& a, bool merge) {
+    const size_t z = blockIdx.z;
+    const size_t qd = (size_t)a.n_heads * a.hd;
+    a.q += z * qd;
+    a.part += z * a.part_z;
+    if (merge) {
+        a.out += z * qd;
+        if (a.q8) a.q8 += z * a.q8_row;
+    }
+    const int pos = a.p0 + (int)z;
+    a.t_start = a.window > 0 ? max(0, pos + 1 - a.window) : 0;
+    a.nwin = pos + 1 - a.t_start;
+}
 
 constexpr int kAttnThreads = 256;
 constexpr int kChunkMax = 1024;     // positions per workgroup
@@ -603,6 +676,7 @@ __host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2) {
 
 template <int HD, int KVM>
 __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
+    if (a.qrows) attn_query_row(a, false);
     constexpr int W = HD / 128;
     constexpr int NW = kAttnThreads / 64;
     constexpr int PPW = chunk_ppw<HD, KVM>();
@@ -662,8 +736,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
         for (int p = 0; p < PPW; p++) {
             const int i = min(r * NW * PPW + wave * PPW + p, cnt - 1);
-            kr[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
-            vr[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
+            const int t = cb + i;   // position (position mode; prompt-chunk rows only)
+            if (a.kchunk && t >= a.p0) {
+                const size_t off = (size_t)(t - a.p0) * a.kv_stride + (size_t)kvh * HD;
+                kr[p].load(a.kchunk + off, lane);
+                vr[p].load(a.vchunk + off, lane);
+            } else {
+                kr[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
+                vr[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
+            }
         }
     };
     if (cnt > 0) load_kv(0);
@@ -750,6 +831,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
                 for (int i = 0; i < W; i++) o[h].v[k][i] *= ah;
 #pragma unroll
             for (int p = 0; p < PPW; p++) {
+                // entries past nvalid were loaded before the position was
+                // known (ring slots no position has written yet may hold any
+                // bits): their weight is 0, but 0 * NaN is not, so skip them
+                if (base + p >= nvalid) continue;
                 const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), xlane(h * PPW + p, LV)));
 #pragma unroll
                 for (int k = 0; k < 2; k++)
@@ -815,6 +900,7 @@ constexpr int kMergeReg = 32;
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+    if (a.qrows) attn_query_row(a, true);
     __shared__ float fw[kMaxChunks];
     __shared__ float red[16];
     __shared__ __align__(16) float mo[256];
@@ -894,20 +980,22 @@ void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
 
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
-    const dim3 grid(a.G, a.n_kv);
+    const int zq = a.qrows > 0 ? a.qrows : 1;
+    const dim3 grid(a.G, a.n_kv, zq);
     // q heads per kv head rounded up to a power of two (the register kernel's
     // template); its LDS must fit the default 64 KB
     const int kp = kvm <= 1 ? 1 : kvm <= 2 ? 2 : kvm <= 4 ? 4 : 8;
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
         if (a.hd == 256) {
             launch_chunk<256>(a, kp, grid);
-            hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1), dim3(256), 0, g4_stream(), a);
+            hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1, zq), dim3(256), 0, g4_stream(), a);
         } else {
             launch_chunk<512>(a, kp, grid);
-            hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2), dim3(256), 0, g4_stream(), a);
+            hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2, zq), dim3(256), 0, g4_stream(), a);
         }
         return g4_check_launch("attn_chunk_kernel/attn_merge_kernel");
     }
+    if (a.qrows) return g4_fail(G4_ERR_ARG, "attention over query rows: %d q heads per kv head at head_dim %d unsupported", kvm, a.hd);
     const size_t lds = attn_lds(a.hd, kvm, a.q_norm != nullptr);
     if (a.hd == 256) {
         hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
@@ -1021,6 +1109,76 @@ extern "C" int g4_kv_append_rope(float* k, float* v, const float* k_norm, float*
 }
 
 extern "C" size_t g4_attn_part_bytes(int n_heads, int hd, int G) { return (size_t)n_heads * G * (hd + 2) * 4; }
+
+// (cos, sin) tables of positions pos0 .. pos0+m-1, n_rot/2 pairs each
+extern "C" int g4_rope_table_rows(float* tab, int pos0, int m, int n_rot, float freq_base, float freq_scale,
+                                  const float* freq_factors) {
+    G4_CHECK_ARG(tab && pos0 >= 0 && m > 0 && n_rot > 0 && n_rot % 2 == 0 && n_rot <= 2048,
+                 "g4_rope_table_rows: bad arguments");
+    const float ts = powf(freq_base, -2.0f / (float)n_rot);
+    hipLaunchKernelGGL(rope_table_rows_kernel, dim3(m), dim3(256), 0, g4_stream(), (float2*)tab, pos0, n_rot / 2, ts,
+                       freq_scale, freq_factors);
+    return g4_check_launch("rope_table_rows_kernel");
+}
+
+// qkv_post over m tokens: q rows normalised and rotated in place; k/v rows
+// (nullable) normalised (k rotated) into rows of kout/vout (stride kv_stride)
+extern "C" int g4_qkv_post_rows(float* q, const float* q_norm, const float* k, const float* v, const float* k_norm,
+                                float* kout, float* vout, int kv_stride, const float* tab_rows, int m, int n_heads,
+                                int n_kv, int hd, int n_rot, float eps) {
+    G4_CHECK_ARG(q && q_norm && tab_rows && m > 0 && m <= 65535 && hd > 0 && hd <= 1024 && n_rot > 0 && n_rot <= hd,
+                 "qkv_post_rows: bad arguments");
+    G4_CHECK_ARG(!k || (v && k_norm && kout && vout && kv_stride >= n_kv * hd), "qkv_post_rows: bad K/V arguments");
+    QKVArgs a{};
+    a.q = q; a.q_norm = q_norm; a.k = k; a.v = v; a.k_norm = k_norm; a.kc = kout; a.vc = vout;
+    a.dpos = nullptr; a.ff = nullptr; a.pos = 0; a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.n_rot = n_rot;
+    a.kv_stride = kv_stride; a.ring = 0; a.ts = 1.0f; a.fs = 1.0f; a.eps = eps;
+    a.tab = (const float2*)tab_rows;
+    const int grid = n_heads + (k ? 2 * n_kv : 0);
+    hipLaunchKernelGGL(qkv_post_rows_kernel, dim3(grid, m), dim3(256), (size_t)hd * 4, g4_stream(), a);
+    return g4_check_launch("qkv_post_rows_kernel");
+}
+
+// rows 0..m-1 of kin/vin (stride kv_stride) -> the cache slots of positions
+// pos0 .. pos0+m-1 (slot = pos % ring with a ring; only the last `ring`
+// rows are kept)
+extern "C" int g4_kv_store_rows(float* kc, float* vc, const float* kin, const float* vin, int kv_stride, int ring,
+                                int pos0, int m, int kvd) {
+    G4_CHECK_ARG(kc && vc && kin && vin && m > 0 && pos0 >= 0 && kvd > 0 && kv_stride >= kvd && ring >= 0,
+                 "g4_kv_store_rows: bad arguments");
+    const int first = ring > 0 && m > ring ? m - ring : 0;
+    hipLaunchKernelGGL(kv_store_rows_kernel, dim3(m - first), dim3(256), 0, g4_stream(), kc, vc,
+                       kin + (size_t)first * kv_stride, vin + (size_t)first * kv_stride, kv_stride, ring, pos0 + first,
+                       kvd);
+    return g4_check_launch("kv_store_rows_kernel");
+}
+
+// The attention block for m query rows of a prompt chunk at positions
+// p0 .. p0+m-1: q already normalised and rotated (n_heads*hd floats per row),
+// the chunk's own K/V in rows of kchunk/vchunk (stride kv_stride), earlier
+// positions in the (ring) cache; window 0 = full attention.  part holds
+// m * g4_attn_part_bytes(n_heads, hd, G) bytes; out gets n_heads*hd floats
+// per row and, if q8, the Q8_K rows (g4_q8K_row_stride(n_heads*hd) apart).
+extern "C" int g4_attn_decode_rows(const float* q, const float* kc, const float* vc, const float* kchunk,
+                                   const float* vchunk, int kv_stride, int ring, int p0, int m, int window, int n_heads,
+                                   int n_kv, int hd, float attn_scale, int G, float* part, float* out, void* q8) {
+    int rc = check_attn_shape("attn_decode_rows", n_heads, n_kv, hd, G);
+    if (rc) return rc;
+    G4_CHECK_ARG(q && kc && vc && kchunk && vchunk && part && out && p0 >= 0 && m > 0 && m <= 65535,
+                 "attn_decode_rows: bad arguments");
+    G4_CHECK_ARG(kv_stride >= n_kv * hd && ring >= 0 && window >= 0, "attn_decode_rows: bad cache arguments");
+    G4_CHECK_ARG(ring == 0 || (window > 0 && window <= ring), "attn_decode_rows: a ring needs window <= ring");
+    const int nmax = window > 0 && window < p0 + m ? window : p0 + m;
+    G4_CHECK_ARG((nmax + G - 1) / G <= kChunkMax, "attn_decode_rows: %d chunks too few for %d positions", G, nmax);
+    AttnArgs a = {};
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = nullptr; a.out = out; a.q8 = (uint8_t*)q8; a.part = part;
+    a.window = window; a.kv_stride = kv_stride; a.ring = ring;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = G;
+    a.qrows = m; a.p0 = p0; a.kchunk = kchunk; a.vchunk = vchunk;
+    a.part_z = g4_attn_part_bytes(n_heads, hd, G) / 4;
+    a.q8_row = q8 ? g4_q8K_row_stride(n_heads * hd) : 0;
+    return launch_attn(a);
+}
 
 static int attn_common(const char* who, AttnArgs& a) {
     int rc = check_attn_shape(who, a.n_heads, a.n_kv, a.hd, a.G);

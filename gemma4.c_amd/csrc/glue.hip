@@ -77,6 +77,15 @@ __global__ __launch_bounds__(256) void emb_lookup_kernel(float* __restrict__ o, 
     o[i] = use_scale ? v * scale : v;
 }
 
+// token z = blockIdx.y of a prompt chunk -> row z of o
+__global__ __launch_bounds__(256) void emb_lookup_rows_kernel(float* __restrict__ o, const void* w, int type, int rows,
+                                                              int dim, const int* __restrict__ dtok, float scale) {
+    const int id = dtok[blockIdx.y];
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim || id < 0 || id >= rows) return;
+    o[(size_t)blockIdx.y * dim + i] = table_elem(w, type, rows, dim, id, i) * scale;
+}
+
 // build_ple after the context projection (main.c:1751-1777): workgroup l
 // owns slice l of pd elements.
 //   row  = emb_lookup(ple_tok, token)[l*pd + i] * sc_tok
@@ -92,14 +101,12 @@ struct PleArgs {
     float sc_tok, sc_ctx, mix, eps;
 };
 
-__global__ __launch_bounds__(256) void ple_finish_kernel(PleArgs a) {
-    extern __shared__ __align__(16) float c[];
-    __shared__ float red[16];
-    const int l = blockIdx.x, pd = a.pd;
-    const int id = a.dtok ? *a.dtok : a.tok;
+__device__ __forceinline__ void ple_finish_slice(const PleArgs& a, int l, float* __restrict__ ple,
+                                                 const float* __restrict__ ctx, int id, float* c, float* red) {
+    const int pd = a.pd;
     float ss = 0.0f;
     for (int i = threadIdx.x; i < pd; i += blockDim.x) {
-        const float v = a.ctx[(size_t)l * pd + i] * a.sc_ctx;
+        const float v = ctx[(size_t)l * pd + i] * a.sc_ctx;
         c[i] = v;
         ss += v * v;
     }
@@ -109,8 +116,31 @@ __global__ __launch_bounds__(256) void ple_finish_kernel(PleArgs a) {
     for (int i = threadIdx.x; i < pd; i += blockDim.x) {
         const float ctxn = (c[i] * s) * a.proj_norm[i];
         const float row = table_elem(a.ple_tok, a.type, a.rows, pd * a.L, id, l * pd + i) * a.sc_tok;
-        a.ple[(size_t)l * pd + i] = (row + ctxn) * a.mix;
+        ple[(size_t)l * pd + i] = (row + ctxn) * a.mix;
     }
+}
+
+__global__ __launch_bounds__(256) void ple_finish_kernel(PleArgs a) {
+    extern __shared__ __align__(16) float c[];
+    __shared__ float red[16];
+    ple_finish_slice(a, blockIdx.x, a.ple, a.ctx, a.dtok ? *a.dtok : a.tok, c, red);
+}
+
+// token z = blockIdx.y of a prompt chunk: its ple and ctx rows are L*pd apart
+__global__ __launch_bounds__(256) void ple_finish_rows_kernel(PleArgs a) {
+    extern __shared__ __align__(16) float c[];
+    __shared__ float red[16];
+    const size_t z = blockIdx.y, off = z * (size_t)a.L * a.pd;
+    ple_finish_slice(a, blockIdx.x, a.ple + off, a.ctx + off, a.dtok[z], c, red);
+}
+
+// o[z][i] = gelu(g[z][i]) * u[z*ustride + i] (main.c:1976-1980, 1989-1993 for
+// m rows of d)
+__global__ __launch_bounds__(256) void gelu_mul_rows_kernel(float* __restrict__ o, const float* __restrict__ g,
+                                                            const float* __restrict__ u, int d, int ustride) {
+    const size_t z = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < d) o[z * d + i] = gelu_ref(g[z * d + i]) * u[z * ustride + i];
 }
 
 // g = gelu(g) * ple (main.c:1989-1993), then Q8_K of g for the next GEMV
@@ -228,6 +258,32 @@ extern "C" int g4_ple_finish(float* ple, const float* ctx, const void* ple_tok, 
     PleArgs a{ple_tok, ctx, proj_norm, ple, dtok, tok, type, rows, pd, L, sc_tok, sc_ctx, mix, eps};
     hipLaunchKernelGGL(ple_finish_kernel, dim3(L), dim3(256), (size_t)pd * 4, g4_stream(), a);
     return g4_check_launch("ple_finish_kernel");
+}
+
+extern "C" int g4_emb_lookup_rows(float* o, const void* w, int type, int rows, const int* dtok, int m, int dim,
+                                  float scale) {
+    G4_CHECK_ARG(o && w && dtok && dim > 0 && rows > 0 && m > 0 && m <= 65535, "g4_emb_lookup_rows: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    hipLaunchKernelGGL(emb_lookup_rows_kernel, dim3((dim + 255) / 256, m), dim3(256), 0, g4_stream(), o, w, type, rows,
+                       dim, dtok, scale);
+    return g4_check_launch("emb_lookup_rows_kernel");
+}
+
+extern "C" int g4_ple_finish_rows(float* ple, const float* ctx, const void* ple_tok, int type, int rows,
+                                  const float* proj_norm, const int* dtok, int m, int pd, int L, float sc_tok,
+                                  float sc_ctx, float mix, float eps) {
+    G4_CHECK_ARG(ple && ctx && ple_tok && proj_norm && dtok && pd > 0 && pd <= 4096 && L > 0 && m > 0 && m <= 65535,
+                 "g4_ple_finish_rows: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    PleArgs a{ple_tok, ctx, proj_norm, ple, dtok, 0, type, rows, pd, L, sc_tok, sc_ctx, mix, eps};
+    hipLaunchKernelGGL(ple_finish_rows_kernel, dim3(L, m), dim3(256), (size_t)pd * 4, g4_stream(), a);
+    return g4_check_launch("ple_finish_rows_kernel");
+}
+
+extern "C" int g4_gelu_mul_rows(float* o, const float* g, const float* u, int d, int m, int ustride) {
+    G4_CHECK_ARG(o && g && u && d > 0 && m > 0 && m <= 65535 && ustride >= 0, "g4_gelu_mul_rows: bad arguments");
+    hipLaunchKernelGGL(gelu_mul_rows_kernel, dim3((d + 255) / 256, m), dim3(256), 0, g4_stream(), o, g, u, d, ustride);
+    return g4_check_launch("gelu_mul_rows_kernel");
 }
 
 extern "C" int g4_gelu_mul_quant(float* g, const float* ple, int n, void* q8) {

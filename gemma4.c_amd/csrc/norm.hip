@@ -62,6 +62,26 @@ __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArg
     }
 }
 
+// row z = blockIdx.x of m rows of n (x, y, xb2 n apart; q8 rows q8row bytes
+// apart): the same step per row as residual_norm_kernel (same thread count
+// and reduction tree when launched with the same EPT and block size)
+template <int EPT>
+__global__ __launch_bounds__(kNormThreads) void residual_rows_kernel(ResidualArgs a, size_t q8row) {
+    extern __shared__ __align__(16) float buf[];
+    __shared__ float red[16];
+    const size_t z = blockIdx.x, off = z * (size_t)a.n;
+    a.x += off;
+    a.x_out += off;
+    if (a.y) a.y += off;
+    if (a.xb2) a.xb2 += off;
+    if (a.q8) a.q8 += z * q8row;
+    residual_core<EPT>(a, buf, red, true);
+    if (a.q8) {
+        __syncthreads();
+        quantize_blocks_wg(buf, a.q8, a.n / 256);
+    }
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -83,6 +103,37 @@ extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, c
     else if (ept == 4) hipLaunchKernelGGL(residual_norm_kernel<4>, g, b, lds, g4_stream(), a);
     else hipLaunchKernelGGL(residual_norm_kernel<16>, g, b, lds, g4_stream(), a);
     return g4_check_launch("residual_norm_kernel");
+}
+
+// g4_residual_norm over m rows (in place on x; y, xb2 n apart; Q8_K rows of
+// q8 g4_q8K_row_stride(n) bytes apart).  narrow = 0: the thread layout of
+// g4_residual_norm; narrow = 1: 256 threads of n/256 elements, the layout of
+// the residual prologues of g4_mm_residual_q8 (n = 2048, 2560 or 4096).
+extern "C" int g4_residual_norm_rows(float* x, const float* y, const float* w_post, const float* oscale,
+                                     const float* w_next, float* xb2, void* q8, int qsrc, int n, float eps, int m,
+                                     int narrow) {
+    G4_CHECK_ARG(x && n > 0 && n <= kResidualMax && m > 0, "residual_norm_rows: bad x, n=%d or m=%d", n, m);
+    G4_CHECK_ARG(!y || w_post, "residual_norm_rows: y without w_post");
+    G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm_rows: n=%d not a multiple of 256 for Q8_K", n);
+    G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm_rows: quantizing xb2 needs w_next");
+    G4_CHECK_ARG(!narrow || n == 2048 || n == 2560 || n == 4096, "residual_norm_rows: narrow layout needs n = 2048, 2560 or 4096");
+    ResidualArgs a{x, x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    const size_t q8row = g4_q8K_row_stride(n);
+    const size_t lds = (size_t)n * 4;
+    if (narrow) {
+        const dim3 g(m), b(256);
+        if (n == 2048) hipLaunchKernelGGL(residual_rows_kernel<8>, g, b, lds, g4_stream(), a, q8row);
+        else if (n == 2560) hipLaunchKernelGGL(residual_rows_kernel<10>, g, b, lds, g4_stream(), a, q8row);
+        else hipLaunchKernelGGL(residual_rows_kernel<16>, g, b, lds, g4_stream(), a, q8row);
+    } else {
+        const int ept = n <= kNormThreads ? 1 : n <= 4 * kNormThreads ? 4 : 16;
+        const int nt = ((n + ept - 1) / ept + 63) / 64 * 64;
+        const dim3 g(m), b(nt);
+        if (ept == 1) hipLaunchKernelGGL(residual_rows_kernel<1>, g, b, lds, g4_stream(), a, q8row);
+        else if (ept == 4) hipLaunchKernelGGL(residual_rows_kernel<4>, g, b, lds, g4_stream(), a, q8row);
+        else hipLaunchKernelGGL(residual_rows_kernel<16>, g, b, lds, g4_stream(), a, q8row);
+    }
+    return g4_check_launch("residual_rows_kernel");
 }
 
 extern "C" int g4_rmsnorm(float* o, const float* x, const float* w, int n, float eps) {

@@ -65,6 +65,14 @@ _SIGS = {
     "g4_quantize_rows_q8_K": (I, [VP, VP, I, I]),
     "g4_mm_batch_q8": (I, [VP, VP, VP, I, I, I, I]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
+    "g4_emb_lookup_rows": (I, [VP, VP, I, I, VP, I, I, F]),
+    "g4_ple_finish_rows": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
+    "g4_gelu_mul_rows": (I, [VP, VP, VP, I, I, I]),
+    "g4_residual_norm_rows": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, F, I, I]),
+    "g4_rope_table_rows": (I, [VP, I, I, I, F, F, VP]),
+    "g4_qkv_post_rows": (I, [VP, VP, VP, VP, VP, VP, VP, I, VP, I, I, I, I, I, F]),
+    "g4_kv_store_rows": (I, [VP, VP, VP, VP, I, I, I, I, I]),
+    "g4_attn_decode_rows": (I, [VP, VP, VP, VP, VP, I, I, I, I, I, I, I, I, F, I, VP, VP, VP]),
     "g4_rmsnorm": (I, [VP, VP, VP, I, F]),
     "g4_rmsnorm_head_inplace": (I, [VP, VP, I, I, F]),
     "g4_rmsnorm_head_noweight_inplace": (I, [VP, I, I, F]),
@@ -115,6 +123,11 @@ _ENGINE_SIGS = {
     "g4e_layer_x": (C.POINTER(F), [VP]),
     "g4e_generate_greedy": (I, [VP, VP, I, I, VP, C.POINTER(C.c_double), C.POINTER(C.c_double), I]),
     "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
+    "g4e_prefill": (I, [VP, VP, I, I]),
+    "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
+    "g4e_set_prefill_chunk": (I, [VP, I]),
+    "g4e_read_kv": (I, [VP, I, I, I, VP, VP]),
+    "g4e_kv_info": (I, [VP, I, VP]),
 }
 
 
@@ -318,6 +331,39 @@ class Engine:
         self.E.check(self.E.L.g4e_decode_steps(self.h, token, pos0, steps, int(use_graph),
                                                out.ctypes.data if record else None, C.byref(sec)))
         return (out[:steps].copy() if record else None), sec.value
+
+    def prefill(self, tokens, pos0: int = 0) -> None:
+        """forward() with lm_mode 0 of tokens at positions pos0.., in prompt chunks."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        self.E.check(self.E.L.g4e_prefill(self.h, t.ctypes.data, t.size, pos0))
+
+    def prefill_trace(self, tokens, pos0: int = 0) -> np.ndarray:
+        """prefill() that returns each layer's input rows, (n_layers + 1, n, dim):
+        [l, t] is layer l's input for token t, [n_layers, t] the last output."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        tr = np.zeros((self.n_layers + 1, t.size, self.dim), np.float32)
+        self.E.check(self.E.L.g4e_prefill_trace(self.h, t.ctypes.data, t.size, pos0, tr.ctypes.data))
+        return tr
+
+    def kv_info(self, layer: int):
+        """(floats per slot, slots) of a storing layer's KV cache."""
+        out = np.zeros(2, np.int32)
+        self.E.check(self.E.L.g4e_kv_info(self.h, layer, out.ctypes.data))
+        return int(out[0]), int(out[1])
+
+    def set_prefill_chunk(self, tokens: int) -> None:
+        """Tokens per prompt chunk of prefill(); 0: generate_greedy prefills
+        token by token."""
+        self.E.check(self.E.L.g4e_set_prefill_chunk(self.h, tokens))
+
+    def kv(self, layer: int, slot0: int, nslots: int):
+        """(K, V) cache rows slot0..slot0+nslots-1 of a storing layer, each
+        n_kv * head_dim floats."""
+        kvd, _ = self.kv_info(layer)
+        k = np.zeros((nslots, kvd), np.float32)
+        v = np.zeros_like(k)
+        self.E.check(self.E.L.g4e_read_kv(self.h, layer, slot0, nslots, k.ctypes.data, v.ctypes.data))
+        return k, v
 
     def close(self) -> None:
         if self.h:

@@ -92,11 +92,21 @@ struct g4e_model {
     int *hstep;              /* pinned host mirror of dstep */
     void *stream;
     void *graph;             /* captured greedy decode step */
+    /* prompt chunks (allocated on first use for pf_cap tokens; rows of the
+     * chunk are contiguous) */
+    int pf_cap, pf_Gmax;
+    int pf_chunk;            /* tokens per prompt chunk; 0: generate prefills token by token */
+    int *pf_tok;
+    float *pf_x, *pf_xb2, *pf_q, *pf_k, *pf_v, *pf_ao, *pf_o, *pf_g, *pf_u, *pf_h, *pf_d, *pf_ig, *pf_pg, *pf_y;
+    float *pf_ple, *pf_ctx, *pf_tab_swa, *pf_tab_full, *pf_part;
+    void *pf_q8, *pf_q8a, *pf_q8p;
+    float *pf_kch[3], *pf_vch[3];   /* chunk K/V: [0] scratch, [1] donor 22, [2] donor 23 */
     /* host */
     int trace;
     float *layer_x;
     void *allocs[4096];
     int n_allocs;
+    int poison;              /* fill byte of new device buffers (G4E_POISON), -1: none */
 };
 
 /* ---- routing, main.c:716-746 ------------------------------------------------ */
@@ -194,6 +204,7 @@ static int dalloc(g4e_model *m, void **p, size_t bytes) {
     if (m->n_allocs >= (int)(sizeof m->allocs / sizeof m->allocs[0])) return fail(G4_ERR_NOMEM, "too many allocations");
     CK(g4_malloc(p, bytes ? bytes : 1));
     m->allocs[m->n_allocs++] = *p;
+    if (m->poison >= 0) CK(g4_memset(*p, m->poison, bytes ? bytes : 1));
     return 0;
 }
 
@@ -546,6 +557,12 @@ int g4e_open_image(const void *data, size_t size, int max_seq, int device, g4e_m
     int rc = g4_stream_create(&m->stream);
     if (rc) { free(m); return lib_fail(rc, "g4_stream_create"); }
     g4_set_stream(m->stream);
+    /* G4E_POISON=<byte>: fill every device buffer with that byte when it is
+     * allocated (0xff: NaN floats), so that a read of memory no kernel has
+     * written shows in the results */
+    const char *poison = getenv("G4E_POISON");
+    m->poison = poison && *poison ? (int)(strtol(poison, NULL, 0) & 0xff) : -1;
+    m->pf_chunk = G4E_PREFILL_CHUNK;
     rc = open_image((const uint8_t *)data, size, max_seq, m);
     if (rc == 0) rc = g4_sync() ? lib_fail(G4_ERR_HIP, "g4_sync") : 0;
     if (rc) { g4e_close(m); return rc; }
@@ -718,6 +735,217 @@ static int enqueue_step(g4e_model *m, int lm_mode) {
     return 0;
 }
 
+/* ---------------------------------------------------------------------------
+ * Prompt chunks: the forward() of m consecutive prompt tokens with lm_mode 0
+ * (main.c:2366-2384 runs them one at a time), layer by layer over all m
+ * tokens: the Q4_K/Q5_K projections through the batched GEMM (bit-identical
+ * per token to the decode GEMV), norms and residual steps through the rows
+ * forms of the decode step's kernels (same thread layout, so the same bits
+ * per row), attention over m query rows.  A sliding-window ring cannot hold
+ * every query's window while the chunk's own positions are appended, so each
+ * storing layer writes its chunk's K/V to a chunk buffer, the attention reads
+ * positions >= p0 from there and earlier ones from the cache, and the chunk
+ * is appended to the cache afterwards (for the shared-KV donors 22 and 23
+ * after the last layer, when their readers are done).  Only the KV caches
+ * carry over to the next token, as in the reference.
+ * ------------------------------------------------------------------------- */
+static int pf_alloc(g4e_model *m, int cap) {
+    const Config *c = &m->c;
+    const int L = c->n_layers, pd = c->ple_dim;
+    const int hdmax = c->hd_full > c->hd_swa ? c->hd_full : c->hd_swa;
+    const int qmax = c->n_heads * hdmax, kvmax = c->n_kv * hdmax;
+    int q8n = c->hidden > qmax ? c->hidden : qmax;
+    if (c->dim > q8n) q8n = c->dim;
+    q8n = (q8n + 255) / 256 * 256;
+    const size_t M = (size_t)cap;
+    int rc;
+    void *p;
+    m->pf_Gmax = (c->max_seq + 1023) / 1024;
+    if (m->pf_Gmax < 16) m->pf_Gmax = 16;
+#define PA(field, bytes) if ((rc = dalloc(m, &p, (size_t)(bytes)))) return rc; field = p;
+    PA(m->pf_tok, M * 4);
+    PA(m->pf_x, M * c->dim * 4);
+    PA(m->pf_xb2, M * c->dim * 4);
+    PA(m->pf_q, M * qmax * 4);
+    PA(m->pf_k, M * kvmax * 4);
+    PA(m->pf_v, M * kvmax * 4);
+    PA(m->pf_ao, M * qmax * 4);
+    PA(m->pf_o, M * c->dim * 4);
+    PA(m->pf_g, M * c->hidden * 4);
+    PA(m->pf_u, M * c->hidden * 4);
+    PA(m->pf_h, M * c->hidden * 4);
+    PA(m->pf_d, M * c->dim * 4);
+    PA(m->pf_ig, M * pd * 4);
+    PA(m->pf_pg, M * pd * 4);
+    PA(m->pf_y, M * c->dim * 4);
+    PA(m->pf_ple, M * L * pd * 4);
+    PA(m->pf_ctx, M * L * pd * 4);
+    PA(m->pf_tab_swa, M * (size_t)(c->rot_swa / 2) * 8);
+    PA(m->pf_tab_full, M * (size_t)(c->rot_full / 2) * 8);
+    PA(m->pf_part, M * g4_attn_part_bytes(c->n_heads, hdmax, m->pf_Gmax));
+    PA(m->pf_q8, M * g4_q8K_row_stride(q8n));
+    PA(m->pf_q8a, M * g4_q8K_row_stride((qmax + 255) / 256 * 256));
+    PA(m->pf_q8p, M * g4_q8K_row_stride((pd + 255) / 256 * 256));
+    for (int i = 0; i < 3; i++) {
+        PA(m->pf_kch[i], M * kvmax * 4);
+        PA(m->pf_vch[i], M * kvmax * 4);
+    }
+#undef PA
+    m->pf_cap = cap;
+    return 0;
+}
+
+/* chunk K/V buffer of layer l (storing layers) */
+static int pf_slot(int l) { return l == 22 ? 1 : l == 23 ? 2 : 0; }
+
+/* mm over the chunk's rows: K-quant through the batched GEMM on the Q8_K rows
+ * (q8_ready: already quantized by the preceding residual step), the other
+ * types per token */
+static int mm_rows(g4e_model *m, float *o, const float *x, const Tensor *w, int M, int q8_ready) {
+    if (is_q8_type(w->type) && q8_ready) return g4_mm_batch_q8(o, w->p, m->pf_q8, w->n, w->d, M, w->type) ? lib_fail(G4_ERR_HIP, "g4_mm_batch_q8") : 0;
+    return g4_mm_batch(o, x, w->p, w->n, w->d, M, w->type, m->pf_q8) ? lib_fail(G4_ERR_HIP, "g4_mm_batch") : 0;
+}
+
+/* One prompt chunk of M tokens at positions p0..p0+M-1, layer by layer.
+ * trace (optional, host): each layer's input rows go to trace[(l*ntot + t0 +
+ * z)*dim] and the last layer's output to l = n_layers; ntot is the whole
+ * prompt's length and t0 this chunk's first row. */
+static int enqueue_prefill_chunk(g4e_model *m, int p0, int M, float *trace, int ntot, int t0) {
+    const Config *c = &m->c;
+    const int dim = c->dim, L = c->n_layers, pd = c->ple_dim;
+    int rc;
+    CK(g4_emb_lookup_rows(m->pf_x, m->embd.p, m->embd.type, m->embd.d, m->pf_tok, M, dim, sqrtf((float)dim)));
+    for (int z = 0; z < M; z++)
+        CK(g4_mm(m->pf_ctx + (size_t)z * L * pd, m->pf_x + (size_t)z * dim, m->ple_proj.p, m->ple_proj.n,
+                 m->ple_proj.d, m->ple_proj.type, m->q8, 0));
+    CK(g4_ple_finish_rows(m->pf_ple, m->pf_ctx, m->ple_tok.p, m->ple_tok.type, m->ple_tok.d, m->ple_proj_norm,
+                          m->pf_tok, M, pd, L, sqrtf((float)pd), 1.0f / sqrtf((float)dim), 1.0f / sqrtf(2.0f), c->eps));
+    CK(g4_rope_table_rows(m->pf_tab_swa, p0, M, c->rot_swa, c->theta_swa, 1.0f, NULL));
+    CK(g4_rope_table_rows(m->pf_tab_full, p0, M, c->rot_full, c->theta, 1.0f, m->rope_freqs));
+    for (int l = 0; l < L; l++) {
+        const int hd = layer_hd(c, l), swa = is_swa(c, l);
+        const int n_rot = swa ? c->rot_swa : c->rot_full;
+        const int src = kv_source(c, l), has_kv = layer_has_kv(l);
+        const int kvd = c->n_kv * hd, kvd_src = c->n_kv * layer_hd(c, src);
+        const int q8_att = is_q8_type(m->wq[l].type);
+        /* residual step of the previous layer + attn_norm (+ Q8_K rows) */
+        CK(g4_residual_norm_rows(m->pf_x, l ? m->pf_y : NULL, l ? m->post_norm[l - 1] : NULL,
+                                 l ? m->out_scale[l - 1] : NULL, m->attn_norm[l], m->pf_xb2, q8_att ? m->pf_q8 : NULL, 0,
+                                 dim, c->eps, M, pro_ok(c, &m->wq[l])));
+        if (trace) CK(g4_memcpy_d2h(trace + ((size_t)l * ntot + t0) * dim, m->pf_x, (size_t)M * dim * 4));
+        if ((rc = mm_rows(m, m->pf_q, m->pf_xb2, &m->wq[l], M, q8_att))) return rc;
+        float *kch = NULL, *vch = NULL;
+        if (has_kv) {
+            const int q8k = is_q8_type(m->wk[l].type) && q8_att, q8v = is_q8_type(m->wv[l].type) && q8_att;
+            if ((rc = mm_rows(m, m->pf_k, m->pf_xb2, &m->wk[l], M, q8k))) return rc;
+            if ((rc = mm_rows(m, m->pf_v, m->pf_xb2, &m->wv[l], M, q8v))) return rc;
+            kch = m->pf_kch[pf_slot(l)];
+            vch = m->pf_vch[pf_slot(l)];
+        }
+        CK(g4_qkv_post_rows(m->pf_q, m->q_norm[l], has_kv ? m->pf_k : NULL, has_kv ? m->pf_v : NULL,
+                            has_kv ? m->k_norm[l] : NULL, kch, vch, kvd, swa ? m->pf_tab_swa : m->pf_tab_full, M,
+                            c->n_heads, c->n_kv, hd, n_rot, c->eps));
+        /* attention over the query rows; chunks of <= 128 positions */
+        const int window = swa ? c->window : 0;
+        const int nmax = window > 0 && window < p0 + M ? window : p0 + M;
+        int G = (nmax + 127) / 128;
+        if (G > m->pf_Gmax) G = m->pf_Gmax;
+        const int o_q8 = is_q8_type(m->wo[l].type);
+        CK(g4_attn_decode_rows(m->pf_q, m->kc[src], m->vc[src], m->pf_kch[pf_slot(src)], m->pf_vch[pf_slot(src)],
+                               kvd_src, m->kv_ring[src], p0, M, window, c->n_heads, c->n_kv, hd, 1.0f, G, m->pf_part,
+                               m->pf_ao, o_q8 ? m->pf_q8a : NULL));
+        if (has_kv && pf_slot(l) == 0) CK(g4_kv_store_rows(m->kc[l], m->vc[l], kch, vch, kvd, m->kv_ring[l], p0, M, kvd));
+        if (o_q8) {
+            CK(g4_mm_batch_q8(m->pf_o, m->wo[l].p, m->pf_q8a, m->wo[l].n, m->wo[l].d, M, m->wo[l].type));
+        } else if ((rc = mm_rows(m, m->pf_o, m->pf_ao, &m->wo[l], M, 0))) {
+            return rc;
+        }
+        /* post_attention_norm + residual, ffn_norm + Q8_K rows; gelu(gate) * up; down */
+        const int q8_ffn = is_q8_type(m->gate[l].type);
+        CK(g4_residual_norm_rows(m->pf_x, m->pf_o, m->post_attn_norm[l], NULL, m->ffn_norm[l], m->pf_xb2,
+                                 q8_ffn ? m->pf_q8 : NULL, 0, dim, c->eps, M, 0));
+        if ((rc = mm_rows(m, m->pf_g, m->pf_xb2, &m->gate[l], M, q8_ffn))) return rc;
+        if ((rc = mm_rows(m, m->pf_u, m->pf_xb2, &m->up[l], M, q8_ffn && is_q8_type(m->up[l].type)))) return rc;
+        CK(g4_gelu_mul_rows(m->pf_h, m->pf_g, m->pf_u, c->hidden, M, c->hidden));
+        if ((rc = mm_rows(m, m->pf_d, m->pf_h, &m->down[l], M, 0))) return rc;
+        /* post_ffw_norm + residual, Q8_K rows of x; PLE gate and projection */
+        const int q8_ig = is_q8_type(m->inp_gate[l].type);
+        CK(g4_residual_norm_rows(m->pf_x, m->pf_d, m->post_ffw_norm[l], NULL, NULL, NULL, q8_ig ? m->pf_q8 : NULL, 1,
+                                 dim, c->eps, M, pro_ok(c, &m->inp_gate[l])));
+        if ((rc = mm_rows(m, m->pf_ig, m->pf_x, &m->inp_gate[l], M, q8_ig))) return rc;
+        CK(g4_gelu_mul_rows(m->pf_pg, m->pf_ig, m->pf_ple + (size_t)l * pd, pd, M, L * pd));
+        if (is_q8_type(m->proj[l].type)) {
+            CK(g4_quantize_rows_q8_K(m->pf_pg, m->pf_q8p, pd, M));
+            CK(g4_mm_batch_q8(m->pf_y, m->proj[l].p, m->pf_q8p, pd, dim, M, m->proj[l].type));
+        } else if ((rc = mm_rows(m, m->pf_y, m->pf_pg, &m->proj[l], M, 0))) {
+            return rc;
+        }
+    }
+    if (trace) {
+        CK(g4_residual_norm_rows(m->pf_x, m->pf_y, m->post_norm[L - 1], m->out_scale[L - 1], NULL, NULL, NULL, 0, dim,
+                                 c->eps, M, 0));
+        CK(g4_memcpy_d2h(trace + ((size_t)L * ntot + t0) * dim, m->pf_x, (size_t)M * dim * 4));
+    }
+    /* the shared-KV donors' chunks, now that their readers are done */
+    for (int l = 22; l <= 23 && l < L; l++)
+        if (layer_has_kv(l)) {
+            const int kvd = c->n_kv * layer_hd(c, l);
+            CK(g4_kv_store_rows(m->kc[l], m->vc[l], m->pf_kch[pf_slot(l)], m->pf_vch[pf_slot(l)], kvd, m->kv_ring[l],
+                                p0, M, kvd));
+        }
+    return 0;
+}
+
+int g4e_prefill_trace(g4e_model *m, const int *tokens, int n, int pos0, float *trace) {
+    if (!m || !tokens || n < 0 || pos0 < 0) return fail(G4_ERR_ARG, "g4e_prefill: bad arguments");
+    if (pos0 + n > m->c.max_seq) return fail(G4_ERR_ARG, "g4e_prefill: positions past max_seq");
+    g4_set_stream(m->stream);
+    int rc;
+    /* chunk buffers: sized by the first call, up to 512 tokens; longer
+     * prompts run in chunks of that size */
+    const int want = m->pf_chunk > 0 ? m->pf_chunk : G4E_PREFILL_CHUNK;
+    if (m->pf_cap == 0 && n > 0 && (rc = pf_alloc(m, want < m->c.max_seq ? want : m->c.max_seq))) return rc;
+    const int chunk = want < m->pf_cap ? want : m->pf_cap;
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        const int M = n - t0 < chunk ? n - t0 : chunk;
+        CK(g4_memcpy_h2d(m->pf_tok, tokens + t0, (size_t)M * 4));
+        if ((rc = enqueue_prefill_chunk(m, pos0 + t0, M, trace, n, t0))) return rc;
+    }
+    CK(g4_sync());
+    return 0;
+}
+
+int g4e_prefill(g4e_model *m, const int *tokens, int n, int pos0) { return g4e_prefill_trace(m, tokens, n, pos0, NULL); }
+
+int g4e_kv_info(const g4e_model *m, int layer, int out[2]) {
+    if (!m || !out || layer < 0 || layer >= m->c.n_layers || !layer_has_kv(layer))
+        return fail(G4_ERR_ARG, "g4e_kv_info: layer %d stores no KV", layer);
+    const int ring = m->kv_ring[layer];
+    out[0] = m->c.n_kv * layer_hd(&m->c, layer);
+    out[1] = ring > 0 ? ring : m->c.max_seq;
+    return 0;
+}
+
+int g4e_read_kv(g4e_model *m, int layer, int slot0, int nslots, float *k, float *v) {
+    int info[2], rc;
+    if ((rc = g4e_kv_info(m, layer, info))) return rc;
+    if (slot0 < 0 || nslots < 0 || slot0 + nslots > info[1] || !k || !v) return fail(G4_ERR_ARG, "g4e_read_kv: bad range");
+    g4_set_stream(m->stream);
+    CK(g4_sync());
+    CK(g4_memcpy_d2h(k, m->kc[layer] + (size_t)slot0 * info[0], (size_t)nslots * info[0] * 4));
+    CK(g4_memcpy_d2h(v, m->vc[layer] + (size_t)slot0 * info[0], (size_t)nslots * info[0] * 4));
+    return 0;
+}
+
+int g4e_set_prefill_chunk(g4e_model *m, int tokens) {
+    if (!m || tokens < 0 || tokens > G4E_PREFILL_CHUNK)
+        return fail(G4_ERR_ARG, "g4e_set_prefill_chunk: %d tokens (0..%d)", tokens, G4E_PREFILL_CHUNK);
+    if (m->pf_cap > 0 && tokens > m->pf_cap)
+        return fail(G4_ERR_STATE, "g4e_set_prefill_chunk: chunk buffers hold %d tokens", m->pf_cap);
+    m->pf_chunk = tokens;
+    return 0;
+}
+
 static int set_step(g4e_model *m, int token, int pos) {
     const Config *c = &m->c;
     if (token < 0 || token >= c->vocab) return fail(G4_ERR_ARG, "token %d out of range", token);
@@ -824,10 +1052,16 @@ int g4e_generate_greedy(g4e_model *m, const int *prompt, int n_prompt, int max_n
     g4_set_stream(m->stream);
     const double t0 = now_s();
     int gen = 0, rc;
-    /* prefill: token-serial, lm_mode 0 except for the last prompt token (main.c:2366-2384) */
-    for (int pos = 0; pos < n_prompt - 1; pos++) {
-        if (pos >= m->c.max_seq) return gen;
-        if ((rc = set_step(m, prompt[pos], pos)) || (rc = enqueue_step(m, 0))) return -rc;
+    /* prefill: lm_mode 0 except for the last prompt token (main.c:2366-2384),
+     * in prompt chunks or token by token */
+    if (m->pf_chunk > 0) {
+        const int np = n_prompt - 1 < m->c.max_seq ? n_prompt - 1 : m->c.max_seq;
+        if (np > 0 && (rc = g4e_prefill(m, prompt, np, 0))) return -rc;
+    } else {
+        for (int pos = 0; pos < n_prompt - 1; pos++) {
+            if (pos >= m->c.max_seq) return gen;
+            if ((rc = set_step(m, prompt[pos], pos)) || (rc = enqueue_step(m, 0))) return -rc;
+        }
     }
     const int last = n_prompt - 1;
     if (last >= m->c.max_seq) return gen;

@@ -66,6 +66,31 @@ int g4e_generate_greedy(g4e_model *m, const int *prompt, int n_prompt, int max_n
  * seconds through *sec.  Tokens are written to out (steps ints, nullable). */
 int g4e_decode_steps(g4e_model *m, int token, int pos0, int steps, int use_graph, int *out, double *sec);
 
+/* forward() of n consecutive tokens at positions pos0.. with lm_mode 0, as
+ * the prompt loop of generate (main.c:2366-2384) runs them, processed in
+ * chunks (g4e_set_prefill_chunk, default G4E_PREFILL_CHUNK tokens) layer by
+ * layer: batched GEMMs, attention over the chunk's query rows against the
+ * cache and the chunk's own K/V.  Each layer agrees with the token loop to
+ * fp32 tolerance; the result does not depend on the chunk length or on how
+ * the prompt is split over calls (bit for bit).  The chunk buffers are
+ * allocated by the first call.  Returns after the work has completed. */
+int g4e_prefill(g4e_model *m, const int *tokens, int n, int pos0);
+/* g4e_prefill that also copies each layer's input rows to the host: trace
+ * holds (n_layers + 1) x n x dim floats; row (l, t) is the input of layer l
+ * for token t, row (n_layers, t) the last layer's output */
+int g4e_prefill_trace(g4e_model *m, const int *tokens, int n, int pos0, float *trace);
+/* longest prompt chunk of g4e_prefill, and its default */
+#define G4E_PREFILL_CHUNK 512
+/* tokens per prompt chunk (1..G4E_PREFILL_CHUNK; at most what the chunk
+ * buffers hold once g4e_prefill has sized them); 0 makes g4e_generate_greedy
+ * prefill token by token as the reference's prompt loop does */
+int g4e_set_prefill_chunk(g4e_model *m, int tokens);
+/* KV cache of a storing layer: out[0] = floats per slot (n_kv * head_dim),
+ * out[1] = slots (the window for a sliding-window ring, else max_seq) */
+int g4e_kv_info(const g4e_model *m, int layer, int out[2]);
+/* copy slots slot0..slot0+nslots-1 of the layer's K and V caches to the host */
+int g4e_read_kv(g4e_model *m, int layer, int slot0, int nslots, float *k, float *v);
+
 #ifdef __cplusplus
 }
 #endif

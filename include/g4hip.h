@@ -174,6 +174,44 @@ int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m,
 int g4_mm_batch(float *o, const float *x, const void *w, int n, int d, int m, int type, void *q8);
 
 /* ---------------------------------------------------------------------------
+ * Prompt-chunk forms of the step glue (the reference runs forward() once per
+ * prompt token, main.c:2366-2384; these run the same per-token operations
+ * on m tokens of a chunk in one launch each).  Rows of a chunk are
+ * contiguous; Q8_K rows are g4_q8K_row_stride(n) bytes apart.
+ * ------------------------------------------------------------------------- */
+/* emb_lookup + x * sqrt(dim) (main.c:1696-1723, 1849-1854) of tokens dtok[0..m) */
+int g4_emb_lookup_rows(float *o, const void *w, int type, int rows, const int *dtok, int m, int dim, float scale);
+/* build_ple after its projection (main.c:1751-1777) for tokens dtok[0..m):
+ * ple, ctx rows of L*pd floats */
+int g4_ple_finish_rows(float *ple, const float *ctx, const void *ple_tok, int type, int rows, const float *proj_norm,
+                       const int *dtok, int m, int pd, int L, float sc_tok, float sc_ctx, float mix, float eps);
+/* o[z][i] = gelu(g[z][i]) * u[z*ustride + i]: gelu(gate)*up (main.c:1976-1980)
+ * and the PLE gate (main.c:1989-1993) */
+int g4_gelu_mul_rows(float *o, const float *g, const float *u, int d, int m, int ustride);
+/* g4_residual_norm on m rows of x (in place); narrow = 1 uses the thread
+ * layout of g4_mm_residual_q8's prologue (n = 2048, 2560, 4096), narrow = 0
+ * that of g4_residual_norm, so each row matches the decode step's bits */
+int g4_residual_norm_rows(float *x, const float *y, const float *w_post, const float *oscale, const float *w_next,
+                          float *xb2, void *q8, int qsrc, int n, float eps, int m, int narrow);
+/* RoPE (cos, sin) tables of positions pos0..pos0+m-1 (main.c:1725-1742), n_rot/2 pairs each */
+int g4_rope_table_rows(float *tab, int pos0, int m, int n_rot, float freq_base, float freq_scale,
+                       const float *freq_factors);
+/* per-head norms + RoPE of m tokens (main.c:1886-1900): q rows in place, k/v
+ * rows (nullable) into rows of kout/vout (stride kv_stride) */
+int g4_qkv_post_rows(float *q, const float *q_norm, const float *k, const float *v, const float *k_norm, float *kout,
+                     float *vout, int kv_stride, const float *tab_rows, int m, int n_heads, int n_kv, int hd, int n_rot,
+                     float eps);
+/* the KV append (main.c:1901-1904) of positions pos0..pos0+m-1 from rows of kin/vin */
+int g4_kv_store_rows(float *kc, float *vc, const float *kin, const float *vin, int kv_stride, int ring, int pos0, int m,
+                     int kvd);
+/* the attention block (main.c:1909-1950) for m query rows at positions
+ * p0..p0+m-1: the chunk's K/V in rows of kchunk/vchunk, earlier positions in
+ * the cache (ring: window <= ring); part: m * g4_attn_part_bytes(n_heads, hd, G) */
+int g4_attn_decode_rows(const float *q, const float *kc, const float *vc, const float *kchunk, const float *vchunk,
+                        int kv_stride, int ring, int p0, int m, int window, int n_heads, int n_kv, int hd,
+                        float attn_scale, int G, float *part, float *out, void *q8);
+
+/* ---------------------------------------------------------------------------
  * Norms, RoPE, attention (main.c:1451-1488, 1725-1745, 1886-1950)
  * ------------------------------------------------------------------------- */
 /* rmsnorm(float *o, const float *x, const float *w, int n, float eps), main.c:1451 */

@@ -93,8 +93,10 @@ def test_greedy_graph_matches_host_loop(pair):
     """generate() with the decode step replayed as one HIP graph (token and
     position advanced on the device by the argmax kernel) equals the eager
     launches and a host loop of forward() + first-index argmax over the
-    read-back logits (main.c:2045-2049)."""
+    read-back logits (main.c:2045-2049).  The prompt runs token by token here;
+    test_gpu_prefill_engine.py covers generate() over prompt chunks."""
     _, em = pair
+    em.set_prefill_chunk(0)                         # the prompt token by token, as the loop below
     prompt = [5, 77, 301, 12, 9, 400, 31]
     n_new = 24
     g_graph, _, _ = em.generate_greedy(prompt, n_new, use_graph=True)

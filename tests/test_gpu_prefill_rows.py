@@ -1,0 +1,309 @@
+"""GPU parity of the prompt-chunk ("rows") forms of the step glue, at the E4B
+shapes the batched prefill runs them on (8 query / 2 KV heads, head_dim 256
+and 512, window 512, hidden 2560, 42 x 256 PLE).
+
+The reference runs forward() once per prompt token (main.c:2366-2384); each
+rows entry point runs one of its per-token operations on m tokens in one
+launch.  Where the decode step has the same operation as its own entry point
+and the two share the kernel body and thread layout (embedding lookup, PLE
+finish, RoPE tables, q/k/v norms + RoPE, residual + norm + Q8_K, GELU gate),
+every row must equal the decode entry point bit for bit.  The attention over
+the chunk's query rows is held to the decode attention's bar (1e-4 of max|o|)
+against the oracle's attention per query row, with every cache slot and chunk
+row it must not read filled with NaN.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+from oracle import Q8K_DTYPE
+
+pytestmark = pytest.mark.gpu
+
+P = lambda a: a.ctypes.data  # noqa: E731
+F = C.c_float
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from g4 import Lib
+    L = Lib.get()
+    L.init(0)
+    L.L.g4_set_stream(None)
+    return L
+
+
+def dbuf(lib, a):
+    from g4 import DBuf
+    return DBuf.from_array(lib, np.ascontiguousarray(a))
+
+
+def empty(lib, nbytes):
+    from g4 import DBuf
+    return DBuf(lib, nbytes)
+
+
+def rel_err(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_emb_lookup_rows(lib, qtype):
+    """Rows of tokens equal the decode step's g4_emb_lookup_dev per token."""
+    rng = np.random.default_rng(20 + qtype)
+    vocab, dim = 96, 2560
+    raw = synth.rand_q4K(rng, vocab, dim) if qtype == 12 else synth.rand_q6K(rng, vocab, dim)
+    from g4 import upload_quant
+    w = upload_quant(lib, raw, qtype, dim, vocab)
+    toks = np.array([3, 95, 0, 17, 3, 64], np.int32)
+    scale = np.float32(np.sqrt(np.float32(dim)))
+    out, td = empty(lib, 4 * dim * len(toks)), dbuf(lib, toks)
+    lib.g4_emb_lookup_rows(out.ptr, w.ptr, qtype, vocab, td.ptr, len(toks), dim, F(scale))
+    got = out.to_array(np.float32).reshape(len(toks), dim)
+    one = empty(lib, 4 * dim)
+    for z, t in enumerate(toks):
+        t1 = dbuf(lib, np.array([t], np.int32))
+        lib.g4_emb_lookup_dev(one.ptr, w.ptr, qtype, vocab, t1.ptr, dim, F(scale))
+        assert same_bits(got[z], one.to_array(np.float32)), z
+
+
+def test_ple_finish_rows(lib):
+    """build_ple's finish (main.c:1751-1777) over rows equals g4_ple_finish
+    per token."""
+    rng = np.random.default_rng(21)
+    L, pd, vocab, dim = 42, 256, 64, 2560
+    raw = synth.rand_q6K(rng, vocab, pd * L)
+    from g4 import upload_quant
+    w = upload_quant(lib, raw, 14, pd * L, vocab)
+    toks = np.array([37, 0, 63, 5], np.int32)
+    m = len(toks)
+    ctx = (rng.standard_normal((m, pd * L)) * 20).astype(np.float32)
+    norm = dbuf(lib, rng.uniform(0.8, 1.2, pd).astype(np.float32))
+    st, sc, mix = np.float32(16.0), np.float32(1) / np.sqrt(np.float32(dim)), np.float32(1) / np.sqrt(np.float32(2))
+    ctxd, td = dbuf(lib, ctx), dbuf(lib, toks)
+    out = empty(lib, 4 * m * pd * L)
+    lib.g4_ple_finish_rows(out.ptr, ctxd.ptr, w.ptr, 14, vocab, norm.ptr, td.ptr, m, pd, L, F(st), F(sc),
+                           F(mix), F(1e-6))
+    got = out.to_array(np.float32).reshape(m, pd * L)
+    one = empty(lib, 4 * pd * L)
+    for z in range(m):
+        cz = dbuf(lib, ctx[z])
+        lib.g4_ple_finish(one.ptr, cz.ptr, w.ptr, 14, vocab, norm.ptr, None, int(toks[z]), pd, L,
+                          F(st), F(sc), F(mix), F(1e-6))
+        assert same_bits(got[z], one.to_array(np.float32)), z
+
+
+def test_gelu_mul_rows(lib):
+    """gelu(gate) * up over rows, the multiplier read with a row stride (the
+    PLE rows of one layer), equals g4_gelu_mul_quant per row."""
+    rng = np.random.default_rng(22)
+    m, d, L = 5, 256, 42
+    g = (rng.standard_normal((m, d)) * 3).astype(np.float32)
+    u = rng.standard_normal((m, L * d)).astype(np.float32)
+    layer = 17
+    gd, ud, o = dbuf(lib, g), dbuf(lib, u), empty(lib, 4 * m * d)
+    lib.g4_gelu_mul_rows(o.ptr, gd.ptr, ud.ptr + 4 * layer * d, d, m, L * d)
+    got = o.to_array(np.float32).reshape(m, d)
+    for z in range(m):
+        gz, uz = dbuf(lib, g[z]), dbuf(lib, u[z, layer * d:(layer + 1) * d])
+        lib.g4_gelu_mul_quant(gz.ptr, uz.ptr, d, None)
+        assert same_bits(got[z], gz.to_array(np.float32)), z
+
+
+@pytest.mark.parametrize("n_rot,base,ff", [(256, 1e4, False), (512, 1e6, True)])
+def test_rope_table_rows(lib, n_rot, base, ff):
+    """(cos, sin) tables of positions pos0.. equal g4_rope_table per position."""
+    rng = np.random.default_rng(23)
+    ffd = dbuf(lib, rng.uniform(1.0, 4.0, n_rot // 2).astype(np.float32)) if ff else None
+    pos0, m = 500, 37
+    tab = empty(lib, 8 * m * (n_rot // 2))
+    lib.g4_rope_table_rows(tab.ptr, pos0, m, n_rot, F(base), F(1.0), ffd.ptr if ff else None)
+    got = tab.to_array(np.float32).reshape(m, n_rot)
+    one = empty(lib, 8 * (n_rot // 2))
+    for z in range(m):
+        lib.g4_rope_table(one.ptr, None, pos0 + z, n_rot, F(base), F(1.0), ffd.ptr if ff else None)
+        assert same_bits(got[z], one.to_array(np.float32)), z
+
+
+@pytest.mark.parametrize("hd,with_kv", [(256, True), (512, True), (512, False)])
+def test_qkv_post_rows(lib, orc, hd, with_kv):
+    """q_norm + RoPE of the chunk's q rows and k_norm + RoPE / unweighted norm
+    of its k/v rows (main.c:1886-1900) equal g4_qkv_post per token (flat
+    cache, the token's position), and the oracle's norms + RoPE."""
+    rng = np.random.default_rng(24 + hd)
+    n_heads, n_kv, eps = 8, 2, 1e-6
+    base = 1e4 if hd == 256 else 1e6
+    qd_, kvd = n_heads * hd, n_kv * hd
+    pos0, m = 77, 9
+    q = rng.standard_normal((m, qd_)).astype(np.float32)
+    k = rng.standard_normal((m, kvd)).astype(np.float32)
+    v = rng.standard_normal((m, kvd)).astype(np.float32)
+    qn = dbuf(lib, rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    kn = dbuf(lib, rng.uniform(0.5, 1.5, hd).astype(np.float32))
+    tab = empty(lib, 8 * m * (hd // 2))
+    lib.g4_rope_table_rows(tab.ptr, pos0, m, hd, F(base), F(1.0), None)
+    qd = dbuf(lib, q)
+    kd, vd = dbuf(lib, k), dbuf(lib, v)
+    kout, vout = empty(lib, 4 * m * kvd), empty(lib, 4 * m * kvd)
+    lib.g4_qkv_post_rows(qd.ptr, qn.ptr, kd.ptr if with_kv else None, vd.ptr if with_kv else None,
+                         kn.ptr if with_kv else None, kout.ptr if with_kv else None, vout.ptr if with_kv else None,
+                         kvd, tab.ptr, m, n_heads, n_kv, hd, hd, F(eps))
+    gq = qd.to_array(np.float32).reshape(m, qd_)
+    gk = kout.to_array(np.float32).reshape(m, kvd)
+    gv = vout.to_array(np.float32).reshape(m, kvd)
+    kc, vc = empty(lib, 4 * (pos0 + m) * kvd), empty(lib, 4 * (pos0 + m) * kvd)
+    one_tab = empty(lib, 8 * (hd // 2))
+    qn_h = qn.to_array(np.float32)
+    for z in range(m):
+        pos = pos0 + z
+        lib.g4_rope_table(one_tab.ptr, None, pos, hd, F(base), F(1.0), None)
+        qz = dbuf(lib, q[z])
+        kz, vz = dbuf(lib, k[z]), dbuf(lib, v[z])
+        lib.g4_qkv_post(qz.ptr, qn.ptr, kz.ptr if with_kv else None, vz.ptr if with_kv else None,
+                        kn.ptr if with_kv else None, kc.ptr if with_kv else None, vc.ptr if with_kv else None,
+                        kvd, 0, None, pos, n_heads, n_kv, hd, hd, F(base), F(1.0), None, F(eps), one_tab.ptr)
+        assert same_bits(gq[z], qz.to_array(np.float32)), z
+        if with_kv:
+            row = slice(pos * kvd, (pos + 1) * kvd)
+            assert same_bits(gk[z], kc.to_array(np.float32)[row]), z
+            assert same_bits(gv[z], vc.to_array(np.float32)[row]), z
+        # the oracle: rmsnorm_head_inplace + apply_rope_neox (main.c:1458, 1725)
+        wq = q[z].copy()
+        orc.L.or_rmsnorm_head_inplace(P(wq), P(qn_h), n_heads, hd, F(eps))
+        wq = orc.rope(wq, n_heads, hd, hd, pos, base)
+        assert rel_err(gq[z], wq) < 2e-5
+
+
+@pytest.mark.parametrize("ring,pos0,m", [(8, 5, 21), (8, 40, 3), (0, 10, 6), (512, 700, 100)])
+def test_kv_store_rows(lib, ring, pos0, m):
+    """The append of positions pos0..pos0+m-1: slot t % ring (flat: t); of a
+    chunk longer than the ring only the last ring rows are kept, as the token
+    loop leaves them."""
+    rng = np.random.default_rng(25 + m)
+    kvd = 64
+    slots = ring if ring else pos0 + m
+    kin = rng.standard_normal((m, kvd)).astype(np.float32)
+    vin = rng.standard_normal((m, kvd)).astype(np.float32)
+    init = np.full((slots, kvd), 7.0, np.float32)
+    kc, vc = dbuf(lib, init), dbuf(lib, init)
+    kd, vd = dbuf(lib, kin), dbuf(lib, vin)
+    lib.g4_kv_store_rows(kc.ptr, vc.ptr, kd.ptr, vd.ptr, kvd, ring, pos0, m, kvd)
+    want_k, want_v = init.copy(), init.copy()
+    for z in range(m):
+        t = pos0 + z
+        s = t % ring if ring else t
+        want_k[s], want_v[s] = kin[z], vin[z]
+    assert same_bits(kc.to_array(np.float32).reshape(slots, kvd), want_k)
+    assert same_bits(vc.to_array(np.float32).reshape(slots, kvd), want_v)
+
+
+ATTN_CASES = [
+    # hd, n_heads, n_kv, window, ring, p0, m, G
+    (256, 8, 2, 512, 512, 0, 37, 4),       # first chunk of a prompt
+    (256, 8, 2, 512, 512, 700, 100, 4),    # ring wrapped; the window spans cache and chunk
+    (256, 8, 2, 8, 8, 13, 20, 1),          # chunk longer than the window
+    (512, 8, 2, 0, 0, 300, 64, 3),         # full attention, flat cache
+    (512, 2, 1, 0, 0, 0, 24, 1),           # the small test model's full layers
+    (256, 8, 2, 512, 512, 0, 511, 4),      # the 511-token prompt of the decode workload
+]
+
+
+@pytest.mark.parametrize("hd,n_heads,n_kv,window,ring,p0,m,G", ATTN_CASES)
+def test_attn_decode_rows(lib, orc, hd, n_heads, n_kv, window, ring, p0, m, G):
+    """The attention block (main.c:1909-1950) for query rows at positions
+    p0..p0+m-1: positions < p0 from the cache, the chunk's own from its K/V
+    rows.  Against the oracle's attention over one flat cache per row, 1e-4 of
+    max|o|; the Q8_K rows of the output are the oracle's quantization of the
+    fp32 rows.  Cache slots and chunk rows the rows must not read hold NaN."""
+    rng = np.random.default_rng(hd + p0 + m)
+    kvd, qd_ = n_kv * hd, n_heads * hd
+    T = p0 + m
+    K = rng.standard_normal((T, kvd)).astype(np.float32)
+    V = rng.standard_normal((T, kvd)).astype(np.float32)
+    q = rng.standard_normal((m, qd_)).astype(np.float32)
+    slots = ring if ring else T
+    kc = np.full((slots, kvd), np.nan, np.float32)
+    vc = np.full((slots, kvd), np.nan, np.float32)
+    lo = max(0, p0 - ring) if ring else 0
+    for t in range(lo, p0):
+        s = t % ring if ring else t
+        kc[s], vc[s] = K[t], V[t]
+    pad = np.full((3, kvd), np.nan, np.float32)
+    kch, vch = np.concatenate([K[p0:], pad]), np.concatenate([V[p0:], pad])
+    part = empty(lib, m * lib.L.g4_attn_part_bytes(n_heads, hd, G))
+    out = empty(lib, 4 * m * qd_)
+    rs = lib.L.g4_q8K_row_stride(qd_)
+    q8 = empty(lib, m * rs)
+    qd, kcd, vcd, kchd, vchd = dbuf(lib, q), dbuf(lib, kc), dbuf(lib, vc), dbuf(lib, kch), dbuf(lib, vch)
+    lib.g4_attn_decode_rows(qd.ptr, kcd.ptr, vcd.ptr, kchd.ptr, vchd.ptr, kvd, ring, p0, m, window, n_heads, n_kv, hd,
+                            F(1.0), G, part.ptr, out.ptr, q8.ptr)
+    got = out.to_array(np.float32).reshape(m, qd_)
+    assert np.isfinite(got).all()
+    h = np.zeros(qd_ // 256, Q8K_DTYPE)
+    for z in range(0, m, max(1, m // 12)):
+        pos = p0 + z
+        t_start = max(0, pos + 1 - window) if window else 0
+        want = orc.attn(q[z], K, V, kvd, t_start, pos + 1 - t_start, n_heads, n_kv, hd, 1.0)
+        assert rel_err(got[z], want) < 1e-4, z
+        lib.g4_download_q8K(q8.ptr + z * rs, P(h), qd_)
+        assert h.tobytes() == orc.quantize_q8K(got[z]).tobytes(), z
+
+
+def test_attn_decode_rows_checks(lib):
+    """Too few chunks for the window, or a ring narrower than the window, is
+    an argument error before any launch."""
+    from g4 import G4Error
+    b = empty(lib, 1 << 20)
+    with pytest.raises(G4Error):
+        lib.g4_attn_decode_rows(b.ptr, b.ptr, b.ptr, b.ptr, b.ptr, 512, 0, 0, 1100, 0, 8, 2, 256, F(1.0), 1,
+                                b.ptr, b.ptr, None)
+    with pytest.raises(G4Error):
+        lib.g4_attn_decode_rows(b.ptr, b.ptr, b.ptr, b.ptr, b.ptr, 512, 256, 0, 4, 512, 8, 2, 256, F(1.0), 1,
+                                b.ptr, b.ptr, None)
+
+
+@pytest.mark.parametrize("n,narrow", [(2560, 0), (256, 0), (2560, 1)])
+def test_residual_norm_rows(lib, n, narrow):
+    """post-norm + residual (+ out_scale), next norm and Q8_K over rows equal
+    the decode step's entry point per row: g4_residual_norm (narrow 0) or the
+    residual prologue of g4_mm_residual_q8 (narrow 1)."""
+    from g4 import upload_quant
+    rng = np.random.default_rng(26 + n + narrow)
+    m, eps = 5, 1e-6
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    y = (rng.standard_normal((m, n)) * 4).astype(np.float32)
+    wp = dbuf(lib, rng.uniform(0.5, 1.5, n).astype(np.float32))
+    wn = dbuf(lib, rng.uniform(0.5, 1.5, n).astype(np.float32))
+    osc = dbuf(lib, np.array([0.9], np.float32))
+    rs = lib.L.g4_q8K_row_stride(n)
+    xd, yd = dbuf(lib, x), dbuf(lib, y)
+    xb2, q8 = empty(lib, 4 * m * n), empty(lib, m * rs)
+    lib.g4_residual_norm_rows(xd.ptr, yd.ptr, wp.ptr, osc.ptr, wn.ptr, xb2.ptr, q8.ptr, 0, n, F(eps), m, narrow)
+    gx = xd.to_array(np.float32).reshape(m, n)
+    gxb2 = xb2.to_array(np.float32).reshape(m, n)
+    ha, hb = np.zeros(n // 256, Q8K_DTYPE), np.zeros(n // 256, Q8K_DTYPE)
+    if narrow:
+        raw = synth.rand_q4K(rng, 16, n)
+        w = upload_quant(lib, raw, 12, n, 16)
+        o = empty(lib, 4 * 16)
+    for z in range(m):
+        x1, xo, y1 = dbuf(lib, x[z]), empty(lib, 4 * n), dbuf(lib, y[z])
+        b1, q1 = empty(lib, 4 * n), empty(lib, rs)
+        if narrow:
+            lib.g4_mm_residual_q8(o.ptr, w.ptr, None, n, 16, 12, None, x1.ptr, xo.ptr, y1.ptr, wp.ptr,
+                                  osc.ptr, wn.ptr, b1.ptr, q1.ptr, 0, F(eps))
+        else:
+            lib.g4_residual_norm(x1.ptr, y1.ptr, wp.ptr, osc.ptr, wn.ptr, b1.ptr, q1.ptr, 0, n, F(eps))
+            xo = x1
+        assert same_bits(gx[z], xo.to_array(np.float32)), z
+        assert same_bits(gxb2[z], b1.to_array(np.float32)), z
+        lib.g4_download_q8K(q8.ptr + z * rs, P(ha), n)
+        lib.g4_download_q8K(q1.ptr, P(hb), n)
+        assert ha.tobytes() == hb.tobytes(), z
