@@ -329,6 +329,181 @@ void launch_mm_batch(const uint8_t* w, const uint8_t* q8, float* o, int nb, int 
                        nb, d, m);
 }
 
+// ---- fp32 activations: Q6_K and bf16 matrices --------------------------
+// Y[m x d] = X[m x n] . W[d x n]^T where the reference multiplies fp32
+// activations by the dequantized weights (mm_quant_rows for Q6_K,
+// gemma4-4b/cpu-blas/main.c:1539-1556 with dequant_q6_k main.c:213-236;
+// mm_bf16 main.c:1529-1537).  Each weight is dequantized to the reference's fp32 value
+// (Q6_K: (d * sc) * (q - 32) in that order; bf16: the high half of the
+// fp32) and multiplied by the fp32 activation on the matrix cores
+// (v_mfma_f32_16x16x4_f32: fp32 products, fp32 sums); only the order of
+// the sums differs from the per-token dot.
+//
+// Operands: the 16 tokens of a tile are the A rows, 16 weight rows the B
+// columns, so a lane's results are one weight row of four tokens and a
+// store writes 16 consecutive rows of a token.  Lane group g (lanes
+// 16g..16g+15) supplies K index g of every 16x16x4 step; over one 256-long
+// block it walks 64 elements of its row:
+//   Q6_K: g = 2h + s -> elements 128h + 32k + 16s + t (k < 4, t < 16), i.e.
+//         the 32 ql bytes at 32g, the 16 qh bytes at 16g and the scales
+//         8h + s + 2k of the planar block (layout.hip);
+//   bf16: elements 64g .. 64g+63.
+// The activations of the workgroup's tokens are staged per block in LDS in
+// natural order (260 floats per token: conflict-free 16-byte reads).
+constexpr int kF32XS = 260;
+
+template <bool BF, int RW, int NT>
+__global__ __launch_bounds__(64 * RW) void mm_batch_f32_kernel(const uint8_t* __restrict__ w,
+                                                               const float* __restrict__ x, float* __restrict__ out,
+                                                               int n, int d, int m) {
+    constexpr int NTHR = 64 * RW;
+    constexpr int TOK = 16 * NT;
+    constexpr int XV = TOK * 64 / NTHR;             // float4 of activations per thread and block
+    static_assert(XV * NTHR == TOK * 64, "token tile must divide among the threads");
+    __shared__ __align__(16) float sx[TOK * kF32XS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, g = lane >> 4;
+    const int row0 = blockIdx.x * (16 * RW) + wave * 16;
+    const int tok0 = blockIdx.y * TOK;
+    const int nb = n >> 8;
+    const size_t rj = (size_t)min(row0 + i, d - 1);  // this lane's weight row
+    const Q6KPlanes P = q6k_planes((size_t)d * nb);
+    const int h = g >> 1, s = g & 1;
+
+    struct WRaw {
+        uint4 v[BF ? 8 : 3];     // bf16: 64 values; Q6_K: ql (2) and qh (1)
+        uint2 sc;
+        uint32_t dh;
+    };
+    auto load_w = [&](int b, WRaw& r) {
+        if (BF) {
+            const uint4* p = reinterpret_cast<const uint4*>(w + (rj * n + (size_t)b * 256 + 64 * g) * 2);
+#pragma unroll
+            for (int k = 0; k < 8; k++) r.v[k] = p[k];
+        } else {
+            const size_t blk = rj * nb + b;
+            const uint4* ql = reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 32 * g);
+            r.v[0] = ql[0];
+            r.v[1] = ql[1];
+            r.v[2] = *reinterpret_cast<const uint4*>(w + P.qh + blk * 64 + 16 * g);
+            r.sc = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+            r.dh = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+        }
+    };
+    struct XRaw {
+        f4_t v[XV];
+    };
+    // unit u = tid + j * NTHR: token u >> 6, float4 u & 63 of the block
+    auto load_x = [&](int b, XRaw& r) {
+#pragma unroll
+        for (int j = 0; j < XV; j++) {
+            const int u = tid + j * NTHR;
+            const int t = min(tok0 + (u >> 6), m - 1);
+            r.v[j] = reinterpret_cast<const f4_t*>(x + (size_t)t * n + (size_t)b * 256)[u & 63];
+        }
+    };
+    auto stage = [&](const XRaw& r) {
+#pragma unroll
+        for (int j = 0; j < XV; j++) {
+            const int u = tid + j * NTHR;
+            *reinterpret_cast<f4_t*>(sx + (u >> 6) * kF32XS + 4 * (u & 63)) = r.v[j];
+        }
+    };
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    WRaw wn;
+    XRaw xn;
+    load_w(0, wn);
+    load_x(0, xn);
+    for (int b = 0; b < nb; b++) {
+        __syncthreads();   // the previous block's LDS reads are done
+        stage(xn);
+        const WRaw wc = wn;
+        // the next block (the last one again at the end: an unconditional
+        // load keeps the prefetch registers out of scratch memory)
+        const int bn = min(b + 1, nb - 1);
+        load_w(bn, wn);
+        load_x(bn, xn);
+        __syncthreads();
+
+        const float* xa = sx + i * kF32XS;
+        if (BF) {
+#pragma unroll
+            for (int t4 = 0; t4 < 16; t4++) {
+                const uint32_t lo = t4 & 1 ? wc.v[t4 >> 1].z : wc.v[t4 >> 1].x;
+                const uint32_t hi = t4 & 1 ? wc.v[t4 >> 1].w : wc.v[t4 >> 1].y;
+                const float wv[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
+                                     __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const float4 a = *reinterpret_cast<const float4*>(xa + 16 * t * kF32XS + 64 * g + 4 * t4);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, wv[0], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, wv[1], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, wv[2], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, wv[3], acc[t], 0, 0, 0);
+                }
+            }
+        } else {
+            const float df = hbits_to_f32(wc.dh);
+            const uint32_t qlw[8] = {wc.v[0].x, wc.v[0].y, wc.v[0].z, wc.v[0].w,
+                                     wc.v[1].x, wc.v[1].y, wc.v[1].z, wc.v[1].w};
+            const uint32_t qhw[4] = {wc.v[2].x, wc.v[2].y, wc.v[2].z, wc.v[2].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                // scale of sub-block 8h + s + 2k (bytes s + 2k of this half's 8)
+                const int sb = s + 2 * k;
+                const float dsc = df * (float)(int8_t)byte_of(sb < 4 ? wc.sc.x : wc.sc.y, sb & 3);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; t4++) {
+                    // elements t = 4t4..4t4+3: ql bytes 16(t>>3) + 8(k&1) + (t&7),
+                    // nibble k>>1; qh bytes t, bits 2k..2k+1
+                    const uint32_t ql = qlw[4 * (t4 >> 1) + 2 * (k & 1) + (t4 & 1)];
+                    const uint32_t q = ((ql >> (4 * (k >> 1))) & 0x0f0f0f0fu) |
+                                       (((qhw[t4] >> (2 * k)) & 0x03030303u) << 4);
+                    const uint32_t qx = q ^ 0x20202020u;   // 6-bit two's complement of q - 32
+                    float wv[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        wv[c] = dsc * (float)(int)__builtin_amdgcn_sbfe(qx, 8 * c, 6);   // the builtin's type is unsigned
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        const float4 a = *reinterpret_cast<const float4*>(xa + 16 * t * kF32XS + 128 * h + 16 * s +
+                                                                          32 * k + 4 * t4);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, wv[0], acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, wv[1], acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, wv[2], acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, wv[3], acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // lane (g, i) holds tokens 4g + v of each tile, weight row row0 + i
+    const int row = row0 + i;
+    if (row < d) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int tok = tok0 + 16 * t + 4 * g + v;
+                if (tok < m) out[(size_t)tok * d + row] = acc[t][v];
+            }
+    }
+}
+
+constexpr int kF32RW = 4, kF32NT = 2;
+
+template <bool BF>
+void launch_mm_batch_f32(const uint8_t* w, const float* x, float* o, int n, int d, int m) {
+    const dim3 grid((d + 16 * kF32RW - 1) / (16 * kF32RW), (m + 16 * kF32NT - 1) / (16 * kF32NT));
+    hipLaunchKernelGGL((mm_batch_f32_kernel<BF, kF32RW, kF32NT>), grid, dim3(64 * kF32RW), 0, g4_stream(), w, x, o, n,
+                       d, m);
+}
+
 // m rows of k floats -> m consecutive device Q8_K rows of k/256 blocks
 __global__ __launch_bounds__(256) void quantize_rows_q8k_kernel(const float* __restrict__ x, uint8_t* __restrict__ y,
                                                                 int nb, int m, size_t stride) {
@@ -385,6 +560,12 @@ extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, in
 
 extern "C" int g4_mm_batch(float* o, const float* x, const void* w, int n, int d, int m, int type, void* q8) {
     G4_CHECK_ARG(o && x && w && m > 0, "g4_mm_batch: bad arguments");
+    if ((type == G4_Q6_K || type == G4_BF16) && n > 0 && n % 256 == 0 && d > 0 && al16(x) && al16(w)) {
+        G4_CHECK_ARG((m + 16 * kF32NT - 1) / (16 * kF32NT) <= 65535, "g4_mm_batch: m=%d too large", m);
+        if (type == G4_Q6_K) launch_mm_batch_f32<false>((const uint8_t*)w, x, o, n, d, m);
+        else launch_mm_batch_f32<true>((const uint8_t*)w, x, o, n, d, m);
+        return g4_check_launch("mm_batch_f32_kernel");
+    }
     if (type == G4_Q4_K || type == G4_Q5_K) {
         G4_CHECK_ARG(q8, "g4_mm_batch: null q8 workspace");
         int rc = g4_quantize_rows_q8_K(x, q8, n, m);

@@ -815,9 +815,7 @@ static int enqueue_prefill_chunk(g4e_model *m, int p0, int M, float *trace, int 
     const int dim = c->dim, L = c->n_layers, pd = c->ple_dim;
     int rc;
     CK(g4_emb_lookup_rows(m->pf_x, m->embd.p, m->embd.type, m->embd.d, m->pf_tok, M, dim, sqrtf((float)dim)));
-    for (int z = 0; z < M; z++)
-        CK(g4_mm(m->pf_ctx + (size_t)z * L * pd, m->pf_x + (size_t)z * dim, m->ple_proj.p, m->ple_proj.n,
-                 m->ple_proj.d, m->ple_proj.type, m->q8, 0));
+    if ((rc = mm_rows(m, m->pf_ctx, m->pf_x, &m->ple_proj, M, 0))) return rc;
     CK(g4_ple_finish_rows(m->pf_ple, m->pf_ctx, m->ple_tok.p, m->ple_tok.type, m->ple_tok.d, m->ple_proj_norm,
                           m->pf_tok, M, pd, L, sqrtf((float)pd), 1.0f / sqrtf((float)dim), 1.0f / sqrtf(2.0f), c->eps));
     CK(g4_rope_table_rows(m->pf_tab_swa, p0, M, c->rot_swa, c->theta_swa, 1.0f, NULL));

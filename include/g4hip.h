@@ -169,8 +169,11 @@ int g4_quantize_rows_q8_K(const float *x, void *y, int k, int m);
  * Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
 int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m, int type);
 /* m tokens through mm(o_t, x_t, w, n, d, type, q8, 0) (main.c:1669): Q4_K /
- * Q5_K quantize all rows into q8 (m * g4_q8K_bytes(n) bytes) and take the
- * batched GEMM; Q6_K and BF16 run the per-token GEMV m times. */
+ * Q5_K quantize all rows into q8 (m * g4_q8K_row_stride(n) bytes) and take
+ * the batched GEMM (bit-identical to the per-token path); Q6_K and BF16 with
+ * n a multiple of 256 and 16-byte aligned x, w: one matrix-core GEMM on the
+ * fp32 activations (the reference's dequantized fp32 weights, fp32 sums in
+ * another order; q8 unused); otherwise the per-token GEMV m times. */
 int g4_mm_batch(float *o, const float *x, const void *w, int n, int d, int m, int type, void *q8);
 
 /* ---------------------------------------------------------------------------
