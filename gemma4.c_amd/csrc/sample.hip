@@ -1,0 +1,268 @@
+// sample.hip -- the reference's token sampler on the device, so that a
+// sampled decode step needs no logits read-back and can be replayed as one
+// HIP graph together with the forward pass.
+//
+// Reference (gemma4-4b/cpu-blas/main.c):
+//   apply_repetition_penalty  2114-2126 (generate applies it at 2408-2410 to
+//                             the tokens generated so far, before sampling)
+//   rng_f32 (xorshift64*)     2035-2040
+//   sample_token              2044-2112: temp <= 0: first index of the
+//                             maximum; else insertion top-k (DEFAULT_TOP_K 40),
+//                             softmax((v - max) / temp) with sequential fp32
+//                             sums, then a plain draw or a top-p draw
+//
+// Top-k.  The insertion sort keeps equal values in index order and admits a
+// value at the full list's end only if it is strictly larger, so its list
+// is the first k of all (value descending, index ascending) pairs.  A 64-bit
+// key (order-preserving value bits, then the complemented index) orders the
+// pairs exactly so; selecting the k largest keys reproduces the list.
+//
+// Pass 1 (G = n / 4096 workgroups): the penalty for the ids of the
+// workgroup's slice (thread 0, in history order, written back to the logits
+// as the reference does), then each lane sorts its 16 keys in registers,
+// each wave pops its k largest (a wave max per pop), and wave 0 merges the
+// four waves' lists into the workgroup's k keys.  Pass 2 (one workgroup):
+// the same selection over the G*k candidates, then one lane runs the
+// reference's sequential softmax / top-p / draw over the k sorted values.
+#include "g4_device.h"
+#include "g4_internal.h"
+
+namespace g4 {
+namespace {
+
+constexpr int kSampleThreads = 256;
+constexpr int kSamplePer = 4096;            // logits per pass-1 workgroup (16 per thread)
+constexpr int kSampleMaxK = 64;
+constexpr int kSampleMaxParts = 64;         // pass 2 holds kSampleMaxParts * kSampleMaxK keys
+
+typedef unsigned long long u64;
+
+__device__ __forceinline__ u64 sample_key(float v, int i) {
+    uint32_t u = __float_as_uint(v + 0.0f);   // -0.0 == +0.0, as the C comparison
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((u64)u << 32) | (uint32_t)(~(uint32_t)i);
+}
+__device__ __forceinline__ float key_value(u64 k) {
+    uint32_t u = (uint32_t)(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+    return __uint_as_float(u);
+}
+__device__ __forceinline__ int key_index(u64 k) { return (int)(~(uint32_t)(k & 0xffffffffu)); }
+
+__device__ __forceinline__ u64 wave_max_key(u64 k) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const u64 o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+// keys[0..R) sorted descending (bitonic network, constant indices)
+template <int R>
+__device__ __forceinline__ void sort_desc(u64 (&k)[R]) {
+#pragma unroll
+    for (int size = 2; size <= R; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const u64 a = k[i], b = k[j];
+                    const bool swap = desc ? a < b : a > b;
+                    k[i] = swap ? b : a;
+                    k[j] = swap ? a : b;
+                }
+            }
+}
+
+// the wave's kk largest of its lanes' keys (each lane's R keys) -> out[0..kk)
+// in descending order (lane 0 writes); keys are distinct or zero
+template <int R>
+__device__ __forceinline__ void wave_top(u64 (&k)[R], int kk, u64* out, int lane) {
+    sort_desc<R>(k);
+    for (int r = 0; r < kk; r++) {
+        const u64 m = wave_max_key(k[0]);
+        const bool pop = k[0] == m;
+#pragma unroll
+        for (int j = 0; j < R - 1; j++) k[j] = pop ? k[j + 1] : k[j];
+        k[R - 1] = pop ? 0ull : k[R - 1];
+        if (lane == 0) out[r] = m;
+    }
+}
+
+// the four waves' lists sk[w][0..kk) -> the workgroup's kk largest (wave 0)
+__device__ __forceinline__ void merge_waves(const u64 (*sk)[kSampleMaxK], int kk, u64* out, int lane) {
+    u64 k[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) k[w] = lane < kk ? sk[w][lane] : 0ull;
+    wave_top<4>(k, kk, out, lane);
+}
+
+struct SampleArgs {
+    float* logits;
+    int n, topk;
+    int* hist;             // generated tokens (device), *hist_n of them
+    int* hist_n;
+    int hist_cap;
+    float penalty;
+    int last_n;
+    float temp, topp;
+    u64* rng;
+    u64* part;
+    int* out;
+    int* dtok;
+    int* dpos;
+};
+
+__global__ __launch_bounds__(kSampleThreads) void sample_partial_kernel(SampleArgs a) {
+    __shared__ u64 sk[4][kSampleMaxK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int base = blockIdx.x * kSamplePer;
+    const int end = min(base + kSamplePer, a.n);
+    if (a.penalty > 1.0f && tid == 0) {
+        const int nh = min(*a.hist_n, a.hist_cap);
+        const int start = a.last_n > 0 && nh > a.last_n ? nh - a.last_n : 0;
+        for (int i = start; i < nh; i++) {
+            const int id = a.hist[i];
+            if (id >= base && id < end) {
+                const float v = a.logits[id];
+                a.logits[id] = v >= 0.0f ? v / a.penalty : v * a.penalty;
+            }
+        }
+        __threadfence_block();   // the penalised logits before the other threads read them
+    }
+    __syncthreads();
+    u64 k[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int i0 = base + 4 * (tid + kSampleThreads * q);
+        if (i0 + 3 < end) {
+            const float4 v = *reinterpret_cast<const float4*>(a.logits + i0);
+            k[4 * q + 0] = sample_key(v.x, i0);
+            k[4 * q + 1] = sample_key(v.y, i0 + 1);
+            k[4 * q + 2] = sample_key(v.z, i0 + 2);
+            k[4 * q + 3] = sample_key(v.w, i0 + 3);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) k[4 * q + c] = i0 + c < end ? sample_key(a.logits[i0 + c], i0 + c) : 0ull;
+        }
+    }
+    wave_top<16>(k, a.topk, sk[wave], lane);
+    __syncthreads();
+    if (wave == 0) merge_waves(sk, a.topk, a.part + (size_t)blockIdx.x * kSampleMaxK, lane);
+}
+
+__device__ __forceinline__ float rng_f32(u64* s) {
+    u64 x = *s;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *s = x;
+    return (float)((x * 0x2545F4914F6CDD1DULL) >> 40) / (float)(1 << 24);
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_final_kernel(SampleArgs a, int G) {
+    __shared__ u64 sk[4][kSampleMaxK];
+    __shared__ u64 top[kSampleMaxK];
+    __shared__ float p[kSampleMaxK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // candidate c = wave * 1024 + lane + 64 j  (G * kSampleMaxK <= 4096)
+    u64 k[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int c = wave * 1024 + lane + 64 * j;
+        const int wg = c / kSampleMaxK, r = c - wg * kSampleMaxK;
+        k[j] = wg < G && r < a.topk ? a.part[c] : 0ull;
+    }
+    wave_top<16>(k, a.topk, sk[wave], lane);
+    __syncthreads();
+    if (wave == 0) merge_waves(sk, a.topk, top, lane);
+    __syncthreads();
+    if (tid != 0) return;
+    int result;
+    if (a.temp <= 0.0f) {
+        result = key_index(top[0]);
+    } else {
+        // sample_token (main.c:2090-2112) over the sorted top-k
+        const int np = a.topk;
+        const float mx = key_value(top[0]);
+        float sum = 0.0f;
+        for (int i = 0; i < np; i++) {
+            p[i] = expf((key_value(top[i]) - mx) / a.temp);
+            sum += p[i];
+        }
+        for (int i = 0; i < np; i++) p[i] /= sum;
+        u64 st = *a.rng;
+        const float coin = rng_f32(&st);
+        if (a.topp <= 0.0f || a.topp >= 1.0f) {
+            float cdf = 0.0f;
+            result = key_index(top[np - 1]);
+            for (int i = 0; i < np; i++) {
+                cdf += p[i];
+                if (coin < cdf) { result = key_index(top[i]); break; }
+            }
+        } else {
+            float cum = 0.0f;
+            int last = np - 1;
+            for (int i = 0; i < np; i++) {
+                cum += p[i];
+                if (cum > a.topp) { last = i; break; }
+            }
+            const float r = rng_f32(&st) * cum;
+            float cdf = 0.0f;
+            result = key_index(top[last]);
+            for (int i = 0; i <= last; i++) {
+                cdf += p[i];
+                if (r < cdf) { result = key_index(top[i]); break; }
+            }
+        }
+        *a.rng = st;
+    }
+    if (a.out) *a.out = result;
+    if (a.dtok) *a.dtok = result;
+    if (a.dpos) *a.dpos = *a.dpos + 1;
+    if (a.hist_n) {
+        const int nh = *a.hist_n;
+        if (nh < a.hist_cap) {
+            a.hist[nh] = result;
+            *a.hist_n = nh + 1;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" size_t g4_sample_part_bytes(int n) {
+    return n > 0 ? (size_t)((n + kSamplePer - 1) / kSamplePer) * kSampleMaxK * sizeof(u64) : 0;
+}
+
+extern "C" int g4_sample(float* logits, int n, float temp, float topp, int topk, float penalty, int penalty_last_n,
+                         int* hist, int* hist_n, int hist_cap, unsigned long long* rng, void* part, int* out, int* dtok,
+                         int* dpos) {
+    G4_CHECK_ARG(logits && part && n > 0, "g4_sample: bad arguments");
+    G4_CHECK_ARG(((uintptr_t)logits & 15) == 0, "g4_sample: logits must be 16-byte aligned");
+    const int G = (n + kSamplePer - 1) / kSamplePer;
+    G4_CHECK_ARG(G <= kSampleMaxParts, "g4_sample: n=%d exceeds %d", n, kSampleMaxParts * kSamplePer);
+    G4_CHECK_ARG(topk >= 1 && topk <= kSampleMaxK && topk <= n, "g4_sample: top-k %d not in 1..%d", topk,
+                 kSampleMaxK);
+    G4_CHECK_ARG(temp <= 0.0f || rng, "g4_sample: sampling needs the rng state");
+    G4_CHECK_ARG(penalty <= 1.0f || (hist && hist_n), "g4_sample: the penalty needs the token history");
+    G4_CHECK_ARG(!hist_n || (hist && hist_cap >= 0), "g4_sample: history without storage");
+    SampleArgs a = {};
+    a.logits = logits; a.n = n; a.topk = temp <= 0.0f ? 1 : topk;
+    a.hist = hist; a.hist_n = hist_n; a.hist_cap = hist_cap;
+    a.penalty = penalty; a.last_n = penalty_last_n;
+    a.temp = temp; a.topp = topp; a.rng = rng; a.part = (u64*)part;
+    a.out = out; a.dtok = dtok; a.dpos = dpos;
+    hipLaunchKernelGGL(sample_partial_kernel, dim3(G), dim3(kSampleThreads), 0, g4_stream(), a);
+    int rc = g4_check_launch("sample_partial_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(sample_final_kernel, dim3(1), dim3(kSampleThreads), 0, g4_stream(), a, G);
+    return g4_check_launch("sample_final_kernel");
+}

@@ -65,6 +65,8 @@ _SIGS = {
     "g4_quantize_rows_q8_K": (I, [VP, VP, I, I]),
     "g4_mm_batch_q8": (I, [VP, VP, VP, I, I, I, I]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
+    "g4_sample_part_bytes": (SZ, [I]),
+    "g4_sample": (I, [VP, I, F, F, I, F, I, VP, VP, I, VP, VP, VP, VP, VP]),
     "g4_emb_lookup_rows": (I, [VP, VP, I, I, VP, I, I, F]),
     "g4_ple_finish_rows": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
     "g4_gelu_mul_rows": (I, [VP, VP, VP, I, I, I]),
@@ -123,6 +125,8 @@ _ENGINE_SIGS = {
     "g4e_layer_x": (C.POINTER(F), [VP]),
     "g4e_generate_greedy": (I, [VP, VP, I, I, VP, C.POINTER(C.c_double), C.POINTER(C.c_double), I]),
     "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
+    "g4e_generate": (I, [VP, VP, I, I, F, F, I, F, I, C.c_uint64, VP, C.POINTER(C.c_double),
+                         C.POINTER(C.c_double), I]),
     "g4e_prefill": (I, [VP, VP, I, I]),
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
@@ -321,6 +325,20 @@ class Engine:
         ps, ds = C.c_double(), C.c_double()
         n = self.E.L.g4e_generate_greedy(self.h, pr.ctypes.data, pr.size, max_new, out.ctypes.data,
                                          C.byref(ps), C.byref(ds), int(use_graph))
+        if n < 0:
+            self.E.check(-n)
+        return out[:n].copy(), ps.value, ds.value
+
+    def generate(self, prompt, max_new: int, temp: float = 0.6, topp: float = 0.9, topk: int = 40,
+                 penalty: float = 1.0, penalty_last_n: int = 64, seed: int = 1, use_graph: bool = True):
+        """generate() with the device sampler (defaults: the reference's
+        temp 0.6, top-p 0.9, top-k 40, penalty 1.0 over 64 tokens); returns
+        (tokens, prefill seconds, decode seconds)."""
+        pr = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max_new + 1, np.int32)
+        ps, ds = C.c_double(), C.c_double()
+        n = self.E.L.g4e_generate(self.h, pr.ctypes.data, pr.size, max_new, temp, topp, topk, penalty,
+                                  penalty_last_n, seed, out.ctypes.data, C.byref(ps), C.byref(ds), int(use_graph))
         if n < 0:
             self.E.check(-n)
         return out[:n].copy(), ps.value, ds.value

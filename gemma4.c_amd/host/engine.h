@@ -16,6 +16,7 @@
 #define G4_ENGINE_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -60,6 +61,18 @@ const float *g4e_layer_x(const g4e_model *m);
  * live in device memory and are advanced by the argmax kernel). */
 int g4e_generate_greedy(g4e_model *m, const int *prompt, int n_prompt, int max_new, int *out_tokens,
                         double *prefill_sec, double *decode_sec, int use_graph);
+
+/* generate (main.c:2335-2488) with sampling: after each decode step the
+ * device sampler (g4_sample) applies the repetition penalty (penalty > 1)
+ * over the last penalty_last_n generated tokens and draws from top-k
+ * (1..64; the reference uses 40), temperature temp (<= 0: greedy) and top-p
+ * topp with the xorshift64* stream seeded by seed (0 means 1, as the
+ * reference).  Stops at max_new tokens or eos; returns the count (negative:
+ * -status).  use_graph: one captured graph per decode step (forward and
+ * sampler; recaptured when the settings change). */
+int g4e_generate(g4e_model *m, const int *prompt, int n_prompt, int max_new, float temp, float topp, int topk,
+                 float penalty, int penalty_last_n, uint64_t seed, int *out_tokens, double *prefill_sec,
+                 double *decode_sec, int use_graph);
 
 /* Timed decode: runs `steps` greedy decode steps from position pos0 with the
  * given input token (after a prefill that filled positions < pos0); returns

@@ -310,6 +310,22 @@ int g4_ple_finish(float *ple, const float *ctx, const void *ple_tok, int type, i
                   const int *dtok, int tok, int pd, int L, float sc_tok, float sc_ctx, float mix, float eps);
 /* g = gelu(g) * ple, then q8 = Q8_K(g) if q8 (main.c:1989-1993) */
 int g4_gelu_mul_quant(float *g, const float *ple, int n, void *q8);
+/* Sampler of generate (main.c:2035-2126) on the device: the repetition
+ * penalty of the last penalty_last_n of the *hist_n tokens in hist (all when
+ * penalty_last_n <= 0; skipped when penalty <= 1; written back to logits as
+ * apply_repetition_penalty does), then sample_token: temp <= 0 the first
+ * index of the maximum, else top-k (1..64, <= n) by (value, first index),
+ * softmax((v - max) / temp), a plain draw or, for 0 < topp < 1, a top-p draw
+ * from the xorshift64* state *rng (advanced as rng_f32 does).  The token
+ * goes to *out, *dtok (nullable) and is appended to hist when *hist_n <
+ * hist_cap; *dpos (nullable) advances by one.  n <= 262144, logits 16-byte
+ * aligned; part: g4_sample_part_bytes(n) device bytes.  All state is on the
+ * device, so the call can be captured in a graph.  Bit-exact except expf,
+ * which may differ from glibc's by an ulp (a draw within that distance of
+ * a cdf step can pick the neighbour). */
+size_t g4_sample_part_bytes(int n);
+int g4_sample(float *logits, int n, float temp, float topp, int topk, float penalty, int penalty_last_n, int *hist,
+              int *hist_n, int hist_cap, unsigned long long *rng, void *part, int *out, int *dtok, int *dpos);
 /* dst[0] = a, dst[1] = b on the library stream (the step's token and position) */
 int g4_store_i32x2(int *dst, int a, int b);
 

@@ -728,6 +728,19 @@ int or_sample_token(const float *logits, int n, float temp, float topp, int topk
     return result;
 }
 
+/* main.c:2114-2126: each of the last penalty_last_n generated tokens (all of
+ * them when penalty_last_n <= 0) divides a non-negative logit by the penalty
+ * or multiplies a negative one, once per occurrence, in history order. */
+void or_apply_repetition_penalty(float *logits, const int *tokens, int n_tokens, float penalty, int penalty_last_n) {
+    if (penalty <= 1.0f || !tokens || n_tokens <= 0) return;
+    const int start = penalty_last_n > 0 && n_tokens > penalty_last_n ? n_tokens - penalty_last_n : 0;
+    for (int i = start; i < n_tokens; i++) {
+        const int id = tokens[i];
+        if (id < 0) continue;
+        logits[id] = logits[id] >= 0.0f ? logits[id] / penalty : logits[id] * penalty;
+    }
+}
+
 /* main.c:1814-1827 */
 void or_hidden_stats(const float *v, int n, float *sum, float *l2, float *amax) {
     double s = 0.0, q = 0.0;

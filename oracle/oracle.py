@@ -75,6 +75,7 @@ class Oracle:
                                       C.c_float, VP, VP]),
             "or_rng_f32": (C.c_float, [VP]),
             "or_sample_token": (C.c_int, [VP, C.c_int, C.c_float, C.c_float, C.c_int, VP]),
+            "or_apply_repetition_penalty": (None, [VP, VP, C.c_int, C.c_float, C.c_int]),
             "or_argmax_first": (C.c_int, [VP, C.c_int]),
             "or_hidden_stats": (None, [VP, C.c_int, VP, VP, VP]),
             "or_model_open": (VP, [VP, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
@@ -254,6 +255,7 @@ class Ref:
             "ref_emb_lookup": (None, [VP, VP, C.c_int, C.c_int, C.c_int]),
             "ref_rng_f32": (C.c_float, [VP]),
             "ref_sample_token": (C.c_int, [VP, C.c_int, C.c_float, C.c_float, C.c_int, VP]),
+            "ref_apply_repetition_penalty": (None, [VP, VP, C.c_int, C.c_float, C.c_int]),
             "ref_is_swa_layer": (C.c_int, [C.c_int, C.c_int, C.c_int]),
             "ref_kv_source_for_layer": (C.c_int, [C.c_int, C.c_int, C.c_int]),
             "ref_layer_head_dim": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),

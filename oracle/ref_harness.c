@@ -74,6 +74,10 @@ int ref_sample_token(float *logits, int n, float temp, float topp, int topk, uns
     return r;
 }
 
+void ref_apply_repetition_penalty(float *logits, const int *tokens, int n_tokens, float penalty, int penalty_last_n) {
+    apply_repetition_penalty(logits, tokens, n_tokens, penalty, penalty_last_n);
+}
+
 /* layer routing, main.c:716-746, on a Config with only the routing fields set */
 int ref_is_swa_layer(int n_layers, int swa_pattern, int l) {
     Config c;

@@ -149,6 +149,20 @@ def main() -> None:
         draws.append([temp, topp, topk, seed] + toks)
     out.update(sample_logits=lg, sample_draws=np.array(draws, np.float64))
 
+    # apply_repetition_penalty (main.c:2114-2126): a 100-token history with
+    # repeats (a token penalised twice or more), ids at either sign of the
+    # logit, windows 64 / all / longer than the history, penalty 1.0 (no-op)
+    hist = rng.integers(0, 512, 100).astype(np.int32)
+    hist[[10, 50, 90, 95]] = 7
+    hist[[60, 61]] = 300
+    pen_out = []
+    pen_cases = ((1.3, 64), (1.1, 0), (2.0, 200), (1.0, 64), (1.5, 5))
+    for penalty, last_n in pen_cases:
+        work = lg.copy()
+        ref.L.ref_apply_repetition_penalty(P(work), P(hist), hist.size, penalty, last_n)
+        pen_out.append(work)
+    out.update(penalty_hist=hist, penalty_cases=np.array(pen_cases, np.float64), penalty_out=np.array(pen_out))
+
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")

@@ -108,3 +108,14 @@ def test_sampler(orc, g):
             toks.append(orc.L.or_sample_token(P(work), 512, temp, topp, topk, P(st)))
         assert toks == [int(v) for v in row[4:]], (temp, topp, topk, seed)
     assert int(g["sample_draws"][0][4]) == 7          # greedy: first index of the tied maximum
+
+
+def test_repetition_penalty(orc, g):
+    """apply_repetition_penalty (main.c:2114-2126): windows of 64, all, longer
+    than the history and 5 tokens; a token repeated four times is penalised
+    four times in turn; penalty 1.0 changes nothing."""
+    hist = np.ascontiguousarray(g["penalty_hist"], np.int32)
+    for (penalty, last_n), want in zip(g["penalty_cases"], g["penalty_out"]):
+        work = g["sample_logits"].copy()
+        orc.L.or_apply_repetition_penalty(P(work), P(hist), hist.size, float(penalty), int(last_n))
+        assert np.array_equal(bits(work), bits(want)), (penalty, last_n)
