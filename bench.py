@@ -389,6 +389,12 @@ def bench_decode(lib, g4, synth, args):
     toks, sec = eng.decode_steps(tok, n_prompt - 1 + args.warmup, args.steps, use_graph=use_graph, record=False)
     tps = args.steps / sec
     _log(f"decode {args.steps} steps: {tps:.1f} tok/s")
+    # the same steps with the reference's default sampling (temp 0.6, top-p
+    # 0.9, top-k 40) on the device after each forward, in the graph
+    _, _ = eng.decode_steps_sampled(tok, n_prompt - 1, args.warmup, use_graph=use_graph)
+    _, sec_s = eng.decode_steps_sampled(tok, n_prompt - 1 + args.warmup, args.steps, use_graph=use_graph)
+    tps_s = args.steps / sec_s
+    _log(f"sampled decode {args.steps} steps: {tps_s:.1f} tok/s")
     eng.close()
     res = {
         "value": round(tps, 2), "unit": "tok/s", "higher_is_better": True,
@@ -398,6 +404,7 @@ def bench_decode(lib, g4, synth, args):
                                "Q4_K_M mix, seed 4); prompt 512 tokens, 511 prefilled in one chunk, then decode",
                    "positions": [n_prompt - 1 + args.warmup, n_prompt - 1 + args.warmup + args.steps],
                    "graph": use_graph, "weights_bytes_per_token": synth.decode_weight_bytes(synth.E4B),
+                   "decode_tok_s_sampled": round(tps_s, 2),
                    "prefill_tok_s": round((n_prompt - 1) / t_prefill, 1),
                    "prefill_tok_s_token_serial": round(n_serial / t_serial, 1),
                    "gguf_write_s": round(t_gen, 1)},

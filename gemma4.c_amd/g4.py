@@ -127,6 +127,7 @@ _ENGINE_SIGS = {
     "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
     "g4e_generate": (I, [VP, VP, I, I, F, F, I, F, I, C.c_uint64, VP, C.POINTER(C.c_double),
                          C.POINTER(C.c_double), I]),
+    "g4e_decode_steps_sampled": (I, [VP, I, I, I, F, F, I, F, I, C.c_uint64, I, VP, C.POINTER(C.c_double)]),
     "g4e_prefill": (I, [VP, VP, I, I]),
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
@@ -348,6 +349,17 @@ class Engine:
         sec = C.c_double()
         self.E.check(self.E.L.g4e_decode_steps(self.h, token, pos0, steps, int(use_graph),
                                                out.ctypes.data if record else None, C.byref(sec)))
+        return (out[:steps].copy() if record else None), sec.value
+
+    def decode_steps_sampled(self, token: int, pos0: int, steps: int, temp: float = 0.6, topp: float = 0.9,
+                             topk: int = 40, penalty: float = 1.0, penalty_last_n: int = 64, seed: int = 1,
+                             use_graph: bool = True, record: bool = False):
+        """decode_steps() with the device sampler after each step."""
+        out = np.zeros(max(steps, 1), np.int32)
+        sec = C.c_double()
+        self.E.check(self.E.L.g4e_decode_steps_sampled(self.h, token, pos0, steps, temp, topp, topk, penalty,
+                                                       penalty_last_n, seed, int(use_graph),
+                                                       out.ctypes.data if record else None, C.byref(sec)))
         return (out[:steps].copy() if record else None), sec.value
 
     def prefill(self, tokens, pos0: int = 0) -> None:

@@ -74,6 +74,11 @@ int g4e_generate(g4e_model *m, const int *prompt, int n_prompt, int max_new, flo
                  float penalty, int penalty_last_n, uint64_t seed, int *out_tokens, double *prefill_sec,
                  double *decode_sec, int use_graph);
 
+/* g4e_decode_steps with the device sampler after every step (settings as
+ * g4e_generate; the history starts empty and the rng at seed) */
+int g4e_decode_steps_sampled(g4e_model *m, int token, int pos0, int steps, float temp, float topp, int topk,
+                             float penalty, int penalty_last_n, uint64_t seed, int use_graph, int *out, double *sec);
+
 /* Timed decode: runs `steps` greedy decode steps from position pos0 with the
  * given input token (after a prefill that filled positions < pos0); returns
  * seconds through *sec.  Tokens are written to out (steps ints, nullable). */
