@@ -8,12 +8,15 @@ Workloads (synthetic inputs, generated from fixed seeds on the host):
           262144, Q4_K_M weight mix, random init; a step is one decode token
           (the default; the metric's workload)
   gemv    one Q4_K x Q8_K GEMV 10240x2560 (seed 0)
-  layer   one decoder layer's projections at hidden 2560 (seed 1)
+  gateup  the fused gate|up GELU GEMV at its decode shape, Q4_K 2 x 10240x2560
+          (seed 1): the decode's dominant kernel alone
   lmhead  tied LM head, Q6_K 262144x2560 times an fp32 hidden vector, with the
           30*tanh(l/30) soft-cap (seed 2)
-  attn    ISWA decode attention over an fp32 KV cache (seed 3)
+  copy    a 64 MiB device copy: the practical HBM ceiling
   prefill batched prefill GEMM: 512 tokens through one E4B layer's Q4_K
           matrices on the matrix cores (seed 1)
+  prefill_e2e  batched prompt prefill through the engine at the E4B shape:
+          511 tokens in one chunk (seed 4); roofline on the Q6_K GEMM (V, FFN down)
 
 Prints ONE JSON line.  `value` is whole-job throughput with inputs resident
 in HBM; `roofline` is the dominant kernel's algorithmic bytes over its average
@@ -216,6 +219,80 @@ def bench_prefill(lib, g4, synth, args):
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_prefill_baseline(mats[3][3], mats[3][2], mats[3][1])
     return res
+
+
+FP32_MFMA_PEAK_TFLOPS = 157.3     # MI355X dense fp32 matrix peak (the batched Q6_K / bf16 GEMM's instruction)
+
+
+def bench_prefill_e2e(lib, g4, synth, args):
+    """Batched prompt prefill through the engine at the E4B shape: a step is
+    g4e_prefill of 511 tokens (chunk of 511: every layer's GEMMs, attention
+    over the chunk's rows, norms, RoPE, appends, PLE).  The roofline kernel is
+    the one that takes most of the time, the Q6_K GEMM on the fp32 matrix
+    cores (FFN down and V), timed alone with HIP events."""
+    path = _gguf_e4b(synth)
+    eng = g4.Engine(path, max_seq=1024)
+    rng = np.random.default_rng(4)
+    m = 511
+    prompt = rng.integers(0, eng.vocab, m).astype(np.int32)
+    for _ in range(args.warmup):
+        eng.prefill(prompt, 0)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.prefill(prompt, 0)                 # returns after the work has completed
+    sec = (time.perf_counter() - t0) / args.steps
+    eng.close()
+    # the dominant kernel, mm_batch_f32_kernel<Q6_K> (V of the 24 storing
+    # layers and FFN down of all 42 over the chunk's rows), timed alone with
+    # HIP events in the engine's proportion of launches: 20 x V 512x2560,
+    # 4 x V 1024x2560, 42 x down 2560x10240 per step
+    shapes = [(2560, 512, 20), (2560, 1024, 4), (10240, 2560, 42)]
+    mats = []
+    for n, d, cnt in shapes:
+        raw = synth.rand_q6K(rng, d, n)
+        w = g4.upload_quant(lib, raw, g4.Q6_K, n, d)
+        x = g4.DBuf.from_array(lib, rng.standard_normal((m, n)).astype(np.float32))
+        out = g4.DBuf(lib, 4 * m * d)
+        mats.append((n, d, cnt, w, x, out))
+    L = lib.L
+
+    def one(i):
+        for n, d, cnt, w, x, out in mats:
+            for _ in range(cnt):
+                L.g4_mm_batch(out.ptr, x.ptr, w.ptr, n, d, m, g4.Q6_K, None)
+    ms1 = _time_steps(lib, one, args)
+    launches = sum(c for _, _, c, *_ in mats)
+    per1 = ms1 / 1e3 / args.steps / launches
+    flops = sum(2.0 * m * n * d * c for n, d, c, *_ in mats) / launches
+    tf1 = flops / per1 / 1e12
+    name = "mm_batch_f32_kernel<Q6_K> (V and FFN down of one 511-token chunk)"
+    res = {
+        "value": round(m / sec, 1), "unit": "tok/s", "higher_is_better": True, "ms_per_step": sec * 1e3,
+        "dtype": "u4 x int8 exact fp16 matrix products (Q4_K), fp32 matrix products (Q6_K, bf16), fp32 glue",
+        "config": {"workload": "synthetic E4B-shape batched prefill (42 layers, hidden 2560, FFN 10240, 8q/2kv heads, "
+                               "head_dim 256/512, window 512, Q4_K_M mix, seed 4): 511 prompt tokens in one chunk",
+                   "tokens": m, "roofline_launches_per_step": launches},
+        "roofline": {"bound": "mfma", "achieved": round(tf1, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf1 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(name),
+                     "kernel": name, "us_per_launch": round(per1 * 1e6, 2)},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_prefill_e2e_baseline(path)
+    return res
+
+
+def cpu_prefill_e2e_baseline(path: str, tokens: int = 4) -> dict:
+    """The reference's prompt loop (forward() per token, main.c:2366-2384) as
+    the oracle's C forward on the same GGUF, over a bounded sample of tokens."""
+    import oracle as orc_mod
+    thr = cpu_threads()
+    om = orc_mod.OracleModel(orc_mod.Oracle(), path, max_seq=64)
+    prompt = np.array([2, 105, 9731, 107, 12][:tokens + 1], np.int32)
+    _, pf, _ = om.generate_greedy(prompt, 1)
+    om.close()
+    return {"value": round(tokens / pf, 3) if pf > 0 else None, "unit": "tok/s", "cores": thr, "kind": "port",
+            "sample": f"oracle forward() per prompt token (C restatement of the reference, gcc -O3 -std=c11, OpenMP "
+                      f"{thr} threads): the first {tokens} prompt positions on the same GGUF"}
 
 
 def cpu_prefill_baseline(raw, n, d, tokens: int = 4):
@@ -447,7 +524,7 @@ def _time_steps(lib, step, args) -> float:
 
 
 WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
-             "copy": bench_copy, "prefill": bench_prefill}
+             "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e}
 
 
 def main() -> int:
@@ -465,9 +542,9 @@ def main() -> int:
               "(the decode path is single-GPU; multi-GPU sharding is a design note only)", file=sys.stderr)
         return 2
     if args.steps is None:
-        args.steps = 128 if args.workload == "decode" else 200
+        args.steps = {"decode": 128, "prefill_e2e": 10}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = 8 if args.workload == "decode" else 20
+        args.warmup = {"decode": 8, "prefill_e2e": 2}.get(args.workload, 20)
     import g4
     import synth
     lib = g4.Lib.get()

@@ -495,13 +495,18 @@ __global__ __launch_bounds__(64 * RW) void mm_batch_f32_kernel(const uint8_t* __
     }
 }
 
-constexpr int kF32RW = 4, kF32NT = 2;
+// tilings from a sweep over 2-8 row waves x 1-4 token tiles at the E4B
+// shapes and 511 tokens (all bit-identical): Q6_K 64 rows x 16 tokens per
+// workgroup (FFN down 310 us against 334 us at 64 x 32; V 26 against 38 us);
+// bf16 64 rows x 32 tokens (PLE projection 302 us against 325 us)
+constexpr int kF32RW = 4;
 
 template <bool BF>
 void launch_mm_batch_f32(const uint8_t* w, const float* x, float* o, int n, int d, int m) {
-    const dim3 grid((d + 16 * kF32RW - 1) / (16 * kF32RW), (m + 16 * kF32NT - 1) / (16 * kF32NT));
-    hipLaunchKernelGGL((mm_batch_f32_kernel<BF, kF32RW, kF32NT>), grid, dim3(64 * kF32RW), 0, g4_stream(), w, x, o, n,
-                       d, m);
+    constexpr int NT = BF ? 2 : 1;
+    const dim3 grid((d + 16 * kF32RW - 1) / (16 * kF32RW), (m + 16 * NT - 1) / (16 * NT));
+    hipLaunchKernelGGL((mm_batch_f32_kernel<BF, kF32RW, NT>), grid, dim3(64 * kF32RW), 0, g4_stream(), w, x, o, n, d,
+                       m);
 }
 
 // m rows of k floats -> m consecutive device Q8_K rows of k/256 blocks
@@ -561,7 +566,7 @@ extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, in
 extern "C" int g4_mm_batch(float* o, const float* x, const void* w, int n, int d, int m, int type, void* q8) {
     G4_CHECK_ARG(o && x && w && m > 0, "g4_mm_batch: bad arguments");
     if ((type == G4_Q6_K || type == G4_BF16) && n > 0 && n % 256 == 0 && d > 0 && al16(x) && al16(w)) {
-        G4_CHECK_ARG((m + 16 * kF32NT - 1) / (16 * kF32NT) <= 65535, "g4_mm_batch: m=%d too large", m);
+        G4_CHECK_ARG((m + 15) / 16 <= 65535, "g4_mm_batch: m=%d too large", m);
         if (type == G4_Q6_K) launch_mm_batch_f32<false>((const uint8_t*)w, x, o, n, d, m);
         else launch_mm_batch_f32<true>((const uint8_t*)w, x, o, n, d, m);
         return g4_check_launch("mm_batch_f32_kernel");
