@@ -284,6 +284,45 @@ __device__ __forceinline__ void residual_core(const ResidualArgs& a, float* buf,
     residual_finish<EPT>(a, r, buf, red, store);
 }
 
+// element e (0..255) of block blk of a planar K-quant tensor with nblk blocks;
+// the fp32 value dequant_q*_k produces (main.c:172-237)
+__device__ inline float dequant_elem(const uint8_t* __restrict__ w, int type, size_t nblk, size_t blk, int e) {
+    if (type == 14) {   // Q6_K
+        const Q6KPlanes p = q6k_planes(nblk);
+        const int h = e >> 7, idx = e & 127, k = idx >> 5, l = idx & 31;
+        const int gq = 64 * h + (k & 1) * 32 + l;            // GGUF ql byte
+        const int r = gq & 63, u = (r & 31) >> 3, c = (r & 7) + (r >= 32 ? 8 : 0);
+        const uint8_t qlb = w[p.ql + blk * 128 + 16 * (4 * h + u) + c];
+        const uint8_t qhb = w[p.qh + blk * 64 + 32 * h + l];
+        const int lo = k < 2 ? (qlb & 15) : (qlb >> 4);
+        const int q = (int)(int8_t)(lo | (((qhb >> (2 * k)) & 3) << 4)) - 32;
+        const int8_t sc = (int8_t)w[p.sc + blk * 16 + 8 * h + (l >> 4) + 2 * k];
+        const float d = f16_to_f32(*reinterpret_cast<const uint16_t*>(w + p.d + blk * 2));
+        return d * (float)sc * (float)q;
+    }
+    // Q4_K / Q5_K: element e is in 64-group c = e/64, nibble half hi = (e/32)&1
+    const bool q5 = type == 13;   // Q5_K
+    const size_t hdr_off = q5 ? q5k_planes(nblk).hdr : q4k_planes(nblk).hdr;
+    const uint8_t* hdr = w + hdr_off + blk * 16;
+    const int c = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+    const int gw = (32 * c + l) >> 2;                          // GGUF qs word
+    const uint8_t qb = w[blk * 128 + 4 * q4k_word_dev(gw) + (l & 3)];
+    int q = hi ? (qb >> 4) : (qb & 15);
+    if (q5) {
+        const uint8_t qh = w[q5k_planes(nblk).qh + blk * 32 + l];
+        if (qh & (1u << (2 * c + hi))) q += 16;
+    }
+    const int j = 2 * c + hi;
+    int sc, m;
+    const uint8_t* s = hdr + 4;
+    if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+    else { sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+    const float d = f16_to_f32(*reinterpret_cast<const uint16_t*>(hdr));
+    const float mn = f16_to_f32(*reinterpret_cast<const uint16_t*>(hdr + 2));
+    const float d1 = d * (float)sc, m1 = mn * (float)m;
+    return d1 * (float)q - m1;
+}
+
 // Q8_K of the nb blocks in buf (LDS) into y (global or LDS, device layout),
 // one wave per block
 __device__ __forceinline__ void quantize_blocks_wg(const float* buf, uint8_t* y, int nb) {

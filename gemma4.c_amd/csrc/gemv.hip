@@ -1083,6 +1083,106 @@ int launch_q6_q8(const void* w, const void* q8, float* o, int nb, int d) {
     return g4_check_launch("gemv_q6k_q8k_kernel");
 }
 
+bool aligned16(const void* p);
+
+// ---- dense weights of any row length (F32, F16, BF16) -----------------------
+// mm_f32 (main.c:1494-1517, cblas_sgemv over row bands), mm_f16 (1519-1527),
+// mm_bf16 (1529-1537): o[i] = sum_j x[j] * w[i][j] in fp32.  One wave per
+// row, x staged in LDS, the row streamed in 16-byte chunks (8 halves or 4
+// floats), eight chunks per lane in flight; the wave's partial sums are
+// added by a butterfly (a tree, not the reference's sequential order).
+template <int T>   // 0: bf16, 1: f16, 2: f32
+__global__ __launch_bounds__(kWG) void gemv_dense_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                         float* __restrict__ out, int n, int d) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* xs = reinterpret_cast<float*>(smem);
+    constexpr int EPC = T == 2 ? 4 : 8;   // elements per 16-byte chunk
+    constexpr int ES = T == 2 ? 4 : 2;    // element bytes
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nch = n / EPC;
+    const int row = blockIdx.x * (kWG / 64) + wave;
+    for (int k = tid; k < n / 4; k += kWG) reinterpret_cast<float4*>(xs)[k] = reinterpret_cast<const float4*>(x)[k];
+    __syncthreads();
+    if (row >= d) return;
+    const uint4* wr = reinterpret_cast<const uint4*>(w + (size_t)row * n * ES);
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 64 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int ch = c0 + lane + 64 * j;
+            v[j] = ch < nch ? wr[ch] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int ch = c0 + lane + 64 * j;
+            if (ch >= nch) continue;
+            const uint32_t u[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            if (T == 2) {
+                const float4 xa = reinterpret_cast<const float4*>(xs)[ch];
+                acc = __builtin_fmaf(xa.x, __uint_as_float(u[0]), acc);
+                acc = __builtin_fmaf(xa.y, __uint_as_float(u[1]), acc);
+                acc = __builtin_fmaf(xa.z, __uint_as_float(u[2]), acc);
+                acc = __builtin_fmaf(xa.w, __uint_as_float(u[3]), acc);
+            } else {
+                const float4 xa = reinterpret_cast<const float4*>(xs)[2 * ch];
+                const float4 xb = reinterpret_cast<const float4*>(xs)[2 * ch + 1];
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t hbits = (u[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    acc = __builtin_fmaf(xv[e], T == 0 ? bf16_to_f32(hbits) : f16_to_f32(hbits), acc);
+                }
+            }
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) out[row] = acc;
+}
+
+// mm_quant_rows (main.c:1539-1556) for Q4_K / Q5_K, the path of the
+// reference's --f32-matmul switch (main.c:1680-1683): every weight
+// dequantized to its fp32 value (dequant_q4_k / dequant_q5_k, main.c:172-211)
+// and multiplied by the fp32 activation.  One wave per row, x in LDS.
+__global__ __launch_bounds__(kWG) void gemv_kq_f32_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                          float* __restrict__ out, int type, int nb, int d) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* xs = reinterpret_cast<float*>(smem);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = nb * 256;
+    const int row = blockIdx.x * (kWG / 64) + wave;
+    for (int k = tid; k < n / 4; k += kWG) reinterpret_cast<float4*>(xs)[k] = reinterpret_cast<const float4*>(x)[k];
+    __syncthreads();
+    if (row >= d) return;
+    const size_t nblk = (size_t)d * nb;
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const size_t blk = (size_t)row * nb + b;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = lane + 64 * k;
+            acc = __builtin_fmaf(xs[b * 256 + e], dequant_elem(w, type, nblk, blk, e), acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) out[row] = acc;
+}
+
+int launch_dense(int T, const char* who, float* o, const float* x, const void* w, int n, int d) {
+    if (!o || !x || !w) return g4_fail(G4_ERR_ARG, "%s: null pointer", who);
+    if (!aligned16(w) || !aligned16(x)) return g4_fail(G4_ERR_ARG, "%s: w and x must be 16-byte aligned", who);
+    const int mult = T == 2 ? 4 : 8;
+    if (n <= 0 || d <= 0 || n % mult || n > 16384)
+        return g4_fail(G4_ERR_ARG, "%s: n=%d unsupported (multiple of %d, <= 16384), d=%d", who, n, mult, d);
+    const dim3 grid((d + kWG / 64 - 1) / (kWG / 64));
+    const size_t lds = (size_t)n * 4;
+    const uint8_t* wp = (const uint8_t*)w;
+    if (T == 0) hipLaunchKernelGGL(gemv_dense_kernel<0>, grid, dim3(kWG), lds, g4_stream(), wp, x, o, n, d);
+    else if (T == 1) hipLaunchKernelGGL(gemv_dense_kernel<1>, grid, dim3(kWG), lds, g4_stream(), wp, x, o, n, d);
+    else hipLaunchKernelGGL(gemv_dense_kernel<2>, grid, dim3(kWG), lds, g4_stream(), wp, x, o, n, d);
+    return g4_check_launch("gemv_dense_kernel");
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_gemv(const char* who, const void* o, const void* w, const void* x, int n, int d) {
@@ -1126,7 +1226,12 @@ extern "C" int g4_vec_dot_q6_K_q8_K(int n, const void* x, const void* y, float* 
 extern "C" int g4_mm_quant_rows(float* o, const float* x, const void* w, int n, int d, int type) {
     int rc = check_gemv("g4_mm_quant_rows", o, w, x, n, d);
     if (rc) return rc;
-    if (type != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_quant_rows: type %d not supported (Q6_K only)", type);
+    if (type == G4_Q4_K || type == G4_Q5_K) {
+        hipLaunchKernelGGL(gemv_kq_f32_kernel, dim3((d + kWG / 64 - 1) / (kWG / 64)), dim3(kWG), (size_t)n * 4,
+                           g4_stream(), (const uint8_t*)w, x, o, type, n / 256, d);
+        return g4_check_launch("gemv_kq_f32_kernel");
+    }
+    if (type != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_quant_rows: type %d not supported", type);
     return launch_q6_f32<false>(w, x, o, n / 256, d, 0.0f);
 }
 
@@ -1142,7 +1247,8 @@ extern "C" int g4_mm_quant_rows_softcap(float* o, const float* x, const void* w,
 extern "C" int g4_mm_bf16(float* o, const float* x, const void* w, int n, int d) {
     if (!o || !x || !w) return g4_fail(G4_ERR_ARG, "g4_mm_bf16: null pointer");
     if (!aligned16(w) || !aligned16(x)) return g4_fail(G4_ERR_ARG, "g4_mm_bf16: w and x must be 16-byte aligned");
-    if (n <= 0 || d <= 0 || n % 8 || n > 4096) return g4_fail(G4_ERR_ARG, "g4_mm_bf16: n=%d unsupported (multiple of 8, <= 4096)", n);
+    if (n > 4096) return launch_dense(0, "g4_mm_bf16", o, x, w, n, d);
+    if (n <= 0 || d <= 0 || n % 8) return g4_fail(G4_ERR_ARG, "g4_mm_bf16: n=%d unsupported (multiple of 8)", n);
     const int cpl = (n / 8 + 63) / 64;
     const size_t lds = (size_t)n * 4;
     const dim3 grid((d + 7) / 8);
@@ -1152,8 +1258,20 @@ extern "C" int g4_mm_bf16(float* o, const float* x, const void* w, int n, int d)
     return g4_check_launch("gemv_bf16_kernel");
 }
 
+// mm_f16 (main.c:1519-1527)
+extern "C" int g4_mm_f16(float* o, const float* x, const void* w, int n, int d) {
+    return launch_dense(1, "g4_mm_f16", o, x, w, n, d);
+}
+
+// mm_f32 (main.c:1494-1517)
+extern "C" int g4_mm_f32(float* o, const float* x, const void* w, int n, int d) {
+    return launch_dense(2, "g4_mm_f32", o, x, w, n, d);
+}
+
 extern "C" int g4_mm(float* o, const float* x, const void* w, int n, int d, int type, void* q8, int q8_ready) {
     switch (type) {
+    case G4_F32: return g4_mm_f32(o, x, w, n, d);
+    case G4_F16: return g4_mm_f16(o, x, w, n, d);
     case G4_Q4_K:
     case G4_Q5_K: {
         if (n % 256) return g4_fail(G4_ERR_ARG, "mm: n=%d not multiple of QK_K", n);

@@ -65,6 +65,9 @@ _SIGS = {
     "g4_quantize_rows_q8_K": (I, [VP, VP, I, I]),
     "g4_mm_batch_q8": (I, [VP, VP, VP, I, I, I, I]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
+    "g4_mm_f16": (I, [VP, VP, VP, I, I]),
+    "g4_mm_f32": (I, [VP, VP, VP, I, I]),
+    "g4_softcap": (I, [VP, I, F]),
     "g4_sample_part_bytes": (SZ, [I]),
     "g4_sample": (I, [VP, I, F, F, I, F, I, VP, VP, I, VP, VP, VP, VP, VP]),
     "g4_emb_lookup_rows": (I, [VP, VP, I, I, VP, I, I, F]),
@@ -131,6 +134,7 @@ _ENGINE_SIGS = {
     "g4e_prefill": (I, [VP, VP, I, I]),
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
+    "g4e_set_f32_matmul": (I, [VP, I]),
     "g4e_read_kv": (I, [VP, I, I, I, VP, VP]),
     "g4e_kv_info": (I, [VP, I, VP]),
 }
@@ -380,6 +384,11 @@ class Engine:
         out = np.zeros(2, np.int32)
         self.E.check(self.E.L.g4e_kv_info(self.h, layer, out.ctypes.data))
         return int(out[0]), int(out[1])
+
+    def set_f32_matmul(self, on: bool) -> None:
+        """Q4_K/Q5_K through dequantized fp32 weights (the reference's
+        --f32-matmul) instead of Q8_K integer dots."""
+        self.E.check(self.E.L.g4e_set_f32_matmul(self.h, int(on)))
 
     def set_prefill_chunk(self, tokens: int) -> None:
         """Tokens per prompt chunk of prefill(); 0: generate_greedy prefills

@@ -103,6 +103,10 @@ int g4e_prefill_trace(g4e_model *m, const int *tokens, int n, int pos0, float *t
  * buffers hold once g4e_prefill has sized them); 0 makes g4e_generate_greedy
  * prefill token by token as the reference's prompt loop does */
 int g4e_set_prefill_chunk(g4e_model *m, int tokens);
+/* 1: Q4_K/Q5_K matrices through mm_quant_rows (dequantized weights times
+ * fp32 activations) instead of Q8_K integer dots, the reference's
+ * --f32-matmul switch (main.c:1680-1683, 2736); 0: the default */
+int g4e_set_f32_matmul(g4e_model *m, int on);
 /* KV cache of a storing layer: out[0] = floats per slot (n_kv * head_dim),
  * out[1] = slots (the window for a sliding-window ring, else max_seq) */
 int g4e_kv_info(const g4e_model *m, int layer, int out[2]);

@@ -12,6 +12,7 @@ names), so one image feeds both the CPU oracle and the HIP engine.
 from __future__ import annotations
 
 import dataclasses
+import fnmatch
 import os
 import struct
 from typing import Iterable
@@ -184,6 +185,7 @@ class ModelShape:
     v_type: int = Q6_K            # V, down, token embeddings
     ffn_type: int = Q4_K          # gate/up (Q5_K variant possible)
     rope_freqs: bool = False      # include a rope_freqs.weight tensor
+    types: tuple = ()             # (glob over tensor names, type) overrides, first match wins
 
     def is_swa(self, l: int) -> bool:
         return (l % self.swa_pattern) < (self.swa_pattern - 1)
@@ -211,7 +213,15 @@ def model_tensors(s: ModelShape) -> list[TensorSpec]:
         ts.append(TensorSpec(name, F32, (n,), lambda r, n=n: r.uniform(lo, hi, n).astype(np.float32)))
 
     def mat(name, qtype, n, d):
-        if qtype == BF16:
+        for pat, t in s.types:
+            if fnmatch.fnmatchcase(name, pat):
+                qtype = t
+                break
+        if qtype in (F16, F32):
+            dt = np.float16 if qtype == F16 else np.float32
+            ts.append(TensorSpec(name, qtype, (n, d), lambda r, n=n, d=d, dt=dt:
+                                 (r.standard_normal((d, n), dtype=np.float32) * 0.02).astype(dt)))
+        elif qtype == BF16:
             ts.append(TensorSpec(name, qtype, (n, d), lambda r, n=n, d=d: rand_bf16(r, d, n)))
         else:
             ts.append(TensorSpec(name, qtype, (n, d), lambda r, q=qtype, n=n, d=d: rand_kquant(r, q, d, n)))

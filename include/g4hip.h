@@ -103,14 +103,19 @@ int g4_vec_dot_q6_K_q8_K(int n, const void *x, const void *y, float *out);
  * with main.c:476/531) or Q6_K (integer Q6_K x Q8_K, see above). */
 int g4_mm_quant_dot_rows(float *o, const void *w, int n, int d, int type, const void *q8);
 /* mm_quant_rows(float *o, const float *x, const void *w, int n, int d, int type),
- * main.c:1539-1556: dequantized weights times fp32 x. */
+ * main.c:1539-1556: dequantized weights times fp32 x; Q6_K, and Q4_K / Q5_K
+ * (the reference's --f32-matmul path, main.c:1680-1683). */
 int g4_mm_quant_rows(float *o, const float *x, const void *w, int n, int d, int type);
-/* mm_bf16 / mm_f16 / mm_f32, main.c:1494-1537 */
+/* mm_bf16 (main.c:1529-1537), mm_f16 (1519-1527), mm_f32 (1494-1517):
+ * row-major 16- or 32-bit weights times fp32 x; n a multiple of 8 (4 for
+ * f32), at most 16384; w and x 16-byte aligned. */
 int g4_mm_bf16(float *o, const float *x, const void *w, int n, int d);
+int g4_mm_f16(float *o, const float *x, const void *w, int n, int d);
+int g4_mm_f32(float *o, const float *x, const void *w, int n, int d);
 /* mm(float *o, const float *x, const void *w, int n, int d, int type,
  * BlockQ8_K *q8, int q8_ready), main.c:1669-1694: Q4_K/Q5_K quantize x into
- * q8 unless q8_ready, then integer dots; Q6_K -> mm_quant_rows; BF16 ->
- * mm_bf16; other types -> G4_ERR_TYPE. */
+ * q8 unless q8_ready, then integer dots; Q6_K -> mm_quant_rows; BF16 / F16 /
+ * F32 -> mm_bf16 / mm_f16 / mm_f32; other types -> G4_ERR_TYPE. */
 int g4_mm(float *o, const float *x, const void *w, int n, int d, int type, void *q8, int q8_ready);
 /* PLE gate (main.c:1988-1993): o[i] = gelu(W_i . q8) * mul[i], W Q4_K/Q5_K. */
 int g4_mm_quant_dot_rows_gelu_mul(float *o, const void *w, int n, int d, int type, const void *q8, const float *mul);
@@ -326,6 +331,8 @@ int g4_gelu_mul_quant(float *g, const float *ple, int n, void *q8);
 size_t g4_sample_part_bytes(int n);
 int g4_sample(float *logits, int n, float temp, float topp, int topk, float penalty, int penalty_last_n, int *hist,
               int *hist_n, int hist_cap, unsigned long long *rng, void *part, int *out, int *dtok, int *dpos);
+/* logits_tied's soft-cap (main.c:1789-1795): v[i] = cap * tanhf(v[i] * (1/cap)) */
+int g4_softcap(float *v, int n, float cap);
 /* dst[0] = a, dst[1] = b on the library stream (the step's token and position) */
 int g4_store_i32x2(int *dst, int a, int b);
 

@@ -486,7 +486,11 @@ void or_mm_f32(float *o, const float *x, const float *w, int n, int d) {
     }
 }
 
-/* main.c:1669-1694 (the --f32-matmul debug switch is not restated). */
+/* the --f32-matmul switch, main.c:1568 (set by main.c:2736) */
+static int or_f32_matmul = 0;
+void or_set_f32_matmul(int on) { or_f32_matmul = on != 0; }
+
+/* main.c:1669-1694 */
 int or_mm(float *o, const float *x, const void *w, int n, int d, int type, or_q8K *q8, int q8_ready) {
     switch (type) {
     case OR_F32: or_mm_f32(o, x, (const float *)w, n, d); return 0;
@@ -495,6 +499,10 @@ int or_mm(float *o, const float *x, const void *w, int n, int d, int type, or_q8
     case OR_Q4_K:
     case OR_Q5_K:
         if (n % OR_QK_K) return -1;
+        if (or_f32_matmul) {
+            or_mm_quant_rows(o, x, w, n, d, type);
+            return 0;
+        }
         if (!q8_ready) or_quantize_q8K(x, q8, n);
         or_mm_quant_dot_rows(o, w, n, d, type, q8);
         return 0;

@@ -121,6 +121,7 @@ void or_attn_decode(const float *q, const float *kc, const float *vc, int kv_str
 
 /* ---- sampler, main.c:2035-2126 ---------------------------------------- */
 float or_rng_f32(uint64_t *state);
+void  or_set_f32_matmul(int on);
 int   or_sample_token(const float *logits, int n, float temp, float topp, int topk, uint64_t *rng);
 void  or_apply_repetition_penalty(float *logits, const int *tokens, int n_tokens, float penalty, int penalty_last_n);
 int   or_argmax_first(const float *v, int n);

@@ -63,6 +63,7 @@ class Oracle:
             "or_mm_bf16": (None, [VP, VP, VP, C.c_int, C.c_int]),
             "or_mm_f16": (None, [VP, VP, VP, C.c_int, C.c_int]),
             "or_mm_f32": (None, [VP, VP, VP, C.c_int, C.c_int]),
+            "or_set_f32_matmul": (None, [C.c_int]),
             "or_mm": (C.c_int, [VP, VP, VP, C.c_int, C.c_int, C.c_int, VP, C.c_int]),
             "or_rmsnorm": (None, [VP, VP, VP, C.c_int, C.c_float]),
             "or_rmsnorm_head_inplace": (None, [VP, VP, C.c_int, C.c_int, C.c_float]),

@@ -82,12 +82,33 @@ def test_wrong_shape_and_missing(tmp_path, eng):
     _expect(eng, _image(tmp_path, s, ts, name="m3.gguf"), g4.G4_ERR_FORMAT, "missing tensor output_norm.weight")
 
 
-def test_token_embd_must_be_q6K(tmp_path, eng):
+def test_token_embd_types(tmp_path, eng):
+    """The token table goes through emb_lookup (main.c:1696-1723: F32, F16,
+    Q4_K, Q5_K, Q6_K) and mm() for the tied LM head: F32 is accepted, BF16
+    (no emb_lookup case: "Unsupported emb type") is not."""
     import g4
     s = synth.tiny_shape()
     ts = _tensors_with(s, "token_embd.weight", qtype=synth.F32, ne=(s.dim, s.vocab),
                        make=lambda r: np.zeros((s.vocab, s.dim), np.float32))
-    _expect(eng, _image(tmp_path, s, ts), g4.G4_ERR_TYPE, "token_embd.weight")
+    assert eng.check_image(_image(tmp_path, s, ts, name="f32.gguf"))[5] == s.vocab
+    ts = _tensors_with(s, "token_embd.weight", qtype=synth.BF16, ne=(s.dim, s.vocab),
+                       make=lambda r: np.zeros((s.vocab, s.dim), np.uint16))
+    _expect(eng, _image(tmp_path, s, ts, name="bf16.gguf"), g4.G4_ERR_TYPE, "token_embd.weight")
+
+
+def test_matrix_types_as_found(tmp_path, eng):
+    """Every matrix goes through mm() (main.c:1669-1694), so each may be F32,
+    F16, BF16, Q4_K, Q5_K or Q6_K, gate and up of different types; a dense
+    row length the GEMV cannot stream is a format error."""
+    import g4
+    s = dataclasses.replace(synth.tiny_shape(), types=(
+        ("blk.2.attn_output.weight", synth.F16), ("blk.4.ffn_gate.weight", synth.Q6_K),
+        ("blk.4.ffn_up.weight", synth.F32), ("per_layer_model_proj.weight", synth.F16),
+        ("token_embd.weight", synth.Q4_K), ("blk.*.proj.weight", synth.Q5_K)))
+    assert eng.check_image(_image(tmp_path, s, name="mixed.gguf"))[0] == s.dim
+    bad = _tensors_with(s, "blk.2.attn_output.weight", ne=(s.n_heads * s.hd_swa - 4, s.dim),
+                        make=lambda r: np.zeros((s.dim, s.n_heads * s.hd_swa - 4), np.float16))
+    _expect(eng, _image(tmp_path, s, bad, name="bad.gguf"), g4.G4_ERR_FORMAT, "blk.2.attn_output.weight")
 
 
 def test_open_without_gpu_fails_cleanly(tmp_path, eng):

@@ -1,0 +1,140 @@
+"""The engine with the tensor types as found in a GGUF: every matrix goes
+through mm() (main.c:1669-1694) and may be F32, F16, BF16, Q4_K, Q5_K or
+Q6_K; the token tables go through emb_lookup (main.c:1696-1723) and the tied
+LM head through mm() and the soft-cap (main.c:1780-1796).  A synthetic model
+mixes them so that every route of the decode step and the prompt chunks
+runs: dense attention outputs, FFN down and PLE projections, gate and up of
+different types (no fused gate|up kernel), Q projections without Q8_K
+activations beside a Q8_K V, a Q4_K token table for both the lookup and the
+LM head.  And the reference's --f32-matmul switch (main.c:1680-1683): Q4_K /
+Q5_K through dequantized fp32 weights.
+
+Parity as tests/test_gpu_engine.py: each layer teacher-forced against the
+oracle's forward (or_forward_inject), same bars.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+MEDIAN_TOL = 2e-6
+P90_TOL = 2e-5
+FLIP_TOL = 1e-3
+FLIP_SHARE = 0.05
+MAX_TOL = 3e-2
+LOGIT_TOL = 1e-5
+
+MIXED = (
+    ("token_embd.weight", synth.Q4_K),
+    ("per_layer_token_embd.weight", synth.F16),
+    ("per_layer_model_proj.weight", synth.F16),
+    ("blk.1*.attn_output.weight", synth.F16),
+    ("blk.2*.ffn_down.weight", synth.BF16),
+    ("blk.3.ffn_gate.weight", synth.Q6_K), ("blk.3.ffn_up.weight", synth.F32),
+    ("blk.4.ffn_gate.weight", synth.Q5_K), ("blk.4.ffn_up.weight", synth.Q4_K),
+    ("blk.5.attn_q.weight", synth.Q6_K),
+    ("blk.6.attn_q.weight", synth.F16), ("blk.6.attn_k.weight", synth.F32), ("blk.6.attn_v.weight", synth.Q5_K),
+    ("blk.7.inp_gate.weight", synth.F32), ("blk.8.inp_gate.weight", synth.Q6_K),
+    ("blk.9.proj.weight", synth.F16), ("blk.1?.proj.weight", synth.Q5_K),
+    ("blk.2*.attn_q.weight", synth.Q5_K),
+)
+
+
+def _model(tmp_path_factory, types, name):
+    s = dataclasses.replace(synth.tiny_shape(rope_freqs=True), types=types)
+    p = str(tmp_path_factory.mktemp("gguf") / name)
+    synth.write_model_gguf(p, s, seed=4)
+    return p
+
+
+@pytest.fixture(scope="module")
+def mixed_path(tmp_path_factory):
+    return _model(tmp_path_factory, MIXED, "mixed.gguf")
+
+
+@pytest.fixture(scope="module")
+def plain_path(tmp_path_factory):
+    return _model(tmp_path_factory, (), "plain.gguf")
+
+
+def _rel(a, b):
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def _bars(errs, what):
+    errs = np.asarray(errs)
+    print(f"{what}: per-layer rel err median {np.median(errs):.2e} p90 {np.percentile(errs, 90):.2e} "
+          f"max {errs.max():.2e} flips {np.mean(errs > FLIP_TOL):.3f}")
+    assert np.median(errs) < MEDIAN_TOL
+    assert np.percentile(errs, 90) < P90_TOL
+    assert np.mean(errs > FLIP_TOL) < FLIP_SHARE
+    assert errs.max() < MAX_TOL
+
+
+def _decode_and_prefill(path, orc, f32_matmul=False):
+    """teacher-forced decode (24 positions, logits at each) and a batched
+    prefill of the same tokens, both against the oracle"""
+    import g4
+    from oracle import OracleModel
+    om = OracleModel(orc, path, max_seq=64)
+    em = g4.Engine(path, max_seq=64)
+    orc.L.or_set_f32_matmul(int(f32_matmul))
+    try:
+        em.set_f32_matmul(f32_matmul)
+        toks = np.random.default_rng(11).integers(0, om.vocab, 24)
+        em.set_trace(True)
+        errs, lerr = [], []
+        for pos, t in enumerate(toks):
+            em.forward(int(t), pos, 1)
+            X = em.layer_x()
+            out = om.forward_inject(int(t), pos, 1, X)
+            errs += [_rel(X[l + 1], out[l]) for l in range(om.n_layers)]
+            lerr.append(_rel(em.logits(), om.logits()))
+        em.set_trace(False)
+        _bars(errs, "decode")
+        assert max(lerr) < LOGIT_TOL, max(lerr)
+        em.set_prefill_chunk(9)
+        tr = em.prefill_trace(toks, 0)
+        perr = []
+        for i, t in enumerate(toks):
+            X = np.ascontiguousarray(tr[:, i, :])
+            out = om.forward_inject(int(t), i, 0, X)
+            perr += [_rel(X[l + 1], out[l]) for l in range(om.n_layers)]
+        _bars(perr, "prefill")
+    finally:
+        orc.L.or_set_f32_matmul(0)
+        em.close()
+        om.close()
+
+
+def test_mixed_types(mixed_path, orc):
+    _decode_and_prefill(mixed_path, orc)
+
+
+def test_f32_matmul(plain_path, orc):
+    _decode_and_prefill(plain_path, orc, f32_matmul=True)
+
+
+def test_mixed_graph_equals_eager(mixed_path):
+    """One captured graph per decode step equals the eager launches on the
+    mixed model, greedy and sampled, and after switching to --f32-matmul (the
+    graphs are recaptured)."""
+    import g4
+    em = g4.Engine(mixed_path, max_seq=64)
+    prompt = [5, 77, 301, 12, 9, 400, 31]
+    try:
+        for f32 in (False, True):
+            em.set_f32_matmul(f32)
+            a = em.generate_greedy(prompt, 16, use_graph=True)[0]
+            b = em.generate_greedy(prompt, 16, use_graph=False)[0]
+            assert np.array_equal(a, b), (f32, a, b)
+            a = em.generate(prompt, 16, 0.8, 0.9, 40, 1.2, 16, 5, use_graph=True)[0]
+            b = em.generate(prompt, 16, 0.8, 0.9, 40, 1.2, 16, 5, use_graph=False)[0]
+            assert np.array_equal(a, b), (f32, a, b)
+    finally:
+        em.close()

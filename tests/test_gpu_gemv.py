@@ -436,3 +436,64 @@ def test_mm_residual_q8_qkv(lib, orc, qtype, d1, d2, d3):
     mag = W @ np.abs(xb.astype(np.float64))
     err = np.abs(o3.to_array(np.float32).astype(np.float64) - want) / mag
     assert err.max() <= 1e-5, err.max()
+
+
+def _dense(rng, qtype, d, n):
+    """(device bytes, oracle function) of a random dense matrix"""
+    if qtype == 30:
+        return synth.rand_bf16(rng, d, n), "or_mm_bf16"
+    a = (rng.standard_normal((d, n), dtype=np.float32) * 0.05)
+    if qtype == 1:
+        return a.astype(np.float16).view(np.uint16), "or_mm_f16"
+    return a.astype(np.float32), "or_mm_f32"
+
+
+@pytest.mark.parametrize("qtype,n,d", [(1, 2560, 300), (1, 10240, 64), (0, 2560, 77), (0, 10240, 33), (0, 4100, 9),
+                                       (30, 10240, 40), (30, 2560, 96), (1, 256, 16), (1, 16384, 8)])
+def test_dense_gemv(lib, orc, qtype, n, d):
+    """mm_f16 / mm_f32 / mm_bf16 (main.c:1494-1537) through g4_mm, rows up to
+    16384 long: 1e-5 of sum |w x| against the oracle's sequential sums."""
+    from g4 import DBuf
+    rng = np.random.default_rng(n + d + qtype)
+    w, fn = _dense(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    wd, xd, out = dbuf(lib, w), dbuf(lib, x), DBuf(lib, 4 * d)
+    lib.g4_mm(out.ptr, xd.ptr, wd.ptr, n, d, qtype, None, 0)
+    got = out.to_array(np.float32)
+    want = np.empty(d, np.float32)
+    getattr(orc.L, fn)(P(want), P(x), P(w), n, d)
+    W = {30: (w.astype(np.uint32) << 16).view(np.float32), 1: w.view(np.float16).astype(np.float32),
+         0: w}[qtype].astype(np.float64)
+    mag = np.abs(W) @ np.abs(x.astype(np.float64))
+    assert (np.abs(got.astype(np.float64) - want) <= 1e-5 * mag).all()
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+@pytest.mark.parametrize("n,d", [(2560, 96), (10240, 40), (256, 8)])
+def test_quant_rows_f32_q45(lib, orc, qtype, n, d):
+    """mm_quant_rows for Q4_K / Q5_K (the reference's --f32-matmul path,
+    main.c:1680-1683): dequantized weights times fp32 x, 1e-5 of sum |w x|."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(n * 7 + d + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w, xd, out = upload_quant(lib, raw, qtype, n, d), dbuf(lib, x), DBuf(lib, 4 * d)
+    lib.g4_mm_quant_rows(out.ptr, xd.ptr, w.ptr, n, d, qtype)
+    got = out.to_array(np.float32)
+    want = orc.mm_quant_rows(x, raw, n, d, qtype)
+    W = np.abs(kq.dequant_f64(raw.reshape(-1, synth.BLOCK_BYTES[qtype]), qtype).reshape(d, n))
+    mag = W @ np.abs(x.astype(np.float64))
+    assert (np.abs(got.astype(np.float64) - want) / mag).max() <= 1e-5
+
+
+def test_softcap(lib):
+    """logits_tied's soft-cap (main.c:1789-1795) within a few ulp of
+    cap * tanh(v / cap) (device tanhf against the exact value)."""
+    rng = np.random.default_rng(17)
+    v = (rng.standard_normal(100003) * 40).astype(np.float32)
+    vd = dbuf(lib, v)
+    lib.g4_softcap(vd.ptr, v.size, C.c_float(30.0))
+    got = vd.to_array(np.float32).astype(np.float64)
+    inv = np.float32(1.0) / np.float32(30.0)
+    want = 30.0 * np.tanh((v * inv).astype(np.float64))
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) < 2e-6
