@@ -191,6 +191,48 @@ static bool table_type_ok(int type) {
            type == G4_Q6_K;
 }
 
+// hidden_stats (main.c:1813-1826): sum and sum of squares in double, the
+// largest |x|; out = (float)sum, (float)sqrt(sum of squares), amax.  The
+// double sums are a tree instead of the reference's loop (the same floats
+// unless a sum lands within a double rounding of a float boundary).
+__global__ __launch_bounds__(256) void hidden_stats_kernel(const float* __restrict__ v, int n, float* __restrict__ out) {
+    __shared__ double s1[256], s2[256];
+    __shared__ float s3[256];
+    const int tid = threadIdx.x;
+    double a = 0.0, b = 0.0;
+    float m = 0.0f;
+    for (int i = tid; i < n; i += 256) {
+        const float x = v[i];
+        a += (double)x;
+        b += (double)x * (double)x;
+        const float ax = x >= 0.0f ? x : -x;
+        if (ax > m) m = ax;
+    }
+    s1[tid] = a;
+    s2[tid] = b;
+    s3[tid] = m;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) {
+            s1[tid] += s1[tid + st];
+            s2[tid] += s2[tid + st];
+            s3[tid] = s3[tid + st] > s3[tid] ? s3[tid + st] : s3[tid];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        out[0] = (float)s1[0];
+        out[1] = (float)sqrt(s2[0]);
+        out[2] = s3[0];
+    }
+}
+
+extern "C" int g4_hidden_stats(const float* v, int n, float* out) {
+    G4_CHECK_ARG(v && out && n > 0, "g4_hidden_stats: bad arguments");
+    hipLaunchKernelGGL(hidden_stats_kernel, dim3(1), dim3(256), 0, g4_stream(), v, n, out);
+    return g4_check_launch("hidden_stats_kernel");
+}
+
 // logits[i] = cap * tanhf(logits[i] * inv), logits_tied's soft-cap (main.c:1789-1795)
 __global__ __launch_bounds__(256) void softcap_kernel(float* __restrict__ v, int n, float cap, float inv) {
     const int i = blockIdx.x * 256 + threadIdx.x;

@@ -68,6 +68,7 @@ _SIGS = {
     "g4_mm_f16": (I, [VP, VP, VP, I, I]),
     "g4_mm_f32": (I, [VP, VP, VP, I, I]),
     "g4_softcap": (I, [VP, I, F]),
+    "g4_hidden_stats": (I, [VP, I, VP]),
     "g4_sample_part_bytes": (SZ, [I]),
     "g4_sample": (I, [VP, I, F, F, I, F, I, VP, VP, I, VP, VP, VP, VP, VP]),
     "g4_emb_lookup_rows": (I, [VP, VP, I, I, VP, I, I, F]),
@@ -135,6 +136,8 @@ _ENGINE_SIGS = {
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
     "g4e_set_f32_matmul": (I, [VP, I]),
+    "g4e_set_dump_hidden_at": (I, [VP, I]),
+    "g4e_hidden_stats": (I, [VP, VP]),
     "g4e_read_kv": (I, [VP, I, I, I, VP, VP]),
     "g4e_kv_info": (I, [VP, I, VP]),
 }
@@ -384,6 +387,17 @@ class Engine:
         out = np.zeros(2, np.int32)
         self.E.check(self.E.L.g4e_kv_info(self.h, layer, out.ctypes.data))
         return int(out[0]), int(out[1])
+
+    def set_dump_hidden_at(self, pos: int) -> None:
+        """record the --dump-hidden-at fingerprints of position pos (-1: off)"""
+        self.E.check(self.E.L.g4e_set_dump_hidden_at(self.h, pos))
+
+    def hidden_stats(self) -> np.ndarray:
+        """(2 n_layers + 1, 3) (sum, l2, max): after the embedding, then per
+        layer after the attention residual and at the layer's end"""
+        out = np.zeros((2 * self.n_layers + 1, 3), np.float32)
+        self.E.check(self.E.L.g4e_hidden_stats(self.h, out.ctypes.data))
+        return out
 
     def set_f32_matmul(self, on: bool) -> None:
         """Q4_K/Q5_K through dequantized fp32 weights (the reference's

@@ -103,6 +103,15 @@ int g4e_prefill_trace(g4e_model *m, const int *tokens, int n, int pos0, float *t
  * buffers hold once g4e_prefill has sized them); 0 makes g4e_generate_greedy
  * prefill token by token as the reference's prompt loop does */
 int g4e_set_prefill_chunk(g4e_model *m, int tokens);
+/* --dump-hidden-at (main.c:1811, 1857-2010): the forward of position pos
+ * (eager decode steps, token-by-token or chunked prompts; generate runs
+ * without graphs while it is set) records hidden_stats of x after the
+ * embedding, after each layer's attention residual and at each layer's end;
+ * -1 turns it off.  g4e_hidden_stats copies the last record: (2 n_layers + 1)
+ * x (sum, l2, max) floats, rows 0, then 1 + 2l (attention residual of layer
+ * l) and 2 + 2l (end of layer l). */
+int g4e_set_dump_hidden_at(g4e_model *m, int pos);
+int g4e_hidden_stats(g4e_model *m, float *out);
 /* 1: Q4_K/Q5_K matrices through mm_quant_rows (dequantized weights times
  * fp32 activations) instead of Q8_K integer dots, the reference's
  * --f32-matmul switch (main.c:1680-1683, 2736); 0: the default */

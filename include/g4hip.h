@@ -331,6 +331,10 @@ int g4_gelu_mul_quant(float *g, const float *ple, int n, void *q8);
 size_t g4_sample_part_bytes(int n);
 int g4_sample(float *logits, int n, float temp, float topp, int topk, float penalty, int penalty_last_n, int *hist,
               int *hist_n, int hist_cap, unsigned long long *rng, void *part, int *out, int *dtok, int *dpos);
+/* hidden_stats (main.c:1813-1826), the --dump-hidden-at fingerprint of a
+ * vector: out[0] = sum, out[1] = l2 norm (both accumulated in double),
+ * out[2] = max |v| (device pointers; one launch) */
+int g4_hidden_stats(const float *v, int n, float *out);
 /* logits_tied's soft-cap (main.c:1789-1795): v[i] = cap * tanhf(v[i] * (1/cap)) */
 int g4_softcap(float *v, int n, float cap);
 /* dst[0] = a, dst[1] = b on the library stream (the step's token and position) */

@@ -789,6 +789,7 @@ struct or_model {
     float *kc, *vc;
     or_q8K *q8;
     float *stats; /* n_layers*3 + 8 */
+    float *astats; /* n_layers*3: hidden_stats of x after each layer's attention residual (main.c:1964-1969) */
     float *layer_x; /* n_layers*dim: x after each layer of the last forward */
 };
 
@@ -1022,6 +1023,7 @@ or_model *or_model_open(const uint8_t *data, size_t size, int max_seq, char *err
     const int q8n = (m->hidden > OR_MAX_Q_DIM ? m->hidden : OR_MAX_Q_DIM) / OR_QK_K + 1;
     m->q8 = (or_q8K *)calloc((size_t)q8n, sizeof(or_q8K));
     m->stats = (float *)calloc((size_t)L * 3 + 8, 4);
+    m->astats = (float *)calloc((size_t)L * 3, 4);
     m->layer_x = (float *)calloc((size_t)L * m->dim, 4);
     if (!m->kc || !m->vc) { or_model_close(m); set_err(err, errlen, "out of memory"); return NULL; }
     return m;
@@ -1036,7 +1038,7 @@ void or_model_close(or_model *m) {
     free(m->down); free(m->inp_gate); free(m->proj);
     free(m->x); free(m->xb); free(m->xb2); free(m->hb); free(m->hb2); free(m->q); free(m->k);
     free(m->v); free(m->q_out); free(m->ple); free(m->ple_ctx); free(m->ple_gate); free(m->att);
-    free(m->logits); free(m->kc); free(m->vc); free(m->q8); free(m->stats); free(m->layer_x);
+    free(m->logits); free(m->kc); free(m->vc); free(m->q8); free(m->stats); free(m->astats); free(m->layer_x);
     free(m);
 }
 
@@ -1048,6 +1050,7 @@ void or_model_config(const or_model *m, int out[9]) {
 const float *or_model_logits(const or_model *m) { return m->logits; }
 const float *or_model_x(const or_model *m) { return m->x; }
 const float *or_model_layer_stats(const or_model *m) { return m->stats; }
+const float *or_model_attn_stats(const or_model *m) { return m->astats; }
 const float *or_model_layer_x(const or_model *m) { return m->layer_x; }
 
 /* main.c:1747-1778 */
@@ -1119,6 +1122,7 @@ static int layer_step(or_model *m, int l, int pos, float *x_before) {
     if (or_mm(m->xb2, m->q_out, m->wo[l].p, q_dim, dim, m->wo[l].type, m->q8, 0)) return -1;
     or_rmsnorm(m->xb2, m->xb2, m->post_attn_norm[l], dim, m->eps);
     for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
+    or_hidden_stats(m->x, dim, &m->astats[3 * l], &m->astats[3 * l + 1], &m->astats[3 * l + 2]);
     memcpy(x_before, m->x, (size_t)dim * sizeof(float));
     or_rmsnorm(m->xb2, m->x, m->ffn_norm[l], dim, m->eps);
     const int q8_ffn = (m->gate[l].type == OR_Q4_K || m->gate[l].type == OR_Q5_K);

@@ -148,6 +148,7 @@ const float *or_model_x(const or_model *m);
 /* Per-layer fingerprints captured during the last forward (sum,l2,max per layer
  * after the layer, plus K_store and q_out of layer 0). n_layers*3 floats. */
 const float *or_model_layer_stats(const or_model *m);
+const float *or_model_attn_stats(const or_model *m);
 /* x after every layer of the last forward (n_layers*dim floats) */
 const float *or_model_layer_x(const or_model *m);
 /* Greedy generation loop (main.c:2335-2488 with temp=0): prompt is fed

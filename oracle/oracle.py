@@ -87,6 +87,7 @@ class Oracle:
             "or_model_logits": (VP, [VP]),
             "or_model_x": (VP, [VP]),
             "or_model_layer_stats": (VP, [VP]),
+            "or_model_attn_stats": (VP, [VP]),
             "or_model_layer_x": (VP, [VP]),
             "or_generate_greedy": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, VP, VP]),
         }
@@ -196,6 +197,11 @@ class OracleModel:
     def layer_stats(self) -> np.ndarray:
         p = self.o.L.or_model_layer_stats(self.h)
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (self.n_layers * 3 + 8,)).copy()
+
+    def attn_stats(self) -> np.ndarray:
+        """(n_layers, 3): hidden_stats after each layer's attention residual"""
+        p = self.o.L.or_model_attn_stats(self.h)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (self.n_layers * 3,)).copy().reshape(-1, 3)
 
     def layer_x(self) -> np.ndarray:
         p = self.o.L.or_model_layer_x(self.h)
