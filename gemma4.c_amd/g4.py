@@ -136,6 +136,8 @@ _ENGINE_SIGS = {
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
     "g4e_set_f32_matmul": (I, [VP, I]),
+    "g4e_sha256_file": (I, [C.c_char_p, C.c_char_p]),
+    "g4e_check_sha256sum": (I, [C.c_char_p, C.c_char_p]),
     "g4e_set_dump_hidden_at": (I, [VP, I]),
     "g4e_hidden_stats": (I, [VP, VP]),
     "g4e_read_kv": (I, [VP, I, I, I, VP, VP]),
@@ -277,6 +279,15 @@ class EngineLib:
     def check(self, rc: int) -> None:
         if rc != G4_OK:
             raise G4Error(rc, self.L.g4e_last_error().decode())
+
+    def sha256_file(self, path: str) -> str:
+        out = C.create_string_buffer(65)
+        self.check(self.L.g4e_sha256_file(path.encode(), out))
+        return out.value.decode()
+
+    def check_sha256sum(self, path: str, sumfile: str) -> None:
+        """`sha256sum --check` of one file against a checksum file's line"""
+        self.check(self.L.g4e_check_sha256sum(path.encode(), sumfile.encode()))
 
     def check_image(self, data, max_seq: int = 0) -> list[int]:
         buf = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data

@@ -112,6 +112,12 @@ int g4e_set_prefill_chunk(g4e_model *m, int tokens);
  * l) and 2 + 2l (end of layer l). */
 int g4e_set_dump_hidden_at(g4e_model *m, int pos);
 int g4e_hidden_stats(g4e_model *m, float *out);
+/* SHA-256 of a file as 64 lowercase hex digits (hex[64] = 0), and the
+ * `sha256sum --check` of the model download (gemma4-4b/Makefile `model`,
+ * design.md:107-117): the line of sumfile naming path's base name must carry
+ * its digest (G4_ERR_FORMAT otherwise).  Host only. */
+int g4e_sha256_file(const char *path, char hex[65]);
+int g4e_check_sha256sum(const char *path, const char *sumfile);
 /* 1: Q4_K/Q5_K matrices through mm_quant_rows (dequantized weights times
  * fp32 activations) instead of Q8_K integer dots, the reference's
  * --f32-matmul switch (main.c:1680-1683, 2736); 0: the default */

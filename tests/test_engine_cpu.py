@@ -120,3 +120,39 @@ def test_open_without_gpu_fails_cleanly(tmp_path, eng):
     with pytest.raises(g4.G4Error) as e:
         g4.Engine(img)
     assert e.value.code == g4.G4_ERR_NODEV
+
+
+@pytest.mark.parametrize("size", [0, 1, 55, 56, 63, 64, 119, 120, 1000, (1 << 20) + 77, 3 << 20])
+def test_sha256_file(tmp_path, eng, size):
+    """SHA-256 of the model file (the download check of gemma4-4b/Makefile,
+    design.md:107-117) against Python's hashlib, across the padding edges
+    (55/56, 119/120 bytes) and the 1 MiB read chunks."""
+    import hashlib
+    data = np.random.default_rng(size).integers(0, 256, size, dtype=np.uint8).tobytes()
+    p = tmp_path / f"f{size}.bin"
+    p.write_bytes(data)
+    assert eng.sha256_file(str(p)) == hashlib.sha256(data).hexdigest()
+
+
+def test_check_sha256sum(tmp_path, eng):
+    """sha256sum --check semantics for one named file: text and binary marks,
+    upper-case digests; a mismatch or a missing line is an error."""
+    import hashlib
+    import g4
+    data = b"gguf model bytes" * 1000
+    p = tmp_path / "model.gguf"
+    p.write_bytes(data)
+    h = hashlib.sha256(data).hexdigest()
+    ok = tmp_path / "ok.sha256sum"
+    ok.write_text(f"{'0' * 64}  other.gguf\n{h.upper()} *model.gguf\n")
+    eng.check_sha256sum(str(p), str(ok))
+    bad = tmp_path / "bad.sha256sum"
+    bad.write_text(f"{'1' * 64}  model.gguf\n")
+    with pytest.raises(g4.G4Error) as e:
+        eng.check_sha256sum(str(p), str(bad))
+    assert "FAILED" in str(e.value)
+    none = tmp_path / "none.sha256sum"
+    none.write_text(f"{h}  another.gguf\n")
+    with pytest.raises(g4.G4Error) as e:
+        eng.check_sha256sum(str(p), str(none))
+    assert "no checksum line" in str(e.value)
