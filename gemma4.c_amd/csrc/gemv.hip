@@ -565,10 +565,8 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
     constexpr int NWV = PRO ? 4 : 1;              // waves per workgroup
     constexpr int Q8B = NB * 292;                 // device Q8_K bytes
     constexpr int Q8C = Q8B / 16, Q8T = (Q8B - Q8C * 16) / 4;
-    constexpr int HC = RPW * NB;                  // header chunks per matrix and wave
-    constexpr int QPL = PRO ? 0 : (Q8C + 63) / 64, HPL = (HC + 63) / 64;
+    constexpr int QPL = PRO ? 0 : (Q8C + 63) / 64;
     __shared__ __align__(16) uint8_t sq[Q8B + 16];
-    __shared__ __align__(16) uint8_t shw[NWV][NMAT][HC * 16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l = lane & 7, k = l & 3;
     const int grp = (lane >> 3) & (RPW - 1);
     const int m = NMAT == 2 ? lane >> 5 : 0;
@@ -576,11 +574,11 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
     const int row = min(r0 + grp, d - 1);
     const uint32_t nblk = (uint32_t)d * NB;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk, qh_off = 128u * nblk;   // q4k_planes / q5k_planes
-    uint8_t (&sh)[NMAT][HC * 16] = shw[wv];
 
     [[maybe_unused]] ResidualRegs<NB> rr;
     if constexpr (PRO) residual_load<NB>(ra, rr);
-    uint4 qv[QPL > 0 ? QPL : 1], hv[NMAT][HPL];
+    // the Q8_K vector is staged in LDS (the same for every wave)
+    uint4 qv[QPL > 0 ? QPL : 1];
     uint32_t tv = 0u;
 #pragma unroll
     for (int j = 0; j < QPL; j++) {
@@ -589,23 +587,19 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
         if (c < Q8C) qv[j] = reinterpret_cast<const uint4*>(q8)[c];
     }
     if (!PRO && lane < Q8T) tv = reinterpret_cast<const uint32_t*>(q8 + Q8C * 16)[lane];
-#pragma unroll
-    for (int j = 0; j < HPL; j++) {
-        const int c = lane + 64 * j;
-        const uint32_t blk = (uint32_t)min(r0 + c / NB, d - 1) * NB + (uint32_t)(c % NB);
-#pragma unroll
-        for (int mm = 0; mm < NMAT; mm++) {
-            hv[mm][j] = make_uint4(0u, 0u, 0u, 0u);
-            if (c < HC) hv[mm][j] = *reinterpret_cast<const uint4*>((mm ? w1 : w0) + hdr_off + blk * 16u);
-        }
-    }
+    // each lane loads its row's block headers with its weights (the 8 lanes
+    // of a group read the same 16 bytes: one request).  Staged through LDS
+    // instead, the header loads under a lane condition compiled to a branch
+    // whose result copy waited for every load before it (vmcnt(0)), so the
+    // weight loads started only after the staging loads had returned
     const uint8_t* const wm = m ? w1 : w0;
     const uint32_t rb = (uint32_t)row * NB;
-    uint4 wq[NB];
+    uint4 wq[NB], hd[NB];
     uint32_t qh[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         wq[b] = *reinterpret_cast<const uint4*>(wm + (rb + b) * 128u + 16 * l);
+        hd[b] = *reinterpret_cast<const uint4*>(wm + hdr_off + (rb + b) * 16u);
         qh[b] = Q5 ? *reinterpret_cast<const uint32_t*>(wm + qh_off + (rb + b) * 32u + 4 * l) : 0u;
     }
     __builtin_amdgcn_sched_barrier(0);   // all loads issued before the LDS stores wait for the first ones
@@ -624,13 +618,6 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
         }
         if (lane < Q8T) reinterpret_cast<uint32_t*>(sq + Q8C * 16)[lane] = tv;
     }
-#pragma unroll
-    for (int j = 0; j < HPL; j++) {
-        const int c = lane + 64 * j;
-#pragma unroll
-        for (int mm = 0; mm < NMAT; mm++)
-            if (c < HC) reinterpret_cast<uint4*>(sh[mm])[c] = hv[mm][j];
-    }
     __syncthreads();
 
     // byte selectors of the two mins (m_2k, m_2k+1 of min lane k), as int16 pairs
@@ -648,12 +635,11 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
         const uint4 a1 = *reinterpret_cast<const uint4*>(a_qs + 16);
         const uint2 bsw = *reinterpret_cast<const uint2*>(sq + q8k_bsums_off(NB) + b * 32 + 8 * k);
         const float yd = reinterpret_cast<const float*>(sq + q8k_d_off(NB))[b];
-        const uint4 hd = *reinterpret_cast<const uint4*>(sh[m] + (grp * NB + b) * 16);
         // the 6-bit scales (sub-blocks 0..3, 4..7) and this min lane's two mins
-        const uint32_t sc_lo = hd.y & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (hd.w & 0x0f0f0f0fu) | (((hd.y >> 6) & 0x03030303u) << 4);
-        const uint32_t mn_lo = hd.z & 0x3f3f3f3fu;
-        const uint32_t mn_hi = ((hd.w >> 4) & 0x0f0f0f0fu) | (((hd.z >> 6) & 0x03030303u) << 4);
+        const uint32_t sc_lo = hd[b].y & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (hd[b].w & 0x0f0f0f0fu) | (((hd[b].y >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = hd[b].z & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((hd[b].w >> 4) & 0x0f0f0f0fu) | (((hd[b].z >> 6) & 0x03030303u) << 4);
         const uint32_t mnw = (mn_lo & kmask) | (mn_hi & ~kmask);
         int32_t sumi = 0;
 #pragma unroll
@@ -672,8 +658,8 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
         }
         int32_t P = dot2_i16(bsw.x, __builtin_amdgcn_perm(0u, mnw, selA),
                              dot2_i16(bsw.y, __builtin_amdgcn_perm(0u, mnw, selB), 0));
-        const float D = yd * half_bits_to_f32(hd.x & 0xffffu);
-        const float DM = -yd * half_bits_to_f32(hd.x >> 16);
+        const float D = yd * half_bits_to_f32(hd[b].x & 0xffffu);
+        const float DM = -yd * half_bits_to_f32(hd[b].x >> 16);
         if (Q5) {
             // the four min products summed exactly, on every lane of the group
             int32_t pm = l < 4 ? P : 0;
