@@ -701,7 +701,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     if (fuse) {
         wq.load(a.q_norm, lane);
 #pragma unroll
-        for (int i = 0; i < W; i++) rc[i] = W * lane + i < a.n_rot / 2 ? a.tab[W * lane + i] : make_float2(1.0f, 0.0f);
+        // every lane loads a pair (clamped: n_rot >= 2 is checked at
+        // launch; rope_vec leaves pairs past n_rot/2 alone): a load under a
+        // lane condition is followed by a wait for every load issued
+        // before it
+        for (int i = 0; i < W; i++) rc[i] = a.tab[min(W * lane + i, a.n_rot / 2 - 1)];
         if (append) {
             wk.load(a.k_norm, lane);
             kn.load(a.kraw + (size_t)kvh * HD, lane);
