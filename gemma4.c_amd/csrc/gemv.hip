@@ -316,6 +316,9 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
     const uint32_t qh_off = 128u * nblk;
     const uint32_t rb = (uint32_t)rl * (uint32_t)nb;             // first block of the row
+    // the epilogue's multiplier, loaded now (without one: this row of the
+    // output, which only this group writes, read and not used)
+    const float aux_v = (aux ? aux : outp)[rl];
     const uint8_t* a_qs = q8 + 32 * l;
     const uint8_t* a_bs = q8 + q8k_bsums_off(nb) + 8 * k;
     const float* a_d = reinterpret_cast<const float*>(q8 + q8k_d_off(nb));
@@ -421,11 +424,11 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             ResidualRegs<NB> rr;
             residual_load<NB>(ra, rr);
             if (!vwg) {
+                // every group loads NH blocks (past the row's end: its last
+                // block again, not used), so the number of loads behind the
+                // step's own is fixed and the norm waits only for the latter
 #pragma unroll
-                for (int i = 0; i < NH; i++) {
-                    const int b = grp * NH + i;
-                    if (b < nb) load_w(b, raw[i]);
-                }
+                for (int i = 0; i < NH; i++) load_w(min(grp * NH + i, nb - 1), raw[i]);
             }
             extern __shared__ __align__(16) float pbuf[];   // NB*256 floats, the Q8_K blocks, [Q6_K: run sums]
             __shared__ float red[16];
@@ -454,10 +457,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < NH; i++) {
-                const int b = grp * NH + i;
-                if (b < nb) load(b, raw[i]);
-            }
+            for (int i = 0; i < NH; i++) load(min(grp * NH + i, nb - 1), raw[i]);
         }
         int32_t S[NMAT][NH], P[NMAT][NH];
         float D[NMAT][NH], DM[NMAT][NH];
@@ -521,7 +521,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
     }
     if (l == 0 && grp == 0 && row_ < dtot) {
         if (NMAT == 2) outp[rl] = gelu_ref(r[0]) * r[NMAT - 1];
-        else outp[rl] = aux ? gelu_ref(r[0]) * aux[rl] : r[0];
+        else outp[rl] = aux ? gelu_ref(r[0]) * aux_v : r[0];
     }
 }
 
