@@ -286,32 +286,24 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                                                            uint8_t* __restrict__ q8_store,
                                                            const float* __restrict__ aux, const ResidualArgs ra,
                                                            const Stack2 st) {
-    static_assert(!QIN || WG == 64, "the single-block input path runs one wave");
+    static_assert(!QIN || (WG == 64 && NB == 1), "the single-block input path runs one wave over one block");
     static_assert(!PRO || (WG == 256 && NB > 0 && !DBG), "the prologue needs 256 threads and a fixed row length");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
     const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
     const int row_ = blockIdx.x * (WG / GL) + tid / GL;
-    // with the prologue every thread stays for its barriers; rows past the
-    // end compute the last row and do not store.  Rows d.. d+st.d-1 (PRO
-    // only) belong to the stacked second tensor.
+    // with the prologue (or the input quantized in the wave) every thread
+    // stays for its barriers; rows past the end compute the last row and do
+    // not store.  Rows d.. d+st.d-1 (PRO only) belong to the stacked second
+    // tensor.
     const int dtot = d + (PRO ? st.d : 0);
-    const int row = PRO ? min(row_, dtot - 1) : row_;
+    const int row = (PRO || QIN) ? min(row_, dtot - 1) : row_;
     const bool sec = PRO && row >= d;
     const int dl = sec ? st.d : d, rl = sec ? row - d : row;
     const uint8_t* const wa = sec ? st.w : w0;
     float* const outp = sec ? st.out : out;
-    if (QIN) {
-        __shared__ __align__(16) uint8_t q8s[292];
-        const float4 f = reinterpret_cast<const float4*>(xin)[tid];
-        const float v[4] = {f.x, f.y, f.z, f.w};
-        quantize_block_wave(v, tid, q8s, 1, 0);
-        if (blockIdx.x == 0 && q8_store) quantize_block_wave(v, tid, q8_store, 1, 0);
-        __syncthreads();
-        q8 = q8s;
-    }
-    if (!PRO && row >= d) return;   // whole rows (groups of GL lanes) leave together
+    if (!PRO && !QIN && row >= d) return;   // whole rows (groups of GL lanes) leave together
     const uint32_t nblk = (uint32_t)dl * (uint32_t)nb;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk;          // q4k_planes / q5k_planes
     const uint32_t qh_off = 128u * nblk;
@@ -455,6 +447,22 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                     raw[i].yd = a_d_l[b];
                 }
             }
+        } else if constexpr (QIN) {
+            // the inputs, then the weight block, then the wave quantizes the
+            // 256 inputs into LDS (workgroup 0 also stores them) while the
+            // weights are in flight (the load counter retires in order: the
+            // quantize waits only for what was issued before the weights)
+            const float4 f = reinterpret_cast<const float4*>(xin)[tid];
+            load_w(0, raw[0]);
+            __shared__ __align__(16) uint8_t q8s[292];
+            const float v[4] = {f.x, f.y, f.z, f.w};
+            quantize_block_wave(v, tid, q8s, 1, 0);
+            if (blockIdx.x == 0 && q8_store) quantize_block_wave(v, tid, q8_store, 1, 0);
+            __syncthreads();
+            raw[0].a0 = *reinterpret_cast<const uint4*>(q8s + 32 * l);
+            raw[0].a1 = *reinterpret_cast<const uint4*>(q8s + 32 * l + 16);
+            raw[0].bsw = *reinterpret_cast<const uint2*>(q8s + q8k_bsums_off(1) + 8 * k);
+            raw[0].yd = reinterpret_cast<const float*>(q8s + q8k_d_off(1))[0];
         } else {
 #pragma unroll
             for (int i = 0; i < NH; i++) load(min(grp * NH + i, nb - 1), raw[i]);
