@@ -49,13 +49,28 @@ __device__ __forceinline__ float key_value(u64 k) {
 }
 __device__ __forceinline__ int key_index(u64 k) { return (int)(~(uint32_t)(k & 0xffffffffu)); }
 
+// the wave's largest 32-bit value: four DPP steps (max over each row of 16
+// lanes) and the four row maxima read as scalars
+__device__ __forceinline__ uint32_t wave_umax32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
+    v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+
+// the wave's largest key: the largest value half, then (its lane when one
+// lane holds it, else the largest index half among the lanes that do)
 __device__ __forceinline__ u64 wave_max_key(u64 k) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const u64 o = __shfl_xor(k, m, 64);
-        k = o > k ? o : k;
-    }
-    return k;
+    const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+    const uint32_t mh = wave_umax32(hi);
+    const u64 tie = __ballot(hi == mh);
+    uint32_t ml;
+    if (__popcll(tie) == 1) ml = (uint32_t)__builtin_amdgcn_readlane((int)lo, __ffsll((long long)tie) - 1);
+    else ml = wave_umax32(hi == mh ? lo : 0u);
+    return ((u64)mh << 32) | ml;
 }
 
 // keys[0..R) sorted descending (bitonic network, constant indices)
@@ -117,38 +132,57 @@ struct SampleArgs {
     int* dpos;
 };
 
+// Pass 1: workgroup g takes logits [4096 g, 4096 g + 4096).  Every thread
+// loads its 16 logits first (clamped indices: no load waits on a lane
+// condition); meanwhile the workgroup counts, in LDS, how often each logit of
+// the slice occurs in the penalty window of the token history; each logit is
+// then penalised that many times (main.c:2408-2430 applies the penalty once
+// per occurrence, in history order; the operation keeps the sign, so c
+// occurrences are c applications of the same step) and written back if it
+// changed; then the slice's top-k keys go to part[g].
 __global__ __launch_bounds__(kSampleThreads) void sample_partial_kernel(SampleArgs a) {
     __shared__ u64 sk[4][kSampleMaxK];
+    __shared__ int cnt[kSamplePer];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int base = blockIdx.x * kSamplePer;
     const int end = min(base + kSamplePer, a.n);
-    if (a.penalty > 1.0f && tid == 0) {
+    float v[16];
+    if (end - base == kSamplePer) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 t = *reinterpret_cast<const float4*>(a.logits + base + 4 * (tid + kSampleThreads * q));
+            v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = a.logits[min(base + 4 * (tid + kSampleThreads * (j >> 2)) + (j & 3), end - 1)];
+    }
+    const bool pen = a.penalty > 1.0f;
+    if (pen) {
+        for (int i = tid; i < kSamplePer; i += kSampleThreads) cnt[i] = 0;
+        __syncthreads();
         const int nh = min(*a.hist_n, a.hist_cap);
         const int start = a.last_n > 0 && nh > a.last_n ? nh - a.last_n : 0;
-        for (int i = start; i < nh; i++) {
+        for (int i = start + tid; i < nh; i += kSampleThreads) {
             const int id = a.hist[i];
-            if (id >= base && id < end) {
-                const float v = a.logits[id];
-                a.logits[id] = v >= 0.0f ? v / a.penalty : v * a.penalty;
-            }
+            if (id >= base && id < end) atomicAdd(&cnt[id - base], 1);
         }
-        __threadfence_block();   // the penalised logits before the other threads read them
+        __syncthreads();
     }
-    __syncthreads();
     u64 k[16];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int i0 = base + 4 * (tid + kSampleThreads * q);
-        if (i0 + 3 < end) {
-            const float4 v = *reinterpret_cast<const float4*>(a.logits + i0);
-            k[4 * q + 0] = sample_key(v.x, i0);
-            k[4 * q + 1] = sample_key(v.y, i0 + 1);
-            k[4 * q + 2] = sample_key(v.z, i0 + 2);
-            k[4 * q + 3] = sample_key(v.w, i0 + 3);
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++) k[4 * q + c] = i0 + c < end ? sample_key(a.logits[i0 + c], i0 + c) : 0ull;
+    for (int j = 0; j < 16; j++) {
+        const int i = base + 4 * (tid + kSampleThreads * (j >> 2)) + (j & 3);
+        if (pen && i < end) {
+            const int c = cnt[i - base];
+            if (c > 0) {
+                float x = v[j];
+                for (int r = 0; r < c; r++) x = x >= 0.0f ? x / a.penalty : x * a.penalty;
+                v[j] = x;
+                a.logits[i] = x;
+            }
         }
+        k[j] = sample_key(v[j], i) & (i < end ? ~0ull : 0ull);
     }
     wave_top<16>(k, a.topk, sk[wave], lane);
     __syncthreads();
@@ -170,12 +204,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_final_kernel(SampleArgs
     __shared__ float p[kSampleMaxK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // candidate c = wave * 1024 + lane + 64 j  (G * kSampleMaxK <= 4096)
+    // (every lane loads: clamped into the G lists, masked after)
     u64 k[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const int c = wave * 1024 + lane + 64 * j;
         const int wg = c / kSampleMaxK, r = c - wg * kSampleMaxK;
-        k[j] = wg < G && r < a.topk ? a.part[c] : 0ull;
+        k[j] = a.part[min(c, G * kSampleMaxK - 1)] & (wg < G && r < a.topk ? ~0ull : 0ull);
     }
     wave_top<16>(k, a.topk, sk[wave], lane);
     __syncthreads();
