@@ -120,7 +120,8 @@ def test_penalty_and_greedy(lib, orc, penalty, last_n):
     got = s.lg.to_array(np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     st = np.array([1], np.uint64)
-    assert tok == orc.L.or_sample_token(P(want.copy()), N, 0.0, 1.0, 40, P(st))
+    wc = want.copy()                             # held: P() keeps no reference
+    assert tok == orc.L.or_sample_token(P(wc), N, 0.0, 1.0, 40, P(st))
 
 
 def test_greedy_ties_and_sizes(lib, orc):
@@ -153,7 +154,8 @@ def test_draws_match_oracle(lib, orc, temp, topp, topk):
     skipped = 0
     for i in range(60):
         st = np.array([state], np.uint64)
-        want = orc.L.or_sample_token(P(lg.copy()), N, temp, topp, topk, P(st))
+        lc = lg.copy()                           # held: P() keeps no reference
+        want = orc.L.or_sample_token(P(lc), N, temp, topp, topk, P(st))
         margin = _margin(lg, temp, topp, topk, state)
         got = s(temp, topp, topk)
         if got != want:
