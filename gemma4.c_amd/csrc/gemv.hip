@@ -877,6 +877,17 @@ __global__ __launch_bounds__(8 * kQ6SliceMaxNb) void gemv_q6k_kslice_kernel(cons
     const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
     const int r0 = blockIdx.x * R;
     const Q6KPlanes P = q6k_planes((size_t)d * nb);
+    // x of this lane first (runs k = 0..3 of 8 elements at g*256 + 128h +
+    // 32k + 8u), then every weight load of the R rows, all issued before
+    // anything waits: the load counter retires in order, so the run sums
+    // wait only for x and row r only for rows 0..r
+    float4 xa[4], xb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)g * 256 + 128 * h + 32 * k + 8 * u);
+        xa[k] = xp[0];
+        xb[k] = xp[1];
+    }
     uint4 ql[R];
     uint2 qh[R], sc[R];
     uint32_t dv[R];
@@ -888,14 +899,7 @@ __global__ __launch_bounds__(8 * kQ6SliceMaxNb) void gemv_q6k_kslice_kernel(cons
         sc[r] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
         dv[r] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
     }
-    // x of this lane: runs k = 0..3 of 8 elements at g*256 + 128h + 32k + 8u
-    float4 xa[4], xb[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)g * 256 + 128 * h + 32 * k + 8 * u);
-        xa[k] = xp[0];
-        xb[k] = xp[1];
-    }
+    __builtin_amdgcn_sched_barrier(0);
     float s8[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) s8[k] = ((xa[k].x + xa[k].y) + (xa[k].z + xa[k].w)) + ((xb[k].x + xb[k].y) + (xb[k].z + xb[k].w));
