@@ -540,11 +540,11 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
 // runs all NB blocks of it in order, so no lane shuffles are needed between
 // blocks.  With two matrices (gate|up) lanes 0..31 take four gate rows and
 // lanes 32..63 the same four up rows; with one matrix the wave has eight
-// rows.  The wave issues, in this order, its loads of the Q8_K vector and of
-// its rows' 16-byte block headers (both staged in LDS: every lane of a group
-// needs the whole header, and every group the whole vector) and then every
-// weight load of its rows (NB x 16 bytes per lane), so the weight stream is
-// in flight before anything waits.  Per block the lane's integer sums are
+// rows.  The wave issues, in this order, its loads of the Q8_K vector
+// (staged in LDS: every group needs the whole vector) and then, per block,
+// each lane's 16 weight bytes and its row's 16-byte header (the 8 lanes of a
+// group read the same header: one request), so the weight stream is in
+// flight before anything waits.  Per block the lane's integer sums are
 // those of gemv_q45_rows_kernel, formed with fewer instructions: each pair
 // of nibble dots (dl, dh) is packed as two int16 (|dl|, |dh| <= 4*31*127)
 // and multiplied by its two sub-block scales in one v_dot2, and the min
