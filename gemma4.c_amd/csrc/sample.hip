@@ -17,13 +17,22 @@
 // key (order-preserving value bits, then the complemented index) orders the
 // pairs exactly so; selecting the k largest keys reproduces the list.
 //
+// Selection of the k largest of a workgroup's keys (16 per thread) without
+// sequential pops: each thread's largest key (its head) is ranked among the
+// 256 heads; T = the k-th largest head.  The k heads >= T are k keys, so the
+// k largest keys are all >= T: those keys (about k for k << 256) are gathered
+// in LDS and each one's rank among them (the number of larger ones; keys are
+// distinct) is its position in the descending list.  Zero keys fill the
+// positions past the last real key.
+//
 // Pass 1 (G = n / 4096 workgroups): the penalty for the ids of the
-// workgroup's slice (thread 0, in history order, written back to the logits
-// as the reference does), then each lane sorts its 16 keys in registers,
-// each wave pops its k largest (a wave max per pop), and wave 0 merges the
-// four waves' lists into the workgroup's k keys.  Pass 2 (one workgroup):
-// the same selection over the G*k candidates, then one lane runs the
-// reference's sequential softmax / top-p / draw over the k sorted values.
+// workgroup's slice (occurrences in the history window counted in LDS, each
+// logit penalised that many times, written back to the logits as the
+// reference does), then the slice's k largest keys.  Pass 2 (one workgroup):
+// the same selection over the G*k candidates, then wave 0 runs the
+// reference's softmax / top-p / draw over the k sorted values: the
+// exponentials one per lane, the sums and cdf walks in the reference's
+// sequential order over the lanes' values.
 #include "g4_device.h"
 #include "g4_internal.h"
 
@@ -49,71 +58,45 @@ __device__ __forceinline__ float key_value(u64 k) {
 }
 __device__ __forceinline__ int key_index(u64 k) { return (int)(~(uint32_t)(k & 0xffffffffu)); }
 
-// the wave's largest 32-bit value: four DPP steps (max over each row of 16
-// lanes) and the four row maxima read as scalars
-__device__ __forceinline__ uint32_t wave_umax32(uint32_t v) {
-    v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
-    v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
-    v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
-    v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
-}
-
-// the wave's largest key: the largest value half, then (its lane when one
-// lane holds it, else the largest index half among the lanes that do)
-__device__ __forceinline__ u64 wave_max_key(u64 k) {
-    const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
-    const uint32_t mh = wave_umax32(hi);
-    const u64 tie = __ballot(hi == mh);
-    uint32_t ml;
-    if (__popcll(tie) == 1) ml = (uint32_t)__builtin_amdgcn_readlane((int)lo, __ffsll((long long)tie) - 1);
-    else ml = wave_umax32(hi == mh ? lo : 0u);
-    return ((u64)mh << 32) | ml;
-}
-
-// keys[0..R) sorted descending (bitonic network, constant indices)
+// out[0..kk) = the kk largest of the workgroup's keys k[0..R) per thread,
+// descending (kk <= 64 <= 4 * blockDim.x / 16).  hb: blockDim.x keys of LDS,
+// cand: R * blockDim.x keys of LDS, misc: two words of LDS.  out may be LDS
+// or global; every thread reaches every barrier.
 template <int R>
-__device__ __forceinline__ void sort_desc(u64 (&k)[R]) {
+__device__ void wg_topk(const u64 (&k)[R], int kk, u64* out, u64* hb, u64* cand, u64* misc) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    u64 head = k[0];
 #pragma unroll
-    for (int size = 2; size <= R; size <<= 1)
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1)
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const u64 a = k[i], b = k[j];
-                    const bool swap = desc ? a < b : a > b;
-                    k[i] = swap ? b : a;
-                    k[j] = swap ? a : b;
-                }
-            }
-}
-
-// the wave's kk largest of its lanes' keys (each lane's R keys) -> out[0..kk)
-// in descending order (lane 0 writes); keys are distinct or zero
-template <int R>
-__device__ __forceinline__ void wave_top(u64 (&k)[R], int kk, u64* out, int lane) {
-    sort_desc<R>(k);
-    for (int r = 0; r < kk; r++) {
-        const u64 m = wave_max_key(k[0]);
-        const bool pop = k[0] == m;
-#pragma unroll
-        for (int j = 0; j < R - 1; j++) k[j] = pop ? k[j + 1] : k[j];
-        k[R - 1] = pop ? 0ull : k[R - 1];
-        if (lane == 0) out[r] = m;
+    for (int j = 1; j < R; j++) head = k[j] > head ? k[j] : head;
+    hb[tid] = head;
+    if (tid == 0) { misc[0] = ~0ull; misc[1] = 0ull; }
+    if (tid < kk) out[tid] = 0ull;
+    __syncthreads();
+    int r = 0;
+#pragma unroll 16
+    for (int j = 0; j < nt; j += 2) {   // 16 reads in flight per wait
+        const ulonglong2 h2 = *reinterpret_cast<const ulonglong2*>(hb + j);
+        r += (h2.x > head) + (h2.y > head);
     }
-}
-
-// the four waves' lists sk[w][0..kk) -> the workgroup's kk largest (wave 0)
-__device__ __forceinline__ void merge_waves(const u64 (*sk)[kSampleMaxK], int kk, u64* out, int lane) {
-    u64 k[4];
+    // T = the smallest head ranked below kk (heads are distinct keys or 0)
+    if (r < kk) atomicMin(&misc[0], head);
+    __syncthreads();
+    const u64 T = misc[0];
+    unsigned int* cnt = reinterpret_cast<unsigned int*>(&misc[1]);
 #pragma unroll
-    for (int w = 0; w < 4; w++) k[w] = lane < kk ? sk[w][lane] : 0ull;
-    wave_top<4>(k, kk, out, lane);
+    for (int j = 0; j < R; j++)
+        if (k[j] >= T) cand[atomicAdd(cnt, 1u)] = k[j];
+    __syncthreads();
+    const int C = (int)*cnt;
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        if (k[j] >= T && k[j] != 0ull) {
+            int rank = 0;
+#pragma unroll 8
+            for (int i = 0; i < C; i++) rank += cand[i] > k[j];
+            if (rank < kk) out[rank] = k[j];
+        }
+    }
 }
 
 struct SampleArgs {
@@ -141,9 +124,11 @@ struct SampleArgs {
 // occurrences are c applications of the same step) and written back if it
 // changed; then the slice's top-k keys go to part[g].
 __global__ __launch_bounds__(kSampleThreads) void sample_partial_kernel(SampleArgs a) {
-    __shared__ u64 sk[4][kSampleMaxK];
-    __shared__ int cnt[kSamplePer];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) u64 hb[kSampleThreads];
+    __shared__ u64 misc[2];
+    __shared__ u64 cand[kSamplePer];
+    int* cnt = reinterpret_cast<int*>(cand);   // the penalty counts, done before the selection
+    const int tid = threadIdx.x;
     const int base = blockIdx.x * kSamplePer;
     const int end = min(base + kSamplePer, a.n);
     float v[16];
@@ -184,9 +169,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_partial_kernel(SampleAr
         }
         k[j] = sample_key(v[j], i) & (i < end ? ~0ull : 0ull);
     }
-    wave_top<16>(k, a.topk, sk[wave], lane);
-    __syncthreads();
-    if (wave == 0) merge_waves(sk, a.topk, a.part + (size_t)blockIdx.x * kSampleMaxK, lane);
+    wg_topk<16>(k, a.topk, a.part + (size_t)blockIdx.x * kSampleMaxK, hb, cand, misc);
 }
 
 __device__ __forceinline__ float rng_f32(u64* s) {
@@ -198,25 +181,29 @@ __device__ __forceinline__ float rng_f32(u64* s) {
     return (float)((x * 0x2545F4914F6CDD1DULL) >> 40) / (float)(1 << 24);
 }
 
+__device__ __forceinline__ float lane_val(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
 __global__ __launch_bounds__(kSampleThreads) void sample_final_kernel(SampleArgs a, int G) {
-    __shared__ u64 sk[4][kSampleMaxK];
-    __shared__ u64 top[kSampleMaxK];
-    __shared__ float p[kSampleMaxK];
+    __shared__ __align__(16) u64 hb[kSampleThreads];
+    __shared__ u64 misc[2], top[kSampleMaxK];
+    __shared__ u64 cand[16 * kSampleThreads];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // candidate c = wave * 1024 + lane + 64 j  (G * kSampleMaxK <= 4096)
-    // (every lane loads: clamped into the G lists, masked after)
+    // thread t holds entries 16 (t & 3) .. +15 of list t / 4 (G <= 64), so
+    // the heads include every list's maximum: a tight threshold.  (Every
+    // lane loads: clamped into the G lists, masked after.)
+    const int wl = tid >> 2, r0 = 16 * (tid & 3);
     u64 k[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-        const int c = wave * 1024 + lane + 64 * j;
-        const int wg = c / kSampleMaxK, r = c - wg * kSampleMaxK;
-        k[j] = a.part[min(c, G * kSampleMaxK - 1)] & (wg < G && r < a.topk ? ~0ull : 0ull);
+        const int c = wl * kSampleMaxK + r0 + j;
+        k[j] = a.part[min(c, G * kSampleMaxK - 1)] & (wl < G && r0 + j < a.topk ? ~0ull : 0ull);
     }
-    wave_top<16>(k, a.topk, sk[wave], lane);
+    wg_topk<16>(k, a.topk, top, hb, cand, misc);
     __syncthreads();
-    if (wave == 0) merge_waves(sk, a.topk, top, lane);
-    __syncthreads();
-    if (tid != 0) return;
+    if (wave != 0) return;
+    // wave 0, every lane the same path: lane i holds the i-th value's weight
     int result;
     if (a.temp <= 0.0f) {
         result = key_index(top[0]);
@@ -224,38 +211,37 @@ __global__ __launch_bounds__(kSampleThreads) void sample_final_kernel(SampleArgs
         // sample_token (main.c:2090-2112) over the sorted top-k
         const int np = a.topk;
         const float mx = key_value(top[0]);
+        const float e = lane < np ? expf((key_value(top[lane]) - mx) / a.temp) : 0.0f;
         float sum = 0.0f;
-        for (int i = 0; i < np; i++) {
-            p[i] = expf((key_value(top[i]) - mx) / a.temp);
-            sum += p[i];
-        }
-        for (int i = 0; i < np; i++) p[i] /= sum;
+        for (int i = 0; i < np; i++) sum += lane_val(e, i);
+        const float pl = e / sum;
         u64 st = *a.rng;
         const float coin = rng_f32(&st);
         if (a.topp <= 0.0f || a.topp >= 1.0f) {
             float cdf = 0.0f;
             result = key_index(top[np - 1]);
             for (int i = 0; i < np; i++) {
-                cdf += p[i];
+                cdf += lane_val(pl, i);
                 if (coin < cdf) { result = key_index(top[i]); break; }
             }
         } else {
             float cum = 0.0f;
             int last = np - 1;
             for (int i = 0; i < np; i++) {
-                cum += p[i];
+                cum += lane_val(pl, i);
                 if (cum > a.topp) { last = i; break; }
             }
             const float r = rng_f32(&st) * cum;
             float cdf = 0.0f;
             result = key_index(top[last]);
             for (int i = 0; i <= last; i++) {
-                cdf += p[i];
+                cdf += lane_val(pl, i);
                 if (r < cdf) { result = key_index(top[i]); break; }
             }
         }
-        *a.rng = st;
+        if (lane == 0) *a.rng = st;
     }
+    if (lane != 0) return;
     if (a.out) *a.out = result;
     if (a.dtok) *a.dtok = result;
     if (a.dpos) *a.dpos = *a.dpos + 1;
