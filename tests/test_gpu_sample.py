@@ -256,3 +256,29 @@ def test_generate_sampled(model_path, orc, temp, topp, topk, penalty, last_n, se
             assert np.array_equal(g1, em.generate_greedy(prompt, n_new, use_graph=False)[0])
     finally:
         em.close()
+
+
+def test_flat_logits_draws(lib, orc):
+    """Nearly flat logits (three larger values, the rest equal): the top-k
+    list holds the three and then the lowest indices in order, many keys
+    differing only in their index; draws and the rng state equal the
+    oracle's."""
+    lg = np.zeros(N, np.float32)
+    lg[[100, 5000, 200000]] = 1.0
+    s = Sampler(lib, lg)
+    state = 777
+    s.seed(state)
+    skipped = 0
+    for i in range(20):
+        st = np.array([state], np.uint64)
+        lc = lg.copy()                           # held: P() keeps no reference
+        want = orc.L.or_sample_token(P(lc), N, 1.0, 1.0, 40, P(st))
+        margin = _margin(lg, 1.0, 1.0, 40, state)
+        got = s(1.0, 1.0, 40)
+        if got != want:
+            assert margin < 1e-5, (i, got, want, margin)
+            skipped += 1
+        assert got in (100, 5000, 200000) or got < 40, got
+        state = int(st[0])
+        assert s.state() == state, i
+    assert skipped <= 1
