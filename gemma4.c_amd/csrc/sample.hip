@@ -87,15 +87,16 @@ __device__ void wg_topk(const u64 (&k)[R], int kk, u64* out, u64* hb, u64* cand,
     for (int j = 0; j < R; j++)
         if (k[j] >= T) cand[atomicAdd(cnt, 1u)] = k[j];
     __syncthreads();
+    // thread t ranks candidate t (one pass for the workgroup; zero keys are
+    // the pre-filled tail)
     const int C = (int)*cnt;
-#pragma unroll
-    for (int j = 0; j < R; j++) {
-        if (k[j] >= T && k[j] != 0ull) {
-            int rank = 0;
+    for (int t = tid; t < C; t += nt) {
+        const u64 v = cand[t];
+        if (v == 0ull) continue;
+        int rank = 0;
 #pragma unroll 8
-            for (int i = 0; i < C; i++) rank += cand[i] > k[j];
-            if (rank < kk) out[rank] = k[j];
-        }
+        for (int i = 0; i < C; i++) rank += cand[i] > v;
+        if (rank < kk) out[rank] = v;
     }
 }
 
