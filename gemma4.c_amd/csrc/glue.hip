@@ -157,10 +157,18 @@ constexpr int kArgmaxPer = 4096;   // elements per partial workgroup
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const float* __restrict__ v, int n,
                                                                         unsigned long long* __restrict__ part) {
     __shared__ unsigned long long red[4];
-    const int base = blockIdx.x * kArgmaxPer;
+    constexpr int E = kArgmaxPer / kArgmaxThreads;
+    const int base = blockIdx.x * kArgmaxPer, end = min(n, base + kArgmaxPer);
+    // every load issued before any waits (clamped indices; the keys past
+    // the end are masked to 0, the reduction's start value)
+    float x[E];
+#pragma unroll
+    for (int j = 0; j < E; j++) x[j] = v[min(base + (int)threadIdx.x + kArgmaxThreads * j, end - 1)];
     unsigned long long k = 0;
-    for (int i = base + threadIdx.x; i < min(n, base + kArgmaxPer); i += kArgmaxThreads) {
-        const unsigned long long t = argmax_key(v[i], i);
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+        const int i = base + (int)threadIdx.x + kArgmaxThreads * j;
+        const unsigned long long t = argmax_key(x[j], i) & (i < end ? ~0ull : 0ull);
         k = t > k ? t : k;
     }
     k = block_max_u64(k, red);
