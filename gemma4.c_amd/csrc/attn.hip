@@ -60,9 +60,9 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ ta
                                                          float ts, float fs, const float* __restrict__ ff) {
     const int p = dpos ? *dpos : pos;
     for (int j = threadIdx.x; j < npair; j += blockDim.x) {
+        const float f = ff ? ff[j] : 1.0f;   // in flight during the product chain
         float theta = (float)p;
         for (int i = 0; i < j; i++) theta *= ts;
-        const float f = ff ? ff[j] : 1.0f;
         const float angle = (fs * theta) / f;
         tab[j] = make_float2(cosf(angle), sinf(angle));
     }
@@ -74,9 +74,9 @@ __global__ __launch_bounds__(256) void rope_table_rows_kernel(float2* __restrict
     const int p = pos0 + blockIdx.x;
     float2* t = tab + (size_t)blockIdx.x * npair;
     for (int j = threadIdx.x; j < npair; j += blockDim.x) {
+        const float f = ff ? ff[j] : 1.0f;   // in flight during the product chain
         float theta = (float)p;
         for (int i = 0; i < j; i++) theta *= ts;
-        const float f = ff ? ff[j] : 1.0f;
         const float angle = (fs * theta) / f;
         t[j] = make_float2(cosf(angle), sinf(angle));
     }
