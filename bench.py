@@ -377,13 +377,7 @@ def bench_copy(lib, g4, synth, args):
 
 def _gguf_e4b(synth, seed: int = 4) -> str:
     """The synthetic E4B-shape GGUF (about 5.4 GB), written once per machine."""
-    d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
-    path = os.path.join(d, f"g4_e4b_seed{seed}.gguf")
-    if not os.path.exists(path):
-        tmp = path + f".{os.getpid()}.part"
-        synth.write_model_gguf(tmp, synth.E4B, seed)
-        os.replace(tmp, path)
-    return path
+    return synth.e4b_gguf(seed)
 
 
 def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):

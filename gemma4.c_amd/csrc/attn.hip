@@ -20,6 +20,8 @@
 // once for the GQA group), keeps (max, sum, o) of its chunk, and a merge
 // kernel combines the chunks by log-sum-exp.  Equal to the reference's
 // softmax-then-PV up to fp32 rounding.
+#include <mutex>
+
 #include "g4_device.h"
 #include "g4_internal.h"
 
@@ -1022,14 +1024,21 @@ int check_attn_shape(const char* who, int n_heads, int n_kv, int hd, int G, bool
     return G4_OK;
 }
 
-// library-owned workspace for the host-position entry points
+// library-owned workspace for the host-position entry points.  It only
+// grows; growing waits for the whole device, since launches on any stream
+// may still read the old buffer.  Calls that overlap in time share it, so
+// concurrent callers on different streams race (one host thread and stream
+// per process is the supported use); the mutex keeps the pointer and size
+// themselves consistent.
 void* g_ws = nullptr;
 size_t g_ws_bytes = 0;
+std::mutex g_ws_mu;
 
 int workspace(size_t bytes, uint8_t** p) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
     if (bytes > g_ws_bytes) {
         if (g_ws) {
-            G4_HIP(hipStreamSynchronize(g4_stream()));
+            G4_HIP(hipDeviceSynchronize());
             G4_HIP(hipFree(g_ws));
             g_ws = nullptr;
             g_ws_bytes = 0;

@@ -125,8 +125,12 @@ __global__ __launch_bounds__(256) void gelu_mul_quant_kernel(float* __restrict__
 // ---- argmax, first index of the maximum ------------------------------------
 // key = order-preserving bits of the value (high word) and ~index (low word):
 // the largest key is the largest value at its smallest index.  -0.0 is taken
-// as +0.0 so that equal values compare equal, as the C comparison does.
+// as +0.0 so that equal values compare equal, as the C comparison does.  The
+// reference's scan (main.c:2046-2048) never moves to a NaN and never leaves
+// one at index 0 (every comparison with it is false): a NaN gets the lowest
+// key, or the highest at index 0.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    if (v != v) return i == 0 ? ~0ull : 0ull;
     uint32_t u = __float_as_uint(v + 0.0f);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)i);

@@ -20,12 +20,14 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     quantize_block_wave(v, lane, y, nb, b);
 }
 
-// device Q8_K layout -> reference BlockQ8_K[nb] (292 B each), for tests
-__global__ void q8k_to_ref_kernel(const uint8_t* __restrict__ y, uint8_t* __restrict__ out, int nb) {
+// device Q8_K layout -> reference BlockQ8_K[nb] (292 B each), for tests;
+// row blockIdx.y of a batch starts ystride bytes after the previous one
+__global__ void q8k_to_ref_kernel(const uint8_t* __restrict__ y, uint8_t* __restrict__ out, int nb, size_t ystride) {
     const int b = blockIdx.x;
     const int t = threadIdx.x;   // 64 threads: word t of GGUF order
     if (b >= nb) return;
-    uint8_t* o = out + (size_t)b * 292;
+    y += blockIdx.y * ystride;
+    uint8_t* o = out + ((size_t)blockIdx.y * nb + b) * 292;
     const uint32_t w = reinterpret_cast<const uint32_t*>(y + (size_t)b * 256)[q8k_word_dev(t)];
     for (int e = 0; e < 4; e++) o[4 + 4 * t + e] = (uint8_t)(w >> (8 * e));
     if (t < 16) {
@@ -76,9 +78,27 @@ extern "C" int g4_download_q8K(const void* y, void* host_blocks, int k) {
     const int nb = k / 256;
     void* tmp = nullptr;
     G4_HIP(hipMalloc(&tmp, (size_t)nb * 292));
-    hipLaunchKernelGGL(q8k_to_ref_kernel, dim3(nb), dim3(64), 0, g4_stream(), (const uint8_t*)y, (uint8_t*)tmp, nb);
+    hipLaunchKernelGGL(q8k_to_ref_kernel, dim3(nb), dim3(64), 0, g4_stream(), (const uint8_t*)y, (uint8_t*)tmp, nb,
+                       (size_t)0);
     int rc = g4_check_launch("q8k_to_ref_kernel");
     if (rc == 0) rc = g4_hip_status(hipMemcpyAsync(host_blocks, tmp, (size_t)nb * 292, hipMemcpyDeviceToHost, g4_stream()));
+    if (rc == 0) rc = g4_hip_status(hipStreamSynchronize(g4_stream()));
+    (void)hipFree(tmp);
+    return rc;
+}
+
+extern "C" int g4_download_q8K_rows(const void* y, void* host_blocks, int k, int m) {
+    G4_CHECK_ARG(y && host_blocks, "g4_download_q8K_rows: null pointer");
+    G4_CHECK_ARG(k > 0 && k % 256 == 0, "g4_download_q8K_rows: k=%d is not a positive multiple of 256", k);
+    G4_CHECK_ARG(m > 0 && m <= 65535, "g4_download_q8K_rows: m=%d rows (1..65535)", m);
+    const int nb = k / 256;
+    const size_t bytes = (size_t)m * nb * 292;
+    void* tmp = nullptr;
+    G4_HIP(hipMalloc(&tmp, bytes));
+    hipLaunchKernelGGL(q8k_to_ref_kernel, dim3(nb, m), dim3(64), 0, g4_stream(), (const uint8_t*)y, (uint8_t*)tmp, nb,
+                       g4_q8K_row_stride(k));
+    int rc = g4_check_launch("q8k_to_ref_kernel");
+    if (rc == 0) rc = g4_hip_status(hipMemcpyAsync(host_blocks, tmp, bytes, hipMemcpyDeviceToHost, g4_stream()));
     if (rc == 0) rc = g4_hip_status(hipStreamSynchronize(g4_stream()));
     (void)hipFree(tmp);
     return rc;

@@ -46,7 +46,12 @@ constexpr int kSampleMaxParts = 64;         // pass 2 holds kSampleMaxParts * kS
 
 typedef unsigned long long u64;
 
+// A NaN logit gets key 0, below every number: the reference's insertion
+// (main.c:2055-2073) compares with '<' and '>', which a NaN never passes once
+// the list holds topk entries.  (A NaN among the first topk logits would
+// enter the reference's list unordered; the keys treat it as masked.)
 __device__ __forceinline__ u64 sample_key(float v, int i) {
+    if (v != v) return 0;
     uint32_t u = __float_as_uint(v + 0.0f);   // -0.0 == +0.0, as the C comparison
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((u64)u << 32) | (uint32_t)(~(uint32_t)i);

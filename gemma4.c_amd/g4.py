@@ -19,6 +19,9 @@ HEADER = os.path.join(ROOT, "include", "g4hip.h")
 ENGINE_HEADER = os.path.join(PKG, "host", "engine.h")
 
 G4_OK, G4_ERR_ARG, G4_ERR_TYPE, G4_ERR_HIP, G4_ERR_NOMEM, G4_ERR_STATE, G4_ERR_NODEV, G4_ERR_FORMAT = range(8)
+# engine trace: quantization points per layer (engine.h G4E_Q8_SLOT_*) and
+# elements per traced Q8_K vector
+Q8_SLOTS, Q8_SLOT_ELEMS = 5, 4096
 F32, F16, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 12, 13, 14, 30
 
 VP, I, SZ, F = C.c_void_p, C.c_int, C.c_size_t, C.c_float
@@ -127,12 +130,14 @@ _ENGINE_SIGS = {
     "g4e_argmax": (I, [VP, C.POINTER(I)]),
     "g4e_set_trace": (I, [VP, I]),
     "g4e_layer_x": (C.POINTER(F), [VP]),
+    "g4e_layer_q8": (VP, [VP]),
     "g4e_generate_greedy": (I, [VP, VP, I, I, VP, C.POINTER(C.c_double), C.POINTER(C.c_double), I]),
     "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
     "g4e_generate": (I, [VP, VP, I, I, F, F, I, F, I, C.c_uint64, VP, C.POINTER(C.c_double),
                          C.POINTER(C.c_double), I]),
     "g4e_decode_steps_sampled": (I, [VP, I, I, I, F, F, I, F, I, C.c_uint64, I, VP, C.POINTER(C.c_double)]),
     "g4e_prefill": (I, [VP, VP, I, I]),
+    "g4e_prefill_trace_q8": (I, [VP, VP, I, I, VP, VP]),
     "g4e_prefill_trace": (I, [VP, VP, I, I, VP]),
     "g4e_set_prefill_chunk": (I, [VP, I]),
     "g4e_set_f32_matmul": (I, [VP, I]),
@@ -338,6 +343,16 @@ class Engine:
         p = self.E.L.g4e_layer_x(self.h)
         return np.ctypeslib.as_array(p, (self.n_layers + 1, self.dim)).copy()
 
+    def layer_q8(self) -> np.ndarray:
+        """Q8_K activations of the last traced step as raw BlockQ8_K bytes,
+        (n_layers, Q8_SLOTS, Q8_SLOT_ELEMS // 256, 292): per layer the
+        attention input, O input, FFN input, PLE inp_gate and proj inputs."""
+        p = self.E.L.g4e_layer_q8(self.h)
+        nb = Q8_SLOT_ELEMS // 256
+        n = self.n_layers * Q8_SLOTS * nb * 292
+        raw = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), (n,)).copy()
+        return raw.reshape(self.n_layers, Q8_SLOTS, nb, 292)
+
     def generate_greedy(self, prompt, max_new: int, use_graph: bool = True):
         pr = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(max_new + 1, np.int32)
@@ -385,13 +400,20 @@ class Engine:
         t = np.ascontiguousarray(tokens, np.int32)
         self.E.check(self.E.L.g4e_prefill(self.h, t.ctypes.data, t.size, pos0))
 
-    def prefill_trace(self, tokens, pos0: int = 0) -> np.ndarray:
+    def prefill_trace(self, tokens, pos0: int = 0, q8: bool = False):
         """prefill() that returns each layer's input rows, (n_layers + 1, n, dim):
-        [l, t] is layer l's input for token t, [n_layers, t] the last output."""
+        [l, t] is layer l's input for token t, [n_layers, t] the last output.
+        With q8, also the Q8_K rows of every quantization point as raw
+        BlockQ8_K bytes, (n_layers, n, Q8_SLOTS, Q8_SLOT_ELEMS // 256, 292)."""
         t = np.ascontiguousarray(tokens, np.int32)
         tr = np.zeros((self.n_layers + 1, t.size, self.dim), np.float32)
-        self.E.check(self.E.L.g4e_prefill_trace(self.h, t.ctypes.data, t.size, pos0, tr.ctypes.data))
-        return tr
+        if not q8:
+            self.E.check(self.E.L.g4e_prefill_trace(self.h, t.ctypes.data, t.size, pos0, tr.ctypes.data))
+            return tr
+        qt = np.empty((self.n_layers, t.size, Q8_SLOTS, Q8_SLOT_ELEMS // 256, 292), np.uint8)
+        self.E.check(self.E.L.g4e_prefill_trace_q8(self.h, t.ctypes.data, t.size, pos0, tr.ctypes.data,
+                                                   qt.ctypes.data))
+        return tr, qt
 
     def kv_info(self, layer: int):
         """(floats per slot, slots) of a storing layer's KV cache."""

@@ -47,12 +47,21 @@ int g4e_read_x(g4e_model *m, float *host);            /* dim floats   */
 /* first index of the maximum logit (sample_token with temp <= 0, main.c:2045-2049) */
 int g4e_argmax(g4e_model *m, int *tok);
 
-/* Per-layer capture: when on, forward() copies x into a host buffer of
- * (n_layers + 1) * dim floats (g4e_layer_x): row 0 after the embedding (the
- * input of layer 0), row l+1 after layer l.  Synchronous and slow; for parity
- * checks and fingerprints (dump_kv_fingerprint, main.c:1829-1836). */
+/* Per-layer capture, for parity checks.  When on, every step (eager or in
+ * the captured decode graph) copies x into a device trace of (n_layers + 1)
+ * * dim floats: row 0 after the embedding (the input of layer 0), row l+1
+ * after layer l; and the Q8_K activation of each quantization point of each
+ * layer whose matrix takes Q8_K inputs (G4E_Q8_SLOT_*: attention input, O
+ * input, FFN input, PLE inp_gate input, PLE proj input).  g4e_forward and
+ * g4e_decode_steps copy the trace of their last step to host buffers:
+ * g4e_layer_x, and g4e_layer_q8 as BlockQ8_K structs (main.c:117-122),
+ * G4E_Q8_SLOT_ELEMS / 256 blocks per slot at block offset
+ * (l * G4E_Q8_SLOTS + slot) * (G4E_Q8_SLOT_ELEMS / 256). */
+enum { G4E_Q8_SLOT_ATTN = 0, G4E_Q8_SLOT_O, G4E_Q8_SLOT_FFN, G4E_Q8_SLOT_INP_GATE, G4E_Q8_SLOT_PROJ, G4E_Q8_SLOTS };
+#define G4E_Q8_SLOT_ELEMS 4096
 int g4e_set_trace(g4e_model *m, int on);
 const float *g4e_layer_x(const g4e_model *m);
+const void *g4e_layer_q8(const g4e_model *m);
 
 /* generate() with temp <= 0 (main.c:2335-2488): the prompt is fed token by
  * token (lm_mode 0 except the last prompt token), then up to max_new greedy
@@ -97,6 +106,10 @@ int g4e_prefill(g4e_model *m, const int *tokens, int n, int pos0);
  * holds (n_layers + 1) x n x dim floats; row (l, t) is the input of layer l
  * for token t, row (n_layers, t) the last layer's output */
 int g4e_prefill_trace(g4e_model *m, const int *tokens, int n, int pos0, float *trace);
+/* ... and the Q8_K rows of every quantization point (G4E_Q8_SLOT_*) as
+ * BlockQ8_K structs: q8trace[l][t][slot][G4E_Q8_SLOT_ELEMS / 256], zero where
+ * the layer's matrix takes no Q8_K input */
+int g4e_prefill_trace_q8(g4e_model *m, const int *tokens, int n, int pos0, float *trace, void *q8trace);
 /* longest prompt chunk of g4e_prefill, and its default */
 #define G4E_PREFILL_CHUNK 512
 /* tokens per prompt chunk (1..G4E_PREFILL_CHUNK; at most what the chunk

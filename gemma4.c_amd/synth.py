@@ -300,3 +300,15 @@ def decode_weight_bytes(s: ModelShape) -> int:
             continue
         total += tensor_nbytes(t.qtype, t.ne)
     return total
+
+
+def e4b_gguf(seed: int = 4) -> str:
+    """Path of the synthetic E4B-shape GGUF of `seed` (about 5.4 GB), written
+    once per machine into /dev/shm (or /tmp)."""
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
+    path = os.path.join(d, f"g4_e4b_seed{seed}.gguf")
+    if not os.path.exists(path):
+        tmp = path + f".{os.getpid()}.part"
+        write_model_gguf(tmp, E4B, seed)
+        os.replace(tmp, path)
+    return path

@@ -84,6 +84,9 @@ size_t g4_q8K_bytes(int k);
 int    g4_quantize_row_q8_K(const float *x, void *y, int k);
 int    g4_download_q8K(const void *y, void *host_blocks, int k);   /* -> BlockQ8_K[k/256] */
 int    g4_upload_q8K(void *y, const void *host_blocks, int k);     /* BlockQ8_K[k/256] -> device */
+/* m Q8_K rows of k elements, g4_q8K_row_stride(k) bytes apart (the batched
+ * forms' layout) -> BlockQ8_K[m][k/256]; for tests and traces */
+int    g4_download_q8K_rows(const void *y, void *host_blocks, int k, int m);
 
 /* ---------------------------------------------------------------------------
  * K-quant GEMV.  o[d] = W[d x n] . x, W row-major with ne[0] = n

@@ -791,6 +791,12 @@ struct or_model {
     float *stats; /* n_layers*3 + 8 */
     float *astats; /* n_layers*3: hidden_stats of x after each layer's attention residual (main.c:1964-1969) */
     float *layer_x; /* n_layers*dim: x after each layer of the last forward */
+    /* Q8_K activations of the five quantization points of every layer
+     * (OR_Q8_SLOT_*): q8_rec records the oracle's own quantize_row_q8_K
+     * results of the last forward; q8_inj (borrowed, NULL unless
+     * or_forward_inject_q8 runs) replaces them before use */
+    or_q8K *q8_rec;
+    const or_q8K *q8_inj;
 };
 
 typedef struct { const uint8_t *d; uint64_t p, size; int bad; } or_rd;
@@ -1025,6 +1031,7 @@ or_model *or_model_open(const uint8_t *data, size_t size, int max_seq, char *err
     m->stats = (float *)calloc((size_t)L * 3 + 8, 4);
     m->astats = (float *)calloc((size_t)L * 3, 4);
     m->layer_x = (float *)calloc((size_t)L * m->dim, 4);
+    m->q8_rec = (or_q8K *)calloc((size_t)L * OR_Q8_SLOTS * OR_Q8_SLOT_BLOCKS, sizeof(or_q8K));
     if (!m->kc || !m->vc) { or_model_close(m); set_err(err, errlen, "out of memory"); return NULL; }
     return m;
 }
@@ -1039,6 +1046,7 @@ void or_model_close(or_model *m) {
     free(m->x); free(m->xb); free(m->xb2); free(m->hb); free(m->hb2); free(m->q); free(m->k);
     free(m->v); free(m->q_out); free(m->ple); free(m->ple_ctx); free(m->ple_gate); free(m->att);
     free(m->logits); free(m->kc); free(m->vc); free(m->q8); free(m->stats); free(m->astats); free(m->layer_x);
+    free(m->q8_rec);
     free(m);
 }
 
@@ -1052,6 +1060,30 @@ const float *or_model_x(const or_model *m) { return m->x; }
 const float *or_model_layer_stats(const or_model *m) { return m->stats; }
 const float *or_model_attn_stats(const or_model *m) { return m->astats; }
 const float *or_model_layer_x(const or_model *m) { return m->layer_x; }
+const or_q8K *or_model_q8_rec(const or_model *m) { return m->q8_rec; }
+int or_model_kv_source(const or_model *m, int layer) { return kv_source(m, layer); }
+
+float *or_model_kv(or_model *m, int layer, int which) {
+    if (layer < 0 || layer >= OR_N_LAYER_KV || layer >= m->n_layers) return NULL;
+    return (which ? m->vc : m->kc) + (size_t)layer * m->max_seq * OR_MAX_KV_DIM;
+}
+
+/* The Q8_K activation of quantization point `slot` of layer l, for a matrix
+ * of `type` with inputs x[n]: quantize_row_q8_K (main.c:282, called by
+ * forward at 1884 and 1975, inside mm at 1685 otherwise) into m->q8,
+ * recorded in q8_rec, then replaced by the injected blocks if any.  Returns
+ * mm's q8_ready flag: 1 when m->q8 holds the activation, 0 when mm does not
+ * take this matrix through Q8_K (other types, --f32-matmul). */
+static int q8_point(or_model *m, int l, int slot, const float *x, int n, int type) {
+    if (!((type == OR_Q4_K || type == OR_Q5_K) && !or_f32_matmul)) return 0;
+    const int nb = n / OR_QK_K;
+    if (n % OR_QK_K || nb > OR_Q8_SLOT_BLOCKS) return 0;
+    or_quantize_q8K(x, m->q8, n);
+    const size_t off = ((size_t)l * OR_Q8_SLOTS + slot) * OR_Q8_SLOT_BLOCKS;
+    memcpy(m->q8_rec + off, m->q8, (size_t)nb * sizeof(or_q8K));
+    if (m->q8_inj) memcpy(m->q8, m->q8_inj + off, (size_t)nb * sizeof(or_q8K));
+    return 1;
+}
 
 /* main.c:1747-1778 */
 static void build_ple(or_model *m, int token) {
@@ -1070,40 +1102,50 @@ static void build_ple(or_model *m, int token) {
     free(row);
 }
 
+/* K and V of a storing layer from m->xb2 (and m->q8 when q8_ready):
+ * projections, k_norm, the unweighted V norm, RoPE of K and the store at
+ * pos (main.c:1888-1904). */
+static int layer_kv(or_model *m, int l, int pos, int q8_ready) {
+    const int dim = m->dim, nkv = m->n_kv, hd = layer_hd(m, l), kv_dim = nkv * hd;
+    const int swa = is_swa(m, l);
+    const int n_rot = swa ? m->rot_swa : m->rot_full;
+    const float base = swa ? m->theta_swa : m->theta;
+    const float *ff = swa ? NULL : m->rope_freqs;
+    if (or_mm(m->k, m->xb2, m->wk[l].p, dim, kv_dim, m->wk[l].type, m->q8, q8_ready)) return -1;
+    if (or_mm(m->v, m->xb2, m->wv[l].p, dim, kv_dim, m->wv[l].type, m->q8, q8_ready)) return -1;
+    or_rmsnorm_head_inplace(m->k, m->k_norm[l], nkv, hd, m->eps);
+    or_rmsnorm_head_noweight_inplace(m->v, nkv, hd, m->eps);
+    or_apply_rope_neox(m->k, nkv, hd, n_rot, pos, base, 1.0f, ff);
+    const size_t off = ((size_t)l * m->max_seq + pos) * OR_MAX_KV_DIM;
+    memcpy(m->kc + off, m->k, (size_t)kv_dim * sizeof(float));
+    memcpy(m->vc + off, m->v, (size_t)kv_dim * sizeof(float));
+    if (l == 0) {
+        float s, q2, a;
+        or_hidden_stats(m->k, kv_dim, &s, &q2, &a);
+        m->stats[(size_t)m->n_layers * 3 + 0] = s;
+        m->stats[(size_t)m->n_layers * 3 + 1] = q2;
+        m->stats[(size_t)m->n_layers * 3 + 2] = a;
+    }
+    return 0;
+}
+
 /* One decoder layer of forward() (main.c:1865-2011) on m->x; x_before is
  * dim floats of scratch. */
 static int layer_step(or_model *m, int l, int pos, float *x_before) {
     const int dim = m->dim, hidden = m->hidden, nh = m->n_heads, nkv = m->n_kv;
-    const int hd = layer_hd(m, l), q_dim = nh * hd, kv_dim = nkv * hd;
+    const int hd = layer_hd(m, l), q_dim = nh * hd;
     const int swa = is_swa(m, l);
     const int n_rot = swa ? m->rot_swa : m->rot_full;
     const float base = swa ? m->theta_swa : m->theta;
     const float *ff = swa ? NULL : m->rope_freqs;
     memcpy(x_before, m->x, (size_t)dim * sizeof(float));
     or_rmsnorm(m->xb2, m->x, m->attn_norm[l], dim, m->eps);
-    const int q8_att = (m->wq[l].type == OR_Q4_K || m->wq[l].type == OR_Q5_K);
-    if (q8_att) or_quantize_q8K(m->xb2, m->q8, dim);
+    const int q8_att = q8_point(m, l, OR_Q8_SLOT_ATTN, m->xb2, dim, m->wq[l].type);
     if (or_mm(m->q, m->xb2, m->wq[l].p, dim, q_dim, m->wq[l].type, m->q8, q8_att)) return -1;
     or_rmsnorm_head_inplace(m->q, m->q_norm[l], nh, hd, m->eps);
     or_apply_rope_neox(m->q, nh, hd, n_rot, pos, base, 1.0f, ff);
     const int src = kv_source(m, l);
-    if (l < OR_N_LAYER_KV) {
-        if (or_mm(m->k, m->xb2, m->wk[l].p, dim, kv_dim, m->wk[l].type, m->q8, q8_att)) return -1;
-        if (or_mm(m->v, m->xb2, m->wv[l].p, dim, kv_dim, m->wv[l].type, m->q8, q8_att)) return -1;
-        or_rmsnorm_head_inplace(m->k, m->k_norm[l], nkv, hd, m->eps);
-        or_rmsnorm_head_noweight_inplace(m->v, nkv, hd, m->eps);
-        or_apply_rope_neox(m->k, nkv, hd, n_rot, pos, base, 1.0f, ff);
-        const size_t off = ((size_t)l * m->max_seq + pos) * OR_MAX_KV_DIM;
-        memcpy(m->kc + off, m->k, (size_t)kv_dim * sizeof(float));
-        memcpy(m->vc + off, m->v, (size_t)kv_dim * sizeof(float));
-        if (l == 0) {
-            float s, q2, a;
-            or_hidden_stats(m->k, kv_dim, &s, &q2, &a);
-            m->stats[(size_t)m->n_layers * 3 + 0] = s;
-            m->stats[(size_t)m->n_layers * 3 + 1] = q2;
-            m->stats[(size_t)m->n_layers * 3 + 2] = a;
-        }
-    }
+    if (l < OR_N_LAYER_KV && layer_kv(m, l, pos, q8_att)) return -1;
     const int src_hd = layer_hd(m, src);
     int t_start = 0;
     if (swa) { t_start = pos + 1 - m->window; if (t_start < 0) t_start = 0; }
@@ -1119,14 +1161,14 @@ static int layer_step(or_model *m, int l, int pos, float *x_before) {
         m->stats[(size_t)m->n_layers * 3 + 4] = q2;
         m->stats[(size_t)m->n_layers * 3 + 5] = a;
     }
-    if (or_mm(m->xb2, m->q_out, m->wo[l].p, q_dim, dim, m->wo[l].type, m->q8, 0)) return -1;
+    const int q8_o = q8_point(m, l, OR_Q8_SLOT_O, m->q_out, q_dim, m->wo[l].type);
+    if (or_mm(m->xb2, m->q_out, m->wo[l].p, q_dim, dim, m->wo[l].type, m->q8, q8_o)) return -1;
     or_rmsnorm(m->xb2, m->xb2, m->post_attn_norm[l], dim, m->eps);
     for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
     or_hidden_stats(m->x, dim, &m->astats[3 * l], &m->astats[3 * l + 1], &m->astats[3 * l + 2]);
     memcpy(x_before, m->x, (size_t)dim * sizeof(float));
     or_rmsnorm(m->xb2, m->x, m->ffn_norm[l], dim, m->eps);
-    const int q8_ffn = (m->gate[l].type == OR_Q4_K || m->gate[l].type == OR_Q5_K);
-    if (q8_ffn) or_quantize_q8K(m->xb2, m->q8, dim);
+    const int q8_ffn = q8_point(m, l, OR_Q8_SLOT_FFN, m->xb2, dim, m->gate[l].type);
     if (or_mm(m->hb, m->xb2, m->gate[l].p, dim, hidden, m->gate[l].type, m->q8, q8_ffn)) return -1;
     if (or_mm(m->hb2, m->xb2, m->up[l].p, dim, hidden, m->up[l].type, m->q8, q8_ffn)) return -1;
     for (int i = 0; i < hidden; i++) m->hb[i] = or_gelu(m->hb[i]) * m->hb2[i];
@@ -1134,11 +1176,13 @@ static int layer_step(or_model *m, int l, int pos, float *x_before) {
     or_rmsnorm(m->xb2, m->xb2, m->post_ffw_norm[l], dim, m->eps);
     for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
     memcpy(x_before, m->x, (size_t)dim * sizeof(float));
-    if (or_mm(m->ple_gate, m->x, m->inp_gate[l].p, dim, m->ple_dim, m->inp_gate[l].type, m->q8, 0)) return -1;
+    const int q8_ig = q8_point(m, l, OR_Q8_SLOT_INP_GATE, m->x, dim, m->inp_gate[l].type);
+    if (or_mm(m->ple_gate, m->x, m->inp_gate[l].p, dim, m->ple_dim, m->inp_gate[l].type, m->q8, q8_ig)) return -1;
     for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = or_gelu(m->ple_gate[i]);
     const float *ple_l = m->ple + (size_t)l * m->ple_dim;
     for (int i = 0; i < m->ple_dim; i++) m->ple_gate[i] = m->ple_gate[i] * ple_l[i];
-    if (or_mm(m->xb2, m->ple_gate, m->proj[l].p, m->ple_dim, dim, m->proj[l].type, m->q8, 0)) return -1;
+    const int q8_pr = q8_point(m, l, OR_Q8_SLOT_PROJ, m->ple_gate, m->ple_dim, m->proj[l].type);
+    if (or_mm(m->xb2, m->ple_gate, m->proj[l].p, m->ple_dim, dim, m->proj[l].type, m->q8, q8_pr)) return -1;
     or_rmsnorm(m->xb2, m->xb2, m->post_norm[l], dim, m->eps);
     for (int i = 0; i < dim; i++) m->x[i] = x_before[i] + m->xb2[i];
     if (m->out_scale[l]) {
@@ -1206,6 +1250,30 @@ int or_forward_inject(or_model *m, int token, int pos, int lm_mode, const float 
     if (lm_mode == 0) return 0;
     memcpy(m->x, x_in + (size_t)m->n_layers * dim, (size_t)dim * sizeof(float));
     return lm_head(m);
+}
+
+int or_forward_inject_q8(or_model *m, int token, int pos, int lm_mode, const float *x_in, const or_q8K *q8_in,
+                         float *x_out) {
+    m->q8_inj = q8_in;
+    const int rc = or_forward_inject(m, token, pos, lm_mode, x_in, x_out);
+    m->q8_inj = NULL;
+    return rc;
+}
+
+/* The K/V part of forward() for every storing layer, each from its injected
+ * input row: attn_norm, Q8_K (main.c:1878-1884), then layer_kv. */
+int or_forward_inject_kv(or_model *m, int token, int pos, const float *x_in, const or_q8K *q8_in) {
+    const int dim = m->dim;
+    if (pos < 0 || pos >= m->max_seq || token < 0 || token >= m->vocab) return -1;
+    m->q8_inj = q8_in;
+    int rc = 0;
+    for (int l = 0; l < m->n_layers && l < OR_N_LAYER_KV && rc == 0; l++) {
+        or_rmsnorm(m->xb2, x_in + (size_t)l * dim, m->attn_norm[l], dim, m->eps);
+        const int q8_att = q8_point(m, l, OR_Q8_SLOT_ATTN, m->xb2, dim, m->wq[l].type);
+        rc = layer_kv(m, l, pos, q8_att);
+    }
+    m->q8_inj = NULL;
+    return rc;
 }
 
 static double now_s(void) {

@@ -143,6 +143,15 @@ int       or_forward(or_model *m, int token, int pos, int lm_mode);   /* main.c:
  * layer's output (n_layers x dim).  Checks every layer of a device run in
  * isolation. */
 int       or_forward_inject(or_model *m, int token, int pos, int lm_mode, const float *x_in, float *x_out);
+/* or_forward_inject with every Q8_K activation taken from q8_in (same
+ * layout as or_model_q8_rec) instead of the oracle's own quantization: a
+ * layer then differs from a device run only by fp32 summation order. */
+int       or_forward_inject_q8(or_model *m, int token, int pos, int lm_mode, const float *x_in,
+                               const or_q8K *q8_in, float *x_out);
+/* the K/V of every storing layer at pos from injected inputs x_in (as
+ * or_forward_inject), without the rest of the layer; q8_in (nullable) as
+ * or_forward_inject_q8 */
+int       or_forward_inject_kv(or_model *m, int token, int pos, const float *x_in, const or_q8K *q8_in);
 const float *or_model_logits(const or_model *m);
 const float *or_model_x(const or_model *m);
 /* Per-layer fingerprints captured during the last forward (sum,l2,max per layer
@@ -151,6 +160,19 @@ const float *or_model_layer_stats(const or_model *m);
 const float *or_model_attn_stats(const or_model *m);
 /* x after every layer of the last forward (n_layers*dim floats) */
 const float *or_model_layer_x(const or_model *m);
+/* Quantization points of a layer whose input goes through Q8_K when the
+ * matrix is Q4_K/Q5_K (main.c:1884, 1975, and mm's own quantize at 1685 for
+ * O, inp_gate and proj): slot s of layer l holds OR_Q8_SLOT_BLOCKS blocks at
+ * block offset (l * OR_Q8_SLOTS + s) * OR_Q8_SLOT_BLOCKS. */
+enum { OR_Q8_SLOT_ATTN = 0, OR_Q8_SLOT_O, OR_Q8_SLOT_FFN, OR_Q8_SLOT_INP_GATE, OR_Q8_SLOT_PROJ, OR_Q8_SLOTS };
+#define OR_Q8_SLOT_BLOCKS 16
+/* the oracle's own Q8_K of every slot in the last forward (n_layers x slots) */
+const or_q8K *or_model_q8_rec(const or_model *m);
+/* the layer whose KV cache layer l reads (itself, or donor 22/23), main.c:739-746 */
+int or_model_kv_source(const or_model *m, int layer);
+/* the K (which 0) or V (1) cache of a storing layer: max_seq rows of
+ * OR_MAX_KV_DIM floats (main.c:1798-1809); NULL for other layers */
+float *or_model_kv(or_model *m, int layer, int which);
 /* Greedy generation loop (main.c:2335-2488 with temp=0): prompt is fed
  * token-serially, then max_new tokens are produced.  out_tokens receives
  * the generated ids; returns the count.  Stops on eos/eot. */

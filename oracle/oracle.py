@@ -20,6 +20,10 @@ REF_SO = os.path.join(HERE, "_ref", "libg4ref.so")
 
 Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
 assert Q8K_DTYPE.itemsize == 292
+# quantization points of a layer (g4_oracle.h OR_Q8_SLOT_*): attention input,
+# O input, FFN input, PLE inp_gate input, PLE proj input
+Q8_SLOTS, Q8_SLOT_BLOCKS = 5, 16
+Q8_SLOT_NAMES = ("attn", "o", "ffn", "inp_gate", "proj")
 
 F32P = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 VP = C.c_void_p
@@ -90,6 +94,11 @@ class Oracle:
             "or_model_attn_stats": (VP, [VP]),
             "or_model_layer_x": (VP, [VP]),
             "or_generate_greedy": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, VP, VP]),
+            "or_forward_inject_q8": (C.c_int, [VP, C.c_int, C.c_int, C.c_int, VP, VP, VP]),
+            "or_forward_inject_kv": (C.c_int, [VP, C.c_int, C.c_int, VP, VP]),
+            "or_model_q8_rec": (VP, [VP]),
+            "or_model_kv_source": (C.c_int, [VP, C.c_int]),
+            "or_model_kv": (C.POINTER(C.c_float), [VP, C.c_int, C.c_int]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -185,6 +194,55 @@ class OracleModel:
         if self.o.L.or_forward_inject(self.h, token, pos, lm_mode, _ptr(x_in), _ptr(out)) != 0:
             raise RuntimeError("or_forward_inject failed")
         return out
+
+    def forward_inject_q8(self, token: int, pos: int, lm_mode: int, x_in: np.ndarray,
+                          q8_in: np.ndarray) -> np.ndarray:
+        """forward_inject with every Q8_K activation taken from q8_in
+        ((n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS) of Q8K_DTYPE, as q8_rec())."""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        assert x_in.shape == (self.n_layers + 1, self.dim)
+        q8_in = np.ascontiguousarray(q8_in)
+        assert q8_in.dtype == Q8K_DTYPE and q8_in.shape == (self.n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS)
+        out = np.empty((self.n_layers, self.dim), np.float32)
+        if self.o.L.or_forward_inject_q8(self.h, token, pos, lm_mode, _ptr(x_in), _ptr(q8_in), _ptr(out)) != 0:
+            raise RuntimeError("or_forward_inject_q8 failed")
+        return out
+
+    def forward_inject_kv(self, token: int, pos: int, x_in: np.ndarray, q8_in: np.ndarray | None = None) -> None:
+        """K/V of every storing layer at pos from the injected layer inputs
+        (and, if given, the injected Q8_K as forward_inject_q8)."""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        assert x_in.shape == (self.n_layers + 1, self.dim)
+        qp = None
+        if q8_in is not None:
+            q8_in = np.ascontiguousarray(q8_in)
+            assert q8_in.dtype == Q8K_DTYPE and q8_in.shape == (self.n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS)
+            qp = _ptr(q8_in)
+        if self.o.L.or_forward_inject_kv(self.h, token, pos, _ptr(x_in), qp) != 0:
+            raise RuntimeError("or_forward_inject_kv failed")
+
+    def q8_rec(self) -> np.ndarray:
+        """The oracle's own Q8_K of every quantization point in the last
+        forward: (n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS) of Q8K_DTYPE."""
+        p = self.o.L.or_model_q8_rec(self.h)
+        n = self.n_layers * Q8_SLOTS * Q8_SLOT_BLOCKS
+        raw = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), (n * Q8K_DTYPE.itemsize,))
+        return raw.copy().view(Q8K_DTYPE).reshape(self.n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS)
+
+    def kv_source(self, layer: int) -> int:
+        """the layer whose KV cache `layer` reads (main.c:739-746)"""
+        return int(self.o.L.or_model_kv_source(self.h, layer))
+
+    def kv(self, layer: int):
+        """(K, V) cache views of a storing layer: (max_seq, 1024) float32,
+        writable (main.c:1798-1809 layout)."""
+        out = []
+        for which in (0, 1):
+            p = self.o.L.or_model_kv(self.h, layer, which)
+            if not p:
+                raise ValueError(f"layer {layer} stores no KV")
+            out.append(np.ctypeslib.as_array(p, (self.max_seq, 1024)))
+        return out[0], out[1]
 
     def logits(self) -> np.ndarray:
         p = self.o.L.or_model_logits(self.h)

@@ -125,3 +125,44 @@ def dequant_f64(blk: np.ndarray, qtype: int) -> np.ndarray:
     dm = f16(blk[:, 2:4].copy().view(np.uint16)[:, 0])[:, None]
     w = d * np.repeat(sc, 32, -1) * vals - dm * np.repeat(mn, 32, -1)
     return w.reshape(-1)
+
+
+def _q6_abs_values(blk: np.ndarray) -> np.ndarray:
+    """[nb, 210] -> |q6 - 32| as float32 [nb, 256] in weight order (vectorised
+    form of q6_values_scales' layout)"""
+    ql = blk[:, 0:128]
+    qh = blk[:, 128:192]
+    q = np.empty((blk.shape[0], 256), np.int16)
+    for h in range(2):
+        lo, hi, b = ql[:, 64 * h:64 * h + 32], ql[:, 64 * h + 32:64 * h + 64], qh[:, 32 * h:32 * h + 32]
+        base = 128 * h
+        q[:, base + 0:base + 32] = (lo & 15) | ((b & 3) << 4)
+        q[:, base + 32:base + 64] = (hi & 15) | (((b >> 2) & 3) << 4)
+        q[:, base + 64:base + 96] = (lo >> 4) | (((b >> 4) & 3) << 4)
+        q[:, base + 96:base + 128] = (hi >> 4) | (((b >> 6) & 3) << 4)
+    return np.abs(q - 32).astype(np.float32)
+
+
+def abs_dot_rows(raw: np.ndarray, qtype: int, n: int, x: np.ndarray, chunk: int = 4096) -> np.ndarray:
+    """sum_i |w_ri| * |x_i| per row of a d x n K-quant matrix (raw bytes), in
+    row chunks so that large matrices (the 262144-row LM head) stay within
+    memory; the normaliser of the fp32 GEMV bars.  Q6_K: the 16-weight
+    sub-block s of a block uses scale s in weight order, so per block
+    |d| * sum_s |sc_s| * sum_{i in s} |q_i - 32| |x_i|."""
+    bpb = {12: 144, 13: 176, 14: 210}[qtype]
+    nb = n // 256
+    rows = raw.reshape(-1, nb * bpb)
+    ax = np.abs(np.asarray(x, np.float64))
+    out = np.empty(rows.shape[0], np.float64)
+    for r0 in range(0, rows.shape[0], chunk):
+        blk = rows[r0:r0 + chunk].reshape(-1, bpb)
+        if qtype == 14:
+            A = _q6_abs_values(blk).reshape(-1, nb, 16, 16)
+            T = np.einsum("rbst,bst->rbs", A, ax.astype(np.float32).reshape(nb, 16, 16), dtype=np.float64)
+            sc = np.abs(blk[:, 192:208].view(np.int8).astype(np.float64)).reshape(-1, nb, 16)
+            d = np.abs(f16(blk[:, 208:210].copy().view(np.uint16)[:, 0])).reshape(-1, nb)
+            out[r0:r0 + chunk] = (d * (sc * T).sum(-1)).sum(-1)
+        else:
+            w = np.abs(dequant_f64(blk, qtype)).reshape(-1, n)
+            out[r0:r0 + chunk] = w @ ax
+    return out

@@ -10,7 +10,8 @@ LM head.  And the reference's --f32-matmul switch (main.c:1680-1683): Q4_K /
 Q5_K through dequantized fp32 weights.
 
 Parity as tests/test_gpu_engine.py: each layer teacher-forced against the
-oracle's forward (or_forward_inject), same bars.
+oracle's forward with its own and with the engine's Q8_K (engine_check.py),
+same bars.
 """
 import dataclasses
 
@@ -18,14 +19,13 @@ import numpy as np
 import pytest
 
 import synth
+from engine_check import StepCheck, assert_bars, prefill_checks, rel
 
 pytestmark = pytest.mark.gpu
 
-MEDIAN_TOL = 2e-6
-P90_TOL = 2e-5
-FLIP_TOL = 1e-3
-FLIP_SHARE = 0.05
-MAX_TOL = 3e-2
+MEDIAN_TOL = 2e-6      # per-layer, oracle's own Q8_K
+Q8_TOL = 1e-4          # per-layer, engine's Q8_K injected: the dense and --f32-matmul GEMVs sum
+                       # up to 2560 fp32 products in another order (observed <= 4e-5)
 LOGIT_TOL = 1e-5
 
 MIXED = (
@@ -61,21 +61,6 @@ def plain_path(tmp_path_factory):
     return _model(tmp_path_factory, (), "plain.gguf")
 
 
-def _rel(a, b):
-    b = np.asarray(b, np.float64)
-    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
-
-
-def _bars(errs, what):
-    errs = np.asarray(errs)
-    print(f"{what}: per-layer rel err median {np.median(errs):.2e} p90 {np.percentile(errs, 90):.2e} "
-          f"max {errs.max():.2e} flips {np.mean(errs > FLIP_TOL):.3f}")
-    assert np.median(errs) < MEDIAN_TOL
-    assert np.percentile(errs, 90) < P90_TOL
-    assert np.mean(errs > FLIP_TOL) < FLIP_SHARE
-    assert errs.max() < MAX_TOL
-
-
 def _decode_and_prefill(path, orc, f32_matmul=False):
     """teacher-forced decode (24 positions, logits at each) and a batched
     prefill of the same tokens, both against the oracle"""
@@ -88,24 +73,18 @@ def _decode_and_prefill(path, orc, f32_matmul=False):
         em.set_f32_matmul(f32_matmul)
         toks = np.random.default_rng(11).integers(0, om.vocab, 24)
         em.set_trace(True)
-        errs, lerr = [], []
+        checks, lerr = [], []
         for pos, t in enumerate(toks):
             em.forward(int(t), pos, 1)
-            X = em.layer_x()
-            out = om.forward_inject(int(t), pos, 1, X)
-            errs += [_rel(X[l + 1], out[l]) for l in range(om.n_layers)]
-            lerr.append(_rel(em.logits(), om.logits()))
+            sc = StepCheck.engine(em, om, int(t), pos, 1)
+            checks.append(sc)
+            lerr.append(rel(em.logits(), sc.logits_q8))
         em.set_trace(False)
-        _bars(errs, "decode")
+        assert_bars(checks, "decode", MEDIAN_TOL, Q8_TOL)
         assert max(lerr) < LOGIT_TOL, max(lerr)
         em.set_prefill_chunk(9)
-        tr = em.prefill_trace(toks, 0)
-        perr = []
-        for i, t in enumerate(toks):
-            X = np.ascontiguousarray(tr[:, i, :])
-            out = om.forward_inject(int(t), i, 0, X)
-            perr += [_rel(X[l + 1], out[l]) for l in range(om.n_layers)]
-        _bars(perr, "prefill")
+        tr, qt = em.prefill_trace(toks, 0, q8=True)
+        assert_bars(prefill_checks(om, toks, tr, qt), "prefill", MEDIAN_TOL, Q8_TOL)
     finally:
         orc.L.or_set_f32_matmul(0)
         em.close()

@@ -169,10 +169,15 @@ def test_q6K_f32_gemv(lib, orc, n, d):
     assert err.max() <= 1e-5, err.max()
 
 
-def test_q6K_softcap(lib, orc):
+@pytest.mark.parametrize("d", [4096, 16384, 262144])
+def test_q6K_softcap(lib, orc, d):
+    """logits_tied's GEMV + soft-cap.  262144 rows is the LM head itself: at
+    that size the launch picks one row group per workgroup and a grid-stride
+    loop (the instantiation the decode step runs); 16384 and 4096 rows take
+    the K-sliced forms."""
     from g4 import DBuf, upload_quant
-    n, d = 2560, 4096
-    rng = np.random.default_rng(2)
+    n = 2560
+    rng = np.random.default_rng(2 + d)
     raw = synth.rand_q6K(rng, d, n)
     x = rng.standard_normal(n).astype(np.float32)
     w = upload_quant(lib, raw, 14, n, d)
@@ -184,15 +189,37 @@ def test_q6K_softcap(lib, orc):
     want = (np.float32(30.0) * np.tanh(raw_l * np.float32(1.0 / 30.0))).astype(np.float32)
     # the cap's derivative is <= 1, so the GEMV bar (1e-5 of sum |w*x|) carries
     # over; a few ulps of 30 cover tanhf itself
-    W = np.abs(kq.dequant_f64(raw.reshape(-1, 210), 14).reshape(d, n))
-    mag = W @ np.abs(x.astype(np.float64))
-    assert (np.abs(got - want) <= 1e-5 * mag + 1e-5).all()
+    mag = kq.abs_dot_rows(raw, 14, n, x)
+    err = np.abs(got.astype(np.float64) - want) - 1e-5
+    assert (err <= 1e-5 * mag).all(), float(np.max(err / mag))
 
 
-def test_q6K_q8K_gemv_bitexact(lib, orc):
+@pytest.mark.parametrize("d", [16384, 262144])
+def test_q6K_f32_gemv_lm_head_rows(lib, orc, d):
+    """mm_quant_rows (no cap) at LM-head row counts."""
     from g4 import DBuf, upload_quant
-    n, d = 2560, 3000
-    rng = np.random.default_rng(21)
+    n = 2560
+    rng = np.random.default_rng(7 + d)
+    raw = synth.rand_q6K(rng, d, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = upload_quant(lib, raw, 14, n, d)
+    xd = dbuf(lib, x)
+    out = DBuf(lib, 4 * d)
+    lib.g4_mm_quant_rows(out.ptr, xd.ptr, w.ptr, n, d, 14)
+    got = out.to_array(np.float32)
+    want = orc.mm_quant_rows(x, raw, n, d, 14)
+    err = np.abs(got.astype(np.float64) - want) / kq.abs_dot_rows(raw, 14, n, x)
+    assert err.max() <= 1e-5, err.max()
+
+
+@pytest.mark.parametrize("d", [3000, 262144])
+def test_q6K_q8K_gemv_bitexact(lib, orc, d):
+    """Q6_K x Q8_K rows (the form the north star names for the LM head): bit
+    for bit with the oracle, at a small row count and at 262144 rows (where
+    the launch picks another rows-per-group tiling)."""
+    from g4 import DBuf, upload_quant
+    n = 2560
+    rng = np.random.default_rng(21 + d)
     raw = synth.rand_q6K(rng, d, n)
     x = rng.standard_normal(n).astype(np.float32)
     w = upload_quant(lib, raw, 14, n, d)

@@ -3,27 +3,25 @@ layer by layer, batched GEMMs, attention over the chunk's query rows) against
 the CPU oracle's token-by-token forward() (main.c:2366-2384 runs the prompt
 that way), on the small synthetic Gemma 4 model of test_gpu_engine.py.
 
-Each layer is checked in isolation, teacher-forced: the engine records every
-layer's input rows (g4e_prefill_trace), the oracle runs the same layer per
-token from those inputs (or_forward_inject, which fills its KV cache from
-them), and the outputs are compared.  The bars are those of the decode test
-(few-ulp medians, rare Q8_K rounding flips at width 256).  Without teacher
-forcing the two paths drift apart with depth on this random model: a flip
-moves a row by ~1e-3 and 20 further layers amplify it, so an end-to-end cache
-comparison tests nothing but that amplification.
+Each layer is checked in isolation, teacher-forced (engine_check.py): the
+engine records every layer's input rows and Q8_K rows (g4e_prefill_trace_q8),
+the oracle runs the same layer per token from those inputs with its own and
+with the engine's Q8_K (which also fills its KV cache), and the outputs are
+compared with the decode test's bars.  Without teacher forcing the two paths
+drift apart with depth on this random model: a flip moves a row by ~1e-3 and
+20 further layers amplify it, so an end-to-end cache comparison tests nothing
+but that amplification.
 """
 import numpy as np
 import pytest
 
 import synth
+from engine_check import StepCheck, assert_bars, prefill_checks, rel
 
 pytestmark = pytest.mark.gpu
 
-MEDIAN_TOL = 2e-6
-P90_TOL = 2e-5
-FLIP_TOL = 1e-3
-FLIP_SHARE = 0.05
-MAX_TOL = 3e-2
+MEDIAN_TOL = 2e-6      # per-layer, oracle's own Q8_K
+Q8_TOL = 1e-5          # engine's Q8_K injected (observed <= 1e-6: fp32 order only)
 LOGIT_TOL = 1e-5
 
 
@@ -43,36 +41,11 @@ def orc_model(model_path, orc):
     om.close()
 
 
-def _rel(a, b):
-    b = np.asarray(b, np.float64)
-    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
-
-
 def _engine(model_path, chunk):
     import g4
     em = g4.Engine(model_path, max_seq=64)
     em.set_prefill_chunk(chunk)
     return em
-
-
-def _check_layers(om, toks, tr, pos0=0):
-    """tr: (n_layers + 1, n, dim) engine inputs; the oracle runs each token's
-    layers from them in position order; returns the per-layer errors."""
-    errs = []
-    for i, t in enumerate(toks):
-        X = np.ascontiguousarray(tr[:, i, :])
-        out = om.forward_inject(int(t), pos0 + i, 0, X)
-        errs += [_rel(X[l + 1], out[l]) for l in range(om.n_layers)]
-    return np.array(errs)
-
-
-def _assert_bars(errs, what):
-    print(f"{what}: per-layer rel err median {np.median(errs):.2e} p90 {np.percentile(errs, 90):.2e} "
-          f"max {errs.max():.2e} flips {np.mean(errs > FLIP_TOL):.3f}")
-    assert np.median(errs) < MEDIAN_TOL
-    assert np.percentile(errs, 90) < P90_TOL
-    assert np.mean(errs > FLIP_TOL) < FLIP_SHARE
-    assert errs.max() < MAX_TOL
 
 
 def test_prefill_one_chunk(model_path, orc_model):
@@ -83,10 +56,10 @@ def test_prefill_one_chunk(model_path, orc_model):
     toks = np.random.default_rng(1).integers(0, om.vocab, 24)
     em = _engine(model_path, 64)
     try:
-        tr = em.prefill_trace(toks, 0)
+        tr, qt = em.prefill_trace(toks, 0, q8=True)
     finally:
         em.close()
-    _assert_bars(_check_layers(om, toks, tr), "one chunk")
+    assert_bars(prefill_checks(om, toks, tr, qt), "one chunk", MEDIAN_TOL, Q8_TOL)
 
 
 def test_prefill_chunks_and_calls(model_path, orc_model):
@@ -97,10 +70,12 @@ def test_prefill_chunks_and_calls(model_path, orc_model):
     toks = np.random.default_rng(2).integers(0, om.vocab, 31)
     em = _engine(model_path, 7)
     try:
-        tr = np.concatenate([em.prefill_trace(toks[:13], 0), em.prefill_trace(toks[13:], 13)], axis=1)
+        a = em.prefill_trace(toks[:13], 0, q8=True)
+        b = em.prefill_trace(toks[13:], 13, q8=True)
     finally:
         em.close()
-    _assert_bars(_check_layers(om, toks, tr), "chunks of 7, two calls")
+    tr, qt = np.concatenate([a[0], b[0]], axis=1), np.concatenate([a[1], b[1]], axis=1)
+    assert_bars(prefill_checks(om, toks, tr, qt), "chunks of 7, two calls", MEDIAN_TOL, Q8_TOL)
 
 
 def test_decode_after_prefill(model_path, orc_model):
@@ -112,21 +87,20 @@ def test_decode_after_prefill(model_path, orc_model):
     toks = np.random.default_rng(3).integers(0, om.vocab, 30)
     n_pre = 21
     em = _engine(model_path, 8)
-    errs, lerr = [], []
+    lerr = []
     try:
-        tr = em.prefill_trace(toks[:n_pre], 0)
-        errs.append(_check_layers(om, toks[:n_pre], tr))
+        tr, qt = em.prefill_trace(toks[:n_pre], 0, q8=True)
+        checks = prefill_checks(om, toks[:n_pre], tr, qt)
         em.set_trace(True)
         for pos in range(n_pre, len(toks)):
             em.forward(int(toks[pos]), pos, 1)
-            X = em.layer_x()
-            out = om.forward_inject(int(toks[pos]), pos, 1, X)
-            errs.append(np.array([_rel(X[l + 1], out[l]) for l in range(om.n_layers)]))
-            lerr.append(_rel(em.logits(), om.logits()))
+            sc = StepCheck.engine(em, om, int(toks[pos]), pos, 1)
+            checks.append(sc)
+            lerr.append(rel(em.logits(), sc.logits_q8))
         em.set_trace(False)
     finally:
         em.close()
-    _assert_bars(np.concatenate(errs), "prefill then decode")
+    assert_bars(checks, "prefill then decode", MEDIAN_TOL, Q8_TOL)
     assert max(lerr) < LOGIT_TOL
 
 

@@ -139,6 +139,32 @@ def test_greedy_ties_and_sizes(lib, orc):
         assert s(0.0, 1.0, 40 if n >= 40 else n) == n // 5
 
 
+def test_nan_logits(lib, orc):
+    """NaN logits after the first top-k positions: the greedy token and the
+    sampled tokens equal or_sample_token's (the reference's comparisons never
+    admit such a NaN into its list)."""
+    rng = np.random.default_rng(17)
+    lg = _logits(rng)
+    lg[[100, 7000, 9000, N - 1]] = np.nan
+    lg[8000] = lg[~np.isnan(lg)].max() + 0.5
+    lg[8001] = np.nan
+    s = Sampler(lib, lg)
+    st = np.array([1], np.uint64)
+    lc = lg.copy()
+    assert s(0.0, 1.0, 40) == orc.L.or_sample_token(P(lc), N, 0.0, 1.0, 40, P(st)) == 8000
+    state = 99
+    s.seed(state)
+    for i in range(20):
+        st = np.array([state], np.uint64)
+        lc = lg.copy()
+        want = orc.L.or_sample_token(P(lc), N, 0.8, 0.9, 40, P(st))
+        got = s(0.8, 0.9, 40)
+        if got != want:
+            assert _margin(lg, 0.8, 0.9, 40, state) < 1e-5, (i, got, want)
+        state = int(st[0])
+        assert s.state() == state
+
+
 @pytest.mark.parametrize("temp,topp,topk", [(0.6, 0.9, 40), (1.0, 1.0, 40), (0.8, 0.95, 40), (0.7, 0.5, 10),
                                             (1.5, 0.0, 64), (0.3, 0.9, 1)])
 def test_draws_match_oracle(lib, orc, temp, topp, topk):

@@ -368,6 +368,29 @@ def test_argmax_first_index(lib):
         assert got == best, (case, got, best, m)
 
 
+def test_argmax_nan(lib, orc):
+    """NaN logits, against the reference's scan (main.c:2046-2048) as the
+    oracle's first-index argmax: a NaN after index 0 never wins; a NaN at
+    index 0 is never left (every comparison with it is false)."""
+    rng = np.random.default_rng(13)
+    n = 262144
+    part = empty(lib, lib.L.g4_argmax_part_bytes(n))
+    out = empty(lib, 4)
+    for case in range(3):
+        v = rng.standard_normal(n).astype(np.float32)
+        if case == 0:
+            v[[5, 4096, 200000]] = np.nan
+        if case == 1:
+            v[int(np.argmax(v)) + 1:int(np.argmax(v)) + 3] = np.nan
+        if case == 2:
+            v[0] = np.nan
+        vd = dbuf(lib, v)
+        lib.g4_argmax(vd.ptr, n, out.ptr, part.ptr, None, None)
+        vc = v.copy()
+        want = orc.L.or_argmax_first(vc.ctypes.data, n)
+        assert int(out.to_array(np.int32)[0]) == want, case
+
+
 def test_residual_norm(lib, orc):
     rng = np.random.default_rng(13)
     n = 2560
