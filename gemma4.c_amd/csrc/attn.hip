@@ -1050,6 +1050,32 @@ int workspace(size_t bytes, uint8_t** p) {
     return G4_OK;
 }
 
+// ---- scratch of the allocation-free entry point ---------------------------
+// g4_attn_decode_noalloc keeps its chunk partials in this file-scope device
+// array instead of the library workspace: one copy per GPU, held until the
+// process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address: g4_init resolves each device's address once
+// (attn_scratch_setup) and only that address is handed to kernels.
+constexpr int kScratchDevices = 64;
+__device__ __align__(256) uint8_t scratch[G4_ATTN_NOALLOC_SCRATCH];
+void* g_scratch_dev[kScratchDevices];   // device address of `scratch` per device
+
+}  // namespace g4
+
+int g4_attn_scratch_setup(int device) {
+    G4_CHECK_ARG(device >= 0 && device < g4::kScratchDevices, "attention scratch: device %d beyond %d", device,
+                 g4::kScratchDevices);
+    if (g4::g_scratch_dev[device]) return G4_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g4::scratch));
+    if (e != hipSuccess || !p)
+        return g4_fail(G4_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g4::g_scratch_dev[device] = p;
+    return G4_OK;
+}
+
+namespace g4 {
+
 // about 16 positions per workgroup, at most 64 chunks per kv head unless a
 // chunk would exceed kChunkMax positions
 int chunks_for(int nwin) {
@@ -1215,6 +1241,34 @@ extern "C" int g4_attn_decode(const float* q, const float* kc, const float* vc, 
     a.t_start = t_start; a.nwin = nwin; a.window = 0; a.kv_stride = kv_stride; a.ring = 0;
     a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = chunks_for(nwin);
     return attn_common("g4_attn_decode", a);
+}
+
+// g4_attn_decode with its partials in the per-GPU scratch array: the same
+// kernels and chunk count, so the same bits; no allocation, no memset (the
+// chunk kernel writes every partial the merge reads, whatever the previous
+// call left there).  Calls that overlap in time on one GPU share the array
+// and race.
+extern "C" int g4_attn_decode_noalloc(const float* q, const float* kc, const float* vc, int kv_stride, int t_start,
+                                      int nwin, int n_heads, int n_kv, int hd, float attn_scale, float* out) {
+    G4_CHECK_ARG(t_start >= 0 && nwin >= 0, "g4_attn_decode_noalloc: t_start=%d nwin=%d", t_start, nwin);
+    AttnArgs a = {};
+    a.q = q; a.kc = kc; a.vc = vc; a.dpos = nullptr; a.out = out; a.q8 = nullptr;
+    a.t_start = t_start; a.nwin = nwin; a.window = 0; a.kv_stride = kv_stride; a.ring = 0;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.scale = attn_scale; a.G = chunks_for(nwin);
+    int rc = check_attn_shape("g4_attn_decode_noalloc", n_heads, n_kv, hd, a.G);
+    if (rc) return rc;
+    G4_CHECK_ARG(q && kc && vc && out, "g4_attn_decode_noalloc: null pointer");
+    G4_CHECK_ARG(kv_stride >= n_kv * hd, "g4_attn_decode_noalloc: kv_stride %d < n_kv*hd", kv_stride);
+    const size_t need = g4_attn_part_bytes(n_heads, hd, a.G);
+    G4_CHECK_ARG(need <= G4_ATTN_NOALLOC_SCRATCH,
+                 "g4_attn_decode_noalloc: %zu B of partials (%d heads x %d chunks x head_dim %d) exceed the %u B "
+                 "scratch", need, n_heads, a.G, hd, (unsigned)G4_ATTN_NOALLOC_SCRATCH);
+    int dev = -1;
+    G4_HIP(hipGetDevice(&dev));
+    G4_CHECK(dev >= 0 && dev < kScratchDevices && g_scratch_dev[dev], G4_ERR_STATE,
+             "g4_attn_decode_noalloc: g4_init has not set up device %d", dev);
+    a.part = (float*)g_scratch_dev[dev];
+    return launch_attn(a);
 }
 
 // Same block over a ring cache of `ring` slots (slot = t % ring) at position

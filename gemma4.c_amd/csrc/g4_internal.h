@@ -11,6 +11,9 @@ int g4_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3))
 int g4_hip_status(hipError_t e);   // 0 or G4_ERR_HIP (message recorded)
 int g4_check_launch(const char* kernel);
 int g4_num_cus();
+// device address of the allocation-free attention's scratch on `device`
+// (current), resolved once per device; called by g4_init
+int g4_attn_scratch_setup(int device);
 
 #define G4_CHECK_ARG(cond, ...)                          \
     do {                                                 \

@@ -45,7 +45,7 @@ extern "C" int g4_init(int device) {
     hipDeviceProp_t p;
     G4_HIP(hipGetDeviceProperties(&p, device));
     g_cus = p.multiProcessorCount;
-    return G4_OK;
+    return g4_attn_scratch_setup(device);
 }
 
 extern "C" int g4_device_info(int* cus, char* arch, int arch_len) {

@@ -89,6 +89,7 @@ _SIGS = {
     "g4_kv_append_rope": (I, [VP, VP, VP, VP, VP, I, I, I, I, I, I, F, F, VP, F]),
     "g4_attn_decode": (I, [VP, VP, VP, I, I, I, I, I, I, F, VP]),
     "g4_attn_decode_ring": (I, [VP, VP, VP, I, I, I, I, I, I, I, F, VP]),
+    "g4_attn_decode_noalloc": (I, [VP, VP, VP, I, I, I, I, I, I, F, VP]),
     "g4_softmax": (I, [VP, I]),
     "g4_emb_lookup": (I, [VP, VP, I, I, I, I]),
     "g4_argmax_part_bytes": (SZ, [I]),

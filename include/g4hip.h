@@ -252,6 +252,20 @@ int g4_attn_decode(const float *q, const float *kc, const float *vc, int kv_stri
  * sliding window of main.c:1910-1915 (window 0 = full attention). */
 int g4_attn_decode_ring(const float *q, const float *kc, const float *vc, int kv_stride, int ring, int pos, int window,
                         int n_heads, int n_kv, int hd, float attn_scale, float *out);
+/* g4_attn_decode that allocates nothing.  No counterpart in the reference:
+ * for callers that cannot call hipMalloc (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Same arguments,
+ * kernels and results (bit for bit) as g4_attn_decode, but the chunk
+ * partials live in a per-GPU scratch array of G4_ATTN_NOALLOC_SCRATCH bytes
+ * that g4_init sets up, instead of the library's growing workspace.
+ * Limit: n_heads * G * (hd + 2) * 4 bytes of partials, G being the chunk
+ * count (about nwin / 32, 1..128 up to 131072 positions, more beyond):
+ * G4_ERR_ARG above it; G4_ERR_STATE if g4_init was not called for the
+ * current device.  Every call on a GPU shares its scratch, so calls that
+ * overlap in time on one GPU race. */
+#define G4_ATTN_NOALLOC_SCRATCH (8u << 20)
+int g4_attn_decode_noalloc(const float *q, const float *kc, const float *vc, int kv_stride, int t_start, int nwin,
+                           int n_heads, int n_kv, int hd, float attn_scale, float *out);
 /* softmax(float *x, int n), main.c:1478 */
 int g4_softmax(float *x, int n);
 
