@@ -186,6 +186,7 @@ class ModelShape:
     ffn_type: int = Q4_K          # gate/up (Q5_K variant possible)
     rope_freqs: bool = False      # include a rope_freqs.weight tensor
     types: tuple = ()             # (glob over tensor names, type) overrides, first match wins
+    zeros: tuple = ()             # globs over tensor names whose bytes are all zero
 
     def is_swa(self, l: int) -> bool:
         return (l % self.swa_pattern) < (self.swa_pattern - 1)
@@ -217,6 +218,10 @@ def model_tensors(s: ModelShape) -> list[TensorSpec]:
             if fnmatch.fnmatchcase(name, pat):
                 qtype = t
                 break
+        if any(fnmatch.fnmatchcase(name, pat) for pat in s.zeros):
+            ts.append(TensorSpec(name, qtype, (n, d), lambda r, q=qtype, n=n, d=d:
+                                 np.zeros(tensor_nbytes(q, (n, d)), np.uint8)))
+            return
         if qtype in (F16, F32):
             dt = np.float16 if qtype == F16 else np.float32
             ts.append(TensorSpec(name, qtype, (n, d), lambda r, n=n, d=d, dt=dt:
@@ -287,8 +292,8 @@ def model_kvs(s: ModelShape) -> list[bytes]:
     return kv
 
 
-def write_model_gguf(path: str, s: ModelShape, seed: int) -> int:
-    return write_gguf(path, model_kvs(s), model_tensors(s), seed)
+def write_model_gguf(path: str, s: ModelShape, seed: int, alignment: int = 32) -> int:
+    return write_gguf(path, model_kvs(s), model_tensors(s), seed, alignment)
 
 
 def decode_weight_bytes(s: ModelShape) -> int:

@@ -1252,6 +1252,31 @@ int or_forward_inject(or_model *m, int token, int pos, int lm_mode, const float 
     return lm_head(m);
 }
 
+int or_embed(or_model *m, int token, int pos) { return embed_ple(m, token, pos); }
+
+int or_layer_inject(or_model *m, int token, int pos, int layer, const float *x_in, float *x_out) {
+    if (layer < 0 || layer >= m->n_layers || embed_ple(m, token, pos)) return -1;
+    float *x_before = (float *)malloc((size_t)m->dim * sizeof(float));
+    memcpy(m->x, x_in, (size_t)m->dim * sizeof(float));
+    const int rc = layer_step(m, layer, pos, x_before);
+    free(x_before);
+    if (rc == 0) memcpy(x_out, m->x, (size_t)m->dim * sizeof(float));
+    return rc;
+}
+
+int or_lm_head_inject(or_model *m, const float *x_in) {
+    memcpy(m->x, x_in, (size_t)m->dim * sizeof(float));
+    return lm_head(m);
+}
+
+float *or_model_state(or_model *m, const char *name) {
+    static const char *names[] = {"x", "xb2", "q", "k", "v", "q_out", "ple", "ple_ctx", "ple_gate", "hb", "hb2", "logits"};
+    float *bufs[] = {m->x, m->xb2, m->q, m->k, m->v, m->q_out, m->ple, m->ple_ctx, m->ple_gate, m->hb, m->hb2, m->logits};
+    for (size_t i = 0; i < sizeof names / sizeof names[0]; i++)
+        if (!strcmp(name, names[i])) return bufs[i];
+    return NULL;
+}
+
 int or_forward_inject_q8(or_model *m, int token, int pos, int lm_mode, const float *x_in, const or_q8K *q8_in,
                          float *x_out) {
     m->q8_inj = q8_in;

@@ -25,8 +25,17 @@
  *     single-token closed forms.
  *   - vec_dot_q6_K_q8_K: has no counterpart in the reference; pinned by an
  *     exact integer brute force over the dequant formula.
- *   - forward()/generate(): composed from the pinned pieces above; checked
- *     against the reference's layer routing table (design.md:841-860).
+ *   - model level (tests/test_oracle_model.py): or_model_open against the
+ *     reference's own parse_gguf/load_weights (configuration, data offset
+ *     at two alignments, vocabulary, KV routing); build_ple, every layer
+ *     step and the final norm + logits_tied bit for bit against a
+ *     composition of the reference's compiled functions over the
+ *     reference loader's weight pointers, in forward()'s statement order
+ *     (main.c:1838-2029), the attention block in float64; invariants
+ *     (zero O/down/proj weights leave out_scale * input exactly; shared
+ *     layers read donor 22 or 23 and nothing else); or_hidden_stats bit
+ *     for bit against the reference's hidden_stats; or_mm_f32 by float64
+ *     brute force.
  */
 #ifndef G4_ORACLE_H
 #define G4_ORACLE_H
@@ -152,6 +161,16 @@ int       or_forward_inject_q8(or_model *m, int token, int pos, int lm_mode, con
  * or_forward_inject), without the rest of the layer; q8_in (nullable) as
  * or_forward_inject_q8 */
 int       or_forward_inject_kv(or_model *m, int token, int pos, const float *x_in, const or_q8K *q8_in);
+/* Pieces of forward() for checks against a composition of the reference's
+ * own functions: the embedding and build_ple of a token (m->x, m->ple);
+ * one layer from an injected input (its intermediates stay in the state
+ * buffers); the final norm + logits_tied from an injected x. */
+int       or_embed(or_model *m, int token, int pos);
+int       or_layer_inject(or_model *m, int token, int pos, int layer, const float *x_in, float *x_out);
+int       or_lm_head_inject(or_model *m, const float *x_in);
+/* a state buffer by name: x, xb2, q, k, v, q_out, ple, ple_ctx, ple_gate,
+ * hb, hb2, logits (main.c:694-701); NULL for other names */
+float    *or_model_state(or_model *m, const char *name);
 const float *or_model_logits(const or_model *m);
 const float *or_model_x(const or_model *m);
 /* Per-layer fingerprints captured during the last forward (sum,l2,max per layer

@@ -98,6 +98,10 @@ class Oracle:
             "or_forward_inject_kv": (C.c_int, [VP, C.c_int, C.c_int, VP, VP]),
             "or_model_q8_rec": (VP, [VP]),
             "or_model_kv_source": (C.c_int, [VP, C.c_int]),
+            "or_embed": (C.c_int, [VP, C.c_int, C.c_int]),
+            "or_layer_inject": (C.c_int, [VP, C.c_int, C.c_int, C.c_int, VP, VP]),
+            "or_lm_head_inject": (C.c_int, [VP, VP]),
+            "or_model_state": (C.POINTER(C.c_float), [VP, C.c_char_p]),
             "or_model_kv": (C.POINTER(C.c_float), [VP, C.c_int, C.c_int]),
         }
         for name, (res, args) in sig.items():
@@ -229,6 +233,32 @@ class OracleModel:
         raw = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), (n * Q8K_DTYPE.itemsize,))
         return raw.copy().view(Q8K_DTYPE).reshape(self.n_layers, Q8_SLOTS, Q8_SLOT_BLOCKS)
 
+    def embed(self, token: int, pos: int) -> None:
+        """embedding and build_ple of a token (state x and ple)"""
+        if self.o.L.or_embed(self.h, token, pos) != 0:
+            raise RuntimeError("or_embed failed")
+
+    def layer_inject(self, token: int, pos: int, layer: int, x_in: np.ndarray) -> np.ndarray:
+        """one layer from an injected input; its intermediates stay in state()"""
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        out = np.empty(self.dim, np.float32)
+        if self.o.L.or_layer_inject(self.h, token, pos, layer, _ptr(x_in), _ptr(out)) != 0:
+            raise RuntimeError("or_layer_inject failed")
+        return out
+
+    def lm_head_inject(self, x_in: np.ndarray) -> np.ndarray:
+        x_in = np.ascontiguousarray(x_in, np.float32)
+        if self.o.L.or_lm_head_inject(self.h, _ptr(x_in)) != 0:
+            raise RuntimeError("or_lm_head_inject failed")
+        return self.logits()
+
+    def state(self, name: str, n: int) -> np.ndarray:
+        """copy of the first n floats of a state buffer"""
+        p = self.o.L.or_model_state(self.h, name.encode())
+        if not p:
+            raise ValueError(name)
+        return np.ctypeslib.as_array(p, (n,)).copy()
+
     def kv_source(self, layer: int) -> int:
         """the layer whose KV cache `layer` reads (main.c:739-746)"""
         return int(self.o.L.or_model_kv_source(self.h, layer))
@@ -324,6 +354,19 @@ class Ref:
             "ref_is_swa_layer": (C.c_int, [C.c_int, C.c_int, C.c_int]),
             "ref_kv_source_for_layer": (C.c_int, [C.c_int, C.c_int, C.c_int]),
             "ref_layer_head_dim": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+            "ref_model_open": (VP, [VP, C.c_size_t]),
+            "ref_model_config": (None, [VP, VP, VP, VP]),
+            "ref_model_is_swa": (C.c_int, [VP, C.c_int]),
+            "ref_model_kv_source": (C.c_int, [VP, C.c_int]),
+            "ref_model_tensor": (VP, [VP, C.c_char_p, VP]),
+            "ref_tok_specials": (None, [VP, VP]),
+            "ref_tok_score": (C.c_float, [VP, C.c_int]),
+            "ref_tok_lookup": (C.c_int, [VP, C.c_char_p, C.c_int]),
+            "ref_bpe_encode": (C.c_int, [VP, C.c_char_p, C.c_int, VP]),
+            "ref_gemma_text": (C.c_int, [VP, C.c_char_p, VP]),
+            "ref_chat_encode": (C.c_int, [VP, C.c_char_p, C.c_int, VP]),
+            "ref_hidden_stats": (None, [VP, C.c_int, VP, VP, VP]),
+            "ref_kv_cache_offset": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)

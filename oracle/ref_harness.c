@@ -102,3 +102,81 @@ int ref_layer_head_dim(int n_layers, int swa_pattern, int hd_swa, int hd_full, i
     c.head_dim_full = hd_full;
     return layer_head_dim(&c, l);
 }
+
+/* ---- GGUF reader and weight loading, main.c:778-966, 1318-1400 ---------- */
+/* The reference's own parse_gguf + init_tokenizer + load_weights over a GGUF
+ * image held in memory (borrowed).  Returns the reference's Model. */
+void *ref_model_open(const void *data, size_t size) {
+    Model *m = (Model *)calloc(1, sizeof(Model));
+    m->fdata = (uint8_t *)data;
+    m->fsz = size;
+    m->fd = -1;
+    char **merges = NULL;
+    int n_merges = 0;
+    parse_gguf(m, &merges, &n_merges);
+    init_tokenizer(&m->tok, merges, n_merges);
+    load_weights(m);
+    return m;
+}
+
+/* i: dim, hidden, n_layers, n_heads, n_kv, vocab, max_seq, ple_dim, window,
+ * shared_kv, swa_pattern, hd_swa, hd_full, rot_swa, rot_full; f: theta,
+ * theta_swa, eps, softcap; doff: the data offset */
+void ref_model_config(const void *mp, int *i, float *f, unsigned long long *doff) {
+    const Model *m = (const Model *)mp;
+    const Config *c = &m->cfg;
+    const int v[15] = {c->dim, c->hidden_dim, c->n_layers, c->n_heads, c->n_kv_heads, c->vocab_size, c->max_seq,
+                       c->ple_dim, c->sliding_window, c->shared_kv_layers, c->swa_pattern, c->head_dim_swa,
+                       c->head_dim_full, c->n_rot_swa, c->n_rot_full};
+    memcpy(i, v, sizeof v);
+    f[0] = c->rope_theta; f[1] = c->rope_theta_swa; f[2] = c->norm_eps; f[3] = c->logit_softcapping;
+    *doff = m->doff;
+}
+
+int ref_model_is_swa(const void *mp, int l) { return is_swa_layer(&((const Model *)mp)->cfg, l); }
+int ref_model_kv_source(const void *mp, int l) { return kv_source_for_layer(&((const Model *)mp)->cfg, l); }
+
+const void *ref_model_tensor(void *mp, const char *name, int *type) {
+    int t = -1;
+    const void *p = find_tensor((Model *)mp, name, &t);
+    if (type) *type = t;
+    return p;
+}
+
+/* ---- tokenizer, main.c:968-1312 ---------------------------------------- */
+/* bos, eos, eot, add_space_prefix, turn_start, turn_end, turn_user,
+ * turn_model, turn_system, think, channel, channel_thought, channel_end */
+void ref_tok_specials(const void *mp, int *out) {
+    const Tok *tk = &((const Model *)mp)->tok;
+    const int v[13] = {tk->bos, tk->eos, tk->eot, tk->add_space_prefix, tk->turn_start, tk->turn_end, tk->turn_user,
+                       tk->turn_model, tk->turn_system, tk->think, tk->channel, tk->channel_thought, tk->channel_end};
+    memcpy(out, v, sizeof v);
+}
+float ref_tok_score(const void *mp, int id) { return ((const Model *)mp)->tok.scores[id]; }
+int ref_tok_lookup(void *mp, const char *s, int len) { return tok_lookup(&((Model *)mp)->tok, s, len); }
+/* gemma_bpe_encode of raw bytes; returns the count */
+int ref_bpe_encode(void *mp, const char *text, int len, int *out) {
+    int n = 0;
+    int *t = gemma_bpe_encode(&((Model *)mp)->tok, text, len, &n);
+    memcpy(out, t, (size_t)n * sizeof(int));
+    free(t);
+    return n;
+}
+/* append_gemma_text (line split, escape, BPE); returns the count */
+int ref_gemma_text(void *mp, const char *text, int *out) {
+    int n = 0;
+    append_gemma_text(&((Model *)mp)->tok, out, &n, text);
+    return n;
+}
+/* chat_encode of one user prompt (with the thinking system turn if asked) */
+int ref_chat_encode(void *mp, const char *prompt, int thinking, int *out) {
+    int n = 0;
+    int *t = chat_encode(&((Model *)mp)->tok, prompt, thinking, &n);
+    memcpy(out, t, (size_t)n * sizeof(int));
+    free(t);
+    return n;
+}
+
+/* ---- fingerprints, main.c:1811-1836 ----------------------------------------- */
+void ref_hidden_stats(const float *v, int n, float *sum, float *l2, float *amax) { hidden_stats(v, n, sum, l2, amax); }
+size_t ref_kv_cache_offset(int layer, int pos, int max_seq) { return kv_cache_offset(layer, pos, 0, max_seq); }
