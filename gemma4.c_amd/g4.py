@@ -22,6 +22,8 @@ G4_OK, G4_ERR_ARG, G4_ERR_TYPE, G4_ERR_HIP, G4_ERR_NOMEM, G4_ERR_STATE, G4_ERR_N
 # engine trace: quantization points per layer (engine.h G4E_Q8_SLOT_*) and
 # elements per traced Q8_K vector
 Q8_SLOTS, Q8_SLOT_ELEMS = 5, 4096
+# layer-0 fingerprint tags (engine.h G4E_FP_*), as dump_kv_fingerprint names them
+FP_TAGS = ("attn_norm", "K_pre_norm", "K_pre_rope", "K_store", "K_read0", "K_readN", "q_out")
 F32, F16, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 12, 13, 14, 30
 
 VP, I, SZ, F = C.c_void_p, C.c_int, C.c_size_t, C.c_float
@@ -132,6 +134,7 @@ _ENGINE_SIGS = {
     "g4e_set_trace": (I, [VP, I]),
     "g4e_layer_x": (C.POINTER(F), [VP]),
     "g4e_layer_q8": (VP, [VP]),
+    "g4e_kv_fingerprint": (I, [VP, VP, VP]),
     "g4e_generate_greedy": (I, [VP, VP, I, I, VP, C.POINTER(C.c_double), C.POINTER(C.c_double), I]),
     "g4e_decode_steps": (I, [VP, I, I, I, I, VP, C.POINTER(C.c_double)]),
     "g4e_generate": (I, [VP, VP, I, I, F, F, I, F, I, C.c_uint64, VP, C.POINTER(C.c_double),
@@ -433,6 +436,14 @@ class Engine:
         self.E.check(self.E.L.g4e_hidden_stats(self.h, out.ctypes.data))
         return out
 
+    def kv_fingerprint(self):
+        """layer-0 dump_kv_fingerprint records of the last dump: ((7, 7)
+        floats: per tag sum, l2, max, v0..v3; have[7])"""
+        out = np.zeros((7, 7), np.float32)
+        have = np.zeros(7, np.int32)
+        self.E.check(self.E.L.g4e_kv_fingerprint(self.h, out.ctypes.data, have.ctypes.data))
+        return out, have.astype(bool)
+
     def set_f32_matmul(self, on: bool) -> None:
         """Q4_K/Q5_K through dequantized fp32 weights (the reference's
         --f32-matmul) instead of Q8_K integer dots."""
@@ -462,3 +473,124 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+
+class Vocab:
+    """The engine's text path (host/text.h) over a GGUF's tokenizer metadata."""
+
+    def __init__(self, path: str):
+        self.E = EngineLib.get()
+        L = self.E.L
+        for name, (res, args) in _TEXT_SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        h = VP()
+        rc = L.g4t_open_file(os.fsencode(path), C.byref(h))
+        if rc:
+            raise G4Error(rc, L.g4t_last_error().decode())
+        self.L, self.h = L, h.value
+        self.size = L.g4t_size(self.h)
+
+    def _check(self, rc: int) -> int:
+        if rc < 0:
+            raise G4Error(rc, self.L.g4t_last_error().decode())
+        return rc
+
+    def specials(self) -> list[int]:
+        out = np.zeros(13, np.int32)
+        self.L.g4t_specials(self.h, out.ctypes.data)
+        return [int(v) for v in out]
+
+    def score(self, i: int) -> float:
+        return float(self.L.g4t_score(self.h, i))
+
+    def lookup(self, piece: bytes) -> int:
+        return int(self.L.g4t_lookup(self.h, piece, len(piece)))
+
+    def encode_raw(self, data: bytes, cap: int = 1 << 16) -> list[int]:
+        out = np.zeros(cap, np.int32)
+        n = self._check(self.L.g4t_encode_raw(self.h, data, len(data), out.ctypes.data, cap))
+        return [int(v) for v in out[:n]]
+
+    def encode_text(self, text: bytes, cap: int = 1 << 16) -> list[int]:
+        out = np.zeros(cap, np.int32)
+        n = self._check(self.L.g4t_encode_text(self.h, text, out.ctypes.data, cap))
+        return [int(v) for v in out[:n]]
+
+    def chat_encode(self, msgs: list[tuple[int, bytes]], thinking: bool, cap: int = 8192) -> list[int]:
+        texts = (C.c_char_p * max(len(msgs), 1))(*[t for _, t in msgs])
+        roles = np.array([r for r, _ in msgs] or [0], np.int32)
+        out = np.zeros(max(cap, 1), np.int32)
+        n = self._check(self.L.g4t_chat_encode(self.h, texts, roles.ctypes.data, len(msgs), int(thinking),
+                                               out.ctypes.data, cap))
+        return [int(v) for v in out[:n]]
+
+    def decode(self, toks, start: int = 0, end: int | None = None, cap: int = 1 << 20) -> bytes:
+        t = np.ascontiguousarray(toks, np.int32)
+        end = t.size if end is None else end
+        buf = C.create_string_buffer(cap)
+        n = self._check(self.L.g4t_decode(self.h, t.ctypes.data, start, end, buf, cap))
+        return buf.raw[:n]
+
+    def split_response(self, toks) -> tuple[int, int, int]:
+        t = np.ascontiguousarray(toks, np.int32)
+        a, b, c = C.c_int(), C.c_int(), C.c_int()
+        self.L.g4t_split_response(self.h, t.ctypes.data, t.size, C.byref(a), C.byref(b), C.byref(c))
+        return a.value, b.value, c.value
+
+    def is_special(self, i: int) -> bool:
+        return bool(self.L.g4t_is_special(self.h, i))
+
+    def close(self) -> None:
+        if self.h:
+            self.L.g4t_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class TextStream:
+    """g4t_stream: the thinking/answer state machine of generation."""
+
+    class _S(C.Structure):
+        _fields_ = [("v", VP)] + [(n, C.c_int) for n in ("thinking", "show", "budget", "mode", "saw_thought",
+                                                         "saw_answer", "skipping_label", "thinking_tokens",
+                                                         "budget_hit")]
+
+    def __init__(self, vocab: Vocab, thinking: bool, show: bool, budget: int):
+        self.v = vocab
+        self.s = TextStream._S()
+        vocab.L.g4t_stream_init(C.byref(self.s), vocab.h, int(thinking), int(show), budget)
+
+    def force(self) -> int:
+        return int(self.v.L.g4t_stream_force(C.byref(self.s)))
+
+    def push(self, tok: int) -> bytes:
+        buf = C.create_string_buffer(4096)
+        n = self.v.L.g4t_stream_push(C.byref(self.s), tok, buf, 4096)
+        return buf.raw[:n]
+
+
+_TEXT_SIGS = {
+    "g4t_last_error": (C.c_char_p, []),
+    "g4t_open_file": (I, [C.c_char_p, C.POINTER(VP)]),
+    "g4t_close": (None, [VP]),
+    "g4t_size": (I, [VP]),
+    "g4t_specials": (None, [VP, VP]),
+    "g4t_score": (F, [VP, I]),
+    "g4t_lookup": (I, [VP, C.c_char_p, I]),
+    "g4t_encode_raw": (I, [VP, C.c_char_p, I, VP, I]),
+    "g4t_encode_text": (I, [VP, C.c_char_p, VP, I]),
+    "g4t_chat_encode": (I, [VP, VP, VP, I, I, VP, I]),
+    "g4t_is_special": (I, [VP, I]),
+    "g4t_decode": (I, [VP, VP, I, I, C.c_char_p, SZ]),
+    "g4t_split_response": (None, [VP, VP, I, VP, VP, VP]),
+    "g4t_stream_init": (None, [VP, VP, I, I, I]),
+    "g4t_stream_force": (I, [VP]),
+    "g4t_stream_push": (I, [VP, I, C.c_char_p, SZ]),
+}

@@ -125,6 +125,14 @@ int g4e_set_prefill_chunk(g4e_model *m, int tokens);
  * l) and 2 + 2l (end of layer l). */
 int g4e_set_dump_hidden_at(g4e_model *m, int pos);
 int g4e_hidden_stats(g4e_model *m, float *out);
+/* The layer-0 dump_kv_fingerprint records of the same dump (main.c:1829-
+ * 1836, 1880-1951): per tag sum, l2, max (hidden_stats) and the first four
+ * values v0..v3, 7 floats, in G4E_FP_* order; have[t] = 0 where the tag was
+ * not recorded (K_readN at pos 0, K_read0 once a sliding-window ring has
+ * overwritten position 0). */
+enum { G4E_FP_ATTN_NORM = 0, G4E_FP_K_PRE_NORM, G4E_FP_K_PRE_ROPE, G4E_FP_K_STORE, G4E_FP_K_READ0, G4E_FP_K_READN,
+       G4E_FP_Q_OUT, G4E_FP_TAGS };
+int g4e_kv_fingerprint(g4e_model *m, float *out, int *have);
 /* SHA-256 of a file as 64 lowercase hex digits (hex[64] = 0), and the
  * `sha256sum --check` of the model download (gemma4-4b/Makefile `model`,
  * design.md:107-117): the line of sumfile naming path's base name must carry
@@ -140,6 +148,20 @@ int g4e_set_f32_matmul(g4e_model *m, int on);
 int g4e_kv_info(const g4e_model *m, int layer, int out[2]);
 /* copy slots slot0..slot0+nslots-1 of the layer's K and V caches to the host */
 int g4e_read_kv(g4e_model *m, int layer, int slot0, int nslots, float *k, float *v);
+
+/* generate() one step at a time (main.c:2366-2470), for hosts that decide
+ * between steps (forced tokens, the thinking budget, logit dumps):
+ * g4e_gen_begin resets the generated-token history and seeds the sampler
+ * (seed 0 -> 1).  g4e_gen_step runs forward(token, pos) with logits, then,
+ * unless the host forces a token (forced >= 0: no draw is taken, as the
+ * reference skips sample_token), the repetition penalty over the tokens
+ * generated so far and sample_token (temp <= 0: first-index argmax) on the
+ * device; the token is appended to that history and returned in next (the
+ * logits stay readable with g4e_read_logits).  The prompt goes through
+ * g4e_prefill first. */
+int g4e_gen_begin(g4e_model *m, uint64_t seed);
+int g4e_gen_step(g4e_model *m, int token, int pos, float temp, float topp, int topk, float penalty, int penalty_last_n,
+                 int forced, int use_graph, int *next);
 
 #ifdef __cplusplus
 }

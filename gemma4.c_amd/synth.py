@@ -187,6 +187,8 @@ class ModelShape:
     rope_freqs: bool = False      # include a rope_freqs.weight tensor
     types: tuple = ()             # (glob over tensor names, type) overrides, first match wins
     zeros: tuple = ()             # globs over tensor names whose bytes are all zero
+    pieces: tuple = ()            # tokenizer pieces (default: <t0>.. placeholders) ...
+    merges: tuple = ()            # ... and merges ("a b") for a model that can tokenize text
 
     def is_swa(self, l: int) -> bool:
         return (l % self.swa_pattern) < (self.swa_pattern - 1)
@@ -287,8 +289,11 @@ def model_kvs(s: ModelShape) -> list[bytes]:
         _kv(a + "attention.sliding_window_pattern", GV_ARR,
             (GV_BOOL, [1 if s.is_swa(l) else 0 for l in range(s.n_layers)])),
         _kv("tokenizer.ggml.eos_token_id", GV_U32, 106 if s.vocab > 106 else s.vocab - 1),
-        _kv("tokenizer.ggml.tokens", GV_ARR, (GV_STR, [f"<t{i}>" for i in range(s.vocab)])),
+        _kv("tokenizer.ggml.tokens", GV_ARR, (GV_STR, list(s.pieces) + [f"<t{i}>" for i in range(len(s.pieces),
+                                                                                                 s.vocab)])),
     ]
+    if s.merges:
+        kv.append(_kv("tokenizer.ggml.merges", GV_ARR, (GV_STR, list(s.merges))))
     return kv
 
 
@@ -317,3 +322,60 @@ def e4b_gguf(seed: int = 4) -> str:
         write_model_gguf(tmp, E4B, seed)
         os.replace(tmp, path)
     return path
+
+
+# ---------------------------------------------------------------------------
+# Synthetic tokenizer vocabularies (tokenizer.ggml.* metadata only)
+# ---------------------------------------------------------------------------
+SP = "▁"   # the escaped space of Gemma pieces
+
+
+def escape_line(line: str, prefix: bool) -> str:
+    """a text line as the tokenizer sees it: spaces as U+2581, and one
+    leading when the vocabulary asks for a space prefix"""
+    s = line.replace(" ", SP)
+    return (SP + s) if (prefix and line) else s
+
+
+def bpe_train(lines: list[str], n_merges: int, prefix: bool) -> list[tuple[str, str]]:
+    """Merges learned greedily from the escaped lines: the most frequent
+    adjacent pair first (ties: the smallest pair)."""
+    seqs = [list(escape_line(l, prefix)) for l in lines if l]
+    merges = []
+    for _ in range(n_merges):
+        counts: dict[tuple[str, str], int] = {}
+        for s in seqs:
+            for a, b in zip(s, s[1:]):
+                counts[(a, b)] = counts.get((a, b), 0) + 1
+        if not counts:
+            break
+        best = min(counts, key=lambda p: (-counts[p], p))
+        merges.append(best)
+        for i, s in enumerate(seqs):
+            out, j = [], 0
+            while j < len(s):
+                if j + 1 < len(s) and (s[j], s[j + 1]) == best:
+                    out.append(s[j] + s[j + 1])
+                    j += 2
+                else:
+                    out.append(s[j])
+                    j += 1
+            seqs[i] = out
+    return merges
+
+
+def write_vocab_gguf(path: str, pieces: list[str | bytes], merges: list[str] | None = None,
+                     scores: list[float] | None = None, bos: int = 2, eos: int = 106,
+                     add_space_prefix: bool | None = None) -> int:
+    """A GGUF that holds only tokenizer metadata (no tensors)."""
+    kvs = [_kv("tokenizer.ggml.model", GV_STR, "gemma4"),
+           _kv("tokenizer.ggml.tokens", GV_ARR, (GV_STR, pieces)),
+           _kv("tokenizer.ggml.bos_token_id", GV_U32, bos),
+           _kv("tokenizer.ggml.eos_token_id", GV_U32, eos)]
+    if scores is not None:
+        kvs.append(_kv("tokenizer.ggml.scores", GV_ARR, (GV_F32, list(scores))))
+    if merges is not None:
+        kvs.append(_kv("tokenizer.ggml.merges", GV_ARR, (GV_STR, merges)))
+    if add_space_prefix is not None:
+        kvs.append(_kv("tokenizer.ggml.add_space_prefix", GV_BOOL, int(add_space_prefix)))
+    return write_gguf(path, kvs, [], seed=0)

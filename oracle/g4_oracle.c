@@ -797,7 +797,18 @@ struct or_model {
      * or_forward_inject_q8 runs) replaces them before use */
     or_q8K *q8_rec;
     const or_q8K *q8_inj;
+    /* layer-0 dump_kv_fingerprint records of the last forward (OR_FP_*):
+     * sum, l2, max, v0..v3 */
+    float fp[OR_FP_TAGS * 7];
+    int fp_have[OR_FP_TAGS];
 };
+
+/* dump_kv_fingerprint (main.c:1829-1836) into tag t */
+static void fp_tag(or_model *m, int t, const float *v, int n) {
+    or_hidden_stats(v, n, &m->fp[7 * t], &m->fp[7 * t + 1], &m->fp[7 * t + 2]);
+    for (int i = 0; i < 4; i++) m->fp[7 * t + 3 + i] = i < n ? v[i] : 0.0f;
+    m->fp_have[t] = 1;
+}
 
 typedef struct { const uint8_t *d; uint64_t p, size; int bad; } or_rd;
 
@@ -1062,6 +1073,10 @@ const float *or_model_attn_stats(const or_model *m) { return m->astats; }
 const float *or_model_layer_x(const or_model *m) { return m->layer_x; }
 const or_q8K *or_model_q8_rec(const or_model *m) { return m->q8_rec; }
 int or_model_kv_source(const or_model *m, int layer) { return kv_source(m, layer); }
+const float *or_model_fingerprint(const or_model *m, int *have) {
+    if (have) memcpy(have, m->fp_have, sizeof m->fp_have);
+    return m->fp;
+}
 
 float *or_model_kv(or_model *m, int layer, int which) {
     if (layer < 0 || layer >= OR_N_LAYER_KV || layer >= m->n_layers) return NULL;
@@ -1113,12 +1128,15 @@ static int layer_kv(or_model *m, int l, int pos, int q8_ready) {
     const float *ff = swa ? NULL : m->rope_freqs;
     if (or_mm(m->k, m->xb2, m->wk[l].p, dim, kv_dim, m->wk[l].type, m->q8, q8_ready)) return -1;
     if (or_mm(m->v, m->xb2, m->wv[l].p, dim, kv_dim, m->wv[l].type, m->q8, q8_ready)) return -1;
+    if (l == 0) fp_tag(m, OR_FP_K_PRE_NORM, m->k, kv_dim);           /* main.c:1893-1894 */
     or_rmsnorm_head_inplace(m->k, m->k_norm[l], nkv, hd, m->eps);
     or_rmsnorm_head_noweight_inplace(m->v, nkv, hd, m->eps);
+    if (l == 0) fp_tag(m, OR_FP_K_PRE_ROPE, m->k, kv_dim);           /* main.c:1897-1898 */
     or_apply_rope_neox(m->k, nkv, hd, n_rot, pos, base, 1.0f, ff);
     const size_t off = ((size_t)l * m->max_seq + pos) * OR_MAX_KV_DIM;
     memcpy(m->kc + off, m->k, (size_t)kv_dim * sizeof(float));
     memcpy(m->vc + off, m->v, (size_t)kv_dim * sizeof(float));
+    if (l == 0) fp_tag(m, OR_FP_K_STORE, m->k, kv_dim);              /* main.c:1905-1906 */
     if (l == 0) {
         float s, q2, a;
         or_hidden_stats(m->k, kv_dim, &s, &q2, &a);
@@ -1140,6 +1158,10 @@ static int layer_step(or_model *m, int l, int pos, float *x_before) {
     const float *ff = swa ? NULL : m->rope_freqs;
     memcpy(x_before, m->x, (size_t)dim * sizeof(float));
     or_rmsnorm(m->xb2, m->x, m->attn_norm[l], dim, m->eps);
+    if (l == 0) {
+        memset(m->fp_have, 0, sizeof m->fp_have);
+        fp_tag(m, OR_FP_ATTN_NORM, m->xb2, dim);                     /* main.c:1880-1881 */
+    }
     const int q8_att = q8_point(m, l, OR_Q8_SLOT_ATTN, m->xb2, dim, m->wq[l].type);
     if (or_mm(m->q, m->xb2, m->wq[l].p, dim, q_dim, m->wq[l].type, m->q8, q8_att)) return -1;
     or_rmsnorm_head_inplace(m->q, m->q_norm[l], nh, hd, m->eps);
@@ -1151,11 +1173,17 @@ static int layer_step(or_model *m, int l, int pos, float *x_before) {
     if (swa) { t_start = pos + 1 - m->window; if (t_start < 0) t_start = 0; }
     const int nwin = pos + 1 - t_start;
     (void)src_hd;
+    if (l == 0) {                                                    /* main.c:1916-1921 */
+        const int kvd0 = nkv * layer_hd(m, 0);
+        fp_tag(m, OR_FP_K_READ0, m->kc, kvd0);
+        if (pos > 0) fp_tag(m, OR_FP_K_READN, m->kc + (size_t)pos * OR_MAX_KV_DIM, kvd0);
+    }
     const float *kc0 = m->kc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
     const float *vc0 = m->vc + (size_t)src * m->max_seq * OR_MAX_KV_DIM;
     or_attn_decode(m->q, kc0, vc0, OR_MAX_KV_DIM, t_start, nwin, nh, nkv, hd, 1.0f, m->att, m->q_out);
     if (l == 0) {
         float s, q2, a;
+        fp_tag(m, OR_FP_Q_OUT, m->q_out, q_dim);
         or_hidden_stats(m->q_out, q_dim, &s, &q2, &a);
         m->stats[(size_t)m->n_layers * 3 + 3] = s;
         m->stats[(size_t)m->n_layers * 3 + 4] = q2;

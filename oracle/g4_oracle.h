@@ -187,6 +187,12 @@ enum { OR_Q8_SLOT_ATTN = 0, OR_Q8_SLOT_O, OR_Q8_SLOT_FFN, OR_Q8_SLOT_INP_GATE, O
 #define OR_Q8_SLOT_BLOCKS 16
 /* the oracle's own Q8_K of every slot in the last forward (n_layers x slots) */
 const or_q8K *or_model_q8_rec(const or_model *m);
+/* Layer-0 dump_kv_fingerprint records of the last forward (main.c:1829-1836,
+ * 1880-1951): per tag sum, l2, max, v0..v3; have[t] = 0 for a tag the last
+ * forward did not record (K_readN at pos 0). */
+enum { OR_FP_ATTN_NORM = 0, OR_FP_K_PRE_NORM, OR_FP_K_PRE_ROPE, OR_FP_K_STORE, OR_FP_K_READ0, OR_FP_K_READN,
+       OR_FP_Q_OUT, OR_FP_TAGS };
+const float *or_model_fingerprint(const or_model *m, int *have);
 /* the layer whose KV cache layer l reads (itself, or donor 22/23), main.c:739-746 */
 int or_model_kv_source(const or_model *m, int layer);
 /* the K (which 0) or V (1) cache of a storing layer: max_seq rows of

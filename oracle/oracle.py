@@ -98,6 +98,7 @@ class Oracle:
             "or_forward_inject_kv": (C.c_int, [VP, C.c_int, C.c_int, VP, VP]),
             "or_model_q8_rec": (VP, [VP]),
             "or_model_kv_source": (C.c_int, [VP, C.c_int]),
+            "or_model_fingerprint": (C.POINTER(C.c_float), [VP, VP]),
             "or_embed": (C.c_int, [VP, C.c_int, C.c_int]),
             "or_layer_inject": (C.c_int, [VP, C.c_int, C.c_int, C.c_int, VP, VP]),
             "or_lm_head_inject": (C.c_int, [VP, VP]),
@@ -259,6 +260,12 @@ class OracleModel:
             raise ValueError(name)
         return np.ctypeslib.as_array(p, (n,)).copy()
 
+    def kv_fingerprint(self):
+        """layer-0 fingerprints of the last forward: ((7 tags, 7) floats, have[7])"""
+        have = np.zeros(7, np.int32)
+        p = self.o.L.or_model_fingerprint(self.h, _ptr(have))
+        return np.ctypeslib.as_array(p, (7, 7)).copy(), have.astype(bool)
+
     def kv_source(self, layer: int) -> int:
         """the layer whose KV cache `layer` reads (main.c:739-746)"""
         return int(self.o.L.or_model_kv_source(self.h, layer))
@@ -367,6 +374,11 @@ class Ref:
             "ref_chat_encode": (C.c_int, [VP, C.c_char_p, C.c_int, VP]),
             "ref_hidden_stats": (None, [VP, C.c_int, VP, VP, VP]),
             "ref_kv_cache_offset": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+            "ref_tok_open": (VP, [VP, C.c_size_t]),
+            "ref_chat_encode_history": (C.c_int, [VP, VP, VP, C.c_int, C.c_int, VP, C.c_int]),
+            "ref_tokens_to_text": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, C.c_int]),
+            "ref_parse_response": (None, [VP, VP, C.c_int, VP, VP, VP, VP, C.c_int]),
+            "ref_is_special": (C.c_int, [VP, C.c_int]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)

@@ -180,3 +180,47 @@ int ref_chat_encode(void *mp, const char *prompt, int thinking, int *out) {
 /* ---- fingerprints, main.c:1811-1836 ----------------------------------------- */
 void ref_hidden_stats(const float *v, int n, float *sum, float *l2, float *amax) { hidden_stats(v, n, sum, l2, amax); }
 size_t ref_kv_cache_offset(int layer, int pos, int max_seq) { return kv_cache_offset(layer, pos, 0, max_seq); }
+
+/* the tokenizer alone: parse_gguf + init_tokenizer (no weights needed) */
+void *ref_tok_open(const void *data, size_t size) {
+    Model *m = (Model *)calloc(1, sizeof(Model));
+    m->fdata = (uint8_t *)data;
+    m->fsz = size;
+    m->fd = -1;
+    char **merges = NULL;
+    int n_merges = 0;
+    parse_gguf(m, &merges, &n_merges);
+    init_tokenizer(&m->tok, merges, n_merges);
+    return m;
+}
+/* chat_encode_history over texts[i] with roles[i] (0 user, 1 model) */
+int ref_chat_encode_history(void *mp, const char *const *texts, const int *roles, int n, int thinking, int *out,
+                            int max_toks) {
+    ChatHistory h;
+    chat_history_init(&h);
+    for (int i = 0; i < n; i++) chat_history_push(&h, roles[i] ? CHAT_ASSISTANT : CHAT_USER, texts[i]);
+    const int r = chat_encode_history(&((Model *)mp)->tok, &h, thinking, out, max_toks);
+    chat_history_free(&h);
+    return r;
+}
+/* tokens_to_text into out (cap bytes); returns the length */
+int ref_tokens_to_text(void *mp, const int *tokens, int start, int end, char *out, int cap) {
+    char *s = tokens_to_text(&((Model *)mp)->tok, tokens, start, end);
+    const int n = (int)strlen(s);
+    if (n < cap) memcpy(out, s, (size_t)n + 1);
+    free(s);
+    return n;
+}
+/* parse_response: (thinking, answer) texts, or thinking absent (-1 length) */
+void ref_parse_response(void *mp, const int *tokens, int n, char *think, int *think_len, char *answer, int *ans_len,
+                        int cap) {
+    char *t = NULL, *a = NULL;
+    parse_response(&((Model *)mp)->tok, tokens, n, &t, &a);
+    *think_len = t ? (int)strlen(t) : -1;
+    *ans_len = a ? (int)strlen(a) : -1;
+    if (t && *think_len < cap) memcpy(think, t, (size_t)*think_len + 1);
+    if (a && *ans_len < cap) memcpy(answer, a, (size_t)*ans_len + 1);
+    free(t);
+    free(a);
+}
+int ref_is_special(void *mp, int id) { return is_special(&((Model *)mp)->tok, id); }

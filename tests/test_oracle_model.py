@@ -431,3 +431,42 @@ def test_mm_f32_bruteforce(orc):
         want = W.astype(np.float64) @ x.astype(np.float64)
         mag = np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64))
         assert np.max(np.abs(o - want) / mag) < 1e-6
+
+
+def test_fingerprints_are_reference_stats(ref, orc, tiny):
+    """The oracle's layer-0 dump_kv_fingerprint records (main.c:1829-1836,
+    1880-1951) are the reference's hidden_stats and first four values of
+    the vectors the composition gives at those statements."""
+    rm = RefModel(ref, tiny)
+    cp = Compose(ref, rm)
+    om = OracleModel(orc, tiny, max_seq=16)
+    try:
+        toks = [7, 300, 12]
+        for pos, tok in enumerate(toks):
+            om.forward(tok, pos, 0)
+        pos, tok = 2, toks[2]
+        x = np.random.default_rng(11).standard_normal(rm.dim).astype(np.float32)
+        om.layer_inject(tok, pos, 0, x)
+        fp, have = om.kv_fingerprint()
+        hd = rm.hd(0)
+        m = rm
+        b = "blk.0."
+        xb2 = cp.rmsnorm(x, m.vec(b + "attn_norm.weight", m.dim))
+        q8 = cp.quantize(xb2)
+        k, _ = cp.mm(xb2, b + "attn_k.weight", m.dim, m.nkv * hd, q8)
+        kn = cp.head_norm(k, m.vec(b + "attn_k_norm.weight", hd), m.nkv, hd)
+        _, k_store, _ = cp.pre_attention(0, pos, x)
+        kc, _ = om.kv(0)
+        vecs = {0: xb2, 1: k, 2: kn, 3: k_store, 4: kc[0, :m.nkv * hd], 5: kc[pos, :m.nkv * hd],
+                6: om.state("q_out", m.nh * hd)}
+        assert have.all()
+        for t, v in vecs.items():
+            st = [np.zeros(1, np.float32) for _ in range(3)]
+            v = np.ascontiguousarray(v, np.float32)
+            ref.L.ref_hidden_stats(_p(v), v.size, *[_p(s) for s in st])
+            assert _bits_equal(fp[t, :3], np.concatenate(st)), t
+            assert _bits_equal(fp[t, 3:], v[:4]), t
+        om.forward(toks[0], 0, 0)
+        assert not om.kv_fingerprint()[1][5]       # K_readN is printed only at pos > 0
+    finally:
+        om.close()
