@@ -17,6 +17,9 @@ Workloads (synthetic inputs, generated from fixed seeds on the host):
           matrices on the matrix cores (seed 1)
   prefill_e2e  batched prompt prefill through the engine at the E4B shape:
           511 tokens in one chunk (seed 4); roofline on the Q6_K GEMM (V, FFN down)
+  attn    ISWA decode attention step (norms, RoPE, K/V append, attention):
+          sliding ring 512 and global T = 4096 / 32768 at head_dim 256 and 512
+          (seed 3); value: the global T=32768 hd 256 case
 
 Prints ONE JSON line.  `value` is whole-job throughput with inputs resident
 in HBM; `roofline` is the dominant kernel's algorithmic bytes over its average
@@ -45,10 +48,38 @@ METRIC = "decode tok/s at E4B shape (1 GPU); K-quant GEMV GB/s as % of HBM peak"
 
 
 def cpu_threads() -> int:
+    """OpenMP threads of the CPU leg: OMP_NUM_THREADS (16 on the GPU boxes,
+    the host-core share of one GPU there), else the usable cores."""
     v = os.environ.get("OMP_NUM_THREADS")
     if v and v.isdigit():
         return int(v)
-    return min(16, os.cpu_count() or 1)
+    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+
+
+def cpu_host() -> dict:
+    """lscpu's model, sockets and physical cores of the host, and the cores
+    this process may use"""
+    info = {"usable_cores": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(ln.split(":", 1) for ln in out.splitlines() if ":" in ln)
+        g = lambda k: kv.get(k, "").strip()
+        info["model"] = g("Model name")
+        sockets, cps = int(g("Socket(s)") or 0), int(g("Core(s) per socket") or 0)
+        info.update(sockets=sockets, physical_cores=sockets * cps, threads_per_core=int(g("Thread(s) per core") or 0))
+    except Exception as e:                     # lscpu absent: the usable cores alone
+        info["lscpu"] = f"unavailable ({e.__class__.__name__})"
+    return info
+
+
+def omp_threads(n: int) -> None:
+    """set the OpenMP team size of the CPU leg's later parallel regions"""
+    import ctypes
+    try:
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+    except OSError:
+        pass
 
 
 class Timer:
@@ -409,6 +440,112 @@ def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):
     return dict(roofline(algo, per, name), kernel=name, bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
 
 
+# ISWA decode attention (8 q / 2 kv heads): (name, positions read, head_dim,
+# ring slots, window, RoPE base, cache slots)
+ATTN_CASES = [("sliding, ring 512, hd 256", 512, 256, 512, 512, 1e4, 512),
+              ("global T=4096, hd 256", 4096, 256, 0, 0, 1e6, 4096),
+              ("global T=32768, hd 256", 32768, 256, 0, 0, 1e6, 32768),
+              ("global T=4096, hd 512", 4096, 512, 0, 0, 1e6, 4096),
+              ("global T=32768, hd 512", 32768, 512, 0, 0, 1e6, 32768)]
+ATTN_HEADLINE = 2
+
+
+def _attn_chunks(cap: int) -> int:
+    """chunk count the engine fixes for a cache of cap slots (engine.c attn_chunks)"""
+    G = min(max((cap + 31) // 32, 1), 128)
+    while (cap + G - 1) // G > 1024:
+        G += 1
+    return G
+
+
+def bench_attn(lib, g4, synth, args):
+    """ISWA decode attention, one layer's step: q/k norms, Neox RoPE, the
+    K/V append and softmax(q.K) V over the cache (g4_attn_decode_fused, the
+    engine's launch pair), N(0,1) inputs (seed 3).  Caches of every case
+    are rotated through >= 512 MB of copies so that the reads come from HBM.
+    value: KV GB/s of the global T=32768 hd 256 case; every case in config."""
+    L = lib.L
+    rng = np.random.default_rng(3)
+    nh, nkv, eps = 8, 2, 1e-6
+    cases = []
+    for name, T, hd, ring, window, theta, slots in ATTN_CASES:
+        kvd = nkv * hd
+        pos = T - 1 if ring == 0 else 1000                  # a sliding ring past its first wrap
+        host = rng.standard_normal((slots, kvd)).astype(np.float32)
+        kv_bytes = 2 * host.nbytes
+        ncp = max(2, -(-MALL_BYTES // kv_bytes))
+        caches = [(g4.DBuf.from_array(lib, host), g4.DBuf.from_array(lib, host)) for _ in range(ncp)]
+        del host
+        qr = g4.DBuf.from_array(lib, rng.standard_normal(nh * hd).astype(np.float32))
+        kr = g4.DBuf.from_array(lib, rng.standard_normal(kvd).astype(np.float32))
+        vr = g4.DBuf.from_array(lib, rng.standard_normal(kvd).astype(np.float32))
+        qn = g4.DBuf.from_array(lib, rng.uniform(0.8, 1.2, hd).astype(np.float32))
+        kn = g4.DBuf.from_array(lib, rng.uniform(0.8, 1.2, hd).astype(np.float32))
+        dpos = g4.DBuf.from_array(lib, np.array([pos, 0], np.int32))
+        tab = g4.DBuf(lib, hd * 4)
+        lib.g4_rope_table(tab.ptr, dpos.ptr, 0, hd, C.c_float(theta), C.c_float(1.0), None)
+        G = _attn_chunks(ring if ring else slots)
+        part = g4.DBuf(lib, L.g4_attn_part_bytes(nh, hd, G))
+        out = g4.DBuf(lib, nh * hd * 4)
+
+        def step(i, caches=caches, qr=qr, kr=kr, vr=vr, qn=qn, kn=kn, kvd=kvd, ring=ring, dpos=dpos,
+                 window=window, hd=hd, tab=tab, G=G, part=part, out=out):
+            kc, vc = caches[i % len(caches)]
+            L.g4_attn_decode_fused(qr.ptr, qn.ptr, kr.ptr, vr.ptr, kn.ptr, kc.ptr, vc.ptr, kc.ptr, vc.ptr, kvd, ring,
+                                   dpos.ptr, window, nh, nkv, hd, hd, tab.ptr, C.c_float(eps), C.c_float(1.0), G,
+                                   part.ptr, out.ptr, None)
+
+        ms = _time_steps(lib, step, args)
+        per = ms / 1e3 / args.steps
+        nwin = min(pos + 1, window) if window else pos + 1
+        algo = 2 * nwin * kvd * 4 + (2 * nh * hd + 2 * kvd) * 4
+        cases.append({"case": name, "positions": nwin, "chunks": G, "us": round(per * 1e6, 2),
+                      "GBps": round(algo / per / 1e9, 1), "frac": round(algo / per / 1e9 / HBM_PEAK_GBS, 4),
+                      "kv_bytes": 2 * nwin * kvd * 4, "copies_rotated": ncp})
+        _log(f"attention {name}: {per * 1e6:.2f} us, {algo / per / 1e9:.0f} GB/s")
+        del caches
+        lib.g4_sync()
+    h = cases[ATTN_HEADLINE]
+    res = {
+        "value": h["GBps"], "unit": "GB/s (KV read)", "higher_is_better": True, "ms_per_step": h["us"] / 1e3,
+        "dtype": "f32",
+        "config": {"workload": "ISWA decode attention step (q/k norms, Neox RoPE, K/V append, softmax(qK)V), 8 q / 2 "
+                               "kv heads, fp32 KV cache, N(0,1) inputs (seed 3); value: global T=32768 hd 256",
+                   "cases": cases},
+        "roofline": {"bound": "hbm", "achieved": h["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": h["frac"],
+                     "traffic": measured_traffic("attn_chunk_kernel<256,4> T=32768"),
+                     "kernel": "attn_chunk_kernel<256,4> + attn_merge_kernel<256> (global T=32768, hd 256)",
+                     "bytes_per_launch": h["kv_bytes"], "us_per_launch": h["us"]},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_attn_baseline()
+    return res
+
+
+def cpu_attn_baseline() -> dict:
+    """The attention block of main.c:1909-1950 as the oracle's plain loops
+    (per head q.K, softmax, p.V) over the global T=4096 hd 256 case."""
+    import oracle as orc_mod
+    orc = orc_mod.Oracle()
+    rng = np.random.default_rng(3)
+    T, hd, nh, nkv = 4096, 256, 8, 2
+    kc = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    orc.attn(q, kc, vc, nkv * hd, 0, T, nh, nkv, hd, 1.0)
+    ts = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end or len(ts) < 20:
+        t0 = time.perf_counter()
+        orc.attn(q, kc, vc, nkv * hd, 0, T, nh, nkv, hd, 1.0)
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(2 * T * nkv * hd * 4 / med / 1e9, 3), "unit": "GB/s (KV read)", "cores": 1,
+            "kind": "port", "host": cpu_host(),
+            "sample": f"oracle or_attn_decode (the attention block as plain loops, one thread) over the global "
+                      f"T=4096 hd 256 case, median of {len(ts)} runs"}
+
+
 def _log(msg: str) -> None:
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
@@ -485,40 +622,72 @@ def bench_decode(lib, g4, synth, args):
     res["decode_hbm_GBps"] = round(synth.decode_weight_bytes(synth.E4B) * tps / 1e9, 1)
     if not args.no_cpu:
         _log("CPU baseline (oracle forward)")
-        res["cpu_baseline"] = cpu_decode_baseline(path)
+        res["cpu_baseline"] = cpu_decode_baseline(path, (n_prompt - 1 + args.warmup, n_prompt - 1 + args.warmup
+                                                          + args.steps))
     return res
 
 
-def cpu_decode_baseline(path: str, steps: int = 6) -> dict:
+def cpu_decode_baseline(path: str, positions: tuple, steps: int = 4) -> dict:
     """The oracle's forward() (the C restatement of main.c:1838-2029, OpenMP)
-    on the same GGUF: a 4-token prompt, then `steps` greedy decode steps."""
+    on the same GGUF at the decode positions the GPU leg times: its caches
+    hold zeros there instead of a prompt's K/V, which costs the same
+    arithmetic (the attention spans the same windows); then one step on one
+    thread."""
     import oracle as orc_mod
     thr = cpu_threads()
-    om = orc_mod.OracleModel(orc_mod.Oracle(), path, max_seq=64)
-    prompt = np.array([2, 105, 9731, 107], np.int32)
-    toks, pf, dec = om.generate_greedy(prompt, steps)
+    p0 = positions[0]
+    om = orc_mod.OracleModel(orc_mod.Oracle(), path, max_seq=p0 + steps + 8)
+    om.forward(2, p0 - 1, 1)                                 # warm-up (page-in of the mapped weights)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        om.forward(2 + i, p0 + i, 1)
+    sec = (time.perf_counter() - t0) / steps
+    omp_threads(1)
+    t1 = time.perf_counter()
+    om.forward(3, p0 + steps, 1)
+    sec1 = time.perf_counter() - t1
+    omp_threads(thr)
     om.close()
-    n = max(len(toks), 1)
-    return {"value": round(n / dec, 3) if dec > 0 else None, "unit": "tok/s", "cores": thr, "kind": "port",
-            "sample": f"oracle forward() (C restatement of the reference, gcc -O3 -std=c11, OpenMP {thr} threads, "
-                      f"plain-loop sgemv): {n} greedy decode steps after a 4-token prompt on the same GGUF"}
+    return {"value": round(1.0 / sec, 3), "unit": "tok/s", "cores": thr, "kind": "port",
+            "tok_s_1_thread": round(1.0 / sec1, 4), "host": cpu_host(),
+            "sample": f"oracle forward() with logits (C restatement of the reference, gcc -O3 -std=c11, OpenMP {thr} "
+                      f"threads, plain-loop sgemv): {steps} decode steps at positions {p0}..{p0 + steps - 1} of the "
+                      f"same GGUF, then 1 step on 1 thread"}
+
+
+_STREAM = [None]    # the stream the kernel workloads run on (created in main)
 
 
 def _time_steps(lib, step, args) -> float:
+    """W eager warm-up launches, then the K timed launches captured as one
+    graph on the library stream and replayed: the host's launch cost stays
+    out of the timed region, which spans the kernels back to back (each
+    launch's fixed dependent-kernel gap included).  Returns milliseconds."""
+    if _STREAM[0] is not None:
+        lib.check(lib.L.g4_set_stream(_STREAM[0]))   # an engine may have left the library on its own stream
     for i in range(args.warmup):
         step(i)
     lib.g4_sync()
-    t = Timer(lib)
-    t.start()
+    g = C.c_void_p()
+    lib.check(lib.L.g4_graph_begin())
     for i in range(args.steps):
         step(i)
-    ms = t.stop_ms()
-    lib.g4_sync()
+    lib.check(lib.L.g4_graph_end(C.byref(g)))
+    try:
+        lib.check(lib.L.g4_graph_launch(g))       # first replay: instantiation costs out of the timing
+        lib.g4_sync()
+        t = Timer(lib)
+        t.start()
+        lib.check(lib.L.g4_graph_launch(g))
+        ms = t.stop_ms()
+        lib.g4_sync()
+    finally:
+        lib.L.g4_graph_destroy(g)
     return ms
 
 
 WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
-             "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e}
+             "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e, "attn": bench_attn}
 
 
 def main() -> int:
@@ -543,6 +712,10 @@ def main() -> int:
     import synth
     lib = g4.Lib.get()
     lib.init(0)
+    stream = C.c_void_p()
+    lib.check(lib.L.g4_stream_create(C.byref(stream)))
+    lib.check(lib.L.g4_set_stream(stream))      # the kernel workloads' launches are captured on it
+    _STREAM[0] = stream
     t0 = time.perf_counter()
     res = WORKLOADS[args.workload](lib, g4, synth, args)
     line = {"metric": METRIC, "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,

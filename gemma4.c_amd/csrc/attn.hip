@@ -737,23 +737,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     };
     const float* kbase = a.kc + (size_t)kvh * HD;
     const float* vbase = a.vc + (size_t)kvh * HD;
-    HVec<HD> kr[PPW], vr[PPW];
-    auto load_kv = [&](int r) {
+    // two register sets: round r + 1's rows load while round r is reduced
+    HVec<HD> kr[PPW], vr[PPW], kr2[PPW], vr2[PPW];
+    auto load_kv = [&](HVec<HD>* K, HVec<HD>* Vv, int r) {
 #pragma unroll
         for (int p = 0; p < PPW; p++) {
             const int i = min(r * NW * PPW + wave * PPW + p, cnt - 1);
             const int t = cb + i;   // position (position mode; prompt-chunk rows only)
             if (a.kchunk && t >= a.p0) {
                 const size_t off = (size_t)(t - a.p0) * a.kv_stride + (size_t)kvh * HD;
-                kr[p].load(a.kchunk + off, lane);
-                vr[p].load(a.vchunk + off, lane);
+                K[p].load(a.kchunk + off, lane);
+                Vv[p].load(a.vchunk + off, lane);
             } else {
-                kr[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
-                vr[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
+                K[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
+                Vv[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
             }
         }
     };
-    if (cnt > 0) load_kv(0);
+    if (cnt > 0) load_kv(kr, vr, 0);
     // the position (slot mode: not needed by the loads above)
     const int dpv = slotm ? *a.dpos : 0;
     __builtin_amdgcn_sched_barrier(0);   // the loads are in flight before anything waits
@@ -804,8 +805,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     for (int k = 0; k < LV; k++) jl |= ((lane & xbit(k)) ? 1 : 0) << (LV - 1 - k);
     const int hl = jl / PPW, pl = jl - hl * PPW;
     const bool counted = (lane & xfree(LV)) == 0;   // one lane of each score's copies
-    for (int r = 0; r < nrounds; r++) {
-        if (r > 0) load_kv(r);
+    auto round = [&](HVec<HD>* kr, HVec<HD>* vr, int r) {
         const int base = r * NW * PPW + wave * PPW;
         if (owner && tl >= base && tl < base + PPW) {
 #pragma unroll
@@ -847,6 +847,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
                     for (int i = 0; i < W; i++) o[h].v[k][i] = __builtin_fmaf(ph, vr[p].v[k][i], o[h].v[k][i]);
             }
+        }
+    };
+    // rounds in pairs over the two register sets; the next round's loads
+    // are issued unconditionally (a clamped round past the last one reloads
+    // rows already in cache) so that no branch separates them from their use
+    if (nrounds == 1) {
+        round(kr, vr, 0);                         // one round (sliding windows): no second set
+    } else {
+        for (int r = 0; r < nrounds; r += 2) {
+            load_kv(kr2, vr2, min(r + 1, nrounds - 1));
+            round(kr, vr, r);
+            load_kv(kr, vr, min(r + 2, nrounds - 1));
+            if (r + 1 < nrounds) round(kr2, vr2, r + 1);
         }
     }
 
@@ -897,14 +910,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
 
 // Merge of the G chunk partials of one q head: workgroup (h, slice) owns
 // 256 output dims.  Every load is issued first: each thread's dim of the
-// first kMergeReg chunks and the (max, sum) of the chunks it reduces; then
+// first MR chunks and the (max, sum) of the chunks it reduces; then
 // the chunk weights f_g = exp(max_g - M) and the total L = sum_g sum_g f_g
 // (through LDS), the thread's dim over the chunks (the rest of them, if G
 // is larger, streamed eight at a time) and, if asked, the Q8_K block of the
 // workgroup's 256 outputs.
-constexpr int kMergeReg = 32;
-
-template <int HD>
+// MR chunk rows per thread are loaded at once (clamped indices: loads under
+// a condition would wait for everything issued before them); the launcher
+// picks MR >= G up to 128.
+template <int HD, int MR>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     if (a.qrows) attn_query_row(a, true);
     __shared__ float fw[kMaxChunks];
@@ -915,9 +929,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     const float* ph = a.part + (size_t)h * G * (HD + 2);
     const int dd = slice * 256 + tid;
     const float* pd = ph + dd;
-    float v[kMergeReg];
+    float v[MR];
 #pragma unroll
-    for (int u = 0; u < kMergeReg; u++) v[u] = u < G ? pd[(size_t)u * (HD + 2)] : 0.0f;
+    for (int u = 0; u < MR; u++) v[u] = pd[(size_t)min(u, G - 1) * (HD + 2)];
     float mg[kMaxChunks / 256], lg[kMaxChunks / 256];
 #pragma unroll
     for (int k = 0; k < kMaxChunks / 256; k++) {
@@ -945,9 +959,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     L = block_sum(L, red + 4);   // its barrier also publishes fw
     float o = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kMergeReg; u++)
+    for (int u = 0; u < MR; u++)
         if (u < G) o = __builtin_fmaf(v[u], fw[u], o);
-    int g = kMergeReg;
+    int g = MR;
     for (; g + 8 <= G; g += 8) {
         float w8[8];
 #pragma unroll
@@ -984,6 +998,13 @@ void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
     else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
 }
 
+template <int HD>
+void launch_merge(const AttnArgs& a, const dim3& grid) {
+    if (a.G <= 16) hipLaunchKernelGGL((attn_merge_kernel<HD, 16>), grid, dim3(256), 0, g4_stream(), a);
+    else if (a.G <= 32) hipLaunchKernelGGL((attn_merge_kernel<HD, 32>), grid, dim3(256), 0, g4_stream(), a);
+    else hipLaunchKernelGGL((attn_merge_kernel<HD, 128>), grid, dim3(256), 0, g4_stream(), a);
+}
+
 int launch_attn(const AttnArgs& a) {
     const int kvm = a.n_heads / a.n_kv;
     const int zq = a.qrows > 0 ? a.qrows : 1;
@@ -994,10 +1015,10 @@ int launch_attn(const AttnArgs& a) {
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
         if (a.hd == 256) {
             launch_chunk<256>(a, kp, grid);
-            hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1, zq), dim3(256), 0, g4_stream(), a);
+            launch_merge<256>(a, dim3(a.n_heads, 1, zq));
         } else {
             launch_chunk<512>(a, kp, grid);
-            hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2, zq), dim3(256), 0, g4_stream(), a);
+            launch_merge<512>(a, dim3(a.n_heads, 2, zq));
         }
         return g4_check_launch("attn_chunk_kernel/attn_merge_kernel");
     }
@@ -1005,10 +1026,10 @@ int launch_attn(const AttnArgs& a) {
     const size_t lds = attn_lds(a.hd, kvm, a.q_norm != nullptr);
     if (a.hd == 256) {
         hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
-        hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.n_heads, 1), dim3(256), 0, g4_stream(), a);
+        launch_merge<256>(a, dim3(a.n_heads, 1));
     } else {
         hipLaunchKernelGGL(attn_decode_kernel<512>, grid, dim3(kAttnThreads), lds, g4_stream(), a);
-        hipLaunchKernelGGL(attn_merge_kernel<512>, dim3(a.n_heads, 2), dim3(256), 0, g4_stream(), a);
+        launch_merge<512>(a, dim3(a.n_heads, 2));
     }
     return g4_check_launch("attn_decode_kernel/attn_merge_kernel");
 }
