@@ -206,7 +206,8 @@ def bench_prefill(lib, g4, synth, args):
     matrices (Q, K, O, gate, up, inp_gate, proj) with pre-quantized Q8_K
     activations; a step is the seven launches.  Reports matrix-core
     throughput (2 * tokens * rows * n algorithmic ops) against the fp16 dense
-    peak, and the dominant launch (gate, 10240x2560) alone."""
+    peak (the kernel issues one fp16 MFMA flop per algorithmic flop, plus the
+    min sums' 1/32), and the dominant launch (gate, 10240x2560) alone."""
     m = 512
     rng = np.random.default_rng(1)
     mats = []
@@ -236,10 +237,10 @@ def bench_prefill(lib, g4, synth, args):
     per1 = ms1 / 1e3 / args.steps
     ops1 = 2.0 * m * d * n
     tf1 = ops1 / per1 / 1e12
-    name = "mm_batch_kq_kernel<Q4_K> 10240x2560, 512 tokens"
+    name = "mm_batch_kq32_kernel<Q4_K> 10240x2560, 512 tokens"
     res = {
         "value": round(m / per_step, 1), "unit": "tok/s (one layer's Q4_K GEMMs)", "higher_is_better": True,
-        "ms_per_step": ms / args.steps, "dtype": "u4 x int8 -> exact fp16 matrix products, fp32 combine",
+        "ms_per_step": ms / args.steps, "dtype": "u4 x int8 -> exact fp16 matrix products, fp32 block combine",
         "config": {"workload": "batched prefill GEMM: 512 tokens x one E4B SWA layer's Q4_K matrices "
                                "(Q 2048, K 512, O 2560<-2048, gate/up 10240, PLE 256/2560) (seed 1)",
                    "tokens": m, "layer_tflops": round(ops / per_step / 1e12, 2)},
@@ -252,15 +253,17 @@ def bench_prefill(lib, g4, synth, args):
     return res
 
 
-FP32_MFMA_PEAK_TFLOPS = 157.3     # MI355X dense fp32 matrix peak (the batched Q6_K / bf16 GEMM's instruction)
+Q6S_MFMA_PER_FLOP = 4     # fp16 MFMA flops the split Q6_K GEMM issues per algorithmic flop
 
 
 def bench_prefill_e2e(lib, g4, synth, args):
     """Batched prompt prefill through the engine at the E4B shape: a step is
     g4e_prefill of 511 tokens (chunk of 511: every layer's GEMMs, attention
     over the chunk's rows, norms, RoPE, appends, PLE).  The roofline kernel is
-    the one that takes most of the time, the Q6_K GEMM on the fp32 matrix
-    cores (FFN down and V), timed alone with HIP events."""
+    the one that takes most of the time, the Q6_K GEMM on split fp16
+    activations (FFN down and V), timed alone with HIP events; it issues four
+    fp16 MFMA flops per algorithmic flop (hi and lo activation terms against
+    the two exact halves of the split scale), reported as mfma_issued."""
     path = _gguf_e4b(synth)
     eng = g4.Engine(path, max_seq=1024)
     rng = np.random.default_rng(4)
@@ -273,39 +276,44 @@ def bench_prefill_e2e(lib, g4, synth, args):
         eng.prefill(prompt, 0)                 # returns after the work has completed
     sec = (time.perf_counter() - t0) / args.steps
     eng.close()
-    # the dominant kernel, mm_batch_f32_kernel<Q6_K> (V of the 24 storing
-    # layers and FFN down of all 42 over the chunk's rows), timed alone with
-    # HIP events in the engine's proportion of launches: 20 x V 512x2560,
-    # 4 x V 1024x2560, 42 x down 2560x10240 per step
+    # the dominant kernel, mm_batch_q6s_kernel (V of the 24 storing layers and
+    # FFN down of all 42 over the chunk's rows), timed alone with HIP events in
+    # the engine's proportion of launches: 20 x V 512x2560, 4 x V 1024x2560,
+    # 42 x down 2560x10240 per step, on activations split once per matrix
     shapes = [(2560, 512, 20), (2560, 1024, 4), (10240, 2560, 42)]
     mats = []
     for n, d, cnt in shapes:
         raw = synth.rand_q6K(rng, d, n)
         w = g4.upload_quant(lib, raw, g4.Q6_K, n, d)
         x = g4.DBuf.from_array(lib, rng.standard_normal((m, n)).astype(np.float32))
+        xs = g4.DBuf(lib, lib.L.g4_split_rows_bytes(n, m))
+        lib.g4_split_rows_f16(x.ptr, xs.ptr, n, m)
         out = g4.DBuf(lib, 4 * m * d)
-        mats.append((n, d, cnt, w, x, out))
+        mats.append((n, d, cnt, w, xs, out))
     L = lib.L
 
     def one(i):
-        for n, d, cnt, w, x, out in mats:
+        for n, d, cnt, w, xs, out in mats:
             for _ in range(cnt):
-                L.g4_mm_batch(out.ptr, x.ptr, w.ptr, n, d, m, g4.Q6_K, None)
+                L.g4_mm_batch_split(out.ptr, w.ptr, xs.ptr, n, d, m, g4.Q6_K)
     ms1 = _time_steps(lib, one, args)
     launches = sum(c for _, _, c, *_ in mats)
     per1 = ms1 / 1e3 / args.steps / launches
     flops = sum(2.0 * m * n * d * c for n, d, c, *_ in mats) / launches
     tf1 = flops / per1 / 1e12
-    name = "mm_batch_f32_kernel<Q6_K> (V and FFN down of one 511-token chunk)"
+    name = "mm_batch_q6s_kernel<Q6_K> (V and FFN down of one 511-token chunk)"
     res = {
         "value": round(m / sec, 1), "unit": "tok/s", "higher_is_better": True, "ms_per_step": sec * 1e3,
-        "dtype": "u4 x int8 exact fp16 matrix products (Q4_K), fp32 matrix products (Q6_K, bf16), fp32 glue",
+        "dtype": "u4/u5 x int8 exact fp16 matrix products (Q4_K/Q5_K), split-fp16 matrix products (Q6_K), "
+                 "fp32 matrix products (bf16), fp32 glue",
         "config": {"workload": "synthetic E4B-shape batched prefill (42 layers, hidden 2560, FFN 10240, 8q/2kv heads, "
                                "head_dim 256/512, window 512, Q4_K_M mix, seed 4): 511 prompt tokens in one chunk",
                    "tokens": m, "roofline_launches_per_step": launches},
-        "roofline": {"bound": "mfma", "achieved": round(tf1, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tf1 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(name),
-                     "kernel": name, "us_per_launch": round(per1 * 1e6, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tf1, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf1 / FP16_MFMA_PEAK_TFLOPS, 4),
+                     "mfma_issued": round(Q6S_MFMA_PER_FLOP * tf1, 2),
+                     "mfma_issued_frac": round(Q6S_MFMA_PER_FLOP * tf1 / FP16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(name), "kernel": name, "us_per_launch": round(per1 * 1e6, 2)},
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_prefill_e2e_baseline(path)

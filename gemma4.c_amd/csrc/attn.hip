@@ -676,7 +676,11 @@ __host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2) {
     return (size_t)4 * kvm_pow2 * (hd + 2) * 4;
 }
 
-template <int HD, int KVM>
+// DB: two register sets, round r + 1's rows loading while round r is
+// reduced (decode: few workgroups, each one's latency counts); without it
+// the register count allows twice the workgroups per CU (prompt-chunk rows:
+// thousands of workgroups, occupancy counts)
+template <int HD, int KVM, bool DB>
 __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     if (a.qrows) attn_query_row(a, false);
     constexpr int W = HD / 128;
@@ -737,8 +741,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     };
     const float* kbase = a.kc + (size_t)kvh * HD;
     const float* vbase = a.vc + (size_t)kvh * HD;
-    // two register sets: round r + 1's rows load while round r is reduced
-    HVec<HD> kr[PPW], vr[PPW], kr2[PPW], vr2[PPW];
+    HVec<HD> kr[PPW], vr[PPW], kr2[DB ? PPW : 1], vr2[DB ? PPW : 1];
     auto load_kv = [&](HVec<HD>* K, HVec<HD>* Vv, int r) {
 #pragma unroll
         for (int p = 0; p < PPW; p++) {
@@ -852,7 +855,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     // rounds in pairs over the two register sets; the next round's loads
     // are issued unconditionally (a clamped round past the last one reloads
     // rows already in cache) so that no branch separates them from their use
-    if (nrounds == 1) {
+    if (!DB) {
+        for (int r = 0; r < nrounds; r++) {
+            if (r > 0) load_kv(kr, vr, r);
+            round(kr, vr, r);
+        }
+    } else if (nrounds == 1) {
         round(kr, vr, 0);                         // one round (sliding windows): no second set
     } else {
         for (int r = 0; r < nrounds; r += 2) {
@@ -992,10 +1000,17 @@ size_t attn_lds(int hd, int kvm, bool fused) {
 template <int HD>
 void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
     const size_t lds = attn_chunk_lds(HD, kp);
-    if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
-    else if (kp == 2) hipLaunchKernelGGL((attn_chunk_kernel<HD, 2>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
-    else if (kp == 4) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
-    else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    if (a.qrows) {
+        if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        else if (kp == 2) hipLaunchKernelGGL((attn_chunk_kernel<HD, 2, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        else if (kp == 4) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        return;
+    }
+    if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else if (kp == 2) hipLaunchKernelGGL((attn_chunk_kernel<HD, 2, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else if (kp == 4) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+    else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
 }
 
 template <int HD>

@@ -1,34 +1,50 @@
-// prefill.hip -- many tokens through one K-quant matrix at once (prefill):
-// Y[m x d] = Q8_K(X[m x n]) . W[d x n]^T on the gfx950 matrix cores, with
-// every output bit-identical to the per-token GEMV (gemv.hip) and hence to
-// the reference's AVX2 dot, vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K
-// (gemma4-4b/cpu-blas/main.c:476-529, 531-593).  The reference has no
-// batched path: generate() calls forward() once per prompt token
-// (main.c:2366-2384), i.e. quantize_row_q8_K + mm_quant_dot_rows per token.
+// prefill.hip -- many tokens through one weight matrix at once (prefill):
+// Y[m x d] = X[m x n] . W[d x n]^T on the gfx950 matrix cores.  The
+// reference has no batched path: generate() calls forward() once per prompt
+// token (gemma4-4b/cpu-blas/main.c:2366-2384), i.e. quantize_row_q8_K +
+// mm_quant_dot_rows per token for Q4_K / Q5_K and mm_quant_rows / mm_bf16 on
+// the fp32 activations for Q6_K / bf16.  Every kernel here computes the same
+// sums from the same integer codes and scales; only the fp32 rounding of the
+// partial sums differs from the per-token dot, so the bar is the GEMVs' one,
+// 1e-5 of sum |w x|.  Each token's outputs are a fixed function of that
+// token's activations (no split over tokens or K that depends on the batch),
+// so a prompt gives the same bits in any chunking.
 //
-// Exactness.  The AVX2 dot keeps, per block, eight int32 lanes
-//   sumi[k] = sum_j sc_j * sum_{e<4} q[32j + 4k + e] * q8[32j + 4k + e]
-// (j = sub-block, k = lane), plus four min lanes (Q4_K)
-//   prod[p] = m_2p * (bs_4p + bs_4p+1) + m_2p+1 * (bs_4p+2 + bs_4p+3)
-// or their sum (Q5_K), and folds them into fp32 accumulators with the
-// block's d = y.d * fp16(x.d) and dmin = -y.d * fp16(x.dmin).  Here the
-// lane-k sums are matrix-core products over a 32-long K axis that gathers
-// positions 4k..4k+3 of all eight sub-blocks, with the sub-block scale
-// folded into the weight (sc * q <= 63 * 31 = 1953) and the activation as
-// fp16 (|q8| <= 128): every product and every partial sum is an integer
-// below 2^24 in magnitude, so the fp32 accumulation inside the matrix core
-// is exact whatever its order, and equals the int32 lane sum.  The min
-// lanes are 16-long products of m_j with the 16-element bsums (|bs| <=
-// 2032, exact in fp16).  The fp32 steps after that (d*sumi FMA per lane and
-// block in block order, the fixed horizontal-add tree) are the reference's.
+// Q4_K / Q5_K (mm_batch_kq32_kernel).  The reference's dot per block is
+//   y.d * d * sum_j sc_j * sum_e q_e * q8_e  -  y.d * dmin * sum_j m_j * bs_j
+// (vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K, main.c:476-529, 531-593; bs_j =
+// the two 16-element bsums of sub-block j).  The first sum runs on
+// v_mfma_f32_32x32x16_f16 with the sub-block scale folded into the weight
+// operand: sc * q <= 63 * 31 is an integer below 2048 and |q8| <= 128, so
+// every product is exact and the matrix core only rounds partial sums above
+// 2^24.  The sixteen 16-long K steps of a block chain in one accumulator, the
+// min sum is two 8-long MFMAs, and the block is folded into the fp32
+// accumulator with three VALU operations per output.  The weights are the B
+// operand, so a lane's outputs share one weight row and its d, dmin and
+// scales come from the block header the lane loads itself.  Work split: a
+// 256-thread workgroup owns 128 weight rows (32 per wave) x 32 NT tokens;
+// per block it stages its tokens' activations in LDS as fp16 in the MFMA K
+// order, and each wave builds its weight operands (codes * scale as fp16) in
+// registers from 64 contiguous bytes per lane, loaded one block ahead.
 //
-// Work split.  A 256-thread workgroup owns 64 weight rows x 32 tokens:
-// four row waves of 16 rows, each with two 16x16 output tiles (32 tokens).
-// Per block the workgroup stages the 32 tokens' activations into LDS as
-// fp16, already in the lane-k order; each wave
-// builds its weight operand (codes * scale as fp16) in registers from the
-// planar Q4_K/Q5_K bytes.  The next block's bytes are loaded into
-// registers while the current block is computed.
+// Q6_K (mm_batch_q6s_kernel).  The reference dequantizes each weight to
+// d * sc * (q - 32) in fp32 (exact: 11 + 7 + 5 significant bits) and
+// multiplies by the fp32 activations (mm_quant_rows, main.c:1539-1556,
+// dequant_q6_k main.c:213-236).  Here:
+//   * each activation row is split (g4_split_rows_f16) into two fp16 terms
+//     after scaling by a power of two that brings its largest |x| into
+//     [2^14, 2^15): x * 2^-s = hi + lo + r with |r| <= 2^-22 |x * 2^-s| (or
+//     below 2^-25 in the scaled units, for elements in fp16's subnormal range);
+//   * the signed 8-bit sub-block scale is split exactly, sc = 16a + b with
+//     a = sc >> 4 in [-8, 7] and b = sc & 15, so the two weight operands
+//     16a * (q - 32) (|.| <= 4096, a multiple of 16 with at most 9 significant
+//     bits) and b * (q - 32) (|.| <= 480) are exact fp16;
+//   * four fp16 MFMAs per 32 weights (hi and lo against both weight operands)
+//     give sum sc * (q - 32) * x over a block with exact products, chained in
+//     one fp32 accumulator; the block's fp16 d is applied with one FMA per
+//     output, and the token's 2^s at the end (exact).
+// The bf16 matrices and the workspace-free g4_mm_batch entry keep the fp32
+// MFMA kernel (mm_batch_f32_kernel, below).
 #include "g4_device.h"
 #include "g4_internal.h"
 
@@ -40,8 +56,6 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kPfTokStride = 528;    // LDS bytes per staged token (512 + pad)
-constexpr int kPfBsStride = 32;      // LDS bytes per token of fp16 bsums
 
 __device__ __forceinline__ uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ h2_t bits_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
@@ -75,259 +89,265 @@ __device__ __forceinline__ float hbits_to_f32(uint32_t h) {
     return (float)v;
 }
 
-// RW row waves x TW token waves; each wave owns 16 rows x NT 16-token tiles.
-// At least WPE waves per SIMD caps the VGPRs at 512 / WPE: at 256 or fewer the
-// compiler writes the matrix-core results straight to VGPRs instead of going
-// through accumulation registers (a v_accvgpr_read per result element).
-template <bool Q5, int RW, int TW, int NT, int WPE = 2>
-__global__ __launch_bounds__(64 * RW * TW) __attribute__((amdgpu_waves_per_eu(WPE))) void mm_batch_kq_kernel(const uint8_t* __restrict__ w,
-                                                                    const uint8_t* __restrict__ q8,
-                                                                    float* __restrict__ out, int nb, int d, int m) {
-    constexpr int NTHR = 64 * RW * TW;
-    constexpr int TOK = 16 * NT * TW;                      // tokens per workgroup
-    constexpr int UNITS = TOK * 8;                          // (token, lane-k) staging units
-    constexpr int UPT = (UNITS + NTHR - 1) / NTHR;          // units per thread
-    constexpr int BQ = (TOK * 4 + NTHR - 1) / NTHR;         // bsums quarters per thread
-    __shared__ __align__(16) uint8_t sB[TOK * kPfTokStride];
-    __shared__ __align__(16) uint8_t sS[TOK * kPfBsStride];
-    __shared__ float sD[TOK];
+// XCD-aware tile order.  Workgroups go to the 8 XCDs round robin by their
+// linear id; tile t = (row group t / gy, token group t % gy) is given to id
+// so that each XCD takes a contiguous run of tiles, i.e. a few row groups
+// with all their token groups: the weights of those rows stay in that XCD's
+// L2 while its workgroups stream the activations.  (A bijection on ids for
+// any tile count; grid = gx * gy workgroups in x.)
+__device__ __forceinline__ void xcd_tile(int gy, int& bx, int& by) {
+    const int n = gridDim.x, id = blockIdx.x;
+    const int q = n >> 3, r = n & 7, x = id & 7, l = id >> 3;
+    const int t = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + l;
+    bx = t / gy;
+    by = t - bx * gy;
+}
+
+// buffer-resource loads (word 3 of the descriptor: 32-bit data format, the
+// value the gfx9 family takes for raw byte-addressed buffers)
+constexpr int kBufWord3 = 0x00020000;
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+constexpr int kKqTok = 528;   // LDS bytes per staged token: 512 of fp16 + pad
+constexpr int kKqBs = 40;     // LDS bytes per token of fp16 bsums: 32 + pad
+
+// up to kMaxSegs matrices over the same activations in one launch: segment
+// s owns row groups [g0[s], g0[s + 1]) of 128 rows
+constexpr int kMaxSegs = 4;
+struct KqSegs {
+    const uint8_t* w[kMaxSegs];
+    float* o[kMaxSegs];
+    int d[kMaxSegs];
+    int g0[kMaxSegs + 1];
+    int n;
+};
+
+template <bool Q5, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
+    const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
+    constexpr int TOK = 32 * NT;
+    constexpr int UPT = TOK * 8 / 256;           // (token, Q8_K lane) units of 32 bytes per thread
+    static_assert(UPT * 256 == TOK * 8, "token tile must divide among the threads");
+    constexpr int BQ = (TOK * 4 + 255) / 256;    // 8-byte bsums quarters per thread
+    __shared__ __align__(16) uint8_t sA[TOK * kKqTok];
+    __shared__ __align__(16) uint8_t sS[TOK * kKqBs];
+    __shared__ __align__(16) float sD[TOK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int i = lane & 15, g = lane >> 4;               // operand row / column, K group
-    const int rw = wave % RW, tw = wave / RW;              // row wave, token wave
-    const int row0 = blockIdx.x * (16 * RW) + rw * 16;
-    const int tokb = blockIdx.y * TOK;
-    const int tw0 = tw * 16 * NT;                          // first token of this wave (in the workgroup)
+    const int i = lane & 31, kg = lane >> 5;
+    int bx, by;
+    xcd_tile((m + TOK - 1) / TOK, bx, by);
+    int seg = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxSegs; k++)
+        if (k < sg.n && bx >= sg.g0[k]) seg = k;
+    const uint8_t* __restrict__ w = sg.w[seg];
+    float* __restrict__ out = sg.o[seg];
+    const int d = sg.d[seg];
+    const int row = (bx - sg.g0[seg]) * 128 + wave * 32 + i;
+    const int tokb = by * TOK;
     const size_t nblk = (size_t)d * nb;
     const size_t hdr_off = (Q5 ? 160 : 128) * nblk, qh_off = 128 * nblk;
     const size_t q8row = ((size_t)nb * 292 + 63) & ~(size_t)63;   // q8_row_stride
-
-    // weight operand row of this lane, and the four output rows 4g+v
-    const size_t rA = (size_t)min(row0 + i, d - 1) * nb;
-    size_t rD[4];
-#pragma unroll
-    for (int v = 0; v < 4; v++) rD[v] = (size_t)min(row0 + 4 * g + v, d - 1) * nb;
+    const size_t rB = (size_t)min(row, d - 1) * nb;
 
     struct WRaw {
-        uint32_t qs[8];
-        uint32_t qh[8];
-        uint4 hdr;
-        uint32_t dh[4];
+        uint4 qs[4];     // device qs words 16kg .. 16kg+15 of the block
+        uint4 qh;        // Q5_K: qh bytes 16kg .. 16kg+15 (positions 4l..4l+3)
+        uint4 hdr;       // d, dmin, scales
     };
     struct XRaw {
         uint4 a0[UPT], a1[UPT];
         uint2 bs[BQ];
         float yd;
     };
+    // buffer loads: a per-lane 32-bit offset fixed for the kernel and the
+    // block's offset in a scalar register (loads past the end read zero)
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(hdr_off + 16 * nblk), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q8, (short)0, (int)(m * q8row), kBufWord3);
+    const int vqs = (int)(rB * 128) + 64 * kg, vqh = (int)(qh_off + rB * 32) + 16 * kg, vhdr = (int)(hdr_off + rB * 16);
+    int vx[UPT], vbs[BQ];
+#pragma unroll
+    for (int j = 0; j < UPT; j++) {
+        const int u = tid + j * 256;
+        vx[j] = min(tokb + (u >> 3), m - 1) * (int)q8row + 32 * (u & 7);
+    }
+#pragma unroll
+    for (int j = 0; j < BQ; j++) {
+        const int u = min(tid + j * 256, TOK * 4 - 1);
+        vbs[j] = min(tokb + (u >> 2), m - 1) * (int)q8row + (int)q8k_bsums_off(nb) + 8 * (u & 3);
+    }
+    const int vyd = min(tokb + min(tid, TOK - 1), m - 1) * (int)q8row + (int)q8k_d_off(nb);
     auto load_w = [&](int b, WRaw& r) {
-        const uint8_t* qa = w + (rA + b) * 128 + 4 * g;
 #pragma unroll
-        for (int k = 0; k < 8; k++) r.qs[k] = *reinterpret_cast<const uint32_t*>(qa + 16 * k);
-        if (Q5) {
-            const uint8_t* ha = w + qh_off + (rA + b) * 32;
-#pragma unroll
-            for (int k = 0; k < 8; k++) r.qh[k] = *reinterpret_cast<const uint32_t*>(ha + 4 * k);
-        }
-        r.hdr = *reinterpret_cast<const uint4*>(w + hdr_off + (rA + b) * 16);
-#pragma unroll
-        for (int v = 0; v < 4; v++) r.dh[v] = *reinterpret_cast<const uint32_t*>(w + hdr_off + (rD[v] + b) * 16);
+        for (int q = 0; q < 4; q++) r.qs[q] = buf_load16(rw, vqs + 16 * q, b * 128);
+        if (Q5) r.qh = buf_load16(rw, vqh, b * 32);
+        r.hdr = buf_load16(rw, vhdr, b * 16);
     };
-    // unit u = tid + j*NTHR: token u >> 3, lane-k u & 7 (its 32 device bytes)
+    // unit u = tid + 256 j: token u >> 3, Q8_K device lane u & 7 (32 bytes:
+    // words (h, jj) = sub-block 2jj + h, positions 4l'..4l'+3); tokens past
+    // m repeat the last one (their outputs are not stored)
     auto load_x = [&](int b, XRaw& r) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
-            const int u = tid + j * NTHR;
-            r.a0[j] = make_uint4(0u, 0u, 0u, 0u);
-            r.a1[j] = r.a0[j];
-            if (UNITS % NTHR == 0 || u < UNITS) {
-                const uint8_t* p = q8 + (size_t)min(tokb + (u >> 3), m - 1) * q8row + (size_t)b * 256 + 32 * (u & 7);
-                r.a0[j] = *reinterpret_cast<const uint4*>(p);
-                r.a1[j] = *reinterpret_cast<const uint4*>(p + 16);
-            }
+            r.a0[j] = buf_load16(rq, vx[j], b * 256);
+            r.a1[j] = buf_load16(rq, vx[j] + 16, b * 256);
         }
 #pragma unroll
-        for (int j = 0; j < BQ; j++) {
-            const int u = tid + j * NTHR;
-            r.bs[j] = make_uint2(0u, 0u);
-            if (u < TOK * 4)
-                r.bs[j] = *reinterpret_cast<const uint2*>(q8 + (size_t)min(tokb + (u >> 2), m - 1) * q8row +
-                                                          q8k_bsums_off(nb) + (size_t)b * 32 + 8 * (u & 3));
-        }
-        r.yd = 0.0f;
-        if (tid < TOK) r.yd = reinterpret_cast<const float*>(q8 + (size_t)min(tokb + tid, m - 1) * q8row +
-                                                             q8k_d_off(nb))[b];
+        for (int j = 0; j < BQ; j++) r.bs[j] = buf_load8(rq, vbs[j], b * 32);
+        r.yd = __uint_as_float(buf_load4(rq, vyd, b * 4));
     };
-    // activations of one block -> LDS: token t, lane k: the K group g entry
-    // is 8 halves = device words g of a0 (sub-block 2g) and of a1 (sub-block
-    // 2g+1), i.e. q8 elements 64g+4k+e and 64g+32+4k+e
+    // unit (t, l'): for jj = 0..3 the K step s = 4 (l' & 3) + jj, group
+    // kg = l' >> 2 entry [cvt(word (0, jj)), cvt(word (1, jj))]
     auto stage = [&](const XRaw& r) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
-            const int u = tid + j * NTHR;
-            if (UNITS % NTHR == 0 || u < UNITS) {
-                const bool ok = tokb + (u >> 3) < m;
-                uint8_t* dst = sB + (u >> 3) * kPfTokStride + 64 * (u & 7);
-                const uint32_t a0[4] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w};
-                const uint32_t a1[4] = {r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
+            const int u = tid + j * 256, lq = u & 7;
+            uint8_t* dst = sA + (u >> 3) * kKqTok + 128 * (lq & 3) + 16 * (lq >> 2);
+            const uint32_t a0[4] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w};
+            const uint32_t a1[4] = {r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
 #pragma unroll
-                for (int gg = 0; gg < 4; gg++) {
-                    uint4 h = make_uint4(0u, 0u, 0u, 0u);
-                    if (ok) {
-                        const uint2 l = i8x4_to_h4(a0[gg]), hh = i8x4_to_h4(a1[gg]);
-                        h = make_uint4(l.x, l.y, hh.x, hh.y);
-                    }
-                    *reinterpret_cast<uint4*>(dst + 16 * gg) = h;
-                }
+            for (int jj = 0; jj < 4; jj++) {
+                const uint2 l = i8x4_to_h4(a0[jj]), hh = i8x4_to_h4(a1[jj]);
+                *reinterpret_cast<uint4*>(dst + 32 * jj) = make_uint4(l.x, l.y, hh.x, hh.y);
             }
         }
 #pragma unroll
         for (int j = 0; j < BQ; j++) {
-            const int u = tid + j * NTHR;
+            const int u = tid + j * 256;
             if (u < TOK * 4) {
-                uint2 h = make_uint2(0u, 0u);
-                if (tokb + (u >> 2) < m) {
-                    const h2_t lo = {(_Float16)(int16_t)(r.bs[j].x & 0xffffu), (_Float16)(int16_t)(r.bs[j].x >> 16)};
-                    const h2_t hi = {(_Float16)(int16_t)(r.bs[j].y & 0xffffu), (_Float16)(int16_t)(r.bs[j].y >> 16)};
-                    h = make_uint2(h2_bits(lo), h2_bits(hi));
-                }
-                *reinterpret_cast<uint2*>(sS + (u >> 2) * kPfBsStride + 8 * (u & 3)) = h;
+                const h2_t lo = {(_Float16)(int16_t)(r.bs[j].x & 0xffffu), (_Float16)(int16_t)(r.bs[j].x >> 16)};
+                const h2_t hi = {(_Float16)(int16_t)(r.bs[j].y & 0xffffu), (_Float16)(int16_t)(r.bs[j].y >> 16)};
+                *reinterpret_cast<uint2*>(sS + (u >> 2) * kKqBs + 8 * (u & 3)) = make_uint2(h2_bits(lo), h2_bits(hi));
             }
         }
-        if (tid < TOK) sD[tid] = tokb + tid < m ? r.yd : 0.0f;
+        if (tid < TOK) sD[tid] = r.yd;
     };
 
-    f4_t acc[NT][8];
-    f4_t accm[NT][4];
+    f16v_t acc[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
+    for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc[t][k] = f4_t{0.f, 0.f, 0.f, 0.f};
+        for (int v = 0; v < 16; v++) acc[nt][v] = 0.0f;
+    f16v_t zero;
 #pragma unroll
-        for (int p = 0; p < 4; p++) accm[t][p] = f4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < 16; v++) zero[v] = 0.0f;
 
-    WRaw wn;
+    // one block: stage its activations, start the next block's loads into
+    // the other weight set, compute from this one (the block loop runs two
+    // blocks per trip so that the sets alternate without copies)
     XRaw xn;
-    load_w(0, wn);
-    load_x(0, xn);
-    for (int b = 0; b < nb; b++) {
+    auto block = [&](int b, const WRaw& wc, WRaw& wnext) {
         __syncthreads();   // the previous block's LDS reads are done
         stage(xn);
-        const WRaw wc = wn;
         if (b + 1 < nb) {
-            load_w(b + 1, wn);
+            load_w(b + 1, wnext);
             load_x(b + 1, xn);
         }
         __syncthreads();
 
-        // scales of this lane's operand row: sub-blocks 2g, 2g+1
+        // scales of row i: sub-blocks 2j, 2j+1 as exact fp16 multipliers
         uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
         unpack_scales(wc.hdr.y, wc.hdr.z, wc.hdr.w, sc_lo, sc_hi, mn_lo, mn_hi);
-        const int sh = 16 * (g & 1);
-        const uint32_t scw = g < 2 ? sc_lo : sc_hi, mnw = g < 2 ? mn_lo : mn_hi;
-        const _Float16 sa = (_Float16)(float)((scw >> sh) & 0xffu), sb = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
-        const _Float16 ma = (_Float16)(float)((mnw >> sh) & 0xffu), mb = (_Float16)(float)((mnw >> (sh + 8)) & 0xffu);
-        const h2_t SA = {sa, sa}, SB = {sb, sb};
-        const h2_t NA = {(_Float16)(-1024.0f) * sa, (_Float16)(-1024.0f) * sa};
-        const h2_t NB = {(_Float16)(-1024.0f) * sb, (_Float16)(-1024.0f) * sb};
+        h2_t SA[4], SB[4], NA[4], NB[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t scw = j < 2 ? sc_lo : sc_hi;
+            const int sh = 16 * (j & 1);
+            const _Float16 sa = (_Float16)(float)((scw >> sh) & 0xffu), sb = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
+            SA[j] = h2_t{sa, sa};
+            SB[j] = h2_t{sb, sb};
+            NA[j] = h2_t{(_Float16)(-1024.0f) * sa, (_Float16)(-1024.0f) * sa};
+            NB[j] = h2_t{(_Float16)(-1024.0f) * sb, (_Float16)(-1024.0f) * sb};
+        }
 
-        // fp32 scales of the four output rows x the token tiles
-        float dd[NT][4], dm[NT][4];
+        f16v_t S[NT];
+        const uint8_t* at0 = sA + i * kKqTok + 16 * kg;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const float yd = sD[tw0 + 16 * t + i];
+        for (int s = 0; s < 16; s++) {
+            const int j = s & 3;
+            const uint4 Q = wc.qs[s >> 2];
+            const uint32_t word = j == 0 ? Q.x : j == 1 ? Q.y : j == 2 ? Q.z : Q.w;
+            uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
+            if (Q5) {
+                const uint32_t hw = (s >> 2) == 0 ? wc.qh.x : (s >> 2) == 1 ? wc.qh.y : (s >> 2) == 2 ? wc.qh.z : wc.qh.w;
+                lo |= ((hw >> (2 * j)) & 0x01010101u) << 4;
+                hi |= ((hw >> (2 * j + 1)) & 0x01010101u) << 4;
+            }
+            const uint2 al = codes_to_h4(lo, SA[j], NA[j]), ah = codes_to_h4(hi, SB[j], NB[j]);
+            const h8_t B = __builtin_bit_cast(h8_t, make_uint4(al.x, al.y, ah.x, ah.y));
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                dd[t][v] = yd * hbits_to_f32(wc.dh[v] & 0xffffu);
-                dm[t][v] = -yd * hbits_to_f32(wc.dh[v] >> 16);
+            for (int nt = 0; nt < NT; nt++) {
+                const h8_t A = *reinterpret_cast<const h8_t*>(at0 + 32 * nt * kKqTok + 32 * s);
+                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s == 0 ? zero : S[nt], 0, 0, 0);
             }
         }
-        const uint8_t* bt0 = sB + (tw0 + i) * kPfTokStride + 16 * g;
+        // min sums (bsums 4kg.. and 8+4kg..: sub-blocks 2kg, 2kg+1, 4+2kg,
+        // 5+2kg) and the block's scales
+        const int msh = 16 * kg;
+        const _Float16 m0 = (_Float16)(float)((mn_lo >> msh) & 0xffu), m1 = (_Float16)(float)((mn_lo >> (msh + 8)) & 0xffu);
+        const _Float16 m4 = (_Float16)(float)((mn_hi >> msh) & 0xffu), m5 = (_Float16)(float)((mn_hi >> (msh + 8)) & 0xffu);
+        const h4_t Bm1 = {m0, m0, m1, m1}, Bm2 = {m4, m4, m5, m5};
+        const float dx = hbits_to_f32(wc.hdr.x & 0xffffu), dmx = hbits_to_f32(wc.hdr.x >> 16);
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            uint32_t lo = wc.qs[k] & 0x0f0f0f0fu, hi = (wc.qs[k] >> 4) & 0x0f0f0f0fu;
-            if (Q5) {
-                lo |= ((wc.qh[k] >> (2 * g)) & 0x01010101u) << 4;
-                hi |= ((wc.qh[k] >> (2 * g + 1)) & 0x01010101u) << 4;
-            }
-            const uint2 al = codes_to_h4(lo, SA, NA), ah = codes_to_h4(hi, SB, NB);
-            const h8_t A = __builtin_bit_cast(h8_t, make_uint4(al.x, al.y, ah.x, ah.y));
+        for (int nt = 0; nt < NT; nt++) {
+            const uint8_t* bs = sS + (32 * nt + i) * kKqBs + 8 * kg;
+            const h4_t A1 = *reinterpret_cast<const h4_t*>(bs), A2 = *reinterpret_cast<const h4_t*>(bs + 16);
+            f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
+            M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const h8_t B = *reinterpret_cast<const h8_t*>(bt0 + 16 * t * kPfTokStride + 64 * k);
-                const f4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, zero, 0, 0, 0);
+            for (int a = 0; a < 4; a++) {
+                const float4 yd = *reinterpret_cast<const float4*>(sD + 32 * nt + 8 * a + 4 * kg);
+                const float y4[4] = {yd.x, yd.y, yd.z, yd.w};
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[t][k][v] = __builtin_fmaf(dd[t][v], D[v], acc[t][k][v]);
-            }
-        }
-        // min lanes: lane group g carries bsums 4g..4g+3 (sub-blocks 2g, 2g+1)
-        const _Float16 z = (_Float16)0.0f;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const h4_t Bm = *reinterpret_cast<const h4_t*>(sS + (tw0 + 16 * t + i) * kPfBsStride + 8 * g);
-            if (Q5) {
-                const h4_t Am = {ma, ma, mb, mb};
-                const f4_t P = __builtin_amdgcn_mfma_f32_16x16x16f16(Am, Bm, zero, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const float tm = dm[t][v] * P[v];
-                    accm[t][0][v] = accm[t][0][v] + tm;
-                }
-            } else {
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const h4_t Am = g == p ? h4_t{ma, ma, mb, mb} : h4_t{z, z, z, z};
-                    const f4_t P = __builtin_amdgcn_mfma_f32_16x16x16f16(Am, Bm, zero, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) accm[t][p][v] = __builtin_fmaf(dm[t][v], P[v], accm[t][p][v]);
+                for (int c = 0; c < 4; c++) {
+                    const int v = 4 * a + c;
+                    const float u = __builtin_fmaf(dx, S[nt][v], -(dmx * M[v]));
+                    acc[nt][v] = __builtin_fmaf(y4[c], u, acc[nt][v]);
                 }
             }
         }
+    };
+    WRaw w0, w1;
+    load_w(0, w0);
+    load_x(0, xn);
+    for (int b = 0; b < nb; b += 2) {
+        block(b, w0, w1);
+        if (b + 1 < nb) block(b + 1, w1, w0);
     }
 
-    // the reference's horizontal adds (hsum_float_8, then the min lanes)
+    if (row < d) {
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tok = tokb + tw0 + 16 * t + i;
-        float r[4];
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const float h = ((acc[t][4][v] + acc[t][0][v]) + (acc[t][6][v] + acc[t][2][v])) +
-                            ((acc[t][5][v] + acc[t][1][v]) + (acc[t][7][v] + acc[t][3][v]));
-            if (Q5) {
-                r[v] = h + accm[t][0][v];
-            } else {
-                const float hm = (accm[t][0][v] + accm[t][2][v]) + (accm[t][1][v] + accm[t][3][v]);
-                r[v] = h + hm;
+            for (int v = 0; v < 16; v++) {
+                const int tok = tokb + 32 * nt + 8 * (v >> 2) + 4 * kg + (v & 3);
+                if (tok < m) out[(size_t)tok * d + row] = acc[nt][v];
             }
-        }
-        if (tok < m) {
-            const int rowo = row0 + 4 * g;
-            float* o = out + (size_t)tok * d + rowo;
-            if (rowo + 3 < d && ((d & 3) == 0)) {
-                *reinterpret_cast<float4*>(o) = make_float4(r[0], r[1], r[2], r[3]);
-            } else {
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    if (rowo + v < d) o[v] = r[v];
-            }
-        }
     }
 }
 
-// the shipped tiling (fastest of a sweep over 1..8 row waves, 1..4 token
-// waves, 1..4 tiles at E4B shapes and 512 tokens): 4 row waves x 1 token
-// wave x 2 tiles = 64 rows x 32 tokens per 256-thread workgroup
-constexpr int kRW = 4, kTW = 1, kNT = 2;
-constexpr int kPfToks = 16 * kNT * kTW;
-
-template <bool Q5, int RW, int TW, int NT, int WPE = 2>
-void launch_mm_batch(const uint8_t* w, const uint8_t* q8, float* o, int nb, int d, int m) {
-    const dim3 grid((d + 16 * RW - 1) / (16 * RW), (m + 16 * NT * TW - 1) / (16 * NT * TW));
-    hipLaunchKernelGGL((mm_batch_kq_kernel<Q5, RW, TW, NT, WPE>), grid, dim3(64 * RW * TW), 0, g4_stream(), w, q8, o,
-                       nb, d, m);
+template <bool Q5, int NT>
+void launch_mm_batch32(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
+    const int gy = (m + 32 * NT - 1) / (32 * NT);
+    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, NT>), dim3(sg.g0[sg.n] * gy), dim3(256), 0, g4_stream(), sg, q8, nb, m);
 }
+
+// the shipped tiling: 128 rows x 32 tokens per workgroup (a sweep over 32 and
+// 64 tokens, one or two accumulator chains and preloaded A operands at the
+// E4B shapes over 511 tokens: 10240x2560 60 us, 2048x2560 18 us, 2560x2048
+// 22 us; the 64-token tile needs 211 VGPRs, two waves per SIMD)
+constexpr int kKqNT = 1;
 
 // ---- fp32 activations: Q6_K and bf16 matrices --------------------------
 // Y[m x d] = X[m x n] . W[d x n]^T where the reference multiplies fp32
@@ -509,6 +529,232 @@ void launch_mm_batch_f32(const uint8_t* w, const float* x, float* o, int n, int 
                        m);
 }
 
+// ---- Q6_K on fp16 matrix cores: split activations ------------------------
+// Row layout of the split activations: n/256 blocks of 1024 bytes, the 256 hi
+// terms of the block then its 256 lo terms, each in K-step order: step c
+// (0..7), lane group g (0..3), 8 elements, where (c, g, t) is element
+//   128h + 32k + 16s + 8 half + t   (g = 2h + s, c = 2k + half)
+// of the block, i.e. lane group g's elements of the planar Q6_K block
+// (layout.hip) in the order its ql/qh bytes hold them.  After the m rows come
+// m floats: 2^s of each row, the factor that undoes the row's scaling.
+constexpr int kSplitBlk = 1024;      // bytes per 256-element block of a split row
+
+__device__ __forceinline__ int split_pos(int e) {
+    const int h = e >> 7, k = (e >> 5) & 3, s = (e >> 4) & 1, half = (e >> 3) & 1;
+    return ((((2 * k + half) << 2) | (2 * h + s)) << 3) | (e & 7);
+}
+
+// one workgroup per row: max |x|, then x * 2^-s -> hi + lo (fp16, round to
+// nearest even; x * 2^-s - hi is exact in fp32)
+__global__ __launch_bounds__(256) void split_rows_f16_kernel(const float* __restrict__ x, uint8_t* __restrict__ xs,
+                                                             int n, int m) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * n);
+    float mx = 0.0f;
+    for (int u = tid; u < n / 4; u += 256) {
+        const float4 f = xr[u];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // mx = f * 2^E, f in [0.5, 1): scaled max in [2^14, 2^15)
+    int E = 0;
+    (void)frexpf(mx, &E);
+    const int k = mx > 0.0f && mx <= 3.402823466e38f ? min(max(15 - E, -126), 126) : 0;
+    const float sf = ldexpf(1.0f, k);
+    uint8_t* row = xs + (size_t)t * n * 4;
+    for (int u = tid; u < n / 8; u += 256) {
+        const float4 f0 = xr[2 * u], f1 = xr[2 * u + 1];
+        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        h8_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float sv = v[j] * sf;
+            const _Float16 hv = (_Float16)sv;
+            hi[j] = hv;
+            lo[j] = (_Float16)(sv - (float)hv);
+        }
+        const int e = 8 * u;
+        uint8_t* dst = row + (size_t)(e >> 8) * kSplitBlk + 2 * split_pos(e & 255);
+        *reinterpret_cast<h8_t*>(dst) = hi;
+        *reinterpret_cast<h8_t*>(dst + 512) = lo;
+    }
+    if (tid == 0) reinterpret_cast<float*>(xs + (size_t)m * n * 4)[t] = ldexpf(1.0f, -k);
+}
+
+// Y[m x d] = X . W^T for planar Q6_K W over split activations.  A operand
+// (tokens): lane (g, i) holds the hi (or lo) terms (c, g, 0..7) of token
+// 16 nt + i; B operand (weights): 16a * (q - 32) or b * (q - 32) of the same
+// elements of row 16 rt + i.  Result lane (g, i): tokens 16 nt + 4g + v of
+// row 16 rt + i.
+constexpr int kXsStride = kSplitBlk + 16;   // LDS bytes per staged token
+
+template <int RT, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_q6s_kernel(
+    const uint8_t* __restrict__ w, const uint8_t* __restrict__ xs, float* __restrict__ out, int n, int d, int m) {
+    constexpr int TOK = 16 * NT;
+    constexpr int XU = TOK * (kSplitBlk / 16) / 256;   // 16-byte pieces per thread and block
+    static_assert(XU * 256 == TOK * (kSplitBlk / 16), "token tile must divide among the threads");
+    __shared__ __align__(16) uint8_t sx[TOK * kXsStride];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, g = lane >> 4, h = g >> 1, s = g & 1;
+    int bx, by;
+    xcd_tile((m + TOK - 1) / TOK, bx, by);
+    const int rbase = bx * (64 * RT) + wave * (16 * RT);
+    const int tokb = by * TOK;
+    const int nb = n >> 8;
+    const Q6KPlanes P = q6k_planes((size_t)d * nb);
+    const size_t xrow = (size_t)n * 4;
+
+    size_t rB[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) rB[rt] = (size_t)min(rbase + 16 * rt + i, d - 1) * nb;
+
+    struct WRaw {
+        uint4 ql[RT][2];   // lane group g's 32 ql bytes
+        uint4 qh[RT];      // its 16 qh bytes
+        uint2 sc[RT];      // scales of sub-blocks 8h .. 8h+7
+        uint32_t dh[RT];
+    };
+    struct XRaw {
+        uint4 v[XU];
+    };
+    auto load_w = [&](int b, WRaw& r) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const size_t blk = rB[rt] + b;
+            const uint4* ql = reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 32 * g);
+            r.ql[rt][0] = ql[0];
+            r.ql[rt][1] = ql[1];
+            r.qh[rt] = *reinterpret_cast<const uint4*>(w + P.qh + blk * 64 + 16 * g);
+            r.sc[rt] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+            r.dh[rt] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+        }
+    };
+    // piece u = tid + j * 256: token u >> 6, bytes 16 (u & 63) of its block
+    auto load_x = [&](int b, XRaw& r) {
+#pragma unroll
+        for (int j = 0; j < XU; j++) {
+            const int u = tid + j * 256;
+            r.v[j] = *reinterpret_cast<const uint4*>(xs + (size_t)min(tokb + (u >> 6), m - 1) * xrow +
+                                                     (size_t)b * kSplitBlk + 16 * (u & 63));
+        }
+    };
+    auto stage = [&](const XRaw& r) {
+#pragma unroll
+        for (int j = 0; j < XU; j++) {
+            const int u = tid + j * 256;
+            *reinterpret_cast<uint4*>(sx + (u >> 6) * kXsStride + 16 * (u & 63)) =
+                tokb + (u >> 6) < m ? r.v[j] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+
+    f4_t acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+    const h2_t m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+
+    WRaw wn;
+    XRaw xn;
+    load_w(0, wn);
+    load_x(0, xn);
+    for (int b = 0; b < nb; b++) {
+        __syncthreads();   // the previous block's LDS reads are done
+        stage(xn);
+        const WRaw wc = wn;
+        if (b + 1 < nb) {
+            load_w(b + 1, wn);
+            load_x(b + 1, xn);
+        }
+        __syncthreads();
+
+        f4_t S[RT][NT];
+        const uint8_t* xa0 = sx + i * kXsStride + 16 * g;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int k = c >> 1, half = c & 1;
+            h8_t Wa[RT], Wb[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                // codes of elements (c, g, 0..7): ql bytes 16 half + 8 (k & 1) + t,
+                // nibble k >> 1; qh bytes 8 half + t, bits 2k .. 2k+1
+                const uint4 L = wc.ql[rt][half];
+                const uint32_t l0 = (k & 1) ? L.z : L.x, l1 = (k & 1) ? L.w : L.y;
+                const uint32_t h0 = half ? wc.qh[rt].z : wc.qh[rt].x, h1 = half ? wc.qh[rt].w : wc.qh[rt].y;
+                const uint32_t q0 = ((l0 >> (4 * (k >> 1))) & 0x0f0f0f0fu) | (((h0 >> (2 * k)) & 0x03030303u) << 4);
+                const uint32_t q1 = ((l1 >> (4 * (k >> 1))) & 0x0f0f0f0fu) | (((h1 >> (2 * k)) & 0x03030303u) << 4);
+                // q - 32 exactly: fp16(1024 + q) - 1056
+                const h2_t v0 = bits_h2(__builtin_amdgcn_perm(kMagic, q0, kSelLo)) + m1056;
+                const h2_t v1 = bits_h2(__builtin_amdgcn_perm(kMagic, q0, kSelHi)) + m1056;
+                const h2_t v2 = bits_h2(__builtin_amdgcn_perm(kMagic, q1, kSelLo)) + m1056;
+                const h2_t v3 = bits_h2(__builtin_amdgcn_perm(kMagic, q1, kSelHi)) + m1056;
+                // scale of sub-block 8h + 2k + s: byte 2k + s; sc = 16a + b, b in [-8, 7]
+                const int sb = 2 * k + s;
+                const int sc = (int)(int8_t)byte_of(sb < 4 ? wc.sc[rt].x : wc.sc[rt].y, sb & 3);
+                const int a = (sc + 8) >> 4;
+                const _Float16 fa = (_Float16)(float)(16 * a), fb = (_Float16)(float)(sc - 16 * a);
+                const h2_t FA = {fa, fa}, FB = {fb, fb};
+                Wa[rt] = __builtin_bit_cast(h8_t, make_uint4(h2_bits(v0 * FA), h2_bits(v1 * FA), h2_bits(v2 * FA),
+                                                             h2_bits(v3 * FA)));
+                Wb[rt] = __builtin_bit_cast(h8_t, make_uint4(h2_bits(v0 * FB), h2_bits(v1 * FB), h2_bits(v2 * FB),
+                                                             h2_bits(v3 * FB)));
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint8_t* xa = xa0 + 16 * nt * kXsStride + 64 * c;
+                const h8_t Ah = *reinterpret_cast<const h8_t*>(xa);
+                const h8_t Al = *reinterpret_cast<const h8_t*>(xa + 512);
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wa[rt], c == 0 ? zero : S[rt][nt], 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wb[rt], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Wa[rt], t, 0, 0, 0);
+                    S[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Wb[rt], t, 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const float dw = hbits_to_f32(wc.dh[rt]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[rt][nt][v] = __builtin_fmaf(dw, S[rt][nt][v], acc[rt][nt][v]);
+        }
+    }
+
+    const float* tsc = reinterpret_cast<const float*>(xs + (size_t)m * xrow);
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int tok = tokb + 16 * nt + 4 * g + v;
+            if (tok >= m) continue;
+            const float ts = tsc[tok];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const int row = rbase + 16 * rt + i;
+                if (row < d) out[(size_t)tok * d + row] = acc[rt][nt][v] * ts;
+            }
+        }
+}
+
+constexpr int kQ6RT = 1, kQ6NT = 2;
+
+template <int RT, int NT>
+void launch_mm_batch_q6s(const uint8_t* w, const uint8_t* xs, float* o, int n, int d, int m) {
+    const int gx = (d + 64 * RT - 1) / (64 * RT), gy = (m + 16 * NT - 1) / (16 * NT);
+    hipLaunchKernelGGL((mm_batch_q6s_kernel<RT, NT>), dim3(gx * gy), dim3(256), 0, g4_stream(), w, xs, o, n, d, m);
+}
+
 // m rows of k floats -> m consecutive device Q8_K rows of k/256 blocks
 __global__ __launch_bounds__(256) void quantize_rows_q8k_kernel(const float* __restrict__ x, uint8_t* __restrict__ y,
                                                                 int nb, int m, size_t stride) {
@@ -546,21 +792,38 @@ extern "C" int g4_quantize_rows_q8_K(const float* x, void* y, int k, int m) {
     return g4_check_launch("quantize_rows_q8k_kernel");
 }
 
-extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, int d, int m, int type) {
-    G4_CHECK_ARG(o && w && q8, "g4_mm_batch_q8: null pointer");
-    G4_CHECK_ARG(al16(o), "g4_mm_batch_q8: o must be 16-byte aligned");
-    G4_CHECK_ARG(al16(w) && al16(q8), "g4_mm_batch_q8: w and q8 must be 16-byte aligned");
-    G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0 && m > 0, "g4_mm_batch_q8: n=%d d=%d m=%d", n, d, m);
-    G4_CHECK_ARG(m <= 65535 * kPfToks, "g4_mm_batch_q8: m=%d too large", m);
+extern "C" int g4_mm_batch_q8_multi(float* const* o, const void* const* w, const int* d, int nseg, const void* q8,
+                                    int n, int m, int type) {
+    G4_CHECK_ARG(o && w && d && q8, "g4_mm_batch_q8: null pointer");
+    G4_CHECK_ARG(nseg >= 1 && nseg <= kMaxSegs, "g4_mm_batch_q8: %d matrices (1..%d)", nseg, kMaxSegs);
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && m > 0, "g4_mm_batch_q8: n=%d m=%d", n, m);
+    G4_CHECK_ARG(al16(q8), "g4_mm_batch_q8: q8 must be 16-byte aligned");
     const int nb = n / 256;
-    if (type == G4_Q4_K) {
-        launch_mm_batch<false, kRW, kTW, kNT>((const uint8_t*)w, (const uint8_t*)q8, o, nb, d, m);
-    } else if (type == G4_Q5_K) {
-        launch_mm_batch<true, kRW, kTW, kNT>((const uint8_t*)w, (const uint8_t*)q8, o, nb, d, m);
-    } else {
-        return g4_fail(G4_ERR_TYPE, "g4_mm_batch_q8: type %d has no Q8_K batched path", type);
+    // the kernel addresses both operands with 32-bit buffer offsets
+    G4_CHECK_ARG((size_t)m * q8_row_stride(nb) < (1u << 31), "g4_mm_batch_q8: %d Q8_K rows exceed 2 GiB", m);
+    KqSegs sg{};
+    sg.n = nseg;
+    long long gx = 0;
+    for (int k = 0; k < nseg; k++) {
+        G4_CHECK_ARG(o[k] && w[k], "g4_mm_batch_q8: null pointer");
+        G4_CHECK_ARG(al16(o[k]) && al16(w[k]), "g4_mm_batch_q8: o and w must be 16-byte aligned");
+        G4_CHECK_ARG(d[k] > 0 && (size_t)d[k] * nb * 176 < (1u << 31), "g4_mm_batch_q8: d=%d", d[k]);
+        sg.w[k] = (const uint8_t*)w[k];
+        sg.o[k] = o[k];
+        sg.d[k] = d[k];
+        sg.g0[k] = (int)gx;
+        gx += (d[k] + 127) / 128;
     }
-    return g4_check_launch("mm_batch_kq_kernel");
+    sg.g0[nseg] = (int)gx;
+    G4_CHECK_ARG(gx * ((m + 32 * kKqNT - 1) / (32 * kKqNT)) < (1LL << 31), "g4_mm_batch_q8: %d tokens too many", m);
+    if (type == G4_Q4_K) launch_mm_batch32<false, kKqNT>(sg, (const uint8_t*)q8, nb, m);
+    else if (type == G4_Q5_K) launch_mm_batch32<true, kKqNT>(sg, (const uint8_t*)q8, nb, m);
+    else return g4_fail(G4_ERR_TYPE, "g4_mm_batch_q8: type %d has no Q8_K batched path", type);
+    return g4_check_launch("mm_batch_kq32_kernel");
+}
+
+extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, int d, int m, int type) {
+    return g4_mm_batch_q8_multi(&o, &w, &d, 1, q8, n, m, type);
 }
 
 extern "C" int g4_mm_batch(float* o, const float* x, const void* w, int n, int d, int m, int type, void* q8) {
@@ -583,4 +846,28 @@ extern "C" int g4_mm_batch(float* o, const float* x, const void* w, int n, int d
         if (rc) return rc;
     }
     return G4_OK;
+}
+
+extern "C" size_t g4_split_rows_bytes(int n, int m) {
+    return n > 0 && n % 256 == 0 && m > 0 ? (size_t)m * n * 4 + (size_t)m * 4 : 0;
+}
+
+extern "C" int g4_split_rows_f16(const float* x, void* xs, int n, int m) {
+    G4_CHECK_ARG(x && xs, "g4_split_rows_f16: null pointer");
+    G4_CHECK_ARG(n > 0 && n % 256 == 0, "g4_split_rows_f16: n=%d is not a positive multiple of 256", n);
+    G4_CHECK_ARG(m > 0, "g4_split_rows_f16: m=%d", m);
+    G4_CHECK_ARG(al16(x) && al16(xs), "g4_split_rows_f16: x and xs must be 16-byte aligned");
+    hipLaunchKernelGGL(split_rows_f16_kernel, dim3(m), dim3(256), 0, g4_stream(), x, (uint8_t*)xs, n, m);
+    return g4_check_launch("split_rows_f16_kernel");
+}
+
+extern "C" int g4_mm_batch_split(float* o, const void* w, const void* xs, int n, int d, int m, int type) {
+    G4_CHECK_ARG(o && w && xs, "g4_mm_batch_split: null pointer");
+    G4_CHECK_ARG(al16(w) && al16(xs), "g4_mm_batch_split: w and xs must be 16-byte aligned");
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0 && m > 0, "g4_mm_batch_split: n=%d d=%d m=%d", n, d, m);
+    G4_CHECK_ARG((long long)((d + 64 * kQ6RT - 1) / (64 * kQ6RT)) * ((m + 16 * kQ6NT - 1) / (16 * kQ6NT)) < (1LL << 31),
+                 "g4_mm_batch_split: %d x %d outputs too many", m, d);
+    if (type != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_batch_split: type %d has no split-activation path", type);
+    launch_mm_batch_q6s<kQ6RT, kQ6NT>((const uint8_t*)w, (const uint8_t*)xs, o, n, d, m);
+    return g4_check_launch("mm_batch_q6s_kernel");
 }

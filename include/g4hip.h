@@ -173,16 +173,38 @@ size_t g4_q8K_row_stride(int k);
  * bytes apart: quantize_row_q8_K (main.c:282) per row. */
 int g4_quantize_rows_q8_K(const float *x, void *y, int k, int m);
 /* o[t*d + r] = mm_quant_dot_rows row r on Q8_K row t (main.c:1558-1566,
- * vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K main.c:476-593), t < m, r < d.
- * Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
+ * vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K main.c:476-593), t < m, r < d:
+ * the same integer block sums and scales on the fp16 matrix cores, fp32
+ * partial sums in another order (within 1e-5 of sum |terms| of the per-token
+ * dot).  Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
 int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m, int type);
+/* g4_mm_batch_q8 for nseg (1..4) matrices of one type over the same Q8_K
+ * rows in one launch (gate and up, Q and K): o[k][t*d[k] + r] for matrix
+ * w[k] of d[k] rows.  Each output equals g4_mm_batch_q8's for that matrix. */
+int g4_mm_batch_q8_multi(float *const *o, const void *const *w, const int *d, int nseg, const void *q8, int n, int m,
+                         int type);
 /* m tokens through mm(o_t, x_t, w, n, d, type, q8, 0) (main.c:1669): Q4_K /
  * Q5_K quantize all rows into q8 (m * g4_q8K_row_stride(n) bytes) and take
- * the batched GEMM (bit-identical to the per-token path); Q6_K and BF16 with
- * n a multiple of 256 and 16-byte aligned x, w: one matrix-core GEMM on the
- * fp32 activations (the reference's dequantized fp32 weights, fp32 sums in
- * another order; q8 unused); otherwise the per-token GEMV m times. */
+ * g4_mm_batch_q8; Q6_K and BF16 with n a multiple of 256 and 16-byte aligned
+ * x, w: one fp32 matrix-core GEMM on the fp32 activations (the reference's
+ * dequantized fp32 weights, fp32 sums in another order; q8 unused);
+ * otherwise the per-token GEMV m times. */
 int g4_mm_batch(float *o, const float *x, const void *w, int n, int d, int m, int type, void *q8);
+/* Bytes of m split activation rows of n floats (n a multiple of 256): m * 4n
+ * for the rows plus 4m for the per-row scale factors; 0 for bad sizes. */
+size_t g4_split_rows_bytes(int n, int m);
+/* m fp32 rows (row stride n) -> split rows for g4_mm_batch_split: each row
+ * scaled by the power of two 2^-s that brings its largest |x| into
+ * [2^14, 2^15), written as two fp16 terms hi + lo (x 2^-s - hi - lo within
+ * 2^-22 of |x 2^-s|), permuted into the matrix-core K order; the m factors
+ * 2^s follow the rows.  x, xs 16-byte aligned. */
+int g4_split_rows_f16(const float *x, void *xs, int n, int m);
+/* o[t*d + r] = mm_quant_rows row r of split row t (main.c:1539-1556) for a
+ * planar Q6_K w: the exact products sc * (q - 32) * (hi + lo) on the fp16
+ * matrix cores (sc split as 16a + b), the block's d and the row's 2^s in
+ * fp32; within 1e-5 of sum |w x| of the reference's fp32 dot.  Q6_K only
+ * (others: G4_ERR_TYPE). */
+int g4_mm_batch_split(float *o, const void *w, const void *xs, int n, int d, int m, int type);
 
 /* ---------------------------------------------------------------------------
  * Prompt-chunk forms of the step glue (the reference runs forward() once per

@@ -166,3 +166,23 @@ def abs_dot_rows(raw: np.ndarray, qtype: int, n: int, x: np.ndarray, chunk: int 
             w = np.abs(dequant_f64(blk, qtype)).reshape(-1, n)
             out[r0:r0 + chunk] = w @ ax
     return out
+
+
+def abs_terms_q8(raw: np.ndarray, qtype: int, n: int, q8rows) -> np.ndarray:
+    """[d, m] sum of |terms| of the Q4_K / Q5_K x Q8_K dot of every row with
+    every Q8_K row (q8rows: BlockQ8_K [m, n/256]): per block
+    |y.d| * (|d| * sum_e sc_j(e) * q_e * |q8_e| + |dmin| * sum_j m_j * |bs_j|),
+    the scale of the fp32 rounding in any order of the partial sums."""
+    bpb = {12: 144, 13: 176}[qtype]
+    nb = n // 256
+    blk = raw.reshape(-1, bpb)
+    vals = (q4_values(blk) if qtype == 12 else q5_values(blk)).astype(np.float64)
+    sc, mn = unpack_scales(blk[..., 4:16])
+    d = np.abs(f16(blk[:, 0:2].copy().view(np.uint16)[:, 0]))[:, None]
+    dm = np.abs(f16(blk[:, 2:4].copy().view(np.uint16)[:, 0]))[:, None]
+    A = (d * np.repeat(sc, 32, -1) * vals).reshape(-1, n)                 # [d, n]
+    C = (dm * np.repeat(mn, 2, -1)).reshape(-1, nb * 16)                  # [d, nb*16]
+    yd = np.abs(q8rows["d"].astype(np.float64))                           # [m, nb]
+    B = (np.abs(q8rows["qs"].astype(np.float64)) * yd[..., None]).reshape(-1, n)
+    D = (np.abs(q8rows["bsums"].astype(np.float64)) * yd[..., None]).reshape(-1, nb * 16)
+    return A @ B.T + C @ D.T

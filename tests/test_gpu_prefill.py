@@ -1,26 +1,28 @@
-"""GPU parity of the batched prefill GEMMs (g4_mm_batch_q8 / g4_mm_batch):
-m tokens through one matrix on the matrix cores.
+"""GPU parity of the batched prefill GEMMs: g4_mm_batch_q8 (Q4_K / Q5_K on
+Q8_K rows), g4_split_rows_f16 + g4_mm_batch_split (Q6_K) and g4_mm_batch.
 
 The reference has no batched path; its prefill is forward() per token
 (main.c:2366-2384), i.e. quantize_row_q8_K + mm_quant_dot_rows per token for
 Q4_K / Q5_K, mm_quant_rows / mm_bf16 on the fp32 activations for Q6_K / bf16.
-Q4_K / Q5_K: bit-equality with the per-token path -- every output of the
-batched kernel has the same fp32 bits as the per-token GEMV (itself bit-exact
-to the oracle's AVX2 dot), and, for sampled tokens, as the oracle.  Q6_K /
-bf16: the weights are dequantized to the reference's fp32 values and only the
-order of the fp32 sums differs, so the bar is that of the GEMVs, 1e-5 of
-sum |w x| against the oracle; and a token's outputs do not depend on the
-other tokens of the batch or its place in it (bit for bit).
+The batched kernels compute the same sums from the same integer codes and
+scales on the matrix cores; the fp32 rounding of the partial sums is the only
+difference, so the bar is the GEMVs' one: 1e-5 of sum |terms| against the
+oracle, for every token of the small shapes and sampled tokens of the large
+ones (the 511-token E4B shapes included).  A token's outputs must not depend
+on the other tokens of the batch or its place in it (bit for bit), which is
+what makes a prompt's result independent of its chunking.
 """
 import numpy as np
 import pytest
 
+import kquant_np as kq
 import synth
 from oracle import Q8K_DTYPE
 
 pytestmark = pytest.mark.gpu
 
 P = lambda a: a.ctypes.data  # noqa: E731
+TOL = 1e-5
 
 
 @pytest.fixture(scope="module")
@@ -33,24 +35,28 @@ def lib():
 
 def _acts(rng, m, n):
     x = rng.standard_normal((m, n)).astype(np.float32)
-    x[m // 2] = 0.0                      # an all-zero token: Q8_K d = 0
+    x[m // 2] = 0.0                      # an all-zero token: Q8_K d = 0, split scale 1
     if m > 3:
         x[1] *= 1e3
         x[2, :256] = 0.0                 # one all-zero block inside a token
+    if m > 4:
+        x[3] *= 1e-6                     # small activations (the split scales them up)
     return x
 
 
-def _batch(lib, raw, qtype, n, d, x):
-    from g4 import DBuf, upload_quant
-    m = x.shape[0]
-    w = upload_quant(lib, raw, qtype, n, d)
-    xd = DBuf.from_array(lib, x)
+def _q8rows(lib, xd, n, m):
+    from g4 import DBuf
     qb = lib.L.g4_q8K_row_stride(n)
     q8 = DBuf(lib, qb * m)
     lib.g4_quantize_rows_q8_K(xd.ptr, q8.ptr, n, m)
+    return q8, qb
+
+
+def _mm_q8(lib, w, q8ptr, n, d, m, qtype):
+    from g4 import DBuf
     out = DBuf(lib, 4 * m * d)
-    lib.g4_mm_batch_q8(out.ptr, w.ptr, q8.ptr, n, d, m, qtype)
-    return w, q8, qb, out.to_array(np.float32).reshape(m, d)
+    lib.g4_mm_batch_q8(out.ptr, w.ptr, q8ptr, n, d, m, qtype)
+    return out.to_array(np.float32).reshape(m, d)
 
 
 def test_quantize_rows_equals_per_row(lib, orc):
@@ -59,9 +65,7 @@ def test_quantize_rows_equals_per_row(lib, orc):
     m, n = 7, 2560
     x = _acts(rng, m, n)
     xd = DBuf.from_array(lib, x)
-    qb = lib.L.g4_q8K_row_stride(n)
-    q8 = DBuf(lib, qb * m)
-    lib.g4_quantize_rows_q8_K(xd.ptr, q8.ptr, n, m)
+    q8, qb = _q8rows(lib, xd, n, m)
     for t in range(m):
         got = np.zeros(n // 256, Q8K_DTYPE)
         lib.g4_download_q8K(q8.ptr + t * qb, P(got), n)
@@ -71,74 +75,180 @@ def test_quantize_rows_equals_per_row(lib, orc):
 SHAPES = [(256, 80, 37), (2560, 70, 17), (2560, 2048, 64), (2048, 2560, 100), (10240, 192, 65), (2560, 10240, 130)]
 
 
+def _check_q8(orc, raw, qtype, n, d, x, got, toks):
+    q8s = np.stack([orc.quantize_q8K(x[t]) for t in toks])
+    mag = kq.abs_terms_q8(raw, qtype, n, q8s)           # [d, len(toks)]
+    for z, t in enumerate(toks):
+        want = orc.mm_quant_dot_rows(raw, n, d, qtype, q8s[z])
+        err = np.abs(got[t].astype(np.float64) - want)
+        bad = np.flatnonzero(err > TOL * mag[:, z] + 1e-30)
+        assert bad.size == 0, f"token {t}: {bad.size} rows, first {bad[:4]}: {got[t][bad[:4]]} vs {want[bad[:4]]}"
+
+
 @pytest.mark.parametrize("qtype", [12, 13])
 @pytest.mark.parametrize("n,d,m", SHAPES)
-def test_mm_batch_bitexact_vs_per_token(lib, orc, qtype, n, d, m):
-    from g4 import DBuf
+def test_mm_batch_q8_vs_oracle(lib, orc, qtype, n, d, m):
+    """Every token (every 8th on the two largest shapes) against the
+    oracle's mm_quant_dot_rows on its Q8_K row; the same token rows in a
+    batch shifted by 5 tokens give the same bits."""
+    from g4 import DBuf, upload_quant
     rng = np.random.default_rng(100 * qtype + n + d + m)
     raw = synth.rand_kquant(rng, qtype, d, n)
-    x = _acts(rng, m, n)
-    w, q8, qb, got = _batch(lib, raw, qtype, n, d, x)
-    one = DBuf(lib, 4 * d)
-    for t in range(m):
-        lib.g4_mm_quant_dot_rows(one.ptr, w.ptr, n, d, qtype, q8.ptr + t * qb)
-        want = one.to_array(np.float32)
-        bad = np.flatnonzero(got[t].view(np.uint32) != want.view(np.uint32))
-        assert bad.size == 0, f"token {t}: {bad.size} rows differ, first {bad[:4]}: {got[t][bad[:4]]} vs {want[bad[:4]]}"
-    for t in sorted({0, 1, m // 2, m - 1}):
-        want = orc.mm_quant_dot_rows(raw, n, d, qtype, orc.quantize_q8K(x[t]))
-        assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), t
-
-
-def test_mm_batch_wrapper(lib, orc):
-    """g4_mm_batch against mm() per token for every type: Q4_K/Q5_K equal it
-    bit for bit; Q6_K and bf16 (fp32 matrix-core sums) to 1e-5 of sum |w x|."""
-    from g4 import DBuf, upload_quant
-    rng = np.random.default_rng(9)
-    n, d, m = 2560, 96, 9
-    x = _acts(rng, m, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = _acts(rng, m + 5, n)
     xd = DBuf.from_array(lib, x)
-    q8 = DBuf(lib, lib.L.g4_q8K_row_stride(n) * m)
-    for qtype in (12, 13, 14, 30):
-        raw = synth.rand_bf16(rng, d, n) if qtype == 30 else synth.rand_kquant(rng, qtype, d, n)
-        w = upload_quant(lib, raw, qtype, n, d) if qtype != 30 else DBuf.from_array(lib, raw)
-        out = DBuf(lib, 4 * m * d)
-        lib.g4_mm_batch(out.ptr, xd.ptr, w.ptr, n, d, m, qtype, q8.ptr)
-        got = out.to_array(np.float32).reshape(m, d)
-        one = DBuf(lib, 4 * d)
-        q1 = DBuf(lib, lib.L.g4_q8K_bytes(n))
-        for t in range(m):
-            xt = DBuf.from_array(lib, x[t])
-            lib.g4_mm(one.ptr, xt.ptr, w.ptr, n, d, qtype, q1.ptr, 0)
-            if qtype in (12, 13):
-                assert np.array_equal(got[t].view(np.uint32), one.to_array(np.float32).view(np.uint32)), (qtype, t)
-            else:
-                mag = _mag(raw, qtype, n, d, x[t])
-                assert (np.abs(got[t] - one.to_array(np.float32)) <= 1e-5 * mag).all(), (qtype, t)
+    q8, qb = _q8rows(lib, xd, n, m + 5)
+    got = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    got2 = _mm_q8(lib, w, q8.ptr + 5 * qb, n, d, m, qtype)
+    assert np.array_equal(got[5:].view(np.uint32), got2[:m - 5].view(np.uint32))
+    toks = range(m) if d * m <= 200_000 else sorted(set(range(0, m, 8)) | {1, 2, 3, m - 1})
+    _check_q8(orc, raw, qtype, n, d, x, got, list(toks))
 
 
-def _mag(raw, qtype, n, d, x):
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_batch_q8_prefill_shape(lib, orc, qtype):
+    """The benchmarked shape: gate/up 10240 x 2560 over a 511-token chunk,
+    sampled tokens against the oracle."""
+    from g4 import DBuf, upload_quant
+    n, d, m = 2560, 10240, 511
+    rng = np.random.default_rng(31 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    got = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    _check_q8(orc, raw, qtype, n, d, x, got, [0, 1, 2, 3, 63, 64, 255, 256, 509, 510])
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_batch_q8_multi(lib, orc, qtype):
+    """Three matrices of one type over the same Q8_K rows in one launch (the
+    engine's Q|K and gate|up): each output equals the single-matrix launch
+    bit for bit, and sampled tokens are within the bar of the oracle."""
+    import ctypes as C
+    from g4 import DBuf, G4Error, upload_quant
+    n, m = 2560, 77
+    ds = (2048, 512, 200)
+    rng = np.random.default_rng(41 + qtype)
+    raws = [synth.rand_kquant(rng, qtype, d, n) for d in ds]
+    ws = [upload_quant(lib, r, qtype, n, d) for r, d in zip(raws, ds)]
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    outs = [DBuf(lib, 4 * m * d) for d in ds]
+    O = (C.c_void_p * 3)(*[o.ptr for o in outs])
+    W = (C.c_void_p * 3)(*[w.ptr for w in ws])
+    D = (C.c_int * 3)(*ds)
+    lib.g4_mm_batch_q8_multi(O, W, D, 3, q8.ptr, n, m, qtype)
+    for k, d in enumerate(ds):
+        got = outs[k].to_array(np.float32).reshape(m, d)
+        one = _mm_q8(lib, ws[k], q8.ptr, n, d, m, qtype)
+        assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), k
+        _check_q8(orc, raws[k], qtype, n, d, x, got, [0, 3, m - 1])
+    with pytest.raises(G4Error):
+        lib.g4_mm_batch_q8_multi(O, W, D, 5, q8.ptr, n, m, qtype)
+    with pytest.raises(G4Error):
+        lib.g4_mm_batch_q8_multi(O, W, D, 0, q8.ptr, n, m, qtype)
+
+
+# ---- Q6_K over split activations ----------------------------------------
+
+def _split_pos(e):
+    """element (0..255) of a block -> its half index in the split layout"""
+    h, k, s, half = e >> 7, (e >> 5) & 3, (e >> 4) & 1, (e >> 3) & 1
+    return (((2 * k + half) * 4 + 2 * h + s) << 3) | (e & 7)
+
+
+def _unsplit(raw, n, m):
+    """split bytes -> (hi, lo) as float64 [m, n] in element order, scales [m]"""
+    rows = np.frombuffer(raw[:m * n * 4].tobytes(), np.float16).reshape(m, n // 256, 2, 256)
+    perm = np.array([_split_pos(e) for e in range(256)])
+    hi = rows[:, :, 0, perm].reshape(m, n).astype(np.float64)
+    lo = rows[:, :, 1, perm].reshape(m, n).astype(np.float64)
+    sc = np.frombuffer(raw[m * n * 4:m * n * 4 + 4 * m].tobytes(), np.float32)
+    return hi, lo, sc
+
+
+def test_split_rows(lib):
+    """hi + lo reproduce x * 2^-s to 2^-22 of each |x 2^-s| (2^-25 absolute in
+    fp16's subnormal range); 2^s is a power of two that brings the row's
+    largest |x| into [2^14, 2^15); an all-zero row has factor 1."""
+    from g4 import DBuf
+    rng = np.random.default_rng(11)
+    m, n = 9, 2560
+    x = _acts(rng, m, n)
+    x[5] *= 3e4                         # above fp16's range before scaling
+    x[6, ::7] = 1e-9                    # tiny elements beside normal ones
+    x[7] *= 1e-6
+    x[7, 7] = 50.0                      # one large element among small ones
+    xd = DBuf.from_array(lib, x)
+    nbytes = lib.L.g4_split_rows_bytes(n, m)
+    assert nbytes == m * n * 4 + 4 * m
+    xs = DBuf(lib, nbytes)
+    lib.g4_split_rows_f16(xd.ptr, xs.ptr, n, m)
+    hi, lo, sc = _unsplit(xs.to_array(np.uint8), n, m)
+    for t in range(m):
+        mx = np.abs(x[t]).max()
+        if mx == 0:
+            assert sc[t] == 1.0 and not hi[t].any() and not lo[t].any()
+            continue
+        e = np.frexp(sc[t])
+        assert e[0] == 0.5, sc[t]                           # a power of two
+        xsd = x[t].astype(np.float64) / float(sc[t])
+        assert 2.0 ** 14 <= np.abs(xsd).max() < 2.0 ** 15, (t, np.abs(xsd).max())
+        err = np.abs(xsd - hi[t] - lo[t])
+        assert (err <= 2.0 ** -22 * np.abs(xsd) + 2.0 ** -25).all(), (t, err.max())
+        assert (np.abs(hi[t]) <= 2.0 ** 15).all()
+
+
+def _mag_f32(raw, qtype, n, d, x):
     """sum_j |w_ij x_j| per row, the scale of an fp32 dot's rounding"""
-    import kquant_np as kq
     if qtype == 30:
         W = (raw.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(d, n)
-    else:
-        W = kq.dequant_f64(raw.reshape(-1, 210), 14).reshape(d, n)
-    return np.abs(W) @ np.abs(x.astype(np.float64))
+        return np.abs(W) @ np.abs(x.astype(np.float64))
+    return kq.abs_dot_rows(raw, 14, n, x)
 
 
 F32W_SHAPES = [(2560, 512, 511), (2560, 1024, 130), (10240, 2560, 37), (2560, 10752, 33), (256, 40, 5),
-               (512, 256, 24), (2560, 96, 1)]
+               (512, 256, 24), (2560, 96, 1), (10240, 2560, 511)]
+
+
+def _split_mm(lib, w, xptr, n, d, m):
+    from g4 import DBuf
+    xs = DBuf(lib, lib.L.g4_split_rows_bytes(n, m))
+    lib.g4_split_rows_f16(xptr, xs.ptr, n, m)
+    out = DBuf(lib, 4 * m * d)
+    lib.g4_mm_batch_split(out.ptr, w.ptr, xs.ptr, n, d, m, 14)
+    return out.to_array(np.float32).reshape(m, d)
+
+
+@pytest.mark.parametrize("n,d,m", F32W_SHAPES)
+def test_mm_batch_split_q6k(lib, orc, n, d, m):
+    """Q6_K (V, FFN down) over m tokens: sampled tokens within 1e-5 of
+    sum |w x| of the oracle's mm_quant_rows (main.c:1539-1556); the same token
+    rows in a batch shifted by 5 tokens give the same bits."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(7 * n + d + m)
+    raw = synth.rand_q6K(rng, d, n)
+    w = upload_quant(lib, raw, 14, n, d)
+    x = _acts(rng, m + 5, n)
+    xd = DBuf.from_array(lib, x)
+    got = _split_mm(lib, w, xd.ptr, n, d, m)
+    got2 = _split_mm(lib, w, xd.ptr + 4 * 5 * n, n, d, m)
+    assert np.array_equal(got[5:].view(np.uint32), got2[:m - 5].view(np.uint32))
+    for t in sorted({0, min(1, m - 1), min(3, m - 1), m // 2, m - 1}):
+        want = orc.mm_quant_rows(x[t], raw, n, d, 14)
+        mag = _mag_f32(raw, 14, n, d, x[t])
+        err = np.abs(got[t].astype(np.float64) - want)
+        assert (err <= TOL * mag + 1e-30).all(), (t, float((err / (mag + 1e-30)).max()))
 
 
 @pytest.mark.parametrize("qtype", [14, 30])
-@pytest.mark.parametrize("n,d,m", F32W_SHAPES)
+@pytest.mark.parametrize("n,d,m", [(2560, 512, 130), (256, 40, 5), (2560, 96, 1), (512, 10752, 33)])
 def test_mm_batch_f32_weights(lib, orc, qtype, n, d, m):
-    """Q6_K (V, FFN down) and bf16 (PLE projection) over m tokens: each
-    sampled token within 1e-5 of sum |w x| of the oracle's mm_quant_rows /
-    mm_bf16 (main.c:1539-1556, 1529-1537); the same token rows in a batch
-    shifted by 5 tokens (other tile positions, other neighbours) give the
-    same bits."""
+    """The workspace-free g4_mm_batch for Q6_K and bf16 (the PLE projection):
+    fp32 matrix-core sums of the reference's dequantized weights, sampled
+    tokens within 1e-5 of sum |w x| of mm_quant_rows / mm_bf16
+    (main.c:1539-1556, 1529-1537), shift-invariant bit for bit."""
     from g4 import DBuf, upload_quant
     rng = np.random.default_rng(7 * n + d + m + qtype)
     raw = synth.rand_bf16(rng, d, n) if qtype == 30 else synth.rand_q6K(rng, d, n)
@@ -153,8 +263,33 @@ def test_mm_batch_f32_weights(lib, orc, qtype, n, d, m):
     assert np.array_equal(got[5:].view(np.uint32), got2[:m - 5].view(np.uint32))
     for t in sorted({0, min(1, m - 1), m // 2, m - 1}):
         want = orc.mm_bf16(x[t], raw, n, d) if qtype == 30 else orc.mm_quant_rows(x[t], raw, n, d, 14)
-        mag = _mag(raw, qtype, n, d, x[t])
-        assert (np.abs(got[t].astype(np.float64) - want) <= 1e-5 * mag + 1e-30).all(), t
+        mag = _mag_f32(raw, qtype, n, d, x[t])
+        assert (np.abs(got[t].astype(np.float64) - want) <= TOL * mag + 1e-30).all(), t
+
+
+def test_mm_batch_wrapper(lib, orc):
+    """g4_mm_batch for every type against the oracle per token: Q4_K / Q5_K
+    through Q8_K rows (1e-5 of sum |terms| of the Q8_K dot), Q6_K and bf16
+    (1e-5 of sum |w x|)."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(9)
+    n, d, m = 2560, 96, 9
+    x = _acts(rng, m, n)
+    xd = DBuf.from_array(lib, x)
+    q8 = DBuf(lib, lib.L.g4_q8K_row_stride(n) * m)
+    for qtype in (12, 13, 14, 30):
+        raw = synth.rand_bf16(rng, d, n) if qtype == 30 else synth.rand_kquant(rng, qtype, d, n)
+        w = upload_quant(lib, raw, qtype, n, d) if qtype != 30 else DBuf.from_array(lib, raw)
+        out = DBuf(lib, 4 * m * d)
+        lib.g4_mm_batch(out.ptr, xd.ptr, w.ptr, n, d, m, qtype, q8.ptr)
+        got = out.to_array(np.float32).reshape(m, d)
+        if qtype in (12, 13):
+            _check_q8(orc, raw, qtype, n, d, x, got, list(range(m)))
+            continue
+        for t in range(m):
+            want = orc.mm_bf16(x[t], raw, n, d) if qtype == 30 else orc.mm_quant_rows(x[t], raw, n, d, 14)
+            mag = _mag_f32(raw, qtype, n, d, x[t])
+            assert (np.abs(got[t].astype(np.float64) - want) <= TOL * mag + 1e-30).all(), (qtype, t)
 
 
 def test_mm_batch_errors(lib):
@@ -170,3 +305,8 @@ def test_mm_batch_errors(lib):
         lib.g4_mm_batch_q8(o.ptr + 4, w.ptr, q8.ptr, 256, 4, 2, 12)   # unaligned output
     with pytest.raises(G4Error):
         lib.g4_quantize_rows_q8_K(o.ptr, q8.ptr, 256, 0)
+    with pytest.raises(G4Error):
+        lib.g4_mm_batch_split(o.ptr, w.ptr, q8.ptr, 256, 4, 2, 12)   # Q4_K has no split path
+    with pytest.raises(G4Error):
+        lib.g4_split_rows_f16(o.ptr, q8.ptr, 300, 2)                # n not a multiple of 256
+    assert lib.L.g4_split_rows_bytes(300, 2) == 0
