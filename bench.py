@@ -253,7 +253,7 @@ def bench_prefill(lib, g4, synth, args):
     return res
 
 
-Q6S_MFMA_PER_FLOP = 4     # fp16 MFMA flops the split Q6_K GEMM issues per algorithmic flop
+Q6S_MFMA_PER_FLOP = 3     # fp16 MFMA flops the split Q6_K GEMM issues per algorithmic flop (Wh hi, Wh lo, Wl hi)
 
 
 def bench_prefill_e2e(lib, g4, synth, args):
@@ -261,9 +261,10 @@ def bench_prefill_e2e(lib, g4, synth, args):
     g4e_prefill of 511 tokens (chunk of 511: every layer's GEMMs, attention
     over the chunk's rows, norms, RoPE, appends, PLE).  The roofline kernel is
     the one that takes most of the time, the Q6_K GEMM on split fp16
-    activations (FFN down and V), timed alone with HIP events; it issues four
-    fp16 MFMA flops per algorithmic flop (hi and lo activation terms against
-    the two exact halves of the split scale), reported as mfma_issued."""
+    activations (FFN down and V), timed alone with HIP events; it issues three
+    fp16 MFMA flops per algorithmic flop (the weight's fp16 rounding against
+    the hi and lo activation terms, its +-1 residual against the hi term),
+    reported as mfma_issued."""
     path = _gguf_e4b(synth)
     eng = g4.Engine(path, max_seq=1024)
     rng = np.random.default_rng(4)

@@ -35,14 +35,14 @@
 //     after scaling by a power of two that brings its largest |x| into
 //     [2^14, 2^15): x * 2^-s = hi + lo + r with |r| <= 2^-22 |x * 2^-s| (or
 //     below 2^-25 in the scaled units, for elements in fp16's subnormal range);
-//   * the signed 8-bit sub-block scale is split exactly, sc = 16a + b with
-//     a = sc >> 4 in [-8, 7] and b = sc & 15, so the two weight operands
-//     16a * (q - 32) (|.| <= 4096, a multiple of 16 with at most 9 significant
-//     bits) and b * (q - 32) (|.| <= 480) are exact fp16;
-//   * four fp16 MFMAs per 32 weights (hi and lo against both weight operands)
-//     give sum sc * (q - 32) * x over a block with exact products, chained in
-//     one fp32 accumulator; the block's fp16 d is applied with one FMA per
-//     output, and the token's 2^s at the end (exact).
+//   * the integer weight w = sc * (q - 32) (|w| <= 4096) is split exactly
+//     into Wh = fp16(w) and Wl = w - Wh in {-1, 0, 1} (nonzero only for odd
+//     |w| > 2048);
+//   * three fp16 MFMAs per 32 weights, Wh hi + Wh lo + Wl hi, give
+//     sum sc * (q - 32) * x over a block with exact products (the dropped
+//     Wl lo is below 2^-22 of its term), chained in one fp32 accumulator; the
+//     block's fp16 d is applied with one FMA per output, and the token's 2^s
+//     at the end (exact).
 // The bf16 matrices and the workspace-free g4_mm_batch entry keep the fp32
 // MFMA kernel (mm_batch_f32_kernel, below).
 #include "g4_device.h"
@@ -115,6 +115,18 @@ __device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int voff, i
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
+
+// Workgroup barrier for LDS hand-offs: this wave's LDS operations complete,
+// then s_barrier.  __syncthreads() also waits for every outstanding global
+// load (its release fence), which would make each block wait for the next
+// block's prefetch; here the loads stay in flight across the barrier.  The
+// asm is a compiler barrier for memory operations as well.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// s_waitcnt immediate that waits until at most n vector memory operations
+// are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
+// lgkmcnt left at their maxima, i.e. not waited for)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 typedef float f16v_t __attribute__((ext_vector_type(16)));
 constexpr int kKqTok = 528;   // LDS bytes per staged token: 512 of fp16 + pad
@@ -248,13 +260,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     // blocks per trip so that the sets alternate without copies)
     XRaw xn;
     auto block = [&](int b, const WRaw& wc, WRaw& wnext) {
-        __syncthreads();   // the previous block's LDS reads are done
+        lds_barrier();   // the previous block's LDS reads are done
         stage(xn);
-        if (b + 1 < nb) {
-            load_w(b + 1, wnext);
-            load_x(b + 1, xn);
-        }
-        __syncthreads();
+        // the next block's loads (the last block again after the end: no
+        // branch, so the compiler's waits for them are exact)
+        const int bn = min(b + 1, nb - 1);
+        load_w(bn, wnext);
+        load_x(bn, xn);
+        lds_barrier();
 
         // scales of row i: sub-blocks 2j, 2j+1 as exact fp16 multipliers
         uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
@@ -440,7 +453,7 @@ __global__ __launch_bounds__(64 * RW) void mm_batch_f32_kernel(const uint8_t* __
     load_w(0, wn);
     load_x(0, xn);
     for (int b = 0; b < nb; b++) {
-        __syncthreads();   // the previous block's LDS reads are done
+        lds_barrier();   // the previous block's LDS reads are done
         stage(xn);
         const WRaw wc = wn;
         // the next block (the last one again at the end: an unconditional
@@ -448,7 +461,7 @@ __global__ __launch_bounds__(64 * RW) void mm_batch_f32_kernel(const uint8_t* __
         const int bn = min(b + 1, nb - 1);
         load_w(bn, wn);
         load_x(bn, xn);
-        __syncthreads();
+        lds_barrier();
 
         const float* xa = sx + i * kF32XS;
         if (BF) {
@@ -588,18 +601,30 @@ __global__ __launch_bounds__(256) void split_rows_f16_kernel(const float* __rest
 
 // Y[m x d] = X . W^T for planar Q6_K W over split activations.  A operand
 // (tokens): lane (g, i) holds the hi (or lo) terms (c, g, 0..7) of token
-// 16 nt + i; B operand (weights): 16a * (q - 32) or b * (q - 32) of the same
-// elements of row 16 rt + i.  Result lane (g, i): tokens 16 nt + 4g + v of
+// 16 nt + i; B operand (weights): Wh or Wl of the same elements of row
+// 16 rt + i.  Result lane (g, i): tokens 16 nt + 4g + v of
 // row 16 rt + i.
 constexpr int kXsStride = kSplitBlk + 16;   // LDS bytes per staged token
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (the
+// LDS address is wave-uniform: it goes to M0).  A plain device function: in
+// a kernel template's own body the builtin keeps the host pass from
+// emitting the kernel's launch stub.
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
 
 template <int RT, int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_q6s_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ xs, float* __restrict__ out, int n, int d, int m) {
     constexpr int TOK = 16 * NT;
-    constexpr int XU = TOK * (kSplitBlk / 16) / 256;   // 16-byte pieces per thread and block
-    static_assert(XU * 256 == TOK * (kSplitBlk / 16), "token tile must divide among the threads");
-    __shared__ __align__(16) uint8_t sx[TOK * kXsStride];
+    constexpr int DPW = TOK / 4;                  // direct-to-LDS copies per wave and block (one token each)
+    static_assert(DPW * 4 == TOK, "tokens per workgroup must divide among the waves");
+    // two stages: block b + 1's activations land in one while block b is read
+    // from the other
+    __shared__ __align__(16) uint8_t sx0[TOK * kXsStride];
+    __shared__ __align__(16) uint8_t sx1[TOK * kXsStride];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 15, g = lane >> 4, h = g >> 1, s = g & 1;
@@ -608,50 +633,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const int rbase = bx * (64 * RT) + wave * (16 * RT);
     const int tokb = by * TOK;
     const int nb = n >> 8;
-    const Q6KPlanes P = q6k_planes((size_t)d * nb);
+    const size_t nblk = (size_t)d * nb;
+    const Q6KPlanes P = q6k_planes(nblk);
     const size_t xrow = (size_t)n * 4;
 
-    size_t rB[RT];
+    // weights through buffer loads: per-lane offsets fixed, the block's
+    // offset in a scalar register
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(P.d + 2 * nblk), kBufWord3);
+    int vql[RT], vqh[RT], vsc[RT], vd[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) rB[rt] = (size_t)min(rbase + 16 * rt + i, d - 1) * nb;
-
+    for (int rt = 0; rt < RT; rt++) {
+        const int rB = min(rbase + 16 * rt + i, d - 1) * nb;
+        vql[rt] = (int)P.ql + rB * 128 + 32 * g;
+        vqh[rt] = (int)P.qh + rB * 64 + 16 * g;
+        vsc[rt] = (int)P.sc + rB * 16 + 8 * h;
+        vd[rt] = (int)P.d + rB * 2;
+    }
     struct WRaw {
         uint4 ql[RT][2];   // lane group g's 32 ql bytes
         uint4 qh[RT];      // its 16 qh bytes
         uint2 sc[RT];      // scales of sub-blocks 8h .. 8h+7
         uint32_t dh[RT];
     };
-    struct XRaw {
-        uint4 v[XU];
-    };
     auto load_w = [&](int b, WRaw& r) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
-            const size_t blk = rB[rt] + b;
-            const uint4* ql = reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 32 * g);
-            r.ql[rt][0] = ql[0];
-            r.ql[rt][1] = ql[1];
-            r.qh[rt] = *reinterpret_cast<const uint4*>(w + P.qh + blk * 64 + 16 * g);
-            r.sc[rt] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
-            r.dh[rt] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
+            r.ql[rt][0] = buf_load16(rw, vql[rt], b * 128);
+            r.ql[rt][1] = buf_load16(rw, vql[rt] + 16, b * 128);
+            r.qh[rt] = buf_load16(rw, vqh[rt], b * 64);
+            r.sc[rt] = buf_load8(rw, vsc[rt], b * 16);
+            r.dh[rt] = __builtin_amdgcn_raw_buffer_load_b16(rw, vd[rt], b * 2, 0);
         }
     };
-    // piece u = tid + j * 256: token u >> 6, bytes 16 (u & 63) of its block
-    auto load_x = [&](int b, XRaw& r) {
+    constexpr int WLOADS = 5 * RT;                // load instructions of load_w
+    // block b's activations of token tokb + wave + 4q -> stage row wave + 4q:
+    // one 1 KB copy per wave instruction, 16 bytes per lane (tokens past m
+    // repeat the last one; their outputs are not stored)
+    // (buffer-to-LDS loads: one lane offset register, the token's row and the
+    // block in a scalar offset)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, (int)(m * xrow), kBufWord3);
+    int xrows[DPW];
 #pragma unroll
-        for (int j = 0; j < XU; j++) {
-            const int u = tid + j * 256;
-            r.v[j] = *reinterpret_cast<const uint4*>(xs + (size_t)min(tokb + (u >> 6), m - 1) * xrow +
-                                                     (size_t)b * kSplitBlk + 16 * (u & 63));
-        }
-    };
-    auto stage = [&](const XRaw& r) {
+    for (int q = 0; q < DPW; q++) xrows[q] = min(tokb + wave + 4 * q, m - 1) * (int)xrow;
+    auto dma = [&](int b, uint8_t* stage) {
 #pragma unroll
-        for (int j = 0; j < XU; j++) {
-            const int u = tid + j * 256;
-            *reinterpret_cast<uint4*>(sx + (u >> 6) * kXsStride + 16 * (u & 63)) =
-                tokb + (u >> 6) < m ? r.v[j] : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int q = 0; q < DPW; q++)
+            buf_load_lds16(rx, stage + (wave + 4 * q) * kXsStride, 16 * lane, xrows[q] + b * kSplitBlk);
     };
 
     f4_t acc[RT][NT];
@@ -662,22 +689,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const f4_t zero = {0.f, 0.f, 0.f, 0.f};
     const h2_t m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
 
-    WRaw wn;
-    XRaw xn;
-    load_w(0, wn);
-    load_x(0, xn);
-    for (int b = 0; b < nb; b++) {
-        __syncthreads();   // the previous block's LDS reads are done
-        stage(xn);
-        const WRaw wc = wn;
-        if (b + 1 < nb) {
-            load_w(b + 1, wn);
-            load_x(b + 1, xn);
-        }
-        __syncthreads();
+    // one block from stage cur and weight set wc, with block b + 1's weights
+    // and activations on their way into wn and nxt
+    auto block = [&](int b, const uint8_t* cur, uint8_t* nxt, const WRaw& wc, WRaw& wn) {
+        lds_barrier();   // block b - 1's reads of nxt are done
+        // block b + 1's loads (the last block again after the end: no branch,
+        // so the wait counts below are exact on every path)
+        const int bn = min(b + 1, nb - 1);
+        load_w(bn, wn);
+        dma(bn, nxt);
+        // everything issued before them has landed: block b's copies (issued
+        // one block earlier) and its weights
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(WLOADS + DPW));
+        lds_barrier();   // every wave's copies of block b are in cur
 
         f4_t S[RT][NT];
-        const uint8_t* xa0 = sx + i * kXsStride + 16 * g;
+        const uint8_t* xa0 = cur + i * kXsStride + 16 * g;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const int k = c >> 1, half = c & 1;
@@ -696,16 +723,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 const h2_t v1 = bits_h2(__builtin_amdgcn_perm(kMagic, q0, kSelHi)) + m1056;
                 const h2_t v2 = bits_h2(__builtin_amdgcn_perm(kMagic, q1, kSelLo)) + m1056;
                 const h2_t v3 = bits_h2(__builtin_amdgcn_perm(kMagic, q1, kSelHi)) + m1056;
-                // scale of sub-block 8h + 2k + s: byte 2k + s; sc = 16a + b, b in [-8, 7]
+                // scale of sub-block 8h + 2k + s: byte 2k + s.  w = sc * (q - 32)
+                // = Wh + Wl: Wh its fp16 rounding, Wl in {-1, 0, 1} (exact)
                 const int sb = 2 * k + s;
-                const int sc = (int)(int8_t)byte_of(sb < 4 ? wc.sc[rt].x : wc.sc[rt].y, sb & 3);
-                const int a = (sc + 8) >> 4;
-                const _Float16 fa = (_Float16)(float)(16 * a), fb = (_Float16)(float)(sc - 16 * a);
-                const h2_t FA = {fa, fa}, FB = {fb, fb};
-                Wa[rt] = __builtin_bit_cast(h8_t, make_uint4(h2_bits(v0 * FA), h2_bits(v1 * FA), h2_bits(v2 * FA),
-                                                             h2_bits(v3 * FA)));
-                Wb[rt] = __builtin_bit_cast(h8_t, make_uint4(h2_bits(v0 * FB), h2_bits(v1 * FB), h2_bits(v2 * FB),
-                                                             h2_bits(v3 * FB)));
+                const _Float16 scf = (_Float16)(float)(int)(int8_t)byte_of(sb < 4 ? wc.sc[rt].x : wc.sc[rt].y, sb & 3);
+                const h2_t SC = {scf, scf};
+                const h2_t w0 = v0 * SC, w1 = v1 * SC, w2 = v2 * SC, w3 = v3 * SC;
+                Wa[rt] = __builtin_bit_cast(h8_t, make_uint4(h2_bits(w0), h2_bits(w1), h2_bits(w2), h2_bits(w3)));
+                Wb[rt] = __builtin_bit_cast(
+                    h8_t, make_uint4(h2_bits(__builtin_elementwise_fma(v0, SC, -w0)), h2_bits(__builtin_elementwise_fma(v1, SC, -w1)),
+                                     h2_bits(__builtin_elementwise_fma(v2, SC, -w2)), h2_bits(__builtin_elementwise_fma(v3, SC, -w3))));
             }
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
@@ -714,10 +741,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 const h8_t Al = *reinterpret_cast<const h8_t*>(xa + 512);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
+                    // Wh xh + Wh xl + Wl xh (Wl xl is below 2^-22 of the term)
                     f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wa[rt], c == 0 ? zero : S[rt][nt], 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wb[rt], t, 0, 0, 0);
                     t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Wa[rt], t, 0, 0, 0);
-                    S[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Wb[rt], t, 0, 0, 0);
+                    S[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wb[rt], t, 0, 0, 0);
                 }
             }
         }
@@ -729,6 +756,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[rt][nt][v] = __builtin_fmaf(dw, S[rt][nt][v], acc[rt][nt][v]);
         }
+    };
+
+    WRaw w0, w1;
+    load_w(0, w0);
+    dma(0, sx0);
+    for (int b = 0; b < nb; b += 2) {
+        block(b, sx0, sx1, w0, w1);
+        if (b + 1 < nb) block(b + 1, sx1, sx0, w1, w0);
     }
 
     const float* tsc = reinterpret_cast<const float*>(xs + (size_t)m * xrow);
@@ -863,6 +898,9 @@ extern "C" int g4_split_rows_f16(const float* x, void* xs, int n, int m) {
 
 extern "C" int g4_mm_batch_split(float* o, const void* w, const void* xs, int n, int d, int m, int type) {
     G4_CHECK_ARG(o && w && xs, "g4_mm_batch_split: null pointer");
+    // the kernel addresses both operands with 32-bit buffer offsets
+    G4_CHECK_ARG((size_t)m * n * 4 < (1u << 31) && (size_t)d * (n / 256) * 210 < (1u << 31),
+                 "g4_mm_batch_split: %d x %d weights or %d rows exceed 2 GiB", d, n, m);
     G4_CHECK_ARG(al16(w) && al16(xs), "g4_mm_batch_split: w and xs must be 16-byte aligned");
     G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0 && m > 0, "g4_mm_batch_split: n=%d d=%d m=%d", n, d, m);
     G4_CHECK_ARG((long long)((d + 64 * kQ6RT - 1) / (64 * kQ6RT)) * ((m + 16 * kQ6NT - 1) / (16 * kQ6NT)) < (1LL << 31),
