@@ -672,20 +672,20 @@ __host__ __device__ constexpr int chunk_ppw() {   // positions per wave per roun
     return (HD == 256 ? 8 : 4) < 32 / KVM ? (HD == 256 ? 8 : 4) : 32 / KVM;
 }
 
-__host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2) {
-    return (size_t)4 * kvm_pow2 * (hd + 2) * 4;
+__host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2, int nw = kAttnThreads / 64) {
+    return (size_t)nw * kvm_pow2 * (hd + 2) * 4;
 }
 
 // DB: two register sets, round r + 1's rows loading while round r is
 // reduced (decode: few workgroups, each one's latency counts); without it
 // the register count allows twice the workgroups per CU (prompt-chunk rows:
 // thousands of workgroups, occupancy counts)
-template <int HD, int KVM, bool DB>
-__global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
+template <int HD, int KVM, bool DB, int NTH = kAttnThreads, int PPW_ = 0>
+__global__ __launch_bounds__(NTH) void attn_chunk_kernel(AttnArgs a) {
     if (a.qrows) attn_query_row(a, false);
     constexpr int W = HD / 128;
-    constexpr int NW = kAttnThreads / 64;
-    constexpr int PPW = chunk_ppw<HD, KVM>();
+    constexpr int NW = NTH / 64;
+    constexpr int PPW = PPW_ ? PPW_ : chunk_ppw<HD, KVM>();
     constexpr int V = PPW * KVM;                  // score values per wave and round
     constexpr int LV = V == 32 ? 5 : V == 16 ? 4 : V == 8 ? 3 : V == 4 ? 2 : V == 2 ? 1 : 0;
     constexpr int LK = KVM == 8 ? 3 : KVM == 4 ? 2 : KVM == 2 ? 1 : 0;
@@ -886,7 +886,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     // a thread per (head, 4 dims): the waves' weights exp(m_w - M) once,
     // then its dims (the partial rows are 8-byte aligned: float2 stores)
     constexpr int Q4 = HD / 4;
-    for (int i = tid; i < kvm * Q4; i += kAttnThreads) {
+    for (int i = tid; i < kvm * Q4; i += NTH) {
         const int h = i / Q4, d4 = i - h * Q4;
         float mw[NW], M = -INFINITY;
 #pragma unroll
@@ -1005,6 +1005,20 @@ void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
         else if (kp == 2) hipLaunchKernelGGL((attn_chunk_kernel<HD, 2, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
         else if (kp == 4) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
         else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
+        return;
+    }
+    // decode over long windows (64+ chunks, i.e. about one workgroup per CU
+    // for two kv heads): eight waves per workgroup, twice the rows in flight
+    // per CU.  hd 256: two register sets of 4 positions per wave (172 VGPRs);
+    // hd 512: one set (32K positions: 34.6 against 38.6 us at hd 256, 55.1
+    // against 56.1 us at hd 512, chunk + merge)
+    if (kp == 4 && a.G >= 64) {
+        if constexpr (HD == 256)
+            hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true, 512, 4>), grid, dim3(512), attn_chunk_lds(HD, kp, 8),
+                               g4_stream(), a);
+        else
+            hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false, 512>), grid, dim3(512), attn_chunk_lds(HD, kp, 8),
+                               g4_stream(), a);
         return;
     }
     if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
