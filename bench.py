@@ -126,6 +126,9 @@ def _copies(nbytes: int) -> int:
     return max(2, -(-MALL_BYTES // nbytes))
 
 
+GEMV_KERNEL = "gemv_q45_stream_kernel<Q4_K> 10240x2560"
+
+
 def bench_gemv(lib, g4, synth, args):
     """Q4_K x Q8_K GEMV 10240x2560; rotates weight copies so every launch reads HBM."""
     n, d = 2560, 10240
@@ -152,7 +155,7 @@ def bench_gemv(lib, g4, synth, args):
         "ms_per_step": ms / args.steps, "dtype": "int8xu4->int32, fp32 combine",
         "config": {"workload": "Q4_K x Q8_K GEMV 10240x2560 (seed 0), batch 1", "rows": d, "n": n,
                    "weight_copies_rotated": ncp},
-        "roofline": dict(roofline(algo, per_launch, "gemv_q45k_kernel"), kernel="gemv_q45k_kernel",
+        "roofline": dict(roofline(algo, per_launch, GEMV_KERNEL), kernel=GEMV_KERNEL,
                          bytes_per_launch=algo),
     }
     if not args.no_cpu:
@@ -370,6 +373,9 @@ def cpu_prefill_baseline(raw, n, d, tokens: int = 4):
                       f"{len(ts)} runs, OpenMP {thr} threads"}
 
 
+LMHEAD_KERNEL = "gemv_q6k_rows_kernel<Q6_K, softcap> 262144x2560"
+
+
 def bench_lmhead(lib, g4, synth, args):
     """Tied LM head: Q6_K 262144x2560 x fp32 hidden, fused soft-cap (550 MB > MALL)."""
     n, d = 2560, 262144
@@ -391,7 +397,8 @@ def bench_lmhead(lib, g4, synth, args):
         "value": round(algo / per / 1e9, 1), "unit": "GB/s", "higher_is_better": True,
         "ms_per_step": ms / args.steps, "dtype": "f32",
         "config": {"workload": "tied LM head Q6_K 262144x2560 x fp32, softcap 30 (seed 2)"},
-        "roofline": dict(roofline(algo, per), kernel="gemv_q6k_f32_kernel", bytes_per_launch=algo),
+        "roofline": dict(roofline(algo, per, LMHEAD_KERNEL), kernel=LMHEAD_KERNEL, bytes_per_launch=algo,
+                         us_per_launch=round(per * 1e6, 2)),
     }
     return res
 
@@ -467,6 +474,9 @@ def _attn_chunks(cap: int) -> int:
     return G
 
 
+ATTN_KERNEL = "attn_chunk_kernel + attn_merge_kernel (global T=32768, hd 256)"
+
+
 def bench_attn(lib, g4, synth, args):
     """ISWA decode attention, one layer's step: q/k norms, Neox RoPE, the
     K/V append and softmax(q.K) V over the cache (g4_attn_decode_fused, the
@@ -522,8 +532,8 @@ def bench_attn(lib, g4, synth, args):
                                "kv heads, fp32 KV cache, N(0,1) inputs (seed 3); value: global T=32768 hd 256",
                    "cases": cases},
         "roofline": {"bound": "hbm", "achieved": h["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": h["frac"],
-                     "traffic": measured_traffic("attn_chunk_kernel<256,4> T=32768"),
-                     "kernel": "attn_chunk_kernel<256,4> + attn_merge_kernel<256> (global T=32768, hd 256)",
+                     "traffic": measured_traffic(ATTN_KERNEL),
+                     "kernel": ATTN_KERNEL,
                      "bytes_per_launch": h["kv_bytes"], "us_per_launch": h["us"]},
     }
     if not args.no_cpu:
