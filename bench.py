@@ -256,6 +256,7 @@ def bench_prefill(lib, g4, synth, args):
     return res
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3    # MI355X dense fp32 matrix peak (the bf16 PLE projection's instruction)
 Q6S_MFMA_PER_FLOP = 3     # fp16 MFMA flops the split Q6_K GEMM issues per algorithmic flop (Wh hi, Wh lo, Wl hi)
 
 
@@ -636,6 +637,17 @@ def bench_decode(lib, g4, synth, args):
                    "prefill_tok_s_token_serial": round(n_serial / t_serial, 1),
                    "gguf_write_s": round(t_gen, 1)},
     }
+    # matrix-core use of the batched prefill: algorithmic GEMM flops of the
+    # 511 tokens over the prefill's wall time, and the share of that time the
+    # issued matrix-core work would take at its instructions' peaks (fp16
+    # MFMA for the K-quant GEMMs: one issued flop per flop for Q4_K/Q5_K,
+    # three for the split Q6_K; fp32 MFMA for the bf16 PLE projection)
+    mm = synth.prefill_matmuls(synth.E4B)
+    flops = sum(2.0 * n * d for _, _, n, d in mm) * (n_prompt - 1)
+    issued_s = sum(2.0 * n * d * (n_prompt - 1) * (3 if t == g4.Q6_K else 1) /
+                   ((FP32_MFMA_PEAK_TFLOPS if t == synth.BF16 else FP16_MFMA_PEAK_TFLOPS) * 1e12) for _, t, n, d in mm)
+    res["config"]["prefill_gemm_tflops"] = round(flops / t_prefill / 1e12, 1)
+    res["config"]["prefill_mfma_util"] = round(issued_s / t_prefill, 4)
     _log("dominant-kernel roofline")
     res["roofline"] = _gate_up_roofline(lib, g4, synth)
     res["decode_hbm_GBps"] = round(synth.decode_weight_bytes(synth.E4B) * tps / 1e9, 1)

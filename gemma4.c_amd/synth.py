@@ -312,6 +312,14 @@ def decode_weight_bytes(s: ModelShape) -> int:
     return total
 
 
+def prefill_matmuls(s: ModelShape) -> list[tuple[str, int, int, int]]:
+    """(name, type, n, d) of the matrices a prompt token runs through in the
+    batched prefill: every 2-D tensor but the two embedding tables (looked
+    up, not multiplied; the LM head runs only for the last token)."""
+    return [(t.name, t.qtype, t.ne[0], t.ne[1]) for t in model_tensors(s)
+            if len(t.ne) == 2 and t.name not in ("token_embd.weight", "per_layer_token_embd.weight")]
+
+
 def e4b_gguf(seed: int = 4) -> str:
     """Path of the synthetic E4B-shape GGUF of `seed` (about 5.4 GB), written
     once per machine into /dev/shm (or /tmp)."""
