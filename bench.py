@@ -8,6 +8,9 @@ Workloads (synthetic inputs, generated from fixed seeds on the host):
           262144, Q4_K_M weight mix, random init; a step is one decode token
           (the default; the metric's workload)
   gemv    one Q4_K x Q8_K GEMV 10240x2560 (seed 0)
+  layer   one E4B sliding-window layer's decode projections (Q|K|V, O,
+          gate|up, down) as the engine launches them, and the Q5_K gate|up
+          variant (seed 1)
   gateup  the fused gate|up GELU GEMV at its decode shape, Q4_K 2 x 10240x2560
           (seed 1): the decode's dominant kernel alone
   lmhead  tied LM head, Q6_K 262144x2560 times an fp32 hidden vector, with the
@@ -194,6 +197,139 @@ def cpu_gemv_baseline(raw, x, n, d, algo):
     return {"value": round(algo / med / 1e9, 2), "unit": "GB/s", "cores": thr, "kind": kind,
             "sample": f"quantize_row_q8_K + mm_quant_dot_rows (Q4_K 10240x2560), median of {len(ts)} runs "
                       f"after 3 warm-ups, OpenMP {thr} threads"}
+
+
+def bench_layer(lib, g4, synth, args):
+    """One E4B sliding-window layer's decode projections at batch 1 (seed 1),
+    launched as the engine launches them: Q|K (Q4_K) and V (Q6_K) in one
+    launch with the residual/norm/Q8_K prologue, O (Q4_K, Q8_K of the
+    attention output ready), the fused gate|up GELU (Q4_K) and down (Q6_K on
+    the fp32 hidden vector).  Weight copies rotated through >= 512 MB.  value:
+    weight bytes over the four launches' time; config: each projection alone
+    and the Q5_K gate|up variant."""
+    n, hid, nq, nkv = 2560, 10240, 2048, 512
+    rng = np.random.default_rng(1)
+    raws = {"q": synth.rand_q4K(rng, nq, n), "k": synth.rand_q4K(rng, nkv, n),
+            "v": synth.rand_kquant(rng, g4.Q6_K, nkv, n), "o": synth.rand_q4K(rng, n, nq),
+            "gate": synth.rand_q4K(rng, hid, n), "up": synth.rand_q4K(rng, hid, n),
+            "down": synth.rand_kquant(rng, g4.Q6_K, n, hid),
+            "gate5": synth.rand_kquant(rng, g4.Q5_K, hid, n), "up5": synth.rand_kquant(rng, g4.Q5_K, hid, n)}
+    shapes = {"q": (g4.Q4_K, n, nq), "k": (g4.Q4_K, n, nkv), "v": (g4.Q6_K, n, nkv), "o": (g4.Q4_K, nq, n),
+              "gate": (g4.Q4_K, n, hid), "up": (g4.Q4_K, n, hid), "down": (g4.Q6_K, hid, n),
+              "gate5": (g4.Q5_K, n, hid), "up5": (g4.Q5_K, n, hid)}
+    layer_bytes = sum(raws[k].nbytes for k in ("q", "k", "v", "o", "gate", "up", "down"))
+    ncp = _copies(layer_bytes + raws["gate5"].nbytes + raws["up5"].nbytes)
+    W = [{k: g4.upload_quant(lib, raws[k], *shapes[k]) for k in raws} for _ in range(ncp)]
+    vec = lambda m, s=1.0: g4.DBuf.from_array(lib, (rng.standard_normal(m) * s).astype(np.float32))
+    x, y = vec(n), vec(n, 4.0)
+    wpost = g4.DBuf.from_array(lib, rng.uniform(0.5, 1.5, n).astype(np.float32))
+    wnext = g4.DBuf.from_array(lib, rng.uniform(0.5, 1.5, n).astype(np.float32))
+    osc = g4.DBuf.from_array(lib, np.array([0.9], np.float32))
+    attn, hb = vec(nq), vec(hid)
+    xo, xb2 = g4.DBuf(lib, 4 * n), g4.DBuf(lib, 4 * n)
+    q, k, v, o, hbo, down = (g4.DBuf(lib, 4 * m) for m in (nq, nkv, nkv, n, hid, n))
+    q8 = g4.DBuf(lib, lib.L.g4_q8K_bytes(n))
+    q8o = g4.DBuf(lib, lib.L.g4_q8K_bytes(nq))
+    lib.g4_quantize_row_q8_K(attn.ptr, q8o.ptr, nq)
+    lib.g4_quantize_row_q8_K(x.ptr, q8.ptr, n)
+    eps = C.c_float(1e-6)
+    L = lib.L
+
+    def qkv(i):
+        w = W[i % ncp]
+        L.g4_mm_residual_q8_qkv(q.ptr, w["q"].ptr, nq, k.ptr, w["k"].ptr, nkv, v.ptr, w["v"].ptr, nkv, g4.Q6_K, n,
+                                g4.Q4_K, x.ptr, xo.ptr, y.ptr, wpost.ptr, osc.ptr, wnext.ptr, xb2.ptr, None, eps)
+
+    def oproj(i):
+        L.g4_mm_quant_dot_rows(o.ptr, W[i % ncp]["o"].ptr, nq, n, g4.Q4_K, q8o.ptr)
+
+    def gateup(i, sfx=""):
+        w = W[i % ncp]
+        L.g4_mm_gate_up_gelu(hbo.ptr, w["gate" + sfx].ptr, w["up" + sfx].ptr, n, hid,
+                             g4.Q5_K if sfx else g4.Q4_K, q8.ptr)
+
+    def dproj(i):
+        L.g4_mm_quant_rows(down.ptr, hb.ptr, W[i % ncp]["down"].ptr, hid, n, g4.Q6_K)
+
+    def layer(i):
+        qkv(i)
+        oproj(i)
+        gateup(i)
+        dproj(i)
+
+    class A:
+        warmup, steps = args.warmup, args.steps
+    ms = _time_steps(lib, layer, A)
+    per = ms / 1e3 / args.steps
+    parts = {}
+    for name, f, b in (("q|k|v", qkv, raws["q"].nbytes + raws["k"].nbytes + raws["v"].nbytes),
+                       ("o", oproj, raws["o"].nbytes), ("gate|up", gateup, raws["gate"].nbytes + raws["up"].nbytes),
+                       ("down", dproj, raws["down"].nbytes),
+                       ("gate|up Q5_K", lambda i: gateup(i, "5"), raws["gate5"].nbytes + raws["up5"].nbytes)):
+        t = _time_steps(lib, f, A) / 1e3 / args.steps
+        parts[name] = {"us": round(t * 1e6, 2), "weight_bytes": b, "GBps": round(b / t / 1e9, 1)}
+    q5_bytes = layer_bytes - raws["gate"].nbytes - raws["up"].nbytes + raws["gate5"].nbytes + raws["up5"].nbytes
+    q5_per = per - parts["gate|up"]["us"] / 1e6 + parts["gate|up Q5_K"]["us"] / 1e6
+    res = {"value": round(layer_bytes / per / 1e9, 1), "unit": "GB/s", "higher_is_better": True,
+           "ms_per_step": ms / args.steps, "dtype": "int8xu4->int32 (Q4_K/Q5_K), fp32 (Q6_K)",
+           "config": {"workload": "one E4B sliding-window layer's decode projections, batch 1 (seed 1): Q|K Q4_K + V "
+                                  "Q6_K (residual/norm/Q8_K prologue), O Q4_K, gate|up GELU Q4_K, down Q6_K",
+                      "weight_bytes": layer_bytes, "us_per_layer": round(per * 1e6, 2), "launches": 4,
+                      "weight_copies_rotated": ncp, "projections": parts,
+                      "q5k_gateup_variant": {"weight_bytes": q5_bytes, "us_per_layer": round(q5_per * 1e6, 2),
+                                             "GBps": round(q5_bytes / q5_per / 1e9, 1)}},
+           "roofline": dict(roofline(layer_bytes, per, "layer projections"), kernel="the four launches of one layer",
+                            bytes_per_launch=layer_bytes)}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_layer_baseline(raws, shapes, layer_bytes)
+    return res
+
+
+def cpu_layer_baseline(raws, shapes, layer_bytes):
+    """The same projections through the reference's own functions when
+    oracle/_ref is built (quantize_row_q8_K + mm_quant_dot_rows for Q4_K,
+    mm_quant_rows for Q6_K), else the oracle's restatement."""
+    import oracle as orc_mod
+    thr = cpu_threads()
+    rng = np.random.default_rng(11)
+    n = 2560
+    x = rng.standard_normal(n).astype(np.float32)
+    xa = rng.standard_normal(2048).astype(np.float32)
+    hb = rng.standard_normal(10240).astype(np.float32)
+    ref = orc_mod.Ref() if orc_mod.Ref.available() else None
+    orc = orc_mod.Oracle()
+    kind = "reference" if ref else "port"
+    L = ref.L if ref else orc.L
+    pre = "ref_" if ref else "or_"
+    qz, dot, rows = (getattr(L, pre + s) for s in (("quantize_row_q8_K" if ref else "quantize_q8K"),
+                                                  "mm_quant_dot_rows", "mm_quant_rows"))
+    P = lambda a: a.ctypes.data  # noqa: E731
+    q8 = np.zeros(n // 256, orc_mod.Q8K_DTYPE)
+    q8a = np.zeros(2048 // 256, orc_mod.Q8K_DTYPE)
+    outs = {k: np.empty(shapes[k][2], np.float32) for k in raws}
+
+    def run():
+        qz(P(x), P(q8), n)
+        for kname in ("q", "k"):
+            dot(P(outs[kname]), P(raws[kname]), n, shapes[kname][2], 12, P(q8))
+        rows(P(outs["v"]), P(x), P(raws["v"]), n, shapes["v"][2], 14)
+        qz(P(xa), P(q8a), 2048)
+        dot(P(outs["o"]), P(raws["o"]), 2048, n, 12, P(q8a))
+        for kname in ("gate", "up"):
+            dot(P(outs[kname]), P(raws[kname]), n, 10240, 12, P(q8))
+        rows(P(outs["down"]), P(hb), P(raws["down"]), 10240, n, 14)
+    run()
+    ts = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end or len(ts) < 5:
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(layer_bytes / med / 1e9, 2), "unit": "GB/s", "cores": thr, "kind": kind,
+            "host": cpu_host(),
+            "sample": f"one layer's projections (Q8_K of the input, Q/K/O/gate/up mm_quant_dot_rows, V/down "
+                      f"mm_quant_rows), median of {len(ts)} runs, OpenMP {thr} threads"}
 
 
 FP16_MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 matrix peak (the instruction the prefill GEMM issues)
@@ -401,7 +537,37 @@ def bench_lmhead(lib, g4, synth, args):
         "roofline": dict(roofline(algo, per, LMHEAD_KERNEL), kernel=LMHEAD_KERNEL, bytes_per_launch=algo,
                          us_per_launch=round(per * 1e6, 2)),
     }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_lmhead_baseline(raw, x, n)
     return res
+
+
+def cpu_lmhead_baseline(raw, x, n, rows: int = 32768):
+    """logits_tied's product on the CPU: the reference's mm_quant_rows
+    (oracle/_ref when built, else the oracle's restatement) over the first
+    `rows` rows of the same table, soft-cap included, as GB/s of weights."""
+    import oracle as orc_mod
+    thr = cpu_threads()
+    ref = orc_mod.Ref() if orc_mod.Ref.available() else None
+    fn = ref.L.ref_mm_quant_rows if ref else orc_mod.Oracle().L.or_mm_quant_rows
+    part = np.ascontiguousarray(raw[:rows])      # rows of 10 Q6_K blocks: the row-major GGUF layout
+    o = np.empty(rows, np.float32)
+
+    def run():
+        fn(o.ctypes.data, x.ctypes.data, part.ctypes.data, n, rows, 14)
+        np.tanh(o / 30.0) * 30.0
+    run()
+    ts = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end or len(ts) < 5:
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(part.nbytes / med / 1e9, 2), "unit": "GB/s", "cores": thr,
+            "kind": "reference" if ref else "port", "host": cpu_host(),
+            "sample": f"mm_quant_rows + soft-cap over the first {rows} of the 262144 rows ({part.nbytes} B of "
+                      f"weights), median of {len(ts)} runs, OpenMP {thr} threads"}
 
 
 def bench_copy(lib, g4, synth, args):
@@ -718,7 +884,8 @@ def _time_steps(lib, step, args) -> float:
 
 
 WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
-             "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e, "attn": bench_attn}
+             "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e, "attn": bench_attn,
+             "layer": bench_layer}
 
 
 def main() -> int:
