@@ -599,6 +599,60 @@ __global__ __launch_bounds__(256) void split_rows_f16_kernel(const float* __rest
     if (tid == 0) reinterpret_cast<float*>(xs + (size_t)m * n * 4)[t] = ldexpf(1.0f, -k);
 }
 
+// gelu(g) * u of one row (the FFN's GELU gate, main.c:1976-1980) split as
+// split_rows_f16_kernel splits a row: one workgroup per row; each thread
+// keeps the values of its runs of 8 in registers between the max and the
+// split, so the product never goes to memory.  NG: runs of 8 per thread
+// (n = 2048 * NG).
+template <int NG>
+__global__ __launch_bounds__(256) void gelu_mul_split_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                             int ustride, uint8_t* __restrict__ xs, int n, int m) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float4* gr = reinterpret_cast<const float4*>(g + (size_t)t * n);
+    const float4* ur = reinterpret_cast<const float4*>(u + (size_t)t * ustride);
+    float v[NG][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NG; k++) {
+        const int q = tid + 256 * k;
+        const float4 g0 = gr[2 * q], g1 = gr[2 * q + 1], u0 = ur[2 * q], u1 = ur[2 * q + 1];
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            v[k][j] = gelu_ref(gg[j]) * uu[j];
+            mx = fmaxf(mx, fabsf(v[k][j]));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    (void)frexpf(mx, &E);
+    const int k2 = mx > 0.0f && mx <= 3.402823466e38f ? min(max(15 - E, -126), 126) : 0;
+    const float sf = ldexpf(1.0f, k2);
+    uint8_t* row = xs + (size_t)t * n * 4;
+#pragma unroll
+    for (int k = 0; k < NG; k++) {
+        h8_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float sv = v[k][j] * sf;
+            const _Float16 hv = (_Float16)sv;
+            hi[j] = hv;
+            lo[j] = (_Float16)(sv - (float)hv);
+        }
+        const int e = 8 * (tid + 256 * k);
+        uint8_t* dst = row + (size_t)(e >> 8) * kSplitBlk + 2 * split_pos(e & 255);
+        *reinterpret_cast<h8_t*>(dst) = hi;
+        *reinterpret_cast<h8_t*>(dst + 512) = lo;
+    }
+    if (tid == 0) reinterpret_cast<float*>(xs + (size_t)m * n * 4)[t] = ldexpf(1.0f, -k2);
+}
+
 // Y[m x d] = X . W^T for planar Q6_K W over split activations.  A operand
 // (tokens): lane (g, i) holds the hi (or lo) terms (c, g, 0..7) of token
 // 16 nt + i; B operand (weights): Wh or Wl of the same elements of row
@@ -894,6 +948,25 @@ extern "C" int g4_split_rows_f16(const float* x, void* xs, int n, int m) {
     G4_CHECK_ARG(al16(x) && al16(xs), "g4_split_rows_f16: x and xs must be 16-byte aligned");
     hipLaunchKernelGGL(split_rows_f16_kernel, dim3(m), dim3(256), 0, g4_stream(), x, (uint8_t*)xs, n, m);
     return g4_check_launch("split_rows_f16_kernel");
+}
+
+extern "C" int g4_gelu_mul_split_rows(const float* g, const float* u, int ustride, void* xs, int n, int m) {
+    G4_CHECK_ARG(g && u && xs, "g4_gelu_mul_split_rows: null pointer");
+    G4_CHECK_ARG(n == 2048 || n == 4096 || n == 8192 || n == 10240 || n == 12288 || n == 16384,
+                 "g4_gelu_mul_split_rows: n=%d (2048 * k, k in 1, 2, 4, 5, 6, 8)", n);
+    G4_CHECK_ARG(m > 0 && ustride >= n && ustride % 4 == 0, "g4_gelu_mul_split_rows: m=%d ustride=%d", m, ustride);
+    G4_CHECK_ARG(al16(g) && al16(u) && al16(xs), "g4_gelu_mul_split_rows: g, u and xs must be 16-byte aligned");
+    const dim3 grid(m), blk(256);
+    uint8_t* x = (uint8_t*)xs;
+    switch (n / 2048) {
+    case 1: hipLaunchKernelGGL(gelu_mul_split_kernel<1>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    case 2: hipLaunchKernelGGL(gelu_mul_split_kernel<2>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    case 4: hipLaunchKernelGGL(gelu_mul_split_kernel<4>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    case 5: hipLaunchKernelGGL(gelu_mul_split_kernel<5>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    case 6: hipLaunchKernelGGL(gelu_mul_split_kernel<6>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    default: hipLaunchKernelGGL(gelu_mul_split_kernel<8>, grid, blk, 0, g4_stream(), g, u, ustride, x, n, m); break;
+    }
+    return g4_check_launch("gelu_mul_split_kernel");
 }
 
 extern "C" int g4_mm_batch_split(float* o, const void* w, const void* xs, int n, int d, int m, int type) {

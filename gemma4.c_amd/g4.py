@@ -73,6 +73,7 @@ _SIGS = {
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
     "g4_split_rows_bytes": (SZ, [I, I]),
     "g4_split_rows_f16": (I, [VP, VP, I, I]),
+    "g4_gelu_mul_split_rows": (I, [VP, VP, I, VP, I, I]),
     "g4_mm_batch_split": (I, [VP, VP, VP, I, I, I, I]),
     "g4_mm_f16": (I, [VP, VP, VP, I, I]),
     "g4_mm_f32": (I, [VP, VP, VP, I, I]),

@@ -205,6 +205,12 @@ int g4_split_rows_f16(const float *x, void *xs, int n, int m);
  * fp32; within 1e-5 of sum |w x| of the reference's fp32 dot.  Q6_K only
  * (others: G4_ERR_TYPE). */
 int g4_mm_batch_split(float *o, const void *w, const void *xs, int n, int d, int m, int type);
+/* g4_gelu_mul_rows (o = gelu(g) * u, rows of n, u rows ustride floats apart)
+ * followed by g4_split_rows_f16 of o in one launch, without o: the split rows
+ * of the FFN's GELU gate (main.c:1976-1980) for the Q6_K down GEMM.  n =
+ * 2048 * k for k in {1, 2, 4, 5, 6, 8}; xs as for g4_split_rows_f16, bit for
+ * bit what the two launches produce. */
+int g4_gelu_mul_split_rows(const float *g, const float *u, int ustride, void *xs, int n, int m);
 
 /* ---------------------------------------------------------------------------
  * Prompt-chunk forms of the step glue (the reference runs forward() once per

@@ -200,6 +200,30 @@ def test_split_rows(lib):
         assert (np.abs(hi[t]) <= 2.0 ** 15).all()
 
 
+@pytest.mark.parametrize("n,m,ustride", [(10240, 37, 10240), (2048, 5, 2100), (4096, 1, 4096), (10240, 511, 10240)])
+def test_gelu_mul_split_rows(lib, n, m, ustride):
+    """gelu(g) * u split in one launch: byte for byte g4_gelu_mul_rows followed
+    by g4_split_rows_f16, with an all-zero row, a row far above fp16's range,
+    tiny rows and u rows wider than g's; unsupported widths are refused."""
+    from g4 import DBuf, G4Error
+    rng = np.random.default_rng(n + m)
+    g = (rng.standard_normal((m, n)) * 2).astype(np.float32)
+    u = rng.standard_normal((m, ustride)).astype(np.float32)
+    if m > 3:
+        g[1] = 0.0
+        u[2] *= 1e5
+        g[3] *= 1e-4
+    gd, ud = DBuf.from_array(lib, g), DBuf.from_array(lib, u)
+    nbytes = lib.L.g4_split_rows_bytes(n, m)
+    got, h, want = DBuf(lib, nbytes), DBuf(lib, 4 * m * n), DBuf(lib, nbytes)
+    lib.g4_gelu_mul_split_rows(gd.ptr, ud.ptr, ustride, got.ptr, n, m)
+    lib.g4_gelu_mul_rows(h.ptr, gd.ptr, ud.ptr, n, m, ustride)
+    lib.g4_split_rows_f16(h.ptr, want.ptr, n, m)
+    assert np.array_equal(got.to_array(np.uint8), want.to_array(np.uint8))
+    with pytest.raises(G4Error):
+        lib.g4_gelu_mul_split_rows(gd.ptr, ud.ptr, ustride, got.ptr, 2560, m)
+
+
 def _mag_f32(raw, qtype, n, d, x):
     """sum_j |w_ij x_j| per row, the scale of an fp32 dot's rounding"""
     if qtype == 30:
