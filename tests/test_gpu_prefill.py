@@ -266,6 +266,46 @@ def test_mm_batch_split_q6k(lib, orc, n, d, m):
         assert (err <= TOL * mag + 1e-30).all(), (t, float((err / (mag + 1e-30)).max()))
 
 
+@pytest.mark.parametrize("n,d", [(2560, 512), (10240, 2560)])
+def test_mm_batch_split_every_token(lib, n, d):
+    """Every token of a 511-token batch (V and FFN down at the E4B shape)
+    within 1e-5 of sum |w x| of the exact float64 product.  Each wave of the
+    kernel copies its tokens' activation rows straight into LDS one block
+    ahead; a wait that let a wave's last copy still be in flight at the
+    barrier corrupted the rows of one token in sixteen now and then (offsets
+    12-15 of a tile), which sampled tokens did not catch."""
+    from g4 import DBuf, upload_quant
+    m = 511
+    rng = np.random.default_rng(n + d + 9)
+    raw = synth.rand_q6K(rng, d, n)
+    w = upload_quant(lib, raw, 14, n, d)
+    x = _acts(rng, m, n)
+    got = _split_mm(lib, w, DBuf.from_array(lib, x).ptr, n, d, m)
+    W = kq.dequant_f64(raw.reshape(-1, 210), 14).reshape(d, n)
+    want = x.astype(np.float64) @ W.T
+    mag = np.abs(x).astype(np.float64) @ np.abs(W).T
+    err = np.abs(got - want)
+    bad = np.argwhere(err > TOL * mag + 1e-30)
+    assert bad.size == 0, f"{len(bad)} outputs, first (token, row) {bad[:6].tolist()}"
+
+
+@pytest.mark.parametrize("d", [2560, 512])
+def test_mm_batch_split_token_tiles(lib, d):
+    """The launch takes 16- or 32-token workgroups by the grid's size (FFN
+    down at 511 tokens 32, at 37 tokens 16; V 16 at both); a token's outputs
+    are the same bits either way, so a prompt's result does not depend on its
+    chunking."""
+    from g4 import DBuf, upload_quant
+    n = 10240 if d == 2560 else 2560
+    rng = np.random.default_rng(d + 5)
+    raw = synth.rand_q6K(rng, d, n)
+    w = upload_quant(lib, raw, 14, n, d)
+    xd = DBuf.from_array(lib, _acts(rng, 511, n))
+    full = _split_mm(lib, w, xd.ptr, n, d, 511)
+    part = _split_mm(lib, w, xd.ptr, n, d, 37)
+    assert np.array_equal(full[:37].view(np.uint32), part.view(np.uint32))
+
+
 @pytest.mark.parametrize("qtype", [14, 30])
 @pytest.mark.parametrize("n,d,m", [(2560, 512, 130), (256, 40, 5), (2560, 96, 1), (512, 10752, 33)])
 def test_mm_batch_f32_weights(lib, orc, qtype, n, d, m):
