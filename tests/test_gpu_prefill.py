@@ -121,6 +121,29 @@ def test_mm_batch_q8_prefill_shape(lib, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_batch_q8_every_token(lib, orc, qtype):
+    """Every token of the benchmarked gate/up shape (10240 x 2560, 511 tokens)
+    within 1e-5 of sum |terms| of the exact float64 product of the dequantized
+    weights with each token's Q8_K row (the sampled-token checks above would
+    miss an error confined to a few tokens of a tile)."""
+    from g4 import DBuf, upload_quant
+    n, d, m = 2560, 10240, 511
+    rng = np.random.default_rng(61 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    got = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    q8s = np.stack([orc.quantize_q8K(x[t]) for t in range(m)])
+    W = kq.dequant_f64(raw.reshape(-1, {12: 144, 13: 176}[qtype]), qtype).reshape(d, n)
+    X = (q8s["qs"].astype(np.float64) * q8s["d"].astype(np.float64)[..., None]).reshape(m, n)
+    want = X @ W.T
+    mag = kq.abs_terms_q8(raw, qtype, n, q8s).T
+    bad = np.argwhere(np.abs(got - want) > TOL * mag + 1e-30)
+    assert bad.size == 0, f"{len(bad)} outputs, first (token, row) {bad[:6].tolist()}"
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
 def test_mm_batch_q8_multi(lib, orc, qtype):
     """Three matrices of one type over the same Q8_K rows in one launch (the
     engine's Q|K and gate|up): each output equals the single-matrix launch
