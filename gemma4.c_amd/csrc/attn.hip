@@ -991,6 +991,186 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
+// ---- query rows of a prompt chunk on the matrix cores ---------------------
+// The same partials as attn_chunk_kernel's query-row mode (one (o, max, sum)
+// per row, q head and chunk, merged by attn_merge_kernel), for 16 query rows
+// at once: workgroup (c, kvh, rb) takes rows 16rb .. 16rb+15 and chunk c of
+// the key range those rows see, and wave h is q head kvh*4 + h (4 q heads per
+// kv head).  Each 16-key tile of K and V is read from HBM once for the 16
+// rows and 4 heads and staged in LDS; per tile and wave
+//   S^T (16 keys x 16 rows) = K . Q^T      HD/4 v_mfma_f32_16x16x4_f32
+//   O^T (HD x 16 rows)     += V^T . P^T    HD/4 v_mfma_f32_16x16x4_f32
+// with fp32 products and sums (the reference's per-row dot products and
+// weighted V sums, gemma4-4b/cpu-blas/main.c:1909-1950, in another order).
+// 16x16x4 operands: lane l = 16g + j supplies A[j][g] and B[g][j] and holds
+// D[4g + r][j] in register r.  S^T: the K index of step s is dim
+// (HD/4)g + s, so a lane reads 4 consecutive dims of key j (LDS) and of row
+// j's q (registers).  P^T for the second product is S^T's registers as they
+// are: step r takes key 4g + r of lane group g, so A of step r is
+// V[4g + r][.]; A row j of O tile b is dim (HD/16)j + b, so a lane's V reads
+// are 4 consecutive dims too and register r of O tile b in lane 16g + j is
+// dim (HD/16)(4g + r) + b of row j.
+// Chunks: the rows' key range [lo, hi] (lo = the first row's window start,
+// hi = the last row's position) in G pieces of a multiple of 16 keys; keys
+// outside a row's own window get weight 0 (and a chunk without any of a
+// row's keys leaves (0, -inf, 0), which the merge ignores).  Keys are
+// loaded clamped to the chunk, so every row read is a position in [lo, hi]
+// that the cache or the chunk's K/V rows hold.
+constexpr int kRowsKVM = 4;
+typedef float f4_t __attribute__((ext_vector_type(4)));
+// a global-memory f4_t: the integer select between the cache and the chunk's
+// rows below would otherwise leave a generic pointer, i.e. flat loads, which
+// the LDS waits also count
+typedef __attribute__((address_space(1))) const f4_t g4_gf4_t;
+
+template <int HD>
+__global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs a) {
+    constexpr int NTH = 64 * kRowsKVM;
+    constexpr int RS = HD + 4;            // LDS row stride (floats): conflict-free 16-byte K reads
+    constexpr int QS = HD / 4;            // score steps; q values per lane
+    constexpr int NB = HD / 16;           // O tiles
+    constexpr int LU = 16 * (HD / 4) / NTH;   // float4 of K (and of V) per thread and tile
+    static_assert(LU * NTH == 16 * (HD / 4), "tile staging");
+    __shared__ __align__(16) float ks[16 * RS];
+    __shared__ __align__(16) float vs[16 * RS];
+    const int c = blockIdx.x, kvh = blockIdx.y, rb = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, j = lane & 15;
+    const int head = kvh * kRowsKVM + wave;
+    const int M = a.qrows;
+    const int z0 = 16 * rb, z1 = min(z0 + 16, M) - 1;
+    const int lo = a.window > 0 ? max(0, a.p0 + z0 + 1 - a.window) : 0;
+    const int hi = a.p0 + z1;
+    const int cs = ((hi - lo + a.G) / a.G + 15) & ~15;    // ceil((hi - lo + 1) / G), whole tiles
+    const int cb = lo + c * cs, ce = min(cb + cs, hi + 1);
+    // this lane's query row, its position and window start
+    const int z = z0 + j;
+    const int qp = a.p0 + z;
+    const int qlo = a.window > 0 ? max(0, qp + 1 - a.window) : 0;
+
+    // K/V of a tile: thread tid stages float4 c4 of key `key` for u < LU
+    // (the next tile's are loaded while this one is used; past the last tile
+    // the last one is loaded again, so that no branch guards the loads)
+    f4_t kr[LU], vr[LU];   // (HIP's float4 copies as a struct: an array of them stays in scratch)
+    const float* kcb = a.kc + (size_t)kvh * HD;
+    const float* vcb = a.vc + (size_t)kvh * HD;
+    const float* kqb = a.kchunk + (size_t)kvh * HD;
+    const float* vqb = a.vchunk + (size_t)kvh * HD;
+    const int tl = ce - 1;
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int idx = u * NTH + tid, key = idx / (HD / 4), c4 = idx - key * (HD / 4);
+            const int t = min(t0 + key, tl);
+            const bool own = t >= a.p0;
+            const size_t off = (size_t)(own ? t - a.p0 : attn_slot(a, t)) * a.kv_stride;
+            const uintptr_t kb = own ? (uintptr_t)kqb : (uintptr_t)kcb;
+            const uintptr_t vb = own ? (uintptr_t)vqb : (uintptr_t)vcb;
+            kr[u] = reinterpret_cast<const g4_gf4_t*>(kb + 4 * off)[c4];
+            vr[u] = reinterpret_cast<const g4_gf4_t*>(vb + 4 * off)[c4];
+        }
+    };
+    load_tile(cb);   // an empty chunk (cb > hi) loads position hi: ce - 1 = hi
+
+    float q[QS];
+    {
+        const float4* qv = reinterpret_cast<const float4*>(a.q + (size_t)min(z, M - 1) * a.n_heads * HD +
+                                                           (size_t)head * HD + QS * g);
+#pragma unroll
+        for (int s = 0; s < QS / 4; s++) {
+            const float4 t = qv[s];
+            q[4 * s] = t.x;
+            q[4 * s + 1] = t.y;
+            q[4 * s + 2] = t.z;
+            q[4 * s + 3] = t.w;
+        }
+    }
+
+    float m = -INFINITY, lsum = 0.0f;   // lsum: this lane's keys only (summed over the groups at the end)
+    f4_t o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) o[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t0 = cb; t0 < ce; t0 += 16) {
+        __syncthreads();   // every wave is done with the previous tile
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int idx = u * NTH + tid, key = idx / (HD / 4), c4 = idx - key * (HD / 4);
+            *reinterpret_cast<f4_t*>(ks + key * RS + 4 * c4) = kr[u];
+            *reinterpret_cast<f4_t*>(vs + key * RS + 4 * c4) = vr[u];
+        }
+        __syncthreads();
+        load_tile(t0 + 16 < ce ? t0 + 16 : t0);
+
+        // scores: four accumulators, so that no step waits for the previous one
+        f4_t acc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[k] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* kl = ks + j * RS + QS * g;
+#pragma unroll
+        for (int s = 0; s < QS; s += 4) {
+            const float4 kv = *reinterpret_cast<const float4*>(kl + s);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, q[s], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, q[s + 1], acc[1], 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, q[s + 2], acc[2], 0, 0, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, q[s + 3], acc[3], 0, 0, 0);
+        }
+        const f4_t sc = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+
+        // online softmax over the tile's keys 4g + r of row j
+        float sv[4], mt = -INFINITY;
+        bool val[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int kt = t0 + 4 * g + r;
+            val[r] = kt < ce && kt >= qlo && kt <= qp;
+            sv[r] = val[r] ? a.scale * sc[r] : -INFINITY;
+            mt = fmaxf(mt, sv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = val[r] ? expf(sv[r] - mn) : 0.0f;
+            ps += p[r];
+        }
+        lsum = lsum * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int b = 0; b < NB; b++) o[b] *= alpha;
+
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float* vl = vs + (4 * g + r) * RS + NB * j;
+#pragma unroll
+            for (int b = 0; b < NB; b += 4) {
+                const float4 vv = *reinterpret_cast<const float4*>(vl + b);
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[r], o[b], 0, 0, 0);
+                o[b + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[r], o[b + 1], 0, 0, 0);
+                o[b + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[r], o[b + 2], 0, 0, 0);
+                o[b + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[r], o[b + 3], 0, 0, 0);
+            }
+        }
+    }
+
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (z < M) {
+        float* pp = a.part + (size_t)z * a.part_z + ((size_t)head * a.G + c) * (HD + 2);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int b = 0; b < NB; b += 2)
+                *reinterpret_cast<float2*>(pp + NB * (4 * g + r) + b) = make_float2(o[b][r], o[b + 1][r]);
+        if (g == 0) {
+            pp[HD] = m;
+            pp[HD + 1] = lsum;
+        }
+    }
+}
+
 // partial kernel LDS: work region + (max, sum) pairs [+ this position's K, V]
 size_t attn_lds(int hd, int kvm, bool fused) {
     return 4 * (fused ? (size_t)attn_new_kv_off(hd, kvm) + 2 * (size_t)hd
@@ -1041,6 +1221,12 @@ int launch_attn(const AttnArgs& a) {
     // q heads per kv head rounded up to a power of two (the register kernel's
     // template); its LDS must fit the default 64 KB
     const int kp = kvm <= 1 ? 1 : kvm <= 2 ? 2 : kvm <= 4 ? 4 : 8;
+    if (a.qrows && kvm == kRowsKVM && a.hd == 256) {
+        const dim3 rgrid(a.G, a.n_kv, (a.qrows + 15) / 16);
+        hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
+        launch_merge<256>(a, dim3(a.n_heads, 1, zq));
+        return g4_check_launch("attn_rows_mfma_kernel/attn_merge_kernel");
+    }
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
         if (a.hd == 256) {
             launch_chunk<256>(a, kp, grid);
