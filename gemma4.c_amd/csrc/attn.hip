@@ -1017,6 +1017,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
 // loaded clamped to the chunk, so every row read is a position in [lo, hi]
 // that the cache or the chunk's K/V rows hold.
 constexpr int kRowsKVM = 4;
+constexpr float kRowsLazy = 8.0f;
 typedef float f4_t __attribute__((ext_vector_type(4)));
 // a global-memory f4_t: the integer select between the cache and the chunk's
 // rows below would otherwise leave a generic pointer, i.e. flat loads, which
@@ -1024,15 +1025,16 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const f4_t g4_gf4_t;
 
 template <int HD>
-__global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 1))) void attn_rows_mfma_kernel(AttnArgs a) {
     constexpr int NTH = 64 * kRowsKVM;
-    constexpr int RS = HD + 4;            // LDS row stride (floats): conflict-free 16-byte K reads
+    constexpr int RS = HD + 4;            // K row stride (floats): conflict-free 16-byte reads
+    constexpr int RV = HD / 16 * 20;      // V row: every 16 dims followed by 4 floats of padding
     constexpr int QS = HD / 4;            // score steps; q values per lane
     constexpr int NB = HD / 16;           // O tiles
     constexpr int LU = 16 * (HD / 4) / NTH;   // float4 of K (and of V) per thread and tile
     static_assert(LU * NTH == 16 * (HD / 4), "tile staging");
     __shared__ __align__(16) float ks[16 * RS];
-    __shared__ __align__(16) float vs[16 * RS];
+    __shared__ __align__(16) float vs[16 * RV];
     const int c = blockIdx.x, kvh = blockIdx.y, rb = blockIdx.z;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, j = lane & 15;
     const int head = kvh * kRowsKVM + wave;
@@ -1095,7 +1097,7 @@ __global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs 
         for (int u = 0; u < LU; u++) {
             const int idx = u * NTH + tid, key = idx / (HD / 4), c4 = idx - key * (HD / 4);
             *reinterpret_cast<f4_t*>(ks + key * RS + 4 * c4) = kr[u];
-            *reinterpret_cast<f4_t*>(vs + key * RS + 4 * c4) = vr[u];
+            *reinterpret_cast<f4_t*>(vs + key * RV + 4 * c4 + 4 * (c4 >> 2)) = vr[u];
         }
         __syncthreads();
         load_tile(t0 + 16 < ce ? t0 + 16 : t0);
@@ -1106,12 +1108,12 @@ __global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs 
         for (int k = 0; k < 4; k++) acc[k] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         const float* kl = ks + j * RS + QS * g;
 #pragma unroll
-        for (int s = 0; s < QS; s += 4) {
-            const float4 kv = *reinterpret_cast<const float4*>(kl + s);
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, q[s], acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, q[s + 1], acc[1], 0, 0, 0);
-            acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, q[s + 2], acc[2], 0, 0, 0);
-            acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, q[s + 3], acc[3], 0, 0, 0);
+        for (int s = 0; s < QS / 4; s++) {
+            const f4_t k4 = *reinterpret_cast<const f4_t*>(kl + 4 * s);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[0], q[4 * s], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[1], q[4 * s + 1], acc[1], 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[2], q[4 * s + 2], acc[2], 0, 0, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[3], q[4 * s + 3], acc[3], 0, 0, 0);
         }
         const f4_t sc = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
@@ -1127,8 +1129,12 @@ __global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs 
         }
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
-        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+        // the running max moves only when a score exceeds it by more than
+        // kRowsLazy (weights stay <= e^kRowsLazy); o and lsum are rescaled
+        // only then, and only in waves where some row moved it
+        const bool up = mt > m + kRowsLazy;   // also the first finite score (m = -inf)
+        const float mn = up ? mt : m;
+        const float alpha = !up ? 1.0f : m == -INFINITY ? 0.0f : expf(m - mn);
         float p[4], ps = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -1137,20 +1143,22 @@ __global__ __launch_bounds__(64 * kRowsKVM) void attn_rows_mfma_kernel(AttnArgs 
         }
         lsum = lsum * alpha + ps;
         m = mn;
+        if (__ballot(up)) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) o[b] *= alpha;
+            for (int b = 0; b < NB; b++) o[b] *= alpha;
+        }
 
         // O^T += V^T . P^T
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float* vl = vs + (4 * g + r) * RS + NB * j;
+            const float* vl = vs + (4 * g + r) * RV + NB / 16 * 20 * j;   // dim NB*j
 #pragma unroll
             for (int b = 0; b < NB; b += 4) {
-                const float4 vv = *reinterpret_cast<const float4*>(vl + b);
-                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[r], o[b], 0, 0, 0);
-                o[b + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[r], o[b + 1], 0, 0, 0);
-                o[b + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[r], o[b + 2], 0, 0, 0);
-                o[b + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[r], o[b + 3], 0, 0, 0);
+                const f4_t v4 = *reinterpret_cast<const f4_t*>(vl + b + 4 * (b >> 4));
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[0], p[r], o[b], 0, 0, 0);
+                o[b + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[1], p[r], o[b + 1], 0, 0, 0);
+                o[b + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[2], p[r], o[b + 2], 0, 0, 0);
+                o[b + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[3], p[r], o[b + 3], 0, 0, 0);
             }
         }
     }
@@ -1221,10 +1229,15 @@ int launch_attn(const AttnArgs& a) {
     // q heads per kv head rounded up to a power of two (the register kernel's
     // template); its LDS must fit the default 64 KB
     const int kp = kvm <= 1 ? 1 : kvm <= 2 ? 2 : kvm <= 4 ? 4 : 8;
-    if (a.qrows && kvm == kRowsKVM && a.hd == 256) {
+    if (a.qrows && kvm == kRowsKVM) {
         const dim3 rgrid(a.G, a.n_kv, (a.qrows + 15) / 16);
-        hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
-        launch_merge<256>(a, dim3(a.n_heads, 1, zq));
+        if (a.hd == 256) {
+            hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
+            launch_merge<256>(a, dim3(a.n_heads, 1, zq));
+        } else {
+            hipLaunchKernelGGL(attn_rows_mfma_kernel<512>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
+            launch_merge<512>(a, dim3(a.n_heads, 2, zq));
+        }
         return g4_check_launch("attn_rows_mfma_kernel/attn_merge_kernel");
     }
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
