@@ -669,22 +669,25 @@ __device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, uint8_t
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
 }
 
-template <int RT, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_q6s_kernel(
+template <int RT, int NT, int NS, int NWV>
+__global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ xs, float* __restrict__ out, int n, int d, int m) {
     constexpr int TOK = 16 * NT;
-    constexpr int DPW = TOK / 4;                  // direct-to-LDS copies per wave and block (one token each)
-    static_assert(DPW * 4 == TOK, "tokens per workgroup must divide among the waves");
-    // two stages: block b + 1's activations land in one while block b is read
-    // from the other
-    __shared__ __align__(16) uint8_t sx0[TOK * kXsStride];
-    __shared__ __align__(16) uint8_t sx1[TOK * kXsStride];
+    // direct-to-LDS copies per block (one token each): wave w takes tokens
+    // w, w + NWV, ... (DPW or DPW + 1 of them)
+    constexpr int DPW = TOK / NWV, DPX = (TOK + NWV - 1) / NWV;
+    static_assert(DPW >= 1, "every wave copies a token");
+    // NS stages: blocks b + 1 .. b + NS - 1 are on their way while block b is
+    // read (the loads take longer than a block's products)
+    __shared__ __align__(16) uint8_t sx[NS][TOK * kXsStride];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (the wave index read as uniform: the copies' scalar offsets below then
+    // need no per-lane loop)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, g = lane >> 4, h = g >> 1, s = g & 1;
     int bx, by;
     xcd_tile((m + TOK - 1) / TOK, bx, by);
-    const int rbase = bx * (64 * RT) + wave * (16 * RT);
+    const int rbase = bx * (16 * RT * NWV) + wave * (16 * RT);
     const int tokb = by * TOK;
     const int nb = n >> 8;
     const size_t nblk = (size_t)d * nb;
@@ -719,19 +722,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             r.dh[rt] = __builtin_amdgcn_raw_buffer_load_b16(rw, vd[rt], b * 2, 0);
         }
     };
-    // block b's activations of token tokb + wave + 4q -> stage row wave + 4q:
+    // block b's activations of token tokb + wave + NWV q -> stage row wave + NWV q:
     // one 1 KB copy per wave instruction, 16 bytes per lane (tokens past m
     // repeat the last one; their outputs are not stored)
     // (buffer-to-LDS loads: one lane offset register, the token's row and the
     // block in a scalar offset)
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, (int)(m * xrow), kBufWord3);
-    int xrows[DPW];
+    int xrows[DPX];
 #pragma unroll
-    for (int q = 0; q < DPW; q++) xrows[q] = min(tokb + wave + 4 * q, m - 1) * (int)xrow;
+    for (int q = 0; q < DPX; q++) xrows[q] = min(tokb + wave + NWV * q, m - 1) * (int)xrow;
     auto dma = [&](int b, uint8_t* stage) {
 #pragma unroll
-        for (int q = 0; q < DPW; q++)
-            buf_load_lds16(rx, stage + (wave + 4 * q) * kXsStride, 16 * lane, xrows[q] + b * kSplitBlk);
+        for (int q = 0; q < DPX; q++)
+            if (DPX == DPW || wave + NWV * q < TOK)
+                buf_load_lds16(rx, stage + (wave + NWV * q) * kXsStride, 16 * lane, xrows[q] + b * kSplitBlk);
     };
 
     f4_t acc[RT][NT];
@@ -742,29 +746,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const f4_t zero = {0.f, 0.f, 0.f, 0.f};
     const h2_t m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
 
-    // one block from stage cur and weight set wc, with block b + 1's weights
-    // and activations on their way into wn and nxt
+    // one block from stage cur and weight set wc, with block b + NS - 1's
+    // weights and activations sent into wn and nxt
     auto block = [&](int b, const uint8_t* cur, uint8_t* nxt, const WRaw& wc, WRaw& wn) {
         lds_barrier();   // block b - 1's reads of nxt are done
-        // block b + 1's copies (the last block again after the end: no branch),
-        // then a wait that leaves at most those DPW in flight: everything
-        // issued before them has landed, block b's copies (issued one block
-        // earlier) included.  Counting only the copies keeps the wait correct
-        // wherever the compiler places the weight loads: it has moved them
-        // past the compute of the block before, and a wait that also counted
-        // them then let a wave's last copy of block b still be in flight when
-        // the barrier below released the other waves to read it
-        const int bn = min(b + 1, nb - 1);
+        // block b + NS - 1's copies (the last block again after the end: no
+        // branch), then a wait that leaves at most the copies of blocks
+        // b + 1 .. b + NS - 1 in flight: everything issued before them has
+        // landed, block b's copies included.  Counting only the copies keeps
+        // the wait correct wherever the compiler places the weight loads (it
+        // has moved them past the compute of the block before): weight loads
+        // among the most recent operations only make it wait for more
+        const int bn = min(b + NS - 1, nb - 1);
         dma(bn, nxt);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(DPW));
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(DPW * (NS - 1)));   // (DPW: the fewest copies a wave issues)
         load_w(bn, wn);
         lds_barrier();   // every wave's copies of block b are in cur
 
         f4_t S[RT][NT];
         const uint8_t* xa0 = cur + i * kXsStride + 16 * g;
+        // activation operands one step ahead of their products
+        h8_t Ah[2][NT], Al[2][NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            Ah[0][nt] = *reinterpret_cast<const h8_t*>(xa0 + 16 * nt * kXsStride);
+            Al[0][nt] = *reinterpret_cast<const h8_t*>(xa0 + 16 * nt * kXsStride + 512);
+        }
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const int k = c >> 1, half = c & 1;
+            const int k = c >> 1, half = c & 1, cb = c & 1;
+            if (c + 1 < 8) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const uint8_t* xa = xa0 + 16 * nt * kXsStride + 64 * (c + 1);
+                    Ah[cb ^ 1][nt] = *reinterpret_cast<const h8_t*>(xa);
+                    Al[cb ^ 1][nt] = *reinterpret_cast<const h8_t*>(xa + 512);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of this step's products
             h8_t Wa[RT], Wb[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
@@ -793,15 +812,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             }
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const uint8_t* xa = xa0 + 16 * nt * kXsStride + 64 * c;
-                const h8_t Ah = *reinterpret_cast<const h8_t*>(xa);
-                const h8_t Al = *reinterpret_cast<const h8_t*>(xa + 512);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     // Wh xh + Wh xl + Wl xh (Wl xl is below 2^-22 of the term)
-                    f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wa[rt], c == 0 ? zero : S[rt][nt], 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, Wa[rt], t, 0, 0, 0);
-                    S[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, Wb[rt], t, 0, 0, 0);
+                    f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah[cb][nt], Wa[rt], c == 0 ? zero : S[rt][nt], 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al[cb][nt], Wa[rt], t, 0, 0, 0);
+                    S[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah[cb][nt], Wb[rt], t, 0, 0, 0);
                 }
             }
         }
@@ -815,13 +831,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
     };
 
-    WRaw w0, w1;
-    load_w(0, w0);
-    dma(0, sx0);
-    for (int b = 0; b < nb; b += 2) {
-        block(b, sx0, sx1, w0, w1);
-        if (b + 1 < nb) block(b + 1, sx1, sx0, w1, w0);
+    WRaw wr[NS];
+#pragma unroll
+    for (int k = 0; k < NS - 1; k++) {
+        load_w(min(k, nb - 1), wr[k]);
+        dma(min(k, nb - 1), sx[k]);
     }
+    for (int b = 0; b < nb; b += NS) {
+#pragma unroll
+        for (int k = 0; k < NS; k++)
+            if (b + k < nb) block(b + k, sx[k], sx[(k + NS - 1) % NS], wr[k], wr[(k + NS - 1) % NS]);
+    }
+    // the copies of the clamped blocks past the end are still in flight:
+    // they land in LDS before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
     const float* tsc = reinterpret_cast<const float*>(xs + (size_t)m * xrow);
 #pragma unroll
@@ -839,21 +862,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
 }
 
-constexpr int kQ6RT = 1, kQ6NT = 2;
+constexpr int kQ6RT = 1, kQ6NS = 2;
 
-template <int RT, int NT>
+template <int NT, int NWV>
 void launch_mm_batch_q6s(const uint8_t* w, const uint8_t* xs, float* o, int n, int d, int m) {
-    const int gx = (d + 64 * RT - 1) / (64 * RT), gy = (m + 16 * NT - 1) / (16 * NT);
-    hipLaunchKernelGGL((mm_batch_q6s_kernel<RT, NT>), dim3(gx * gy), dim3(256), 0, g4_stream(), w, xs, o, n, d, m);
+    const int gx = (d + 16 * kQ6RT * NWV - 1) / (16 * kQ6RT * NWV), gy = (m + 16 * NT - 1) / (16 * NT);
+    hipLaunchKernelGGL((mm_batch_q6s_kernel<kQ6RT, NT, kQ6NS, NWV>), dim3(gx * gy), dim3(64 * NWV), 0, g4_stream(), w, xs,
+                       o, n, d, m);
 }
 
-// 32 tokens per workgroup, or 16 when the 32-token grid would not fill one
-// round of resident workgroups (two per CU): V (512 rows) over 511 tokens
-// 14.3 against 19.2 us; FFN down (2560 rows) keeps 32 (159 against 174 us)
+// Workgroup shapes, measured at 2560 x 10240 (FFN down) on MI355X:
+//   * 160 rows (ten waves) x 32 tokens when that grid has at least 3/4 of a
+//     workgroup per CU: at 511 tokens exactly one per CU, 131 against 155 us
+//     for 64-row workgroups (640 of them: 1.25 rounds of two per CU); 260
+//     against 281 us at 1024 tokens, equal at 200;
+//   * else 64 rows x 32 tokens, or x 16 when the 32-token grid would not fill
+//     one round of resident workgroups (two per CU): V (512 rows) over 511
+//     tokens 14.3 against 19.2 us; FFN down at 64 tokens 45 against 92 us for
+//     the ten-wave shape.
+// Deeper pipelines (activations 2 or 3 blocks ahead) measured slower in
+// every shape: the copies' throughput, not their latency, sets the pace.
 void launch_q6s_auto(const uint8_t* w, const uint8_t* xs, float* o, int n, int d, int m) {
-    const long long wg32 = (long long)((d + 64 * kQ6RT - 1) / (64 * kQ6RT)) * ((m + 16 * kQ6NT - 1) / (16 * kQ6NT));
-    if (kQ6NT > 1 && wg32 < 2LL * g4_num_cus()) launch_mm_batch_q6s<kQ6RT, 1>(w, xs, o, n, d, m);
-    else launch_mm_batch_q6s<kQ6RT, kQ6NT>(w, xs, o, n, d, m);
+    const long long cus = g4_num_cus();
+    const long long gy32 = (m + 31) / 32;
+    if (d % 160 == 0 && (long long)(d / 160) * gy32 * 4 >= 3 * cus) return launch_mm_batch_q6s<2, 10>(w, xs, o, n, d, m);
+    const long long wg32 = (long long)((d + 63) / 64) * gy32;
+    if (wg32 < 2 * cus) launch_mm_batch_q6s<1, 4>(w, xs, o, n, d, m);
+    else launch_mm_batch_q6s<2, 4>(w, xs, o, n, d, m);
 }
 
 // m rows of k floats -> m consecutive device Q8_K rows of k/256 blocks
@@ -988,8 +1023,9 @@ extern "C" int g4_mm_batch_split(float* o, const void* w, const void* xs, int n,
                  "g4_mm_batch_split: %d x %d weights or %d rows exceed 2 GiB", d, n, m);
     G4_CHECK_ARG(al16(w) && al16(xs), "g4_mm_batch_split: w and xs must be 16-byte aligned");
     G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0 && m > 0, "g4_mm_batch_split: n=%d d=%d m=%d", n, d, m);
-    G4_CHECK_ARG((long long)((d + 64 * kQ6RT - 1) / (64 * kQ6RT)) * ((m + 16 * kQ6NT - 1) / (16 * kQ6NT)) < (1LL << 31),
-                 "g4_mm_batch_split: %d x %d outputs too many", m, d);
+    // (the largest grid of the workgroup shapes: 64 rows x 16 tokens)
+    G4_CHECK_ARG((long long)((d + 63) / 64) * ((m + 15) / 16) < (1LL << 31), "g4_mm_batch_split: %d x %d outputs too many",
+                 m, d);
     if (type != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_batch_split: type %d has no split-activation path", type);
     launch_q6s_auto((const uint8_t*)w, (const uint8_t*)xs, o, n, d, m);
     return g4_check_launch("mm_batch_q6s_kernel");
