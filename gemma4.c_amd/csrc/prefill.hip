@@ -143,13 +143,13 @@ struct KqSegs {
     int n;
 };
 
-template <bool Q5, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
+template <bool Q5, int NT, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
+    constexpr int NTH = 64 * NWV;
     constexpr int TOK = 32 * NT;
-    constexpr int UPT = TOK * 8 / 256;           // (token, Q8_K lane) units of 32 bytes per thread
-    static_assert(UPT * 256 == TOK * 8, "token tile must divide among the threads");
-    constexpr int BQ = (TOK * 4 + 255) / 256;    // 8-byte bsums quarters per thread
+    constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, Q8_K lane) units of 32 bytes per thread
+    constexpr int BQ = (TOK * 4 + NTH - 1) / NTH;    // 8-byte bsums quarters per thread
     __shared__ __align__(16) uint8_t sA[TOK * kKqTok];
     __shared__ __align__(16) uint8_t sS[TOK * kKqBs];
     __shared__ __align__(16) float sD[TOK];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const uint8_t* __restrict__ w = sg.w[seg];
     float* __restrict__ out = sg.o[seg];
     const int d = sg.d[seg];
-    const int row = (bx - sg.g0[seg]) * 128 + wave * 32 + i;
+    const int row = (bx - sg.g0[seg]) * (32 * NWV) + wave * 32 + i;
     const int tokb = by * TOK;
     const size_t nblk = (size_t)d * nb;
     const size_t hdr_off = (Q5 ? 160 : 128) * nblk, qh_off = 128 * nblk;
@@ -191,12 +191,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     int vx[UPT], vbs[BQ];
 #pragma unroll
     for (int j = 0; j < UPT; j++) {
-        const int u = tid + j * 256;
+        const int u = min(tid + j * NTH, TOK * 8 - 1);
         vx[j] = min(tokb + (u >> 3), m - 1) * (int)q8row + 32 * (u & 7);
     }
 #pragma unroll
     for (int j = 0; j < BQ; j++) {
-        const int u = min(tid + j * 256, TOK * 4 - 1);
+        const int u = min(tid + j * NTH, TOK * 4 - 1);
         vbs[j] = min(tokb + (u >> 2), m - 1) * (int)q8row + (int)q8k_bsums_off(nb) + 8 * (u & 3);
     }
     const int vyd = min(tokb + min(tid, TOK - 1), m - 1) * (int)q8row + (int)q8k_d_off(nb);
@@ -224,7 +224,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     auto stage = [&](const XRaw& r) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
-            const int u = tid + j * 256, lq = u & 7;
+            const int u = tid + j * NTH, lq = u & 7;
+            if (UPT * NTH != TOK * 8 && u >= TOK * 8) continue;
             uint8_t* dst = sA + (u >> 3) * kKqTok + 128 * (lq & 3) + 16 * (lq >> 2);
             const uint32_t a0[4] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w};
             const uint32_t a1[4] = {r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         }
 #pragma unroll
         for (int j = 0; j < BQ; j++) {
-            const int u = tid + j * 256;
+            const int u = tid + j * NTH;
             if (u < TOK * 4) {
                 const h2_t lo = {(_Float16)(int16_t)(r.bs[j].x & 0xffffu), (_Float16)(int16_t)(r.bs[j].x >> 16)};
                 const h2_t hi = {(_Float16)(int16_t)(r.bs[j].y & 0xffffu), (_Float16)(int16_t)(r.bs[j].y >> 16)};
@@ -350,17 +351,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     }
 }
 
-template <bool Q5, int NT>
+template <bool Q5, int NT, int NWV>
 void launch_mm_batch32(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
     const int gy = (m + 32 * NT - 1) / (32 * NT);
-    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, NT>), dim3(sg.g0[sg.n] * gy), dim3(256), 0, g4_stream(), sg, q8, nb, m);
+    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, NT, NWV>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(), sg, q8,
+                       nb, m);
 }
+
 
 // the shipped tiling: 128 rows x 32 tokens per workgroup (a sweep over 32 and
 // 64 tokens, one or two accumulator chains and preloaded A operands at the
 // E4B shapes over 511 tokens: 10240x2560 60 us, 2048x2560 18 us, 2560x2048
 // 22 us; the 64-token tile needs 211 VGPRs, two waves per SIMD)
 constexpr int kKqNT = 1;
+
+// waves (32 rows each) per workgroup: five when four would need more than
+// one workgroup per CU and five fit in one (a 2560-row matrix at 511 tokens:
+// 320 against 256 workgroups; 2560x2560 23.9 against 26.3 us, O 2560x2048
+// 19.1 against 20.8), else four (gate 10240x2560 63.4 against 87.6 us with
+// five, 256x2560 16.3 against 21.0; 2048 rows, one round either way, 18.5
+// against 23.4; Q|K as two segments of 2048 and 512 rows needs 17 five-wave
+// row groups, and six waves measured the same as four, 25.4 us)
+int kq_waves(const int* d, int nseg, int m) {
+    const long long gy = (m + 32 * kKqNT - 1) / (32 * kKqNT), cus = g4_num_cus();
+    auto grid = [&](int nwv) {
+        long long g = 0;
+        for (int k = 0; k < nseg; k++) g += (d[k] + 32 * nwv - 1) / (32 * nwv) * gy;
+        return g;
+    };
+    return grid(4) > cus && grid(5) <= cus ? 5 : 4;
+}
 
 // ---- fp32 activations: Q6_K and bf16 matrices --------------------------
 // Y[m x d] = X[m x n] . W[d x n]^T where the reference multiplies fp32
@@ -937,24 +957,32 @@ extern "C" int g4_mm_batch_q8_multi(float* const* o, const void* const* w, const
     const int nb = n / 256;
     // the kernel addresses both operands with 32-bit buffer offsets
     G4_CHECK_ARG((size_t)m * q8_row_stride(nb) < (1u << 31), "g4_mm_batch_q8: %d Q8_K rows exceed 2 GiB", m);
-    KqSegs sg{};
-    sg.n = nseg;
-    long long gx = 0;
+    if (type != G4_Q4_K && type != G4_Q5_K) return g4_fail(G4_ERR_TYPE, "g4_mm_batch_q8: type %d has no Q8_K batched path", type);
     for (int k = 0; k < nseg; k++) {
         G4_CHECK_ARG(o[k] && w[k], "g4_mm_batch_q8: null pointer");
         G4_CHECK_ARG(al16(o[k]) && al16(w[k]), "g4_mm_batch_q8: o and w must be 16-byte aligned");
         G4_CHECK_ARG(d[k] > 0 && (size_t)d[k] * nb * 176 < (1u << 31), "g4_mm_batch_q8: d=%d", d[k]);
+    }
+    const int nwv = kq_waves(d, nseg, m), rg = 32 * nwv;   // rows per workgroup
+    KqSegs sg{};
+    sg.n = nseg;
+    long long gx = 0;
+    for (int k = 0; k < nseg; k++) {
         sg.w[k] = (const uint8_t*)w[k];
         sg.o[k] = o[k];
         sg.d[k] = d[k];
         sg.g0[k] = (int)gx;
-        gx += (d[k] + 127) / 128;
+        gx += (d[k] + rg - 1) / rg;
     }
     sg.g0[nseg] = (int)gx;
     G4_CHECK_ARG(gx * ((m + 32 * kKqNT - 1) / (32 * kKqNT)) < (1LL << 31), "g4_mm_batch_q8: %d tokens too many", m);
-    if (type == G4_Q4_K) launch_mm_batch32<false, kKqNT>(sg, (const uint8_t*)q8, nb, m);
-    else if (type == G4_Q5_K) launch_mm_batch32<true, kKqNT>(sg, (const uint8_t*)q8, nb, m);
-    else return g4_fail(G4_ERR_TYPE, "g4_mm_batch_q8: type %d has no Q8_K batched path", type);
+    if (type == G4_Q4_K) {
+        if (nwv == 5) launch_mm_batch32<false, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
+        else launch_mm_batch32<false, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
+    } else {
+        if (nwv == 5) launch_mm_batch32<true, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
+        else launch_mm_batch32<true, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
+    }
     return g4_check_launch("mm_batch_kq32_kernel");
 }
 

@@ -144,6 +144,25 @@ def test_mm_batch_q8_every_token(lib, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_batch_q8_wave_shapes(lib, orc, qtype):
+    """A 2560-row matrix at 511 tokens takes 160-row (five-wave) workgroups,
+    at 37 tokens 128-row ones: a token's outputs are the same bits either way,
+    and sampled tokens of the five-wave launch are within the bar of the
+    oracle."""
+    from g4 import DBuf, upload_quant
+    n, d = 2048, 2560
+    rng = np.random.default_rng(71 + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = _acts(rng, 511, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, 511)
+    full = _mm_q8(lib, w, q8.ptr, n, d, 511, qtype)
+    part = _mm_q8(lib, w, q8.ptr, n, d, 37, qtype)
+    assert np.array_equal(full[:37].view(np.uint32), part.view(np.uint32))
+    _check_q8(orc, raw, qtype, n, d, x, full, [0, 1, 2, 3, 159, 160, 255, 256, 479, 510])
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
 def test_mm_batch_q8_multi(lib, orc, qtype):
     """Three matrices of one type over the same Q8_K rows in one launch (the
     engine's Q|K and gate|up): each output equals the single-matrix launch
