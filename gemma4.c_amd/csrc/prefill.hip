@@ -143,7 +143,9 @@ struct KqSegs {
     int n;
 };
 
-template <bool Q5, int NT, int NWV>
+// PB: one block per workgroup (blockIdx.y), whose per-block term u (before
+// the token's Q8_K d) is stored instead of folded: out gets nb slices of m x d
+template <bool Q5, int NT, int NWV, bool PB = false>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
     constexpr int NTH = 64 * NWV;
@@ -163,8 +165,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int k = 1; k < kMaxSegs; k++)
         if (k < sg.n && bx >= sg.g0[k]) seg = k;
     const uint8_t* __restrict__ w = sg.w[seg];
-    float* __restrict__ out = sg.o[seg];
     const int d = sg.d[seg];
+    float* __restrict__ out = sg.o[seg] + (PB ? (size_t)blockIdx.y * m * d : 0);
+    const int b0 = PB ? (int)blockIdx.y : 0, b1 = PB ? b0 + 1 : nb;   // this workgroup's blocks
     const int row = (bx - sg.g0[seg]) * (32 * NWV) + wave * 32 + i;
     const int tokb = by * TOK;
     const size_t nblk = (size_t)d * nb;
@@ -265,9 +268,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         stage(xn);
         // the next block's loads (the last block again after the end: no
         // branch, so the compiler's waits for them are exact)
-        const int bn = min(b + 1, nb - 1);
-        load_w(bn, wnext);
-        load_x(bn, xn);
+        if (!PB) {
+            const int bn = min(b + 1, nb - 1);
+            load_w(bn, wnext);
+            load_x(bn, xn);
+        }
         lds_barrier();
 
         // scales of row i: sub-blocks 2j, 2j+1 as exact fp16 multipliers
@@ -327,17 +332,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
                 for (int c = 0; c < 4; c++) {
                     const int v = 4 * a + c;
                     const float u = __builtin_fmaf(dx, S[nt][v], -(dmx * M[v]));
-                    acc[nt][v] = __builtin_fmaf(y4[c], u, acc[nt][v]);
+                    acc[nt][v] = PB ? u : __builtin_fmaf(y4[c], u, acc[nt][v]);
                 }
             }
         }
     };
     WRaw w0, w1;
-    load_w(0, w0);
-    load_x(0, xn);
-    for (int b = 0; b < nb; b += 2) {
+    load_w(b0, w0);
+    load_x(b0, xn);
+    for (int b = b0; b < b1; b += 2) {
         block(b, w0, w1);
-        if (b + 1 < nb) block(b + 1, w1, w0);
+        if (b + 1 < b1) block(b + 1, w1, w0);
     }
 
     if (row < d) {
@@ -356,6 +361,48 @@ void launch_mm_batch32(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
     const int gy = (m + 32 * NT - 1) / (32 * NT);
     hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, NT, NWV>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(), sg, q8,
                        nb, m);
+}
+
+template <bool Q5>
+void launch_mm_batch32_blocks(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
+    const int gy = (m + 31) / 32;
+    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, true>), dim3(sg.g0[sg.n] * gy, nb), dim3(256), 0, g4_stream(), sg,
+                       q8, nb, m);
+}
+
+// The fold of g4_mm_batch_q8_blocks' per-block terms, in block order as the
+// GEMM kernel folds them (g = fma(d_tb, u_b, g) from 0), optionally followed
+// by gelu(g) * ple (main.c:1989-1993, as gelu_mul_rows_kernel) and the Q8_K
+// rows of the result (as quantize_rows_q8k_kernel): one workgroup per token
+constexpr int kFoldMaxD = 1024, kFoldMaxBlocks = 64;
+__global__ __launch_bounds__(256) void fold_gelu_mul_q8_kernel(const float* __restrict__ u, const uint8_t* __restrict__ q8,
+                                                               int nb, const float* __restrict__ ple, int pstride,
+                                                               float* __restrict__ out, uint8_t* __restrict__ q8o, int d,
+                                                               int m) {
+    __shared__ float yd[kFoldMaxBlocks];
+    __shared__ __align__(16) float row[kFoldMaxD];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t qrow = ((size_t)nb * 292 + 63) & ~(size_t)63;   // q8_row_stride(nb)
+    const float* qd = reinterpret_cast<const float*>(q8 + (size_t)t * qrow + q8k_d_off(nb));
+    for (int b = tid; b < nb; b += 256) yd[b] = qd[b];
+    __syncthreads();
+    for (int r = tid; r < d; r += 256) {
+        float g = 0.0f;
+        for (int b = 0; b < nb; b++) g = __builtin_fmaf(yd[b], u[((size_t)b * m + t) * d + r], g);
+        const float v = ple ? gelu_ref(g) * ple[(size_t)t * pstride + r] : g;
+        out[(size_t)t * d + r] = v;
+        row[r] = v;
+    }
+    if (q8o) {
+        __syncthreads();
+        const int db = d / 256;
+        const size_t orow = ((size_t)db * 292 + 63) & ~(size_t)63;   // q8_row_stride(db)
+        for (int blk = wave; blk < db; blk += 4) {
+            const float4 f = reinterpret_cast<const float4*>(row + blk * 256)[lane];
+            const float v4[4] = {f.x, f.y, f.z, f.w};
+            quantize_block_wave(v4, lane, q8o + (size_t)t * orow, db, blk);
+        }
+    }
 }
 
 
@@ -988,6 +1035,37 @@ extern "C" int g4_mm_batch_q8_multi(float* const* o, const void* const* w, const
 
 extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, int d, int m, int type) {
     return g4_mm_batch_q8_multi(&o, &w, &d, 1, q8, n, m, type);
+}
+
+extern "C" int g4_mm_batch_q8_blocks(float* u, const void* w, const void* q8, int n, int d, int m, int type) {
+    G4_CHECK_ARG(u && w && q8, "g4_mm_batch_q8_blocks: null pointer");
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && m > 0 && d > 0, "g4_mm_batch_q8_blocks: n=%d d=%d m=%d", n, d, m);
+    G4_CHECK_ARG(al16(u) && al16(w) && al16(q8), "g4_mm_batch_q8_blocks: u, w and q8 must be 16-byte aligned");
+    const int nb = n / 256;
+    G4_CHECK_ARG(nb <= 65535 && (size_t)m * q8_row_stride(nb) < (1u << 31) && (size_t)d * nb * 176 < (1u << 31),
+                 "g4_mm_batch_q8_blocks: %d x %d weights or %d rows too large", d, n, m);
+    if (type != G4_Q4_K && type != G4_Q5_K) return g4_fail(G4_ERR_TYPE, "g4_mm_batch_q8_blocks: type %d has no Q8_K batched path", type);
+    KqSegs sg{};
+    sg.n = 1;
+    sg.w[0] = (const uint8_t*)w;
+    sg.o[0] = u;
+    sg.d[0] = d;
+    sg.g0[0] = 0;
+    sg.g0[1] = (d + 127) / 128;
+    G4_CHECK_ARG((long long)sg.g0[1] * ((m + 31) / 32) < (1LL << 31), "g4_mm_batch_q8_blocks: %d tokens too many", m);
+    if (type == G4_Q4_K) launch_mm_batch32_blocks<false>(sg, (const uint8_t*)q8, nb, m);
+    else launch_mm_batch32_blocks<true>(sg, (const uint8_t*)q8, nb, m);
+    return g4_check_launch("mm_batch_kq32_kernel (per block)");
+}
+
+extern "C" int g4_fold_gelu_mul_q8(const float* u, const void* q8, int n, const float* ple, int pstride, float* out,
+                                   void* q8o, int d, int m) {
+    G4_CHECK_ARG(u && q8 && out && n > 0 && n % 256 == 0 && n / 256 <= kFoldMaxBlocks, "g4_fold_gelu_mul_q8: bad u, q8, out or n=%d", n);
+    G4_CHECK_ARG(d > 0 && d <= kFoldMaxD && m > 0 && (!ple || pstride >= d), "g4_fold_gelu_mul_q8: d=%d m=%d", d, m);
+    G4_CHECK_ARG(!q8o || d % 256 == 0, "g4_fold_gelu_mul_q8: Q8_K rows need d a multiple of 256 (d=%d)", d);
+    hipLaunchKernelGGL(fold_gelu_mul_q8_kernel, dim3(m), dim3(256), 0, g4_stream(), u, (const uint8_t*)q8, n / 256, ple,
+                       pstride, out, (uint8_t*)q8o, d, m);
+    return g4_check_launch("fold_gelu_mul_q8_kernel");
 }
 
 extern "C" int g4_mm_batch(float* o, const float* x, const void* w, int n, int d, int m, int type, void* q8) {

@@ -69,6 +69,8 @@ _SIGS = {
     "g4_q8K_row_stride": (SZ, [I]),
     "g4_quantize_rows_q8_K": (I, [VP, VP, I, I]),
     "g4_mm_batch_q8": (I, [VP, VP, VP, I, I, I, I]),
+    "g4_mm_batch_q8_blocks": (I, [VP, VP, VP, I, I, I, I]),
+    "g4_fold_gelu_mul_q8": (I, [VP, VP, I, VP, I, VP, VP, I, I]),
     "g4_mm_batch_q8_multi": (I, [VP, VP, VP, I, VP, I, I, I]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
     "g4_split_rows_bytes": (SZ, [I, I]),

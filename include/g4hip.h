@@ -183,6 +183,21 @@ int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m,
  * w[k] of d[k] rows.  Each output equals g4_mm_batch_q8's for that matrix. */
 int g4_mm_batch_q8_multi(float *const *o, const void *const *w, const int *d, int nseg, const void *q8, int n, int m,
                          int type);
+/* g4_mm_batch_q8 split by K block, for small d (the PLE gate, main.c:1988,
+ * 256 rows: one workgroup per 128 rows x 32 tokens x block instead of ten
+ * blocks in series): u[(b*m + t)*d + r] = the block-b term of row r for token
+ * t before the token's Q8_K d, i.e. fma(d_w, S_b, -dmin_w * M_b) of
+ * vec_dot_q4_K_q8_K / q5_K (main.c:476-593) on n/256 blocks.  Folding them
+ * in block order, g = fma(d_tb, u_b, g) from 0 (g4_fold_gelu_mul_q8), gives
+ * g4_mm_batch_q8's output bit for bit.  u holds (n/256) * m * d floats. */
+int g4_mm_batch_q8_blocks(float *u, const void *w, const void *q8, int n, int d, int m, int type);
+/* the fold of g4_mm_batch_q8_blocks' terms over the Q8_K rows q8 (n wide) ->
+ * out[t*d + r]; with ple, out = gelu(fold) * ple[t*pstride + r] instead
+ * (main.c:1989-1993, as g4_gelu_mul_rows); with q8o, also the Q8_K rows of
+ * out (d a multiple of 256, g4_q8K_row_stride(d) apart, as
+ * g4_quantize_rows_q8_K).  d <= 1024, n <= 16384. */
+int g4_fold_gelu_mul_q8(const float *u, const void *q8, int n, const float *ple, int pstride, float *out, void *q8o,
+                        int d, int m);
 /* m tokens through mm(o_t, x_t, w, n, d, type, q8, 0) (main.c:1669): Q4_K /
  * Q5_K quantize all rows into q8 (m * g4_q8K_row_stride(n) bytes) and take
  * g4_mm_batch_q8; Q6_K and BF16 with n a multiple of 256 and 16-byte aligned

@@ -163,6 +163,43 @@ def test_mm_batch_q8_wave_shapes(lib, orc, qtype):
 
 
 @pytest.mark.parametrize("qtype", [12, 13])
+@pytest.mark.parametrize("d,m", [(256, 511), (256, 37), (512, 5)])
+def test_mm_batch_q8_blocks_fold(lib, qtype, d, m):
+    """The PLE gate split by K block (main.c:1988-1993): folding the per-block
+    terms in block order gives g4_mm_batch_q8's output bit for bit; with the
+    PLE rows, gelu * ple equals g4_gelu_mul_rows on that output and the Q8_K
+    rows equal g4_quantize_rows_q8_K's, bit for bit."""
+    from g4 import DBuf, G4Error, upload_quant
+    n = 2560
+    rng = np.random.default_rng(81 + qtype + d + m)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    want = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    u = DBuf(lib, 4 * (n // 256) * m * d)
+    lib.g4_mm_batch_q8_blocks(u.ptr, w.ptr, q8.ptr, n, d, m, qtype)
+    out = DBuf(lib, 4 * m * d)
+    lib.g4_fold_gelu_mul_q8(u.ptr, q8.ptr, n, None, 0, out.ptr, None, d, m)
+    assert np.array_equal(out.to_array(np.float32).reshape(m, d).view(np.uint32), want.view(np.uint32))
+    pstride = d + 64
+    ple = DBuf.from_array(lib, rng.standard_normal((m, pstride)).astype(np.float32))
+    rs = lib.L.g4_q8K_row_stride(d)
+    q8o = DBuf(lib, rs * m)
+    lib.g4_fold_gelu_mul_q8(u.ptr, q8.ptr, n, ple.ptr, pstride, out.ptr, q8o.ptr, d, m)
+    wd = DBuf.from_array(lib, want)
+    ref = DBuf(lib, 4 * m * d)
+    lib.g4_gelu_mul_rows(ref.ptr, wd.ptr, ple.ptr, d, m, pstride)
+    assert np.array_equal(out.to_array(np.uint32), ref.to_array(np.uint32))
+    q8r = DBuf(lib, rs * m)
+    lib.g4_quantize_rows_q8_K(ref.ptr, q8r.ptr, d, m)
+    used = 292 * (d // 256)   # a Q8_K row's bytes before its padding (qs, bsums, d)
+    assert np.array_equal(q8o.to_array(np.uint8).reshape(m, rs)[:, :used], q8r.to_array(np.uint8).reshape(m, rs)[:, :used])
+    with pytest.raises(G4Error):
+        lib.g4_fold_gelu_mul_q8(u.ptr, q8.ptr, n, None, 0, out.ptr, None, 2048, m)
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
 def test_mm_batch_q8_multi(lib, orc, qtype):
     """Three matrices of one type over the same Q8_K rows in one launch (the
     engine's Q|K and gate|up): each output equals the single-matrix launch
