@@ -171,6 +171,111 @@ __global__ __launch_bounds__(256) void qkv_post_rows_kernel(QKVArgs a) {
     qkv_post_body(a, blockIdx.x, seg, red);
 }
 
+// The same operations with a RoPE table, one wave per head (hd = 256 K):
+// lane l holds dims 256k + 4l .. 256k + 4l + 3, the sum of squares is a wave
+// reduction (no LDS, no barrier), and the pair partner of a dim (j and
+// j + hd/2, j < n_rot/2) is lane l ^ 32 (hd 256) or the lane's other float4
+// (hd 512).  Workgroup (x, z): heads 4x .. 4x + 3 of row z (z > 0: prompt
+// chunk rows, as qkv_post_rows_kernel); g4_qkv_post with a table and
+// g4_qkv_post_rows both run it, so a chunk row equals the per-token result
+// bit for bit.
+template <int HD>
+__global__ __launch_bounds__(256) void qkv_post_wave_kernel(QKVArgs a) {
+    constexpr int K = HD / 256;
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= a.n_heads + (a.k ? 2 * a.n_kv : 0)) return;   // whole waves
+    const size_t z = blockIdx.y;
+    if (z > 0) {
+        a.q += z * (size_t)a.n_heads * HD;
+        if (a.k) {
+            a.k += z * (size_t)a.n_kv * HD;
+            a.v += z * (size_t)a.n_kv * HD;
+            a.kc += z * (size_t)a.kv_stride;
+            a.vc += z * (size_t)a.kv_stride;
+        }
+        a.tab += z * (size_t)(a.n_rot / 2);
+    }
+    const int pos = a.dpos ? *a.dpos : a.pos;
+    const float* src;
+    const float* w;
+    int kind, head;
+    if (b < a.n_heads) { kind = 0; head = b; src = a.q + (size_t)head * HD; w = a.q_norm; }
+    else if (b < a.n_heads + a.n_kv) { kind = 1; head = b - a.n_heads; src = a.k + (size_t)head * HD; w = a.k_norm; }
+    else { kind = 2; head = b - a.n_heads - a.n_kv; src = a.v + (size_t)head * HD; w = nullptr; }
+
+    float x[K][4];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const float4 t = reinterpret_cast<const float4*>(src)[64 * k + lane];
+        x[k][0] = t.x; x[k][1] = t.y; x[k][2] = t.z; x[k][3] = t.w;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) ss += x[k][c] * x[k][c];
+    ss = wave_sum(ss);
+    const float s = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        if (w) {
+            const float4 wv = reinterpret_cast<const float4*>(w)[64 * k + lane];
+            x[k][0] = x[k][0] * (s * wv.x); x[k][1] = x[k][1] * (s * wv.y);
+            x[k][2] = x[k][2] * (s * wv.z); x[k][3] = x[k][3] * (s * wv.w);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) x[k][c] = x[k][c] * s;
+        }
+    }
+    if (kind != 2) {
+        // dim e = 256k + 4 lane + c; first half (e < HD/2): j = e, partner
+        // e + HD/2; second half: j = e - HD/2, partner e - HD/2
+        float y[K][4];
+#pragma unroll
+        for (int k = 0; k < K; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int e = 256 * k + 4 * lane + c;
+                const bool first = e < HD / 2;
+                const int j = first ? e : e - HD / 2;
+                const float vp = K == 1 ? __shfl_xor(x[k][c], 32) : x[k ^ 1][c];
+                y[k][c] = x[k][c];
+                if (j < a.n_rot / 2) {
+                    const float2 cs = a.tab[j];
+                    y[k][c] = first ? x[k][c] * cs.x - vp * cs.y : vp * cs.y + x[k][c] * cs.x;
+                }
+            }
+#pragma unroll
+        for (int k = 0; k < K; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) x[k][c] = y[k][c];
+    }
+    float* dst;
+    if (kind == 0) {
+        dst = a.q + (size_t)head * HD;
+    } else {
+        const int slot = a.ring > 0 ? pos % a.ring : pos;
+        dst = (kind == 1 ? a.kc : a.vc) + (size_t)slot * a.kv_stride + (size_t)head * HD;
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++)
+        reinterpret_cast<float4*>(dst)[64 * k + lane] = make_float4(x[k][0], x[k][1], x[k][2], x[k][3]);
+}
+
+// the wave form when it applies (hd 256 or 512, a RoPE table, 16-byte rows)
+bool qkv_wave_ok(const QKVArgs& a) {
+    auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    return (a.hd == 256 || a.hd == 512) && a.tab && al(a.q) && al(a.q_norm) && (!a.k || (al(a.k) && al(a.v) && al(a.k_norm) &&
+           al(a.kc) && al(a.vc) && a.kv_stride % 4 == 0));
+}
+
+void launch_qkv_wave(const QKVArgs& a, int m) {
+    const dim3 grid((a.n_heads + (a.k ? 2 * a.n_kv : 0) + 3) / 4, m);
+    if (a.hd == 256) hipLaunchKernelGGL(qkv_post_wave_kernel<256>, grid, dim3(256), 0, g4_stream(), a);
+    else hipLaunchKernelGGL(qkv_post_wave_kernel<512>, grid, dim3(256), 0, g4_stream(), a);
+}
+
 // rows z of the chunk buffers -> cache slots of positions pos0 + z (a ring
 // keeps the last `ring` of them)
 __global__ __launch_bounds__(256) void kv_store_rows_kernel(float* __restrict__ kc, float* __restrict__ vc,
@@ -1375,6 +1480,10 @@ extern "C" int g4_qkv_post(float* q, const float* q_norm, const float* k, const 
     a.ts = powf(freq_base, -2.0f / (float)n_rot);
     a.fs = freq_scale; a.eps = eps;
     a.tab = (const float2*)rope_tab;
+    if (qkv_wave_ok(a)) {
+        launch_qkv_wave(a, 1);
+        return g4_check_launch("qkv_post_wave_kernel");
+    }
     const int grid = n_heads + (k ? 2 * n_kv : 0);
     hipLaunchKernelGGL(qkv_post_kernel, dim3(grid), dim3(256), (size_t)hd * 4, g4_stream(), a);
     return g4_check_launch("qkv_post_kernel");
@@ -1422,6 +1531,10 @@ extern "C" int g4_qkv_post_rows(float* q, const float* q_norm, const float* k, c
     a.dpos = nullptr; a.ff = nullptr; a.pos = 0; a.n_heads = n_heads; a.n_kv = n_kv; a.hd = hd; a.n_rot = n_rot;
     a.kv_stride = kv_stride; a.ring = 0; a.ts = 1.0f; a.fs = 1.0f; a.eps = eps;
     a.tab = (const float2*)tab_rows;
+    if (qkv_wave_ok(a)) {
+        launch_qkv_wave(a, m);
+        return g4_check_launch("qkv_post_wave_kernel");
+    }
     const int grid = n_heads + (k ? 2 * n_kv : 0);
     hipLaunchKernelGGL(qkv_post_rows_kernel, dim3(grid, m), dim3(256), (size_t)hd * 4, g4_stream(), a);
     return g4_check_launch("qkv_post_rows_kernel");
