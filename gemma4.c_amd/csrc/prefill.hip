@@ -736,7 +736,10 @@ __device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, uint8_t
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
 }
 
-template <int RT, int NT, int NS, int NWV>
+// SP (two stages only): the next block's copies are issued one per product
+// step of this block instead of all at its start, and one barrier per block
+// suffices
+template <int RT, int NT, int NS, int NWV, bool SP = false>
 __global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ xs, float* __restrict__ out, int n, int d, int m) {
     constexpr int TOK = 16 * NT;
@@ -744,6 +747,7 @@ __global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
     // w, w + NWV, ... (DPW or DPW + 1 of them)
     constexpr int DPW = TOK / NWV, DPX = (TOK + NWV - 1) / NWV;
     static_assert(DPW >= 1, "every wave copies a token");
+    static_assert(!SP || (NS == 2 && DPX <= 8), "spread copies: two stages, at most one copy per product step");
     // NS stages: blocks b + 1 .. b + NS - 1 are on their way while block b is
     // read (the loads take longer than a block's products)
     __shared__ __align__(16) uint8_t sx[NS][TOK * kXsStride];
@@ -816,19 +820,29 @@ __global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
     // one block from stage cur and weight set wc, with block b + NS - 1's
     // weights and activations sent into wn and nxt
     auto block = [&](int b, const uint8_t* cur, uint8_t* nxt, const WRaw& wc, WRaw& wn) {
-        lds_barrier();   // block b - 1's reads of nxt are done
-        // block b + NS - 1's copies (the last block again after the end: no
-        // branch), then a wait that leaves at most the copies of blocks
-        // b + 1 .. b + NS - 1 in flight: everything issued before them has
-        // landed, block b's copies included.  Counting only the copies keeps
-        // the wait correct wherever the compiler places the weight loads (it
-        // has moved them past the compute of the block before): weight loads
-        // among the most recent operations only make it wait for more
         const int bn = min(b + NS - 1, nb - 1);
-        dma(bn, nxt);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(DPW * (NS - 1)));   // (DPW: the fewest copies a wave issues)
-        load_w(bn, wn);
-        lds_barrier();   // every wave's copies of block b are in cur
+        if (SP) {
+            // this wave's copies of block b (issued during block b - 1) and
+            // everything before them have landed; after the barrier every
+            // wave's have, and every wave is done reading nxt (block b - 1)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            lds_barrier();
+            load_w(bn, wn);
+        } else {
+            lds_barrier();   // block b - 1's reads of nxt are done
+            // block b + NS - 1's copies (the last block again after the end:
+            // no branch), then a wait that leaves at most the copies of
+            // blocks b + 1 .. b + NS - 1 in flight: everything issued before
+            // them has landed, block b's copies included.  Counting only the
+            // copies keeps the wait correct wherever the compiler places the
+            // weight loads (it has moved them past the compute of the block
+            // before): weight loads among the most recent operations only
+            // make it wait for more
+            dma(bn, nxt);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(DPW * (NS - 1)));   // (DPW: the fewest copies a wave issues)
+            load_w(bn, wn);
+            lds_barrier();   // every wave's copies of block b are in cur
+        }
 
         f4_t S[RT][NT];
         const uint8_t* xa0 = cur + i * kXsStride + 16 * g;
@@ -850,6 +864,8 @@ __global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
                     Al[cb ^ 1][nt] = *reinterpret_cast<const h8_t*>(xa + 512);
                 }
             }
+            if (SP && c < DPX && (DPX == DPW || wave + NWV * c < TOK))   // copy c of block bn
+                buf_load_lds16(rx, nxt + (wave + NWV * c) * kXsStride, 16 * lane, xrows[c < DPX ? c : 0] + bn * kSplitBlk);
             __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of this step's products
             h8_t Wa[RT], Wb[RT];
 #pragma unroll
@@ -931,11 +947,11 @@ __global__ __launch_bounds__(64 * NWV) void mm_batch_q6s_kernel(
 
 constexpr int kQ6RT = 1, kQ6NS = 2;
 
-template <int NT, int NWV>
+template <int NT, int NWV, bool SP = false>
 void launch_mm_batch_q6s(const uint8_t* w, const uint8_t* xs, float* o, int n, int d, int m) {
     const int gx = (d + 16 * kQ6RT * NWV - 1) / (16 * kQ6RT * NWV), gy = (m + 16 * NT - 1) / (16 * NT);
-    hipLaunchKernelGGL((mm_batch_q6s_kernel<kQ6RT, NT, kQ6NS, NWV>), dim3(gx * gy), dim3(64 * NWV), 0, g4_stream(), w, xs,
-                       o, n, d, m);
+    hipLaunchKernelGGL((mm_batch_q6s_kernel<kQ6RT, NT, kQ6NS, NWV, SP>), dim3(gx * gy), dim3(64 * NWV), 0, g4_stream(), w,
+                       xs, o, n, d, m);
 }
 
 // Workgroup shapes, measured at 2560 x 10240 (FFN down) on MI355X:
@@ -948,11 +964,14 @@ void launch_mm_batch_q6s(const uint8_t* w, const uint8_t* xs, float* o, int n, i
 //     tokens 14.3 against 19.2 us; FFN down at 64 tokens 45 against 92 us for
 //     the ten-wave shape.
 // Deeper pipelines (activations 2 or 3 blocks ahead) measured slower in
-// every shape: the copies' throughput, not their latency, sets the pace.
+// every shape: the copies' throughput, not their latency, sets the pace;
+// issuing them one per product step instead of all at a block's start helps
+// the ten-wave shape (128 against 135 us) but not the 64-row one (V 15.1
+// against 14.2 us).
 void launch_q6s_auto(const uint8_t* w, const uint8_t* xs, float* o, int n, int d, int m) {
     const long long cus = g4_num_cus();
     const long long gy32 = (m + 31) / 32;
-    if (d % 160 == 0 && (long long)(d / 160) * gy32 * 4 >= 3 * cus) return launch_mm_batch_q6s<2, 10>(w, xs, o, n, d, m);
+    if (d % 160 == 0 && (long long)(d / 160) * gy32 * 4 >= 3 * cus) return launch_mm_batch_q6s<2, 10, true>(w, xs, o, n, d, m);
     const long long wg32 = (long long)((d + 63) / 64) * gy32;
     if (wg32 < 2 * cus) launch_mm_batch_q6s<1, 4>(w, xs, o, n, d, m);
     else launch_mm_batch_q6s<2, 4>(w, xs, o, n, d, m);
