@@ -152,9 +152,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     constexpr int TOK = 32 * NT;
     constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, Q8_K lane) units of 32 bytes per thread
     constexpr int BQ = (TOK * 4 + NTH - 1) / NTH;    // 8-byte bsums quarters per thread
-    __shared__ __align__(16) uint8_t sA[TOK * kKqTok];
-    __shared__ __align__(16) uint8_t sS[TOK * kKqBs];
-    __shared__ __align__(16) float sD[TOK];
+    // two stages: block b + 1's activations are staged half-way through
+    // block b's products, so one barrier per block suffices
+    __shared__ __align__(16) uint8_t sA[2][TOK * kKqTok];
+    __shared__ __align__(16) uint8_t sS[2][TOK * kKqBs];
+    __shared__ __align__(16) float sD[2][TOK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 31, kg = lane >> 5;
@@ -224,12 +226,12 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     };
     // unit (t, l'): for jj = 0..3 the K step s = 4 (l' & 3) + jj, group
     // kg = l' >> 2 entry [cvt(word (0, jj)), cvt(word (1, jj))]
-    auto stage = [&](const XRaw& r) {
+    auto stage = [&](const XRaw& r, int st) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
             const int u = tid + j * NTH, lq = u & 7;
             if (UPT * NTH != TOK * 8 && u >= TOK * 8) continue;
-            uint8_t* dst = sA + (u >> 3) * kKqTok + 128 * (lq & 3) + 16 * (lq >> 2);
+            uint8_t* dst = sA[st] + (u >> 3) * kKqTok + 128 * (lq & 3) + 16 * (lq >> 2);
             const uint32_t a0[4] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w};
             const uint32_t a1[4] = {r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
 #pragma unroll
@@ -244,10 +246,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
             if (u < TOK * 4) {
                 const h2_t lo = {(_Float16)(int16_t)(r.bs[j].x & 0xffffu), (_Float16)(int16_t)(r.bs[j].x >> 16)};
                 const h2_t hi = {(_Float16)(int16_t)(r.bs[j].y & 0xffffu), (_Float16)(int16_t)(r.bs[j].y >> 16)};
-                *reinterpret_cast<uint2*>(sS + (u >> 2) * kKqBs + 8 * (u & 3)) = make_uint2(h2_bits(lo), h2_bits(hi));
+                *reinterpret_cast<uint2*>(sS[st] + (u >> 2) * kKqBs + 8 * (u & 3)) = make_uint2(h2_bits(lo), h2_bits(hi));
             }
         }
-        if (tid < TOK) sD[tid] = r.yd;
+        if (tid < TOK) sD[st][tid] = r.yd;
     };
 
     f16v_t acc[NT];
@@ -259,21 +261,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int v = 0; v < 16; v++) zero[v] = 0.0f;
 
-    // one block: stage its activations, start the next block's loads into
-    // the other weight set, compute from this one (the block loop runs two
-    // blocks per trip so that the sets alternate without copies)
+    // one block from stage st: after the barrier (block b's activations are
+    // in st, and every wave is done with the other stage), the next block's
+    // weight loads; half-way through the products, block b + 1's activations
+    // (loaded during block b - 1) go into the other stage and block b + 2's
+    // loads start (the block loop runs two blocks per trip so that the sets
+    // alternate without copies; loads past the end repeat the last block: no
+    // branch, so the compiler's waits for them are exact)
     XRaw xn;
-    auto block = [&](int b, const WRaw& wc, WRaw& wnext) {
-        lds_barrier();   // the previous block's LDS reads are done
-        stage(xn);
-        // the next block's loads (the last block again after the end: no
-        // branch, so the compiler's waits for them are exact)
-        if (!PB) {
-            const int bn = min(b + 1, nb - 1);
-            load_w(bn, wnext);
-            load_x(bn, xn);
-        }
+    auto block = [&](int b, int st, const WRaw& wc, WRaw& wnext) {
         lds_barrier();
+        if (!PB) load_w(min(b + 1, nb - 1), wnext);
 
         // scales of row i: sub-blocks 2j, 2j+1 as exact fp16 multipliers
         uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
@@ -291,9 +289,13 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         }
 
         f16v_t S[NT];
-        const uint8_t* at0 = sA + i * kKqTok + 16 * kg;
+        const uint8_t* at0 = sA[st] + i * kKqTok + 16 * kg;
 #pragma unroll
         for (int s = 0; s < 16; s++) {
+            if (!PB && s == 8 && b + 1 < b1) {
+                stage(xn, st ^ 1);
+                load_x(min(b + 2, nb - 1), xn);
+            }
             const int j = s & 3;
             const uint4 Q = wc.qs[s >> 2];
             const uint32_t word = j == 0 ? Q.x : j == 1 ? Q.y : j == 2 ? Q.z : Q.w;
@@ -320,13 +322,13 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         const float dx = hbits_to_f32(wc.hdr.x & 0xffffu), dmx = hbits_to_f32(wc.hdr.x >> 16);
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            const uint8_t* bs = sS + (32 * nt + i) * kKqBs + 8 * kg;
+            const uint8_t* bs = sS[st] + (32 * nt + i) * kKqBs + 8 * kg;
             const h4_t A1 = *reinterpret_cast<const h4_t*>(bs), A2 = *reinterpret_cast<const h4_t*>(bs + 16);
             f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
             M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 4; a++) {
-                const float4 yd = *reinterpret_cast<const float4*>(sD + 32 * nt + 8 * a + 4 * kg);
+                const float4 yd = *reinterpret_cast<const float4*>(sD[st] + 32 * nt + 8 * a + 4 * kg);
                 const float y4[4] = {yd.x, yd.y, yd.z, yd.w};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
@@ -340,9 +342,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     WRaw w0, w1;
     load_w(b0, w0);
     load_x(b0, xn);
+    stage(xn, 0);
+    if (!PB) load_x(min(b0 + 1, nb - 1), xn);
     for (int b = b0; b < b1; b += 2) {
-        block(b, w0, w1);
-        if (b + 1 < b1) block(b + 1, w1, w0);
+        block(b, 0, w0, w1);
+        if (b + 1 < b1) block(b + 1, 1, w1, w0);
     }
 
     if (row < d) {
