@@ -374,6 +374,267 @@ void launch_mm_batch32_blocks(const KqSegs& sg, const uint8_t* q8, int nb, int m
                        q8, nb, m);
 }
 
+// ---- Q4_K / Q5_K through fp16 weight images (mm_batch_img_kernel) --------
+// The in-register weight decode of mm_batch_kq32_kernel (nibbles, Q5_K high
+// bits, scale multiply, fp16 packing) is most of its vector instructions and
+// sets its pace.  An image does that decode once per matrix, when the model
+// is loaded: every weight's sc * q (the 6-bit sub-block scale times the
+// 4/5-bit code, an integer <= 63 * 31, exact in fp16) stored as the B operand
+// of v_mfma_f32_32x32x16_f16, plus per row and block d, dmin and the mins.
+// The block sums are the same integers (exact while a block's partial sums
+// stay below 2^24, as in mm_batch_kq32_kernel: then the K order inside the
+// matrix cores does not matter) and the fold the same three fp32 steps, so
+// the outputs are mm_batch_kq32_kernel's bits; the kernel's loop is MFMAs,
+// LDS reads of the activations and the block fold.
+// K positions inside a block follow the device Q8_K byte order: position
+// p = 32l + 16h + 4j + c is element 64j + 32h + 4l + c (sub-block 2j + h),
+// so a token's Q8_K bytes are its A operand in place.
+//   codes : [rg][nb][16 steps][64 lanes] x 16 B, rg = ceil(d / 32): lane
+//           L = i + 32 kg of step s holds row 32 g + i, K positions
+//           16 s + 8 kg .. +7 (8 fp16)
+//   hdr   : [rg][nb][64 lanes] x 16 B: fp32 d, fp32 dmin, fp16 pairs
+//           {m_2kg, m_2kg+1} and {m_4+2kg, m_5+2kg} (the min operands of
+//           lane half kg)
+// Rows past d are zero.
+constexpr int kImgStep = 1024, kImgBlk = 16 * kImgStep, kImgHdr = 1024;
+
+size_t kq_img_bytes(int d, int nb) { return (size_t)((d + 31) / 32) * nb * (kImgBlk + kImgHdr); }
+
+__device__ __forceinline__ uint32_t h16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// one thread per (row group, block, lane) of the image
+template <bool Q5>
+__global__ __launch_bounds__(256) void kq_image_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ img, int d,
+                                                       int nb, int rg) {
+    const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (size_t)rg * nb * 64) return;
+    const int L = (int)(id & 63), i = L & 31, kg = L >> 5;
+    const size_t gb = id >> 6;   // g * nb + b
+    const int b = (int)(gb % nb), g = (int)(gb / nb);
+    const int row = 32 * g + i;
+    uint4* codes = reinterpret_cast<uint4*>(img + gb * kImgBlk + 16 * L);
+    uint4* hdo = reinterpret_cast<uint4*>(img + (size_t)rg * nb * kImgBlk + gb * kImgHdr + 16 * L);
+    if (row >= d) {
+        for (int s = 0; s < 16; s++) codes[s * (kImgStep / 16)] = make_uint4(0, 0, 0, 0);
+        *hdo = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    const size_t nblk = (size_t)d * nb, blk = (size_t)row * nb + b;
+    const uint4 hdr = *reinterpret_cast<const uint4*>(w + (Q5 ? 160 : 128) * nblk + blk * 16);
+    uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
+    unpack_scales(hdr.y, hdr.z, hdr.w, sc_lo, sc_hi, mn_lo, mn_hi);
+    const uint8_t* qs = w + blk * 128;        // device word 4l + j = GGUF qs word 8j + l
+    const uint8_t* qh = w + 128 * nblk + blk * 32;
+    for (int s = 0; s < 16; s++) {
+        uint32_t hv[4];
+        for (int t2 = 0; t2 < 4; t2++) {
+            uint32_t pair = 0;
+            for (int u = 0; u < 2; u++) {
+                const int p = 16 * s + 8 * kg + 2 * t2 + u;
+                const int l = p >> 5, h = (p >> 4) & 1, j = (p >> 2) & 3, c = p & 3, sb = 2 * j + h;
+                const int byte = qs[16 * l + 4 * j + c];
+                int q = h ? byte >> 4 : byte & 15;
+                if (Q5) q |= ((qh[4 * l + c] >> sb) & 1) << 4;
+                pair |= h16_bits((float)(byte_of(sb < 4 ? sc_lo : sc_hi, sb & 3) * q)) << (16 * u);
+            }
+            hv[t2] = pair;
+        }
+        codes[s * (kImgStep / 16)] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+    }
+    const uint32_t ma = h16_bits((float)byte_of(mn_lo, 2 * kg)), mb = h16_bits((float)byte_of(mn_lo, 2 * kg + 1));
+    const uint32_t mc = h16_bits((float)byte_of(mn_hi, 2 * kg)), md = h16_bits((float)byte_of(mn_hi, 2 * kg + 1));
+    *hdo = make_uint4(__float_as_uint(f16_to_f32(hdr.x & 0xffffu)), __float_as_uint(f16_to_f32(hdr.x >> 16)),
+                      ma | (mb << 16), mc | (md << 16));
+}
+
+// NWV waves of 32 rows (one image row group each) x 32 NT tokens per
+// workgroup; segments as in mm_batch_kq32_kernel, in units of 32 NWV rows
+// LDS slot (16 bytes) of step s, lane half kg inside a token's row: the two
+// halves of a step 128 bytes apart, so that the lanes (i, 0) and (i, 1) of
+// one 128-bit read fall in different banks (2 s + kg, the plain order, had
+// three times the bank-conflict cycles and took 8 % longer)
+__device__ __forceinline__ int img_slot(int s, int kg) { return (s & 7) + 8 * kg + 16 * (s >> 3); }
+
+template <int NT, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_img_kernel(
+    const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
+    constexpr int NTH = 64 * NWV;
+    constexpr int TOK = 32 * NT;
+    constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, 32-byte unit) pairs per thread
+    constexpr int BQ = (TOK * 4 + NTH - 1) / NTH;    // 8-byte bsums quarters per thread
+    __shared__ __align__(16) uint8_t sA[2][TOK * kKqTok];
+    __shared__ __align__(16) uint8_t sS[2][TOK * kKqBs];
+    __shared__ __align__(16) float sD[2][TOK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 31, kg = lane >> 5;
+    int bx, by;
+    xcd_tile((m + TOK - 1) / TOK, bx, by);
+    int seg = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxSegs; k++)
+        if (k < sg.n && bx >= sg.g0[k]) seg = k;
+    const uint8_t* __restrict__ img = sg.w[seg];
+    const int d = sg.d[seg];
+    float* __restrict__ out = sg.o[seg];
+    const int rg = (d + 31) / 32;
+    const int gw = (bx - sg.g0[seg]) * NWV + wave;   // this wave's row group
+    const int g = min(gw, rg - 1);
+    const int row = 32 * gw + i;
+    const int tokb = by * TOK;
+    const size_t q8row = ((size_t)nb * 292 + 63) & ~(size_t)63;   // q8_row_stride
+
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, (int)((size_t)rg * nb * (kImgBlk + kImgHdr)), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q8, (short)0, (int)(m * q8row), kBufWord3);
+    const int vw = g * nb * kImgBlk + 16 * lane;
+    const int vh = rg * nb * kImgBlk + g * nb * kImgHdr + 16 * lane;
+    int vx[UPT], vbs[BQ];
+#pragma unroll
+    for (int j = 0; j < UPT; j++) {
+        const int u = min(tid + j * NTH, TOK * 8 - 1);
+        vx[j] = min(tokb + (u >> 3), m - 1) * (int)q8row + 32 * (u & 7);
+    }
+#pragma unroll
+    for (int j = 0; j < BQ; j++) {
+        const int u = min(tid + j * NTH, TOK * 4 - 1);
+        vbs[j] = min(tokb + (u >> 2), m - 1) * (int)q8row + (int)q8k_bsums_off(nb) + 8 * (u & 3);
+    }
+    const int vyd = min(tokb + min(tid, TOK - 1), m - 1) * (int)q8row + (int)q8k_d_off(nb);
+
+    struct XRaw {
+        uint4 a0[UPT], a1[UPT];
+        uint2 bs[BQ];
+        float yd;
+    };
+    auto load_x = [&](int b, XRaw& r) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++) {
+            r.a0[j] = buf_load16(rq, vx[j], b * 256);
+            r.a1[j] = buf_load16(rq, vx[j] + 16, b * 256);
+        }
+#pragma unroll
+        for (int j = 0; j < BQ; j++) r.bs[j] = buf_load8(rq, vbs[j], b * 32);
+        r.yd = __uint_as_float(buf_load4(rq, vyd, b * 4));
+    };
+    // unit (t, l'): Q8_K device bytes 32l' .. 32l'+31 of the block -> fp16 at
+    // K positions 32l' .. 32l'+31 of token row t
+    auto stage = [&](const XRaw& r, int st) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++) {
+            const int u = tid + j * NTH;
+            if (UPT * NTH != TOK * 8 && u >= TOK * 8) continue;
+            uint8_t* dst = sA[st] + (u >> 3) * kKqTok;
+            const int s0 = 2 * (u & 7);   // steps s0, s0 + 1
+            const uint2 c0 = i8x4_to_h4(r.a0[j].x), c1 = i8x4_to_h4(r.a0[j].y);
+            const uint2 c2 = i8x4_to_h4(r.a0[j].z), c3 = i8x4_to_h4(r.a0[j].w);
+            const uint2 c4 = i8x4_to_h4(r.a1[j].x), c5 = i8x4_to_h4(r.a1[j].y);
+            const uint2 c6 = i8x4_to_h4(r.a1[j].z), c7 = i8x4_to_h4(r.a1[j].w);
+            *reinterpret_cast<uint4*>(dst + 16 * img_slot(s0, 0)) = make_uint4(c0.x, c0.y, c1.x, c1.y);
+            *reinterpret_cast<uint4*>(dst + 16 * img_slot(s0, 1)) = make_uint4(c2.x, c2.y, c3.x, c3.y);
+            *reinterpret_cast<uint4*>(dst + 16 * img_slot(s0 + 1, 0)) = make_uint4(c4.x, c4.y, c5.x, c5.y);
+            *reinterpret_cast<uint4*>(dst + 16 * img_slot(s0 + 1, 1)) = make_uint4(c6.x, c6.y, c7.x, c7.y);
+        }
+#pragma unroll
+        for (int j = 0; j < BQ; j++) {
+            const int u = tid + j * NTH;
+            if (u < TOK * 4) {
+                const h2_t lo = {(_Float16)(int16_t)(r.bs[j].x & 0xffffu), (_Float16)(int16_t)(r.bs[j].x >> 16)};
+                const h2_t hi = {(_Float16)(int16_t)(r.bs[j].y & 0xffffu), (_Float16)(int16_t)(r.bs[j].y >> 16)};
+                *reinterpret_cast<uint2*>(sS[st] + (u >> 2) * kKqBs + 8 * (u & 3)) = make_uint2(h2_bits(lo), h2_bits(hi));
+            }
+        }
+        if (tid < TOK) sD[st][tid] = r.yd;
+    };
+
+    f16v_t acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[nt][v] = 0.0f;
+    f16v_t zero;
+#pragma unroll
+    for (int v = 0; v < 16; v++) zero[v] = 0.0f;
+
+    // the weights of block b + 1 are loaded step by step as block b's
+    // products consume block b's (W[s] is reloaded right after its MFMAs);
+    // loads past the last block repeat it (no branch: the compiler's waits
+    // stay exact)
+    uint4 W[16], H;
+#pragma unroll
+    for (int s = 0; s < 16; s++) W[s] = buf_load16(rw, vw, s * kImgStep);
+    H = buf_load16(rw, vh, 0);
+    XRaw xn;
+    load_x(0, xn);
+    stage(xn, 0);
+    load_x(min(1, nb - 1), xn);
+    auto block = [&](int b, int st) {
+        lds_barrier();
+        const uint4 Hc = H;
+        const int bn = min(b + 1, nb - 1);
+        H = buf_load16(rw, vh, bn * kImgHdr);
+        f16v_t S[NT];
+        const uint8_t* at0 = sA[st] + i * kKqTok;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            if (s == 8 && b + 1 < nb) {
+                stage(xn, st ^ 1);
+                load_x(min(b + 2, nb - 1), xn);
+            }
+            const h8_t B = __builtin_bit_cast(h8_t, W[s]);
+            const int so = 16 * img_slot(s, kg);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const h8_t A = *reinterpret_cast<const h8_t*>(at0 + 32 * nt * kKqTok + so);
+                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s == 0 ? zero : S[nt], 0, 0, 0);
+            }
+            W[s] = buf_load16(rw, vw, bn * kImgBlk + s * kImgStep);
+        }
+        const uint32_t ml = (Hc.z & 0xffffu) | (Hc.z << 16), mh = (Hc.z >> 16) | (Hc.z & 0xffff0000u);
+        const uint32_t nl = (Hc.w & 0xffffu) | (Hc.w << 16), nh = (Hc.w >> 16) | (Hc.w & 0xffff0000u);
+        const h4_t Bm1 = __builtin_bit_cast(h4_t, make_uint2(ml, mh)), Bm2 = __builtin_bit_cast(h4_t, make_uint2(nl, nh));
+        const float dx = __uint_as_float(Hc.x), dmx = __uint_as_float(Hc.y);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint8_t* bs = sS[st] + (32 * nt + i) * kKqBs + 8 * kg;
+            const h4_t A1 = *reinterpret_cast<const h4_t*>(bs), A2 = *reinterpret_cast<const h4_t*>(bs + 16);
+            f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
+            M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const float4 yd = *reinterpret_cast<const float4*>(sD[st] + 32 * nt + 8 * a + 4 * kg);
+                const float y4[4] = {yd.x, yd.y, yd.z, yd.w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int v = 4 * a + c;
+                    acc[nt][v] = __builtin_fmaf(y4[c], __builtin_fmaf(dx, S[nt][v], -(dmx * M[v])), acc[nt][v]);
+                }
+            }
+        }
+    };
+    for (int b = 0; b < nb; b += 2) {
+        block(b, 0);
+        if (b + 1 < nb) block(b + 1, 1);
+    }
+
+    if (gw < rg && row < d) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int tok = tokb + 32 * nt + 8 * (v >> 2) + 4 * kg + (v & 3);
+                if (tok < m) out[(size_t)tok * d + row] = acc[nt][v];
+            }
+    }
+}
+
+template <int NT, int NWV>
+void launch_mm_batch_img(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
+    const int gy = (m + 32 * NT - 1) / (32 * NT);
+    hipLaunchKernelGGL((mm_batch_img_kernel<NT, NWV>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(), sg, q8,
+                       nb, m);
+}
+
 // The fold of g4_mm_batch_q8_blocks' per-block terms, in block order as the
 // GEMM kernel folds them (g = fma(d_tb, u_b, g) from 0), optionally followed
 // by gelu(g) * ple (main.c:1989-1993, as gelu_mul_rows_kernel) and the Q8_K
@@ -1079,6 +1340,97 @@ extern "C" int g4_mm_batch_q8_blocks(float* u, const void* w, const void* q8, in
     if (type == G4_Q4_K) launch_mm_batch32_blocks<false>(sg, (const uint8_t*)q8, nb, m);
     else launch_mm_batch32_blocks<true>(sg, (const uint8_t*)q8, nb, m);
     return g4_check_launch("mm_batch_kq32_kernel (per block)");
+}
+
+extern "C" size_t g4_kq_image_bytes(int n, int d) {
+    return n > 0 && n % 256 == 0 && d > 0 ? kq_img_bytes(d, n / 256) : 0;
+}
+
+extern "C" int g4_kq_image(void* img, const void* w, int n, int d, int type) {
+    G4_CHECK_ARG(img && w, "g4_kq_image: null pointer");
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0, "g4_kq_image: n=%d d=%d", n, d);
+    G4_CHECK_ARG(al16(img) && al16(w), "g4_kq_image: img and w must be 16-byte aligned");
+    if (type != G4_Q4_K && type != G4_Q5_K) return g4_fail(G4_ERR_TYPE, "g4_kq_image: type %d has no image", type);
+    const int nb = n / 256, rg = (d + 31) / 32;
+    G4_CHECK_ARG(kq_img_bytes(d, nb) < (1u << 31), "g4_kq_image: the image of %d x %d weights exceeds 2 GiB", d, n);
+    const size_t threads = (size_t)rg * nb * 64;
+    if (type == G4_Q4_K)
+        hipLaunchKernelGGL(kq_image_kernel<false>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g4_stream(),
+                           (const uint8_t*)w, (uint8_t*)img, d, nb, rg);
+    else
+        hipLaunchKernelGGL(kq_image_kernel<true>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, g4_stream(),
+                           (const uint8_t*)w, (uint8_t*)img, d, nb, rg);
+    return g4_check_launch("kq_image_kernel");
+}
+
+// tile: tokens per workgroup 32 nt, waves (32-row groups) nwv; 0 picks
+static int mm_batch_img_tiled(float* const* o, const void* const* img, const int* d, int nseg, const void* q8, int n,
+                              int m, int nt, int nwv) {
+    G4_CHECK_ARG(o && img && d && q8, "g4_mm_batch_img: null pointer");
+    G4_CHECK_ARG(nseg >= 1 && nseg <= kMaxSegs, "g4_mm_batch_img: %d matrices (1..%d)", nseg, kMaxSegs);
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && m > 0, "g4_mm_batch_img: n=%d m=%d", n, m);
+    G4_CHECK_ARG(al16(q8), "g4_mm_batch_img: q8 must be 16-byte aligned");
+    const int nb = n / 256;
+    G4_CHECK_ARG((size_t)m * q8_row_stride(nb) < (1u << 31), "g4_mm_batch_img: %d Q8_K rows exceed 2 GiB", m);
+    for (int k = 0; k < nseg; k++) {
+        G4_CHECK_ARG(o[k] && img[k], "g4_mm_batch_img: null pointer");
+        G4_CHECK_ARG(al16(o[k]) && al16(img[k]), "g4_mm_batch_img: o and img must be 16-byte aligned");
+        G4_CHECK_ARG(d[k] > 0 && kq_img_bytes(d[k], nb) < (1u << 31), "g4_mm_batch_img: d=%d", d[k]);
+    }
+    if (nt == 0 || nwv == 0) {
+        // 64-token tiles when they give every CU a workgroup (eight-wave ones
+        // from eight per CU), else 32-token tiles of 128 or 64 rows (511
+        // tokens: 2x10240 rows 81.8 us with 64 x 128 tiles against 102.5 with
+        // 32 x 128; 2560 x 2048 14.5 us with 32 x 128 against 19.5)
+        auto wgs = [&](int t, int w) {
+            long long g = 0;
+            for (int k = 0; k < nseg; k++) g += (long long)((d[k] + 32 * w - 1) / (32 * w)) * ((m + 32 * t - 1) / (32 * t));
+            return g;
+        };
+        const long long cus = g4_num_cus();
+        if (wgs(2, 4) >= 8 * cus) nt = 2, nwv = 8;
+        else if (wgs(2, 4) >= cus) nt = 2, nwv = 4;
+        else if (wgs(1, 4) >= cus) nt = 1, nwv = 4;
+        else nt = 1, nwv = 2;
+    }
+    G4_CHECK_ARG((nt == 1 && (nwv == 2 || nwv == 4 || nwv == 8)) || (nt == 2 && (nwv == 4 || nwv == 8)),
+                 "g4_mm_batch_img: tile %d x %d", nt, nwv);
+    const int rgw = 32 * nwv;   // rows per workgroup
+    KqSegs sg{};
+    sg.n = nseg;
+    long long gx = 0;
+    for (int k = 0; k < nseg; k++) {
+        sg.w[k] = (const uint8_t*)img[k];
+        sg.o[k] = o[k];
+        sg.d[k] = d[k];
+        sg.g0[k] = (int)gx;
+        gx += (d[k] + rgw - 1) / rgw;
+    }
+    sg.g0[nseg] = (int)gx;
+    G4_CHECK_ARG(gx * ((m + 32 * nt - 1) / (32 * nt)) < (1LL << 31), "g4_mm_batch_img: %d tokens too many", m);
+    const uint8_t* q = (const uint8_t*)q8;
+    switch (10 * nt + nwv) {
+    case 12: launch_mm_batch_img<1, 2>(sg, q, nb, m); break;
+    case 14: launch_mm_batch_img<1, 4>(sg, q, nb, m); break;
+    case 18: launch_mm_batch_img<1, 8>(sg, q, nb, m); break;
+    case 24: launch_mm_batch_img<2, 4>(sg, q, nb, m); break;
+    default: launch_mm_batch_img<2, 8>(sg, q, nb, m); break;
+    }
+    return g4_check_launch("mm_batch_img_kernel");
+}
+
+extern "C" int g4_mm_batch_img_multi(float* const* o, const void* const* img, const int* d, int nseg, const void* q8,
+                                     int n, int m) {
+    return mm_batch_img_tiled(o, img, d, nseg, q8, n, m, 0, 0);
+}
+
+extern "C" int g4_mm_batch_img(float* o, const void* img, const void* q8, int n, int d, int m) {
+    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, 0, 0);
+}
+
+// the same with the tile given (tokens 32 nt, rows 32 nwv): shape sweeps
+extern "C" int g4_mm_batch_img_tile(float* o, const void* img, const void* q8, int n, int d, int m, int nt, int nwv) {
+    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, nt, nwv);
 }
 
 extern "C" int g4_fold_gelu_mul_q8(const float* u, const void* q8, int n, const float* ple, int pstride, float* out,

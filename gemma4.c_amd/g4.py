@@ -72,6 +72,11 @@ _SIGS = {
     "g4_mm_batch_q8_blocks": (I, [VP, VP, VP, I, I, I, I]),
     "g4_fold_gelu_mul_q8": (I, [VP, VP, I, VP, I, VP, VP, I, I]),
     "g4_mm_batch_q8_multi": (I, [VP, VP, VP, I, VP, I, I, I]),
+    "g4_kq_image_bytes": (SZ, [I, I]),
+    "g4_kq_image": (I, [VP, VP, I, I, I]),
+    "g4_mm_batch_img": (I, [VP, VP, VP, I, I, I]),
+    "g4_mm_batch_img_multi": (I, [VP, VP, VP, I, VP, I, I]),
+    "g4_mm_batch_img_tile": (I, [VP, VP, VP, I, I, I, I, I]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
     "g4_split_rows_bytes": (SZ, [I, I]),
     "g4_split_rows_f16": (I, [VP, VP, I, I]),

@@ -191,6 +191,23 @@ int g4_mm_batch_q8_multi(float *const *o, const void *const *w, const int *d, in
  * in block order, g = fma(d_tb, u_b, g) from 0 (g4_fold_gelu_mul_q8), gives
  * g4_mm_batch_q8's output bit for bit.  u holds (n/256) * m * d floats. */
 int g4_mm_batch_q8_blocks(float *u, const void *w, const void *q8, int n, int d, int m, int type);
+/* fp16 weight image of a Q4_K / Q5_K matrix for the batched GEMM: each
+ * weight's sc * q (sub-block scale times code, get_scale_min_k4 and the
+ * dequantize loops of main.c:170-211) in the matrix cores' operand order, d,
+ * dmin and the mins per row and block.  Built once (at model load); the
+ * decode-step GEMVs keep reading the quantized tensor.  Bytes of the image
+ * of d rows x n (0 if n is not a positive multiple of 256). */
+size_t g4_kq_image_bytes(int n, int d);
+/* write the image of w (Q4_K / Q5_K, d x n, device layout) into img
+ * (g4_kq_image_bytes(n, d) bytes, 16-byte aligned) */
+int g4_kq_image(void *img, const void *w, int n, int d, int type);
+/* g4_mm_batch_q8 / g4_mm_batch_q8_multi on images instead of the quantized
+ * tensors: the same integer block sums and the same fold, so the same
+ * outputs (bit for bit while every block's partial sums stay below 2^24;
+ * always within 1e-5 of sum |terms| of mm_quant_dot_rows, main.c:1558-1566) */
+int g4_mm_batch_img(float *o, const void *img, const void *q8, int n, int d, int m);
+int g4_mm_batch_img_multi(float *const *o, const void *const *img, const int *d, int nseg, const void *q8, int n,
+                          int m);
 /* the fold of g4_mm_batch_q8_blocks' terms over the Q8_K rows q8 (n wide) ->
  * out[t*d + r]; with ple, out = gelu(fold) * ple[t*pstride + r] instead
  * (main.c:1989-1993, as g4_gelu_mul_rows); with q8o, also the Q8_K rows of

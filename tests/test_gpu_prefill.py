@@ -453,3 +453,72 @@ def test_mm_batch_errors(lib):
     with pytest.raises(G4Error):
         lib.g4_split_rows_f16(o.ptr, q8.ptr, 300, 2)                # n not a multiple of 256
     assert lib.L.g4_split_rows_bytes(300, 2) == 0
+
+
+def _image(lib, w, qtype, n, d):
+    from g4 import DBuf
+    img = DBuf(lib, lib.L.g4_kq_image_bytes(n, d))
+    lib.g4_kq_image(img.ptr, w.ptr, n, d, qtype)
+    return img
+
+
+IMG_SHAPES = [(256, 80, 37), (2560, 70, 17), (2560, 2048, 64), (2048, 2560, 100), (10240, 192, 65), (2560, 10240, 130)]
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+@pytest.mark.parametrize("n,d,m", IMG_SHAPES)
+def test_mm_batch_img_vs_q8(lib, orc, qtype, n, d, m):
+    """The fp16-image GEMM gives g4_mm_batch_q8's outputs bit for bit (the
+    block sums are exact integers at these sizes), in every tile shape,
+    and each token against the oracle's mm_quant_dot_rows at the 1e-5 bar."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(300 * qtype + n + d + m)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    img = _image(lib, w, qtype, n, d)
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    ref = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    for nt, nwv in [(0, 0), (1, 2), (1, 4), (1, 8), (2, 4), (2, 8)]:
+        out = DBuf(lib, 4 * m * d)
+        lib.g4_mm_batch_img_tile(out.ptr, img.ptr, q8.ptr, n, d, m, nt, nwv)
+        got = out.to_array(np.float32).reshape(m, d)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (nt, nwv)
+    toks = range(m) if d * m <= 200_000 else sorted(set(range(0, m, 8)) | {1, 2, 3, m - 1})
+    _check_q8(orc, raw, qtype, n, d, x, got, list(toks))
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_mm_batch_img_multi_prefill_shape(lib, orc, qtype):
+    """gate and up (10240 x 2560) over a 511-token chunk in one launch on
+    their images: both equal g4_mm_batch_q8_multi's outputs bit for bit, and
+    sampled tokens meet the oracle bar."""
+    from g4 import DBuf, upload_quant
+    import ctypes as C
+    n, d, m = 2560, 10240, 511
+    rng = np.random.default_rng(71 + qtype)
+    raws = [synth.rand_kquant(rng, qtype, d, n) for _ in range(2)]
+    ws = [upload_quant(lib, r, qtype, n, d) for r in raws]
+    imgs = [_image(lib, w, qtype, n, d) for w in ws]
+    x = _acts(rng, m, n)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    outs = [DBuf(lib, 4 * m * d) for _ in range(4)]
+    VPA = C.c_void_p * 2
+    dd = (C.c_int * 2)(d, d)
+    lib.g4_mm_batch_q8_multi(VPA(outs[0].ptr, outs[1].ptr), VPA(ws[0].ptr, ws[1].ptr), dd, 2, q8.ptr, n, m, qtype)
+    lib.g4_mm_batch_img_multi(VPA(outs[2].ptr, outs[3].ptr), VPA(imgs[0].ptr, imgs[1].ptr), dd, 2, q8.ptr, n, m)
+    for k in range(2):
+        ref = outs[k].to_array(np.float32).reshape(m, d)
+        got = outs[2 + k].to_array(np.float32).reshape(m, d)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), k
+        _check_q8(orc, raws[k], qtype, n, d, x, got, [0, 1, 2, 3, 64, 255, 256, 510])
+
+
+def test_kq_image_args(lib):
+    """Sizes and argument checks of the image entry points."""
+    from g4 import DBuf
+    assert lib.L.g4_kq_image_bytes(2560, 100) == 4 * 10 * (16384 + 1024)
+    assert lib.L.g4_kq_image_bytes(100, 100) == 0
+    buf = DBuf(lib, 4096)
+    assert lib.L.g4_kq_image(buf.ptr, buf.ptr, 256, 1, 14) != 0       # Q6_K has no image
+    assert lib.L.g4_mm_batch_img_tile(buf.ptr, buf.ptr, buf.ptr, 256, 1, 1, 3, 4) != 0

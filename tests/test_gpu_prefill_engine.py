@@ -203,3 +203,31 @@ def test_generate_uses_batched_prompt(model_path):
     finally:
         em.close()
     assert np.array_equal(np.array(host, np.int32), g), (host, g)
+
+
+def test_prefill_images_bit_exact(model_path, monkeypatch):
+    """The chunk GEMMs on fp16 weight images (the default) and on the
+    quantized tensors (G4E_PREFILL_IMAGES=0) give bit-identical layer inputs
+    and caches: the images hold the same integers sc * q the quantized
+    kernel forms in registers."""
+    prompt = np.random.default_rng(9).integers(0, 512, 21)
+    runs = []
+    for flag in (None, "0"):
+        if flag:
+            monkeypatch.setenv("G4E_PREFILL_IMAGES", flag)
+        else:
+            monkeypatch.delenv("G4E_PREFILL_IMAGES", raising=False)
+        em = _engine(model_path, 8)
+        try:
+            tr = em.prefill_trace(prompt, 0)
+            kv = []
+            for l in range(2):
+                _, slots = em.kv_info(l)
+                kv.append(em.kv(l, 0, min(slots, len(prompt))))
+            runs.append((tr, kv))
+        finally:
+            em.close()
+    monkeypatch.delenv("G4E_PREFILL_IMAGES", raising=False)
+    assert np.array_equal(runs[0][0], runs[1][0])
+    for (k0, v0), (k1, v1) in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
