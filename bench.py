@@ -342,14 +342,17 @@ PREFILL_MATS = [("q", 2048, 2560), ("k", 512, 2560), ("o", 2560, 2048), ("gate",
 
 def bench_prefill(lib, g4, synth, args):
     """Batched prefill GEMM: 512 prompt tokens through one E4B layer's Q4_K
-    matrices (Q, K, O, gate, up, inp_gate, proj) with pre-quantized Q8_K
-    activations; a step is the seven launches.  Reports matrix-core
-    throughput (2 * tokens * rows * n algorithmic ops) against the fp16 dense
-    peak (the kernel issues one fp16 MFMA flop per algorithmic flop, plus the
-    min sums' 1/32), and the dominant launch (gate, 10240x2560) alone."""
+    matrices with pre-quantized Q8_K activations, launched as the engine
+    launches them: Q|K in one launch, O, gate|up in one launch on their fp16
+    weight images (g4_kq_image, built once as the engine builds them at its
+    first prompt chunk), PLE inp_gate and proj; a step is the five launches.
+    Reports matrix-core throughput (2 * tokens * rows * n algorithmic ops)
+    against the fp16 dense peak (the kernels issue one fp16 MFMA flop per
+    algorithmic flop, plus the min sums' 1/32), and the dominant launch
+    (gate|up, 2 x 10240 x 2560) alone."""
     m = 512
     rng = np.random.default_rng(1)
-    mats = []
+    mats = {}
     for name, d, n in PREFILL_MATS:
         raw = synth.rand_q4K(rng, d, n)
         w = g4.upload_quant(lib, raw, g4.Q4_K, n, d)
@@ -357,38 +360,48 @@ def bench_prefill(lib, g4, synth, args):
         q8 = g4.DBuf(lib, lib.L.g4_q8K_row_stride(n) * m)
         lib.g4_quantize_rows_q8_K(x.ptr, q8.ptr, n, m)
         out = g4.DBuf(lib, 4 * m * d)
-        mats.append((name, d, n, raw, w, q8, out))
+        img = None
+        if name in ("gate", "up"):
+            img = g4.DBuf(lib, lib.L.g4_kq_image_bytes(n, d))
+            lib.g4_kq_image(img.ptr, w.ptr, n, d, g4.Q4_K)
+        mats[name] = (d, n, raw, w, q8, out, img)
     L = lib.L
+    VP2, I2 = C.c_void_p * 2, C.c_int * 2
+    q_, k_, gt, up = mats["q"], mats["k"], mats["gate"], mats["up"]
+    qk = (VP2(q_[5].ptr, k_[5].ptr), VP2(q_[3].ptr, k_[3].ptr), I2(q_[0], k_[0]))
+    gu = (VP2(gt[5].ptr, up[5].ptr), VP2(gt[6].ptr, up[6].ptr), I2(gt[0], up[0]))
+
+    def gate_up(i):
+        L.g4_mm_batch_img_multi(gu[0], gu[1], gu[2], 2, gt[4].ptr, gt[1], m)
 
     def step(i):
-        for _, d, n, _, w, q8, out in mats:
+        L.g4_mm_batch_q8_multi(qk[0], qk[1], qk[2], 2, q_[4].ptr, q_[1], m, g4.Q4_K)
+        for name in ("o", "inp_gate", "proj"):
+            d, n, _, w, q8, out, _ = mats[name]
             L.g4_mm_batch_q8(out.ptr, w.ptr, q8.ptr, n, d, m, g4.Q4_K)
+        gate_up(i)
 
     ms = _time_steps(lib, step, args)
     per_step = ms / 1e3 / args.steps
-    ops = sum(2.0 * m * d * n for _, d, n, *_ in mats)
-    # the dominant launch alone
-    _, d, n, _, w, q8, out = mats[3]
-
-    def one(i):
-        L.g4_mm_batch_q8(out.ptr, w.ptr, q8.ptr, n, d, m, g4.Q4_K)
-    ms1 = _time_steps(lib, one, args)
+    ops = sum(2.0 * m * d * n for d, n, *_ in mats.values())
+    ms1 = _time_steps(lib, gate_up, args)
     per1 = ms1 / 1e3 / args.steps
-    ops1 = 2.0 * m * d * n
+    ops1 = 2.0 * m * (gt[0] + up[0]) * gt[1]
     tf1 = ops1 / per1 / 1e12
-    name = "mm_batch_kq32_kernel<Q4_K> 10240x2560, 512 tokens"
+    name = "mm_batch_img_kernel gate|up 2x10240x2560, 512 tokens"
     res = {
         "value": round(m / per_step, 1), "unit": "tok/s (one layer's Q4_K GEMMs)", "higher_is_better": True,
-        "ms_per_step": ms / args.steps, "dtype": "u4 x int8 -> exact fp16 matrix products, fp32 block combine",
+        "ms_per_step": ms / args.steps,
+        "dtype": "u4 x int8 -> exact fp16 matrix products (gate/up: fp16 sc*q images), fp32 block combine",
         "config": {"workload": "batched prefill GEMM: 512 tokens x one E4B SWA layer's Q4_K matrices "
-                               "(Q 2048, K 512, O 2560<-2048, gate/up 10240, PLE 256/2560) (seed 1)",
+                               "(Q|K 2048+512, O 2560<-2048, gate|up 2x10240 on images, PLE 256/2560) (seed 1)",
                    "tokens": m, "layer_tflops": round(ops / per_step / 1e12, 2)},
         "roofline": {"bound": "mfma", "achieved": round(tf1, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf1 / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(name),
                      "kernel": name, "us_per_launch": round(per1 * 1e6, 2)},
     }
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_prefill_baseline(mats[3][3], mats[3][2], mats[3][1])
+        res["cpu_baseline"] = cpu_prefill_baseline(gt[2], gt[1], gt[0])
     return res
 
 
