@@ -1284,6 +1284,196 @@ __global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(H
     }
 }
 
+// ---- query rows on the fp16 matrix cores, split operands -----------------
+// attn_rows_mfma_kernel's partials with its products on v_mfma_f32_16x16x32
+// / 16x16x16 f16 instead of 16x16x4 f32: every operand v is split into fp16
+// hi = fp16(v) and lo = fp16(v - hi) (v - hi is exact in fp32), and a product
+// a.b is hi_a.hi_b + hi_a.lo_b + lo_a.hi_b (three MFMAs; the dropped lo.lo is
+// below 2^-22 of |a.b|), summed in fp32.  K, V (RMS-normalised rows), q and the
+// softmax weights (<= e^kRowsLazy) lie well inside fp16's range.  Per 16-key
+// tile and wave:
+//   S^T = K . Q^T   HD/32 steps of three 16x16x32 MFMAs: lane (j, g) gives K
+//                   row j and its q row j, dims 32s + 8g .. +7
+//   O^T += V^T.P^T  HD/16 blocks of three 16x16x16 MFMAs: lane (j, g) gives
+//                   V^T row (dim) 16b + j at keys 4g .. 4g+3 (V staged
+//                   transposed) and its own weights p[0..3] (keys 4g + r of
+//                   row j), the layout the softmax leaves them in
+// so that the matrix-core work per tile is about a fifth of the fp32 form's.
+typedef _Float16 ah4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 ah8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ _Float16 split_hi(float v) { return (_Float16)v; }
+__device__ __forceinline__ _Float16 split_lo(float v, _Float16 h) { return (_Float16)(v - (float)h); }
+
+template <int HD>
+__global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 1))) void attn_rows_h16_kernel(AttnArgs a) {
+    constexpr int NTH = 64 * kRowsKVM;
+    constexpr int KS = HD + 8;            // K row stride (fp16)
+    constexpr int VS = 16 + 4;            // V^T row stride (fp16): 16 keys + pad
+    constexpr int NS = HD / 32;           // score steps
+    constexpr int NB = HD / 16;           // O tiles
+    constexpr int LU = 16 * (HD / 4) / NTH;   // float4 of K (and of V) per thread and tile
+    static_assert(LU * NTH == 16 * (HD / 4), "tile staging");
+    __shared__ __align__(16) _Float16 kh[16 * KS], kl[16 * KS];
+    __shared__ __align__(16) _Float16 vh[HD * VS], vl[HD * VS];
+    const int c = blockIdx.x, kvh = blockIdx.y, rb = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, j = lane & 15;
+    const int head = kvh * kRowsKVM + wave;
+    const int M = a.qrows;
+    const int z0 = 16 * rb, z1 = min(z0 + 16, M) - 1;
+    const int lo = a.window > 0 ? max(0, a.p0 + z0 + 1 - a.window) : 0;
+    const int hi = a.p0 + z1;
+    const int cs = ((hi - lo + a.G) / a.G + 15) & ~15;    // ceil((hi - lo + 1) / G), whole tiles
+    const int cb = lo + c * cs, ce = min(cb + cs, hi + 1);
+    const int z = z0 + j;
+    const int qp = a.p0 + z;
+    const int qlo = a.window > 0 ? max(0, qp + 1 - a.window) : 0;
+
+    f4_t kr[LU], vr[LU];
+    const float* kcb = a.kc + (size_t)kvh * HD;
+    const float* vcb = a.vc + (size_t)kvh * HD;
+    const float* kqb = a.kchunk + (size_t)kvh * HD;
+    const float* vqb = a.vchunk + (size_t)kvh * HD;
+    const int tl = ce - 1;
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int idx = u * NTH + tid, key = idx / (HD / 4), c4 = idx - key * (HD / 4);
+            const int t = min(t0 + key, tl);
+            const bool own = t >= a.p0;
+            const size_t off = (size_t)(own ? t - a.p0 : attn_slot(a, t)) * a.kv_stride;
+            const uintptr_t kb = own ? (uintptr_t)kqb : (uintptr_t)kcb;
+            const uintptr_t vb = own ? (uintptr_t)vqb : (uintptr_t)vcb;
+            kr[u] = reinterpret_cast<const g4_gf4_t*>(kb + 4 * off)[c4];
+            vr[u] = reinterpret_cast<const g4_gf4_t*>(vb + 4 * off)[c4];
+        }
+    };
+    load_tile(cb);   // an empty chunk (cb > hi) loads position hi: ce - 1 = hi
+
+    ah8_t qh[NS], ql[NS];
+    {
+        const float* qrow = a.q + (size_t)min(z, M - 1) * a.n_heads * HD + (size_t)head * HD + 8 * g;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const float4 t0 = reinterpret_cast<const float4*>(qrow + 32 * s)[0];
+            const float4 t1 = reinterpret_cast<const float4*>(qrow + 32 * s)[1];
+            const float v[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const _Float16 h = split_hi(v[t]);
+                qh[s][t] = h;
+                ql[s][t] = split_lo(v[t], h);
+            }
+        }
+    }
+
+    float m = -INFINITY, lsum = 0.0f;   // lsum: this lane's keys only (summed over the groups at the end)
+    f4_t o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) o[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t0 = cb; t0 < ce; t0 += 16) {
+        __syncthreads();   // every wave is done with the previous tile
+#pragma unroll
+        for (int u = 0; u < LU; u++) {
+            const int idx = u * NTH + tid, key = idx / (HD / 4), c4 = idx - key * (HD / 4);
+            ah4_t h4, l4;
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                const _Float16 h = split_hi(kr[u][x]);
+                h4[x] = h;
+                l4[x] = split_lo(kr[u][x], h);
+            }
+            *reinterpret_cast<ah4_t*>(kh + key * KS + 4 * c4) = h4;
+            *reinterpret_cast<ah4_t*>(kl + key * KS + 4 * c4) = l4;
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                const _Float16 h = split_hi(vr[u][x]);
+                vh[(4 * c4 + x) * VS + key] = h;
+                vl[(4 * c4 + x) * VS + key] = split_lo(vr[u][x], h);
+            }
+        }
+        __syncthreads();
+        load_tile(t0 + 16 < ce ? t0 + 16 : t0);
+
+        // scores: hi.hi, hi.lo and lo.hi in three accumulators
+        f4_t acc[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) acc[k] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        const _Float16* kph = kh + j * KS + 8 * g;
+        const _Float16* kpl = kl + j * KS + 8 * g;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const ah8_t Ah = *reinterpret_cast<const ah8_t*>(kph + 32 * s);
+            const ah8_t Al = *reinterpret_cast<const ah8_t*>(kpl + 32 * s);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, qh[s], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, ql[s], acc[1], 0, 0, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, qh[s], acc[2], 0, 0, 0);
+        }
+        const f4_t sc = acc[0] + (acc[1] + acc[2]);
+
+        // online softmax over the tile's keys 4g + r of row j (as in attn_rows_mfma_kernel)
+        float sv[4], mt = -INFINITY;
+        bool val[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int kt = t0 + 4 * g + r;
+            val[r] = kt < ce && kt >= qlo && kt <= qp;
+            sv[r] = val[r] ? a.scale * sc[r] : -INFINITY;
+            mt = fmaxf(mt, sv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const bool up = mt > m + kRowsLazy;
+        const float mn = up ? mt : m;
+        const float alpha = !up ? 1.0f : m == -INFINITY ? 0.0f : expf(m - mn);
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = val[r] ? expf(sv[r] - mn) : 0.0f;
+            ps += p[r];
+        }
+        lsum = lsum * alpha + ps;
+        m = mn;
+        if (__ballot(up)) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) o[b] *= alpha;
+        }
+
+        // O^T += V^T . P^T
+        ah4_t Ph, Pl;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const _Float16 h = split_hi(p[r]);
+            Ph[r] = h;
+            Pl[r] = split_lo(p[r], h);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const ah4_t Vh = *reinterpret_cast<const ah4_t*>(vh + (16 * b + j) * VS + 4 * g);
+            const ah4_t Vl = *reinterpret_cast<const ah4_t*>(vl + (16 * b + j) * VS + 4 * g);
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(Vh, Ph, o[b], 0, 0, 0);
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(Vh, Pl, o[b], 0, 0, 0);
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(Vl, Ph, o[b], 0, 0, 0);
+        }
+    }
+
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (z < M) {
+        // o[b][r] is dim 16b + 4g + r of row z
+        float* pp = a.part + (size_t)z * a.part_z + ((size_t)head * a.G + c) * (HD + 2);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g) = make_float2(o[b][0], o[b][1]);
+            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g + 2) = make_float2(o[b][2], o[b][3]);
+        }
+        if (g == 0) {
+            pp[HD] = m;
+            pp[HD + 1] = lsum;
+        }
+    }
+}
+
 // partial kernel LDS: work region + (max, sum) pairs [+ this position's K, V]
 size_t attn_lds(int hd, int kvm, bool fused) {
     return 4 * (fused ? (size_t)attn_new_kv_off(hd, kvm) + 2 * (size_t)hd
@@ -1337,13 +1527,14 @@ int launch_attn(const AttnArgs& a) {
     if (a.qrows && kvm == kRowsKVM) {
         const dim3 rgrid(a.G, a.n_kv, (a.qrows + 15) / 16);
         if (a.hd == 256) {
-            hipLaunchKernelGGL(attn_rows_mfma_kernel<256>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
+            hipLaunchKernelGGL(attn_rows_h16_kernel<256>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
             launch_merge<256>(a, dim3(a.n_heads, 1, zq));
         } else {
+            // (the split form needs 35 VGPRs more than a wave has at hd 512)
             hipLaunchKernelGGL(attn_rows_mfma_kernel<512>, rgrid, dim3(64 * kRowsKVM), 0, g4_stream(), a);
             launch_merge<512>(a, dim3(a.n_heads, 2, zq));
         }
-        return g4_check_launch("attn_rows_mfma_kernel/attn_merge_kernel");
+        return g4_check_launch("attn_rows_h16_kernel/attn_rows_mfma_kernel/attn_merge_kernel");
     }
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
         if (a.hd == 256) {
