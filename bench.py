@@ -372,7 +372,7 @@ def bench_prefill(lib, g4, synth, args):
     gu = (VP2(gt[5].ptr, up[5].ptr), VP2(gt[6].ptr, up[6].ptr), I2(gt[0], up[0]))
 
     def gate_up(i):
-        L.g4_mm_batch_img_multi(gu[0], gu[1], gu[2], 2, gt[4].ptr, gt[1], m)
+        L.g4_mm_batch_img_multi(gu[0], gu[1], gu[2], 2, gt[4].ptr, gt[1], m, g4.Q4_K)
 
     def step(i):
         L.g4_mm_batch_q8_multi(qk[0], qk[1], qk[2], 2, q_[4].ptr, q_[1], m, g4.Q4_K)

@@ -1288,10 +1288,19 @@ __global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(H
 // attn_rows_mfma_kernel's partials with its products on v_mfma_f32_16x16x32
 // / 16x16x16 f16 instead of 16x16x4 f32: every operand v is split into fp16
 // hi = fp16(v) and lo = fp16(v - hi) (v - hi is exact in fp32), and a product
-// a.b is hi_a.hi_b + hi_a.lo_b + lo_a.hi_b (three MFMAs; the dropped lo.lo is
-// below 2^-22 of |a.b|), summed in fp32.  K, V (RMS-normalised rows), q and the
-// softmax weights (<= e^kRowsLazy) lie well inside fp16's range.  Per 16-key
-// tile and wave:
+// a.b is hi_a.hi_b + hi_a.lo_b + lo_a.hi_b (three MFMAs), summed in fp32.
+// Error of the split: |v - hi - lo| <= max(2^-22 |v|, 2^-25) -- relative while
+// lo is an fp16 normal, and half the fp16 subnormal spacing (2^-24) once lo
+// falls below 2^-14, i.e. for |v| below about 2^-3 -- and the dropped lo.lo
+// is below 2^-22 |a.b|; so a product carries at most about
+// 3 * 2^-22 |a.b| + 2^-25 (|a| + |b|).  The softmax weights (<= e^kRowsLazy)
+// are split as 16 p (below fp16's maximum; the partial o is scaled back by
+// 1/16, exactly), which moves their absolute floor to 2^-29: a weight of
+// 1e-3 keeps 2^-19 of relative precision instead of 2^-15.  K and V are the
+// RMS-normalised rows (elements of order 1, at most sqrt(head_dim)) and q
+// the normalised query, well inside fp16's range; operands far smaller than
+// that (V of order 1e-3) would meet the 2^-25 floor.  Per 16-key tile and
+// wave:
 //   S^T = K . Q^T   HD/32 steps of three 16x16x32 MFMAs: lane (j, g) gives K
 //                   row j and its q row j, dims 32s + 8g .. +7
 //   O^T += V^T.P^T  HD/16 blocks of three 16x16x16 MFMAs: lane (j, g) gives
@@ -1443,9 +1452,10 @@ __global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(H
         ah4_t Ph, Pl;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const _Float16 h = split_hi(p[r]);
+            const float p16 = 16.0f * p[r];      // <= 16 e^kRowsLazy < 65504; exact
+            const _Float16 h = split_hi(p16);
             Ph[r] = h;
-            Pl[r] = split_lo(p[r], h);
+            Pl[r] = split_lo(p16, h);
         }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
@@ -1462,10 +1472,11 @@ __global__ __launch_bounds__(64 * kRowsKVM) __attribute__((amdgpu_waves_per_eu(H
     if (z < M) {
         // o[b][r] is dim 16b + 4g + r of row z
         float* pp = a.part + (size_t)z * a.part_z + ((size_t)head * a.G + c) * (HD + 2);
+        constexpr float kUn16 = 1.0f / 16.0f;   // the weights' factor 16, exactly
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g) = make_float2(o[b][0], o[b][1]);
-            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g + 2) = make_float2(o[b][2], o[b][3]);
+            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g) = make_float2(o[b][0] * kUn16, o[b][1] * kUn16);
+            *reinterpret_cast<float2*>(pp + 16 * b + 4 * g + 2) = make_float2(o[b][2] * kUn16, o[b][3] * kUn16);
         }
         if (g == 0) {
             pp[HD] = m;

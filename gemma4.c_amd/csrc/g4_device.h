@@ -132,6 +132,40 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // GELU, tanh form, evaluated in the reference's operation order (main.c:1490-1492)
+// ---- argmax keys: first index of the maximum -------------------------------
+// key = order-preserving bits of the value (high word) and ~index (low word):
+// the largest key is the largest value at its smallest index.  -0.0 is taken
+// as +0.0 so that equal values compare equal, as the C comparison does.  The
+// reference's scan (main.c:2046-2048) never moves to a NaN and never leaves
+// one at index 0 (every comparison with it is false): a NaN gets the lowest
+// key, or the highest at index 0.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    if (v != v) return i == 0 ? ~0ull : 0ull;
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)i);
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+__device__ inline unsigned long long block_max_u64(unsigned long long k, unsigned long long* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    k = wave_max_u64(k);
+    if (lane == 0) red[w] = k;
+    __syncthreads();
+    unsigned long long t = 0;
+    for (int i = 0; i < nw; i++) t = red[i] > t ? red[i] : t;
+    return t;
+}
+
+
 __device__ __forceinline__ float gelu_ref(float x) {
     const float inner = 0.7978845608028654f * x * (1.0f + 0.044715f * x * x);
     return 0.5f * x * (1.0f + tanhf(inner));

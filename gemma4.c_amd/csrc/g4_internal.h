@@ -14,6 +14,9 @@ int g4_num_cus();
 // device address of the allocation-free attention's scratch on `device`
 // (current), resolved once per device; called by g4_init
 int g4_attn_scratch_setup(int device);
+// last pass of an argmax over np per-workgroup keys (argmax_key order):
+// the index to *out / *dtok (each optional), *dpos advanced if given
+int g4_argmax_final(const void* part, int np, int* out, int* dtok, int* dpos);
 
 #define G4_CHECK_ARG(cond, ...)                          \
     do {                                                 \

@@ -714,13 +714,22 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
 // and multiplied by x; a run of 8 contributes sum x*q - 32 * sum x (the run
 // sums of x are computed once per workgroup) scaled once by d*sc (the
 // reference scales every weight, (d*sc)*(q-32); results agree to fp32
-// tolerance, not bit for bit).  The first batch of weight loads is issued
-// before x is staged.
-template <int KS, bool SOFTCAP>
-__global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                            float* __restrict__ out, int nb, int d, float cap) {
+// tolerance, not bit for bit).
+// The weights stream in batches of QB blocks per lane through two register
+// sets: batch j + 1 (the next blocks of the row, or the first of the next
+// row group) is in flight while batch j is multiplied, and every load is
+// issued unconditionally on clamped indices, so the waits count exactly and
+// never drain the next batch.  The first two batches are issued before x is
+// staged.  AM: also the first-index maximum of the outputs (as stored, after
+// the soft-cap) over this workgroup's rows as an argmax key in part[block].
+template <int KS, bool SOFTCAP, bool AM = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void gemv_q6k_rows_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                            float* __restrict__ out, int nb, int d, float cap,
+                                                            unsigned long long* __restrict__ part_am) {
     // LDS: x (n floats), the sums of its runs of 8 (n/8 floats), [32] partials
     extern __shared__ __align__(16) float xs[];
+    __shared__ unsigned long long red[4];
     constexpr int RPW = 32 / KS;
     constexpr int QB = 5;                  // blocks per load batch
     const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
@@ -731,30 +740,33 @@ __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __res
     float* part = x8 + nb * 32;
     const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
     const int ngroups = (d + RPW - 1) / RPW;
+    const int nbt = ((nb + KS - 1) / KS + QB - 1) / QB;   // batches per row slice
+    const int nit = blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int nsteps = nit * nbt;
 
     struct Batch {
         uint4 ql[QB];
         uint2 qh[QB], sc[QB];
         uint32_t dv[QB];
     };
-    // this lane's blocks b0, b0+KS, ... (QB of them) of `row`
-    auto load = [&](int row, int b0, Batch& bt) {
+    // step j: batch j % nbt of this workgroup's row group j / nbt (past the
+    // last step: the last one again; blocks past the row: its last block)
+    auto load = [&](int j, Batch& bt) {
+        j = min(j, nsteps - 1);
+        const int it = j / nbt, b0 = ks + (j - it * nbt) * QB * KS;
+        const int row = min(((int)blockIdx.x + it * (int)gridDim.x) * RPW + rr, d - 1);
 #pragma unroll
         for (int i = 0; i < QB; i++) {
-            const int b = b0 + i * KS;
-            if (b < nb) {
-                const size_t blk = (size_t)row * nb + b;
-                bt.ql[i] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
-                bt.qh[i] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
-                bt.sc[i] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
-                bt.dv[i] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
-            }
+            const size_t blk = (size_t)row * nb + min(b0 + i * KS, nb - 1);
+            bt.ql[i] = *reinterpret_cast<const uint4*>(w + P.ql + blk * 128 + 16 * L);
+            bt.qh[i] = *reinterpret_cast<const uint2*>(w + P.qh + blk * 64 + 8 * L);
+            bt.sc[i] = *reinterpret_cast<const uint2*>(w + P.sc + blk * 16 + 8 * h);
+            bt.dv[i] = *reinterpret_cast<const uint16_t*>(w + P.d + blk * 2);
         }
     };
     // x (kQ6Xpt float4 per thread, the rest in a loop) and then the first
-    // batch of the first row group are in flight before anything waits: a
-    // load-then-store loop would wait for every earlier load on each of its
-    // iterations
+    // two batches are in flight before anything waits: a load-then-store
+    // loop would wait for every earlier load on each of its iterations
     constexpr int kQ6Xpt = 4;
     const int n4 = nb * 64;                // float4 of x; a multiple of 64, so a wave's lanes agree
     float4 xv[kQ6Xpt];
@@ -763,10 +775,11 @@ __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __res
         const int i = tid + 256 * j;
         xv[j] = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    Batch bt;
-    int rg = blockIdx.x;
-    bool pre = rg < ngroups && rg * RPW + rr < d && ks < nb;
-    if (pre) load(rg * RPW + rr, ks, bt);
+    Batch ba, bb;
+    if (nsteps > 0) {
+        load(0, ba);
+        load(1, bb);
+    }
     // i covers elements 4i..4i+3; pairs of float4 make one run of 8
     auto stage = [&](int i, const float4& v) {
         reinterpret_cast<float4*>(xs)[i] = v;
@@ -780,68 +793,99 @@ __global__ __launch_bounds__(256) void gemv_q6k_rows_kernel(const uint8_t* __res
         if (i < n4) stage(i, xv[j]);
     }
     for (int i = tid + 256 * kQ6Xpt; i < n4; i += 256) stage(i, reinterpret_cast<const float4*>(x)[i]);
-    __syncthreads();
-    for (; rg < ngroups; rg += gridDim.x) {
+    if (KS > 1 || n4 > 256 * kQ6Xpt) {
+        __syncthreads();
+    } else {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // LDS only: the batches stay in flight
+    }
+
+    unsigned long long best = 0;           // argmax key of this thread's rows
+    float acc = 0.0f;
+    auto compute = [&](const Batch& bt, int j) {
+        const int it = j / nbt, jb = j - it * nbt, b0 = ks + jb * QB * KS;
+        const int rg = (int)blockIdx.x + it * (int)gridDim.x;
         const int row = rg * RPW + rr;
-        float acc = 0.0f;
-        if (row < d) {
-            for (int b0 = ks; b0 < nb; b0 += QB * KS) {
-                if (!pre) load(row, b0, bt);
-                pre = false;
+        if (jb == 0) acc = 0.0f;
 #pragma unroll
-                for (int i = 0; i < QB; i++) {
-                    const int b = b0 + i * KS;
-                    if (b < nb) {
-                        const uint4 ql = bt.ql[i];
-                        const uint2 qh = bt.qh[i], sc = bt.sc[i];
-                        const float df = half_bits_to_f32(bt.dv[i]);
-                        const float* xb = xs + b * 256 + 128 * h + 8 * u;
-                        const float* sb8 = x8 + b * 32 + 16 * h + u;
+        for (int i = 0; i < QB; i++) {
+            const int b = b0 + i * KS;
+            if (b < nb) {
+                const uint4 ql = bt.ql[i];
+                const uint2 qh = bt.qh[i], sc = bt.sc[i];
+                const float df = half_bits_to_f32(bt.dv[i]);
+                const float* xb = xs + b * 256 + 128 * h + 8 * u;
+                const float* sb8 = x8 + b * 32 + 16 * h + u;
 #pragma unroll
-                        for (int kk = 0; kk < 4; kk++) {
-                            const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
-                            const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
-                            const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
-                            const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
-                            const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);   // q in [0, 63]
-                            const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
-                            const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
-                            const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
-                            // sum_e x_e (q_e - 32) = sum_e x_e q_e - 32 * sum_e x_e
-                            float dot = x0.x * (float)(ca & 0xff);
-                            dot = __builtin_fmaf(x0.y, (float)((ca >> 8) & 0xff), dot);
-                            dot = __builtin_fmaf(x0.z, (float)((ca >> 16) & 0xff), dot);
-                            dot = __builtin_fmaf(x0.w, (float)(ca >> 24), dot);
-                            dot = __builtin_fmaf(x1.x, (float)(cb & 0xff), dot);
-                            dot = __builtin_fmaf(x1.y, (float)((cb >> 8) & 0xff), dot);
-                            dot = __builtin_fmaf(x1.z, (float)((cb >> 16) & 0xff), dot);
-                            dot = __builtin_fmaf(x1.w, (float)(cb >> 24), dot);
-                            dot = __builtin_fmaf(-32.0f, sb8[4 * kk], dot);
-                            const int sbi = (u >> 1) + 2 * kk;
-                            const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
-                            acc = __builtin_fmaf(df * (float)s8, dot, acc);
-                        }
-                    }
+                for (int kk = 0; kk < 4; kk++) {
+                    const uint32_t qa = (kk & 1) ? ql.z : ql.x;      // codes e = 0..3
+                    const uint32_t qb = (kk & 1) ? ql.w : ql.y;      // codes e = 4..7
+                    const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+                    const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+                    const uint32_t ca = la | (((qh.x >> (2 * kk)) & 0x03030303u) << 4);   // q in [0, 63]
+                    const uint32_t cb = lb | (((qh.y >> (2 * kk)) & 0x03030303u) << 4);
+                    const float4 x0 = *reinterpret_cast<const float4*>(xb + 32 * kk);
+                    const float4 x1 = *reinterpret_cast<const float4*>(xb + 32 * kk + 4);
+                    // sum_e x_e (q_e - 32) = sum_e x_e q_e - 32 * sum_e x_e
+                    float dot = x0.x * (float)(ca & 0xff);
+                    dot = __builtin_fmaf(x0.y, (float)((ca >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(x0.z, (float)((ca >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(x0.w, (float)(ca >> 24), dot);
+                    dot = __builtin_fmaf(x1.x, (float)(cb & 0xff), dot);
+                    dot = __builtin_fmaf(x1.y, (float)((cb >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(x1.z, (float)((cb >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(x1.w, (float)(cb >> 24), dot);
+                    dot = __builtin_fmaf(-32.0f, sb8[4 * kk], dot);
+                    const int sbi = (u >> 1) + 2 * kk;
+                    const int8_t s8 = (int8_t)byte_of(sbi < 4 ? sc.x : sc.y, sbi & 3);
+                    acc = __builtin_fmaf(df * (float)s8, dot, acc);
                 }
             }
         }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 4, 64);
+        if (jb != nbt - 1) return;
+        // the row slice is done: sum over the group's 8 lanes (and the KS
+        // slices), store, and keep the argmax key
+        float a = acc;
+        a += __shfl_xor(a, 1, 64);
+        a += __shfl_xor(a, 2, 64);
+        a += __shfl_xor(a, 4, 64);
         if (KS > 1) {
-            if (L == 0) part[g] = acc;
+            if (L == 0) part[g] = a;
             __syncthreads();
             if (tid < RPW) {
                 float s = 0.0f;
 #pragma unroll
-                for (int j = 0; j < KS; j++) s += part[j * RPW + tid];
+                for (int q = 0; q < KS; q++) s += part[q * RPW + tid];
                 const int r = rg * RPW + tid;
-                if (r < d) out[r] = SOFTCAP ? cap * tanhf(s * inv) : s;
+                if (r < d) {
+                    const float v = SOFTCAP ? cap * tanhf(s * inv) : s;
+                    out[r] = v;
+                    if (AM) {
+                        const unsigned long long k = argmax_key(v, r);
+                        best = k > best ? k : best;
+                    }
+                }
             }
             __syncthreads();
         } else if (L == 0 && row < d) {
-            out[row] = SOFTCAP ? cap * tanhf(acc * inv) : acc;
+            const float v = SOFTCAP ? cap * tanhf(a * inv) : a;
+            out[row] = v;
+            if (AM) {
+                const unsigned long long k = argmax_key(v, row);
+                best = k > best ? k : best;
+            }
         }
+    };
+    // steps in pairs over the two register sets (loads past the end repeat
+    // the last step: no branch separates a load from its use)
+    for (int j = 0; j < nsteps; j += 2) {
+        compute(ba, j);
+        load(j + 2, ba);
+        if (j + 1 < nsteps) compute(bb, j + 1);
+        load(j + 3, bb);
+    }
+    if (AM) {
+        best = block_max_u64(best, red);
+        if (tid == 0) part_am[blockIdx.x] = best;
     }
 }
 
@@ -1048,7 +1092,7 @@ void launch_q6_ks(const void* w, const float* x, float* o, int nb, int d, float 
     if (grid > ngroups) grid = ngroups;
     const size_t lds = (size_t)nb * 1024 + (size_t)nb * 128 + 32 * 4;
     hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP>), dim3(grid), dim3(256), lds, g4_stream(),
-                       (const uint8_t*)w, x, o, nb, d, cap);
+                       (const uint8_t*)w, x, o, nb, d, cap, nullptr);
 }
 
 template <bool SOFTCAP>
@@ -1240,6 +1284,61 @@ extern "C" int g4_mm_quant_rows_softcap(float* o, const float* x, const void* w,
     if (type != G4_Q6_K) return g4_fail(G4_ERR_TYPE, "g4_mm_quant_rows_softcap: type %d not supported", type);
     if (!(cap > 0.0f)) return launch_q6_f32<false>(w, x, o, n / 256, d, 0.0f);
     return launch_q6_f32<true>(w, x, o, n / 256, d, cap);
+}
+
+// rows kernel with the argmax keys: returns the grid (number of keys)
+template <bool SOFTCAP, int KS>
+int launch_q6_am(const void* w, const float* x, float* o, int nb, int d, float cap, unsigned long long* part) {
+    const int ngroups = (d + 32 / KS - 1) / (32 / KS);
+    int grid = 4 * g4_num_cus();
+    if (grid > ngroups) grid = ngroups;
+    const size_t lds = (size_t)nb * 1024 + (size_t)nb * 128 + 32 * 4;
+    hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP, true>), dim3(grid), dim3(256), lds, g4_stream(),
+                       (const uint8_t*)w, x, o, nb, d, cap, part);
+    return grid;
+}
+
+template <bool SOFTCAP>
+int launch_q6_am_ks(const void* w, const float* x, float* o, int nb, int d, float cap, unsigned long long* part) {
+    const int target = 2 * g4_num_cus();
+    if ((d + 31) / 32 >= target) return launch_q6_am<SOFTCAP, 1>(w, x, o, nb, d, cap, part);
+    if ((d + 15) / 16 >= target) return launch_q6_am<SOFTCAP, 2>(w, x, o, nb, d, cap, part);
+    if ((d + 7) / 8 >= target) return launch_q6_am<SOFTCAP, 4>(w, x, o, nb, d, cap, part);
+    return launch_q6_am<SOFTCAP, 8>(w, x, o, nb, d, cap, part);
+}
+
+extern "C" size_t g4_mm_argmax_part_bytes(int d) {
+    const size_t a = (size_t)4 * g4_num_cus(), b = g4_argmax_part_bytes(d > 0 ? d : 1) / 8;
+    return 8 * (a > b ? a : b);
+}
+
+// mm_argmax_row (main.c:1570-1667) and the greedy choice after logits_tied
+// (main.c:1780-1796, 2045-2049): the first index of the largest output of
+// W . x, of cap * tanh(W . x / cap) when cap > 0.  Q6_K: one launch of the
+// LM-head rows kernel that also reduces each workgroup's rows to an argmax
+// key, then the final pass; the outputs (d floats) go to logits either way
+// (1 MB at the vocabulary of Gemma 4, small beside the 551 MB of weights).
+// The other types: g4_mm into logits, the soft-cap, g4_argmax.
+extern "C" int g4_mm_argmax_row(const float* x, const void* w, int n, int d, int type, void* q8, float cap,
+                                float* logits, void* part, int* out, int* dtok, int* dpos) {
+    G4_CHECK_ARG(x && w && part && n > 0 && d > 0, "g4_mm_argmax_row: bad arguments");
+    if (type == G4_Q6_K) {
+        if (n % 256) return g4_fail(G4_ERR_ARG, "g4_mm_argmax_row: n=%d is not a multiple of 256", n);
+        G4_CHECK_ARG(aligned16(w) && aligned16(x), "g4_mm_argmax_row: w and x must be 16-byte aligned");
+        float* o = logits;
+        G4_CHECK_ARG(o != nullptr, "g4_mm_argmax_row: the logits buffer (d floats) is required");
+        unsigned long long* pk = (unsigned long long*)part;
+        const int np = cap > 0.0f ? launch_q6_am_ks<true>(w, x, o, n / 256, d, cap, pk)
+                                  : launch_q6_am_ks<false>(w, x, o, n / 256, d, 0.0f, pk);
+        int rc = g4_check_launch("gemv_q6k_rows_kernel (argmax)");
+        if (rc) return rc;
+        return g4_argmax_final(part, np, out, dtok, dpos);
+    }
+    G4_CHECK_ARG(logits, "g4_mm_argmax_row: type %d needs the logits buffer (d floats)", type);
+    int rc = g4_mm(logits, x, w, n, d, type, q8, 0);
+    if (rc) return rc;
+    if (cap > 0.0f && (rc = g4_softcap(logits, d, cap))) return rc;
+    return g4_argmax(logits, d, out, part, dtok, dpos);
 }
 
 extern "C" int g4_mm_bf16(float* o, const float* x, const void* w, int n, int d) {

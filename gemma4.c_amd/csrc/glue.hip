@@ -123,38 +123,7 @@ __global__ __launch_bounds__(256) void gelu_mul_quant_kernel(float* __restrict__
 }
 
 // ---- argmax, first index of the maximum ------------------------------------
-// key = order-preserving bits of the value (high word) and ~index (low word):
-// the largest key is the largest value at its smallest index.  -0.0 is taken
-// as +0.0 so that equal values compare equal, as the C comparison does.  The
-// reference's scan (main.c:2046-2048) never moves to a NaN and never leaves
-// one at index 0 (every comparison with it is false): a NaN gets the lowest
-// key, or the highest at index 0.
-__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
-    if (v != v) return i == 0 ? ~0ull : 0ull;
-    uint32_t u = __float_as_uint(v + 0.0f);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)i);
-}
-
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const unsigned long long o = __shfl_xor(k, m, 64);
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
-__device__ unsigned long long block_max_u64(unsigned long long k, unsigned long long* red) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    k = wave_max_u64(k);
-    if (lane == 0) red[w] = k;
-    __syncthreads();
-    unsigned long long t = 0;
-    for (int i = 0; i < nw; i++) t = red[i] > t ? red[i] : t;
-    return t;
-}
-
+// (keys: argmax_key in g4_device.h)
 constexpr int kArgmaxThreads = 256;
 constexpr int kArgmaxPer = 4096;   // elements per partial workgroup
 
@@ -197,6 +166,14 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const unsi
 }  // namespace g4
 
 using namespace g4;
+
+// the last pass of the argmax over np per-workgroup keys (the fused
+// LM-head kernel's, or argmax_partial_kernel's)
+int g4_argmax_final(const void* part, int np, int* out, int* dtok, int* dpos) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, g4_stream(),
+                       (const unsigned long long*)part, np, out, dtok, dpos);
+    return g4_check_launch("argmax_final_kernel");
+}
 
 static bool table_type_ok(int type) {
     return type == G4_F32 || type == G4_F16 || type == G4_BF16 || type == G4_Q4_K || type == G4_Q5_K ||

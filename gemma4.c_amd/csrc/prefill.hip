@@ -13,13 +13,21 @@
 // Q4_K / Q5_K (mm_batch_kq32_kernel).  The reference's dot per block is
 //   y.d * d * sum_j sc_j * sum_e q_e * q8_e  -  y.d * dmin * sum_j m_j * bs_j
 // (vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K, main.c:476-529, 531-593; bs_j =
-// the two 16-element bsums of sub-block j).  The first sum runs on
+// the two 16-element bsums of sub-block j).  The first sum, S_b, runs on
 // v_mfma_f32_32x32x16_f16 with the sub-block scale folded into the weight
 // operand: sc * q <= 63 * 31 is an integer below 2048 and |q8| <= 128, so
-// every product is exact and the matrix core only rounds partial sums above
-// 2^24.  The sixteen 16-long K steps of a block chain in one accumulator, the
-// min sum is two 8-long MFMAs, and the block is folded into the fp32
-// accumulator with three VALU operations per output.  The weights are the B
+// every product is exact.  A whole block can reach |S_b| = 256 * 63 * 15 *
+// 128 (Q4_K, 3.1e7) or 256 * 63 * 31 * 128 (Q5_K, 6.4e7), past 2^24, so the
+// sixteen 16-long K steps are chained in pieces whose partial sums cannot
+// leave the exact range (kChainSteps: Q4_K 8 steps = 128 products, at most
+// 1.55e7; Q5_K 4 steps = 64 products, at most 1.60e7): every chain is an
+// exact integer whatever order the matrix core adds in.  Q4_K's two chains
+// are added in fp32 (both exact, so the sum is the exact S_b rounded once,
+// the same value as the int32 sum converted); Q5_K's four are converted and
+// added as int32.  The min sum M_b (|M_b| <= 16 * 63 * 2048, exact) is two
+// 8-long MFMAs, and the block is folded into the fp32 accumulator with three
+// VALU operations per output.  MODE 2 stores the int32 S_b and M_b of every
+// (token, row, block) instead (g4_debug_batch_block_sums).  The weights are the B
 // operand, so a lane's outputs share one weight row and its d, dmin and
 // scales come from the block header the lane loads itself.  Work split: a
 // 256-thread workgroup owns 128 weight rows (32 per wave) x 32 NT tokens;
@@ -143,11 +151,56 @@ struct KqSegs {
     int n;
 };
 
-// PB: one block per workgroup (blockIdx.y), whose per-block term u (before
-// the token's Q8_K d) is stored instead of folded: out gets nb slices of m x d
-template <bool Q5, int NT, int NWV, bool PB = false>
+// K steps (16 products each) per exactly summed chain of a block's S_b
+template <bool Q5>
+constexpr int kChainSteps = Q5 ? 4 : 8;
+
+// after K step s of a block: at the end of a chain, keep its exact sum
+// (Q4_K: the first chain in P; Q5_K: added into the int32 sum SI)
+template <bool Q5>
+__device__ __forceinline__ void chain_end(int s, const f16v_t& S, f16v_t& P, int (&SI)[16]) {
+    constexpr int CS = kChainSteps<Q5>;
+    if (s % CS != CS - 1) return;
+    if (Q5) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) SI[v] = (s == CS - 1 ? 0 : SI[v]) + (int)S[v];
+    } else if (s == CS - 1) {
+        P = S;
+    }
+}
+
+// output v's S_b as fp32: Q4_K the fp32 sum of two exact chains (the exact
+// integer rounded once), Q5_K the int32 sum converted
+template <bool Q5>
+__device__ __forceinline__ float chain_block_sum(const f16v_t& S, const f16v_t& P, const int (&SI)[16], int v) {
+    return Q5 ? (float)SI[v] : P[v] + S[v];
+}
+
+// the int32 S_b and M_b of output v = 8 (v >> 2) + (v & 3) of token t0 + ...
+template <bool Q5>
+__device__ __forceinline__ void store_block_sums(int32_t* So, int32_t* Mo, const f16v_t& S, const f16v_t& P,
+                                                 const int (&SI)[16], const f16v_t& M, int row, int d, int t0, int m,
+                                                 int nb, int b) {
+    if (row >= d) return;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int tok = t0 + 8 * (v >> 2) + (v & 3);
+        if (tok >= m) continue;
+        const size_t o = ((size_t)tok * d + row) * nb + b;
+        So[o] = Q5 ? SI[v] : (int)P[v] + (int)S[v];
+        Mo[o] = (int)M[v];
+    }
+}
+
+// MODE 0: the outputs.  MODE 1 (PB): one block per workgroup (blockIdx.y),
+// whose per-block term u (before the token's Q8_K d) is stored instead of
+// folded: out gets nb slices of m x d.  MODE 2 (DB): every block's int32 S_b
+// and M_b into S = o[0] and M = o[1], each [m][d][nb] (one segment).
+template <bool Q5, int NT, int NWV, int MODE = 0>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
+    constexpr bool PB = MODE == 1, DB = MODE == 2;
+    constexpr int CS = kChainSteps<Q5>;
     constexpr int NTH = 64 * NWV;
     constexpr int TOK = 32 * NT;
     constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, Q8_K lane) units of 32 bytes per thread
@@ -288,7 +341,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
             NB[j] = h2_t{(_Float16)(-1024.0f) * sb, (_Float16)(-1024.0f) * sb};
         }
 
-        f16v_t S[NT];
+        // S: the running chain; P: Q4_K's first chain; SI: Q5_K's int32 sum
+        f16v_t S[NT], P[NT];
+        int SI[NT][16];
         const uint8_t* at0 = sA[st] + i * kKqTok + 16 * kg;
 #pragma unroll
         for (int s = 0; s < 16; s++) {
@@ -310,7 +365,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const h8_t A = *reinterpret_cast<const h8_t*>(at0 + 32 * nt * kKqTok + 32 * s);
-                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s == 0 ? zero : S[nt], 0, 0, 0);
+                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s % CS == 0 ? zero : S[nt], 0, 0, 0);
+                chain_end<Q5>(s, S[nt], P[nt], SI[nt]);
             }
         }
         // min sums (bsums 4kg.. and 8+4kg..: sub-blocks 2kg, 2kg+1, 4+2kg,
@@ -326,6 +382,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
             const h4_t A1 = *reinterpret_cast<const h4_t*>(bs), A2 = *reinterpret_cast<const h4_t*>(bs + 16);
             f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
             M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
+            if (DB) {
+                store_block_sums<Q5>(reinterpret_cast<int32_t*>(sg.o[0]), reinterpret_cast<int32_t*>(sg.o[1]), S[nt],
+                                     P[nt], SI[nt], M, row, d, tokb + 32 * nt + 4 * kg, m, nb, b);
+                continue;
+            }
 #pragma unroll
             for (int a = 0; a < 4; a++) {
                 const float4 yd = *reinterpret_cast<const float4*>(sD[st] + 32 * nt + 8 * a + 4 * kg);
@@ -333,7 +394,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const int v = 4 * a + c;
-                    const float u = __builtin_fmaf(dx, S[nt][v], -(dmx * M[v]));
+                    const float u = __builtin_fmaf(dx, chain_block_sum<Q5>(S[nt], P[nt], SI[nt], v), -(dmx * M[v]));
                     acc[nt][v] = PB ? u : __builtin_fmaf(y4[c], u, acc[nt][v]);
                 }
             }
@@ -349,7 +410,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         if (b + 1 < b1) block(b + 1, 1, w1, w0);
     }
 
-    if (row < d) {
+    if (!DB && row < d) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
@@ -370,8 +431,15 @@ void launch_mm_batch32(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
 template <bool Q5>
 void launch_mm_batch32_blocks(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
     const int gy = (m + 31) / 32;
-    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, true>), dim3(sg.g0[sg.n] * gy, nb), dim3(256), 0, g4_stream(), sg,
+    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, 1>), dim3(sg.g0[sg.n] * gy, nb), dim3(256), 0, g4_stream(), sg,
                        q8, nb, m);
+}
+
+template <bool Q5>
+void launch_mm_batch32_sums(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
+    const int gy = (m + 31) / 32;
+    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, 2>), dim3(sg.g0[sg.n] * gy), dim3(256), 0, g4_stream(), sg, q8, nb,
+                       m);
 }
 
 // ---- Q4_K / Q5_K through fp16 weight images (mm_batch_img_kernel) --------
@@ -381,11 +449,13 @@ void launch_mm_batch32_blocks(const KqSegs& sg, const uint8_t* q8, int nb, int m
 // is loaded: every weight's sc * q (the 6-bit sub-block scale times the
 // 4/5-bit code, an integer <= 63 * 31, exact in fp16) stored as the B operand
 // of v_mfma_f32_32x32x16_f16, plus per row and block d, dmin and the mins.
-// The block sums are the same integers (exact while a block's partial sums
-// stay below 2^24, as in mm_batch_kq32_kernel: then the K order inside the
-// matrix cores does not matter) and the fold the same three fp32 steps, so
-// the outputs are mm_batch_kq32_kernel's bits; the kernel's loop is MFMAs,
-// LDS reads of the activations and the block fold.
+// The block sums are the same integers, chained in the same exact pieces as
+// in mm_batch_kq32_kernel (kChainSteps: Q4_K two chains, Q5_K four, so the
+// K order inside the matrix cores does not matter), and the fold the same
+// three fp32 steps, so the outputs are mm_batch_kq32_kernel's bits; the
+// kernel's loop is MFMAs, LDS reads of the activations and the block fold.
+// The image does not record its type: the caller names it (Q5_K needs the
+// shorter chains).
 // K positions inside a block follow the device Q8_K byte order: position
 // p = 32l + 16h + 4j + c is element 64j + 32h + 4l + c (sub-block 2j + h),
 // so a token's Q8_K bytes are its A operand in place.
@@ -455,9 +525,13 @@ __global__ __launch_bounds__(256) void kq_image_kernel(const uint8_t* __restrict
 // three times the bank-conflict cycles and took 8 % longer)
 __device__ __forceinline__ int img_slot(int s, int kg) { return (s & 7) + 8 * kg + 16 * (s >> 3); }
 
-template <int NT, int NWV>
+// MODE 0: the outputs; MODE 2: every block's int32 S_b and M_b, as
+// mm_batch_kq32_kernel's MODE 2
+template <bool Q5, int NT, int NWV, int MODE = 0>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_img_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
+    constexpr bool DB = MODE == 2;
+    constexpr int CS = kChainSteps<Q5>;
     constexpr int NTH = 64 * NWV;
     constexpr int TOK = 32 * NT;
     constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, 32-byte unit) pairs per thread
@@ -573,7 +647,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         const uint4 Hc = H;
         const int bn = min(b + 1, nb - 1);
         H = buf_load16(rw, vh, bn * kImgHdr);
-        f16v_t S[NT];
+        f16v_t S[NT], P[NT];
+        int SI[NT][16];
         const uint8_t* at0 = sA[st] + i * kKqTok;
 #pragma unroll
         for (int s = 0; s < 16; s++) {
@@ -586,7 +661,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const h8_t A = *reinterpret_cast<const h8_t*>(at0 + 32 * nt * kKqTok + so);
-                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s == 0 ? zero : S[nt], 0, 0, 0);
+                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s % CS == 0 ? zero : S[nt], 0, 0, 0);
+                chain_end<Q5>(s, S[nt], P[nt], SI[nt]);
             }
             W[s] = buf_load16(rw, vw, bn * kImgBlk + s * kImgStep);
         }
@@ -600,6 +676,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
             const h4_t A1 = *reinterpret_cast<const h4_t*>(bs), A2 = *reinterpret_cast<const h4_t*>(bs + 16);
             f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
             M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
+            if (DB) {
+                store_block_sums<Q5>(reinterpret_cast<int32_t*>(sg.o[0]), reinterpret_cast<int32_t*>(sg.o[1]), S[nt],
+                                     P[nt], SI[nt], M, gw < rg ? row : d, d, tokb + 32 * nt + 4 * kg, m, nb, b);
+                continue;
+            }
 #pragma unroll
             for (int a = 0; a < 4; a++) {
                 const float4 yd = *reinterpret_cast<const float4*>(sD[st] + 32 * nt + 8 * a + 4 * kg);
@@ -607,7 +688,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const int v = 4 * a + c;
-                    acc[nt][v] = __builtin_fmaf(y4[c], __builtin_fmaf(dx, S[nt][v], -(dmx * M[v])), acc[nt][v]);
+                    acc[nt][v] = __builtin_fmaf(
+                        y4[c], __builtin_fmaf(dx, chain_block_sum<Q5>(S[nt], P[nt], SI[nt], v), -(dmx * M[v])), acc[nt][v]);
                 }
             }
         }
@@ -617,7 +699,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         if (b + 1 < nb) block(b + 1, 1);
     }
 
-    if (gw < rg && row < d) {
+    if (!DB && gw < rg && row < d) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
@@ -628,11 +710,11 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
-template <int NT, int NWV>
+template <bool Q5, int NT, int NWV, int MODE = 0>
 void launch_mm_batch_img(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
     const int gy = (m + 32 * NT - 1) / (32 * NT);
-    hipLaunchKernelGGL((mm_batch_img_kernel<NT, NWV>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(), sg, q8,
-                       nb, m);
+    hipLaunchKernelGGL((mm_batch_img_kernel<Q5, NT, NWV, MODE>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(),
+                       sg, q8, nb, m);
 }
 
 // The fold of g4_mm_batch_q8_blocks' per-block terms, in block order as the
@@ -1365,8 +1447,9 @@ extern "C" int g4_kq_image(void* img, const void* w, int n, int d, int type) {
 
 // tile: tokens per workgroup 32 nt, waves (32-row groups) nwv; 0 picks
 static int mm_batch_img_tiled(float* const* o, const void* const* img, const int* d, int nseg, const void* q8, int n,
-                              int m, int nt, int nwv) {
+                              int m, int type, int nt, int nwv) {
     G4_CHECK_ARG(o && img && d && q8, "g4_mm_batch_img: null pointer");
+    if (type != G4_Q4_K && type != G4_Q5_K) return g4_fail(G4_ERR_TYPE, "g4_mm_batch_img: type %d has no image", type);
     G4_CHECK_ARG(nseg >= 1 && nseg <= kMaxSegs, "g4_mm_batch_img: %d matrices (1..%d)", nseg, kMaxSegs);
     G4_CHECK_ARG(n > 0 && n % 256 == 0 && m > 0, "g4_mm_batch_img: n=%d m=%d", n, m);
     G4_CHECK_ARG(al16(q8), "g4_mm_batch_img: q8 must be 16-byte aligned");
@@ -1387,9 +1470,11 @@ static int mm_batch_img_tiled(float* const* o, const void* const* img, const int
             for (int k = 0; k < nseg; k++) g += (long long)((d[k] + 32 * w - 1) / (32 * w)) * ((m + 32 * t - 1) / (32 * t));
             return g;
         };
+        // (Q5_K's four chains per block do not fit 64-token tiles in registers)
         const long long cus = g4_num_cus();
-        if (wgs(2, 4) >= 8 * cus) nt = 2, nwv = 8;
-        else if (wgs(2, 4) >= cus) nt = 2, nwv = 4;
+        const bool q5 = type == G4_Q5_K;
+        if (!q5 && wgs(2, 4) >= 8 * cus) nt = 2, nwv = 8;
+        else if (!q5 && wgs(2, 4) >= cus) nt = 2, nwv = 4;
         else if (wgs(1, 4) >= cus) nt = 1, nwv = 4;
         else nt = 1, nwv = 2;
     }
@@ -1409,28 +1494,74 @@ static int mm_batch_img_tiled(float* const* o, const void* const* img, const int
     sg.g0[nseg] = (int)gx;
     G4_CHECK_ARG(gx * ((m + 32 * nt - 1) / (32 * nt)) < (1LL << 31), "g4_mm_batch_img: %d tokens too many", m);
     const uint8_t* q = (const uint8_t*)q8;
-    switch (10 * nt + nwv) {
-    case 12: launch_mm_batch_img<1, 2>(sg, q, nb, m); break;
-    case 14: launch_mm_batch_img<1, 4>(sg, q, nb, m); break;
-    case 18: launch_mm_batch_img<1, 8>(sg, q, nb, m); break;
-    case 24: launch_mm_batch_img<2, 4>(sg, q, nb, m); break;
-    default: launch_mm_batch_img<2, 8>(sg, q, nb, m); break;
+    const int key = 10 * nt + nwv;
+    if (type == G4_Q4_K) {
+        switch (key) {
+        case 12: launch_mm_batch_img<false, 1, 2>(sg, q, nb, m); break;
+        case 14: launch_mm_batch_img<false, 1, 4>(sg, q, nb, m); break;
+        case 18: launch_mm_batch_img<false, 1, 8>(sg, q, nb, m); break;
+        case 24: launch_mm_batch_img<false, 2, 4>(sg, q, nb, m); break;
+        default: launch_mm_batch_img<false, 2, 8>(sg, q, nb, m); break;
+        }
+    } else {
+        switch (key) {
+        case 12: launch_mm_batch_img<true, 1, 2>(sg, q, nb, m); break;
+        case 14: launch_mm_batch_img<true, 1, 4>(sg, q, nb, m); break;
+        case 18: launch_mm_batch_img<true, 1, 8>(sg, q, nb, m); break;
+        case 24: launch_mm_batch_img<true, 2, 4>(sg, q, nb, m); break;
+        default: launch_mm_batch_img<true, 2, 8>(sg, q, nb, m); break;
+        }
     }
     return g4_check_launch("mm_batch_img_kernel");
 }
 
 extern "C" int g4_mm_batch_img_multi(float* const* o, const void* const* img, const int* d, int nseg, const void* q8,
-                                     int n, int m) {
-    return mm_batch_img_tiled(o, img, d, nseg, q8, n, m, 0, 0);
+                                     int n, int m, int type) {
+    return mm_batch_img_tiled(o, img, d, nseg, q8, n, m, type, 0, 0);
 }
 
-extern "C" int g4_mm_batch_img(float* o, const void* img, const void* q8, int n, int d, int m) {
-    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, 0, 0);
+extern "C" int g4_mm_batch_img(float* o, const void* img, const void* q8, int n, int d, int m, int type) {
+    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, type, 0, 0);
 }
 
 // the same with the tile given (tokens 32 nt, rows 32 nwv): shape sweeps
-extern "C" int g4_mm_batch_img_tile(float* o, const void* img, const void* q8, int n, int d, int m, int nt, int nwv) {
-    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, nt, nwv);
+extern "C" int g4_mm_batch_img_tile(float* o, const void* img, const void* q8, int n, int d, int m, int type, int nt,
+                                    int nwv) {
+    return mm_batch_img_tiled(&o, &img, &d, 1, q8, n, m, type, nt, nwv);
+}
+
+// every block's int32 S_b and M_b as the batched kernels form them: S and M
+// are [m][d][n/256]; image 0: the quantized tensor w (mm_batch_kq32_kernel),
+// 1: its fp16 image (mm_batch_img_kernel, one-wave row groups of 32 tokens)
+extern "C" int g4_debug_batch_block_sums(const void* w, int image, int n, int d, int m, int type, const void* q8,
+                                         int32_t* S, int32_t* M) {
+    G4_CHECK_ARG(w && q8 && S && M, "g4_debug_batch_block_sums: null pointer");
+    G4_CHECK_ARG(n > 0 && n % 256 == 0 && d > 0 && m > 0, "g4_debug_batch_block_sums: n=%d d=%d m=%d", n, d, m);
+    G4_CHECK_ARG(al16(w) && al16(q8), "g4_debug_batch_block_sums: w and q8 must be 16-byte aligned");
+    if (type != G4_Q4_K && type != G4_Q5_K)
+        return g4_fail(G4_ERR_TYPE, "g4_debug_batch_block_sums: type %d has no Q8_K batched path", type);
+    const int nb = n / 256;
+    G4_CHECK_ARG((size_t)m * q8_row_stride(nb) < (1u << 31) && (size_t)d * nb * 176 < (1u << 31) &&
+                     kq_img_bytes(d, nb) < (1u << 31),
+                 "g4_debug_batch_block_sums: %d x %d weights or %d rows too large", d, n, m);
+    KqSegs sg{};
+    sg.n = 1;
+    sg.w[0] = (const uint8_t*)w;
+    sg.o[0] = reinterpret_cast<float*>(S);
+    sg.o[1] = reinterpret_cast<float*>(M);   // read only by the block-sum mode
+    sg.d[0] = d;
+    sg.g0[0] = 0;
+    const uint8_t* q = (const uint8_t*)q8;
+    if (!image) {
+        sg.g0[1] = (d + 127) / 128;
+        if (type == G4_Q4_K) launch_mm_batch32_sums<false>(sg, q, nb, m);
+        else launch_mm_batch32_sums<true>(sg, q, nb, m);
+        return g4_check_launch("mm_batch_kq32_kernel (block sums)");
+    }
+    sg.g0[1] = (d + 127) / 128;
+    if (type == G4_Q4_K) launch_mm_batch_img<false, 1, 4, 2>(sg, q, nb, m);
+    else launch_mm_batch_img<true, 1, 4, 2>(sg, q, nb, m);
+    return g4_check_launch("mm_batch_img_kernel (block sums)");
 }
 
 extern "C" int g4_fold_gelu_mul_q8(const float* u, const void* q8, int n, const float* ple, int pstride, float* out,

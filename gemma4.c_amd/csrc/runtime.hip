@@ -70,7 +70,11 @@ extern "C" int g4_malloc(void** p, size_t bytes) {
     *p = nullptr;
     if (bytes == 0) return G4_OK;
     hipError_t e = hipMalloc(p, bytes);
-    if (e != hipSuccess) return g4_fail(G4_ERR_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();   // an allocation failure is not a later launch's error
+        return g4_fail(G4_ERR_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
     return G4_OK;
 }
 extern "C" int g4_free(void* p) {

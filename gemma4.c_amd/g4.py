@@ -74,9 +74,10 @@ _SIGS = {
     "g4_mm_batch_q8_multi": (I, [VP, VP, VP, I, VP, I, I, I]),
     "g4_kq_image_bytes": (SZ, [I, I]),
     "g4_kq_image": (I, [VP, VP, I, I, I]),
-    "g4_mm_batch_img": (I, [VP, VP, VP, I, I, I]),
-    "g4_mm_batch_img_multi": (I, [VP, VP, VP, I, VP, I, I]),
-    "g4_mm_batch_img_tile": (I, [VP, VP, VP, I, I, I, I, I]),
+    "g4_mm_batch_img": (I, [VP, VP, VP, I, I, I, I]),
+    "g4_mm_batch_img_multi": (I, [VP, VP, VP, I, VP, I, I, I]),
+    "g4_mm_batch_img_tile": (I, [VP, VP, VP, I, I, I, I, I, I]),
+    "g4_debug_batch_block_sums": (I, [VP, I, I, I, I, I, VP, VP, VP]),
     "g4_mm_batch": (I, [VP, VP, VP, I, I, I, I, VP]),
     "g4_split_rows_bytes": (SZ, [I, I]),
     "g4_split_rows_f16": (I, [VP, VP, I, I]),
@@ -108,6 +109,8 @@ _SIGS = {
     "g4_emb_lookup": (I, [VP, VP, I, I, I, I]),
     "g4_argmax_part_bytes": (SZ, [I]),
     "g4_argmax": (I, [VP, I, VP, VP, VP, VP]),
+    "g4_mm_argmax_part_bytes": (SZ, [I]),
+    "g4_mm_argmax_row": (I, [VP, VP, I, I, I, VP, F, VP, VP, VP, VP, VP]),
     "g4_residual_norm": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, F]),
     "g4_qkv_post": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, F, F, VP, F, VP]),
     "g4_rope_table": (I, [VP, VP, I, I, F, F, VP]),

@@ -40,7 +40,9 @@ const char *g4e_last_error(void);
 void g4e_config(const g4e_model *m, int out[9]);
 
 /* forward(m, token, pos, lm_mode), main.c:1838: lm_mode 0 stops after the
- * layers (prefill), otherwise the logits are computed (soft-capped). */
+ * layers (prefill), otherwise the logits are computed (soft-capped); lm_mode
+ * 2 also picks the greedy token in the LM head's own pass (mm_argmax_row,
+ * main.c:1570-1667, 1784-1786; g4e_argmax then returns the same token). */
 int g4e_forward(g4e_model *m, int token, int pos, int lm_mode);
 int g4e_read_logits(g4e_model *m, float *host);       /* vocab floats */
 int g4e_read_x(g4e_model *m, float *host);            /* dim floats   */

@@ -182,7 +182,8 @@ int g4t_open_image(const void *data, size_t size, g4t_vocab **out) {
         } else if (key_is(k, kl, "tokenizer.ggml.scores") && t == GV_ARR) {
             const uint32_t et = (uint32_t)rdu(&r, 4);
             const uint64_t n = rdu(&r, 8);
-            if (et == GV_F32 && need(&r, n * 4)) {
+            /* n is the file's 64-bit count: bound it before n * 4 can wrap */
+            if (et == GV_F32 && !r.bad && n <= (r.n - r.p) / 4 && need(&r, n * 4)) {
                 scores = (const float *)(r.d + r.p);
                 n_scores = n;
                 r.p += n * 4;

@@ -164,7 +164,10 @@ int g4_mm_residual_q8_qkv(float *o1, const void *w1, int d1, float *o2, const vo
  * once per prompt token (main.c:2366-2384), so for m tokens it performs m
  * times quantize_row_q8_K(x_t) (main.c:282) + mm_quant_dot_rows (main.c:1558).
  * These entry points do the same m products in one launch on the matrix
- * cores; every output equals the per-token result bit for bit.
+ * cores.  Q4_K / Q5_K: every block's integer sums S_b and M_b are the
+ * per-token dot's exactly (g4_debug_batch_block_sums), the fp32 fold of the
+ * blocks runs in another order, so outputs are within 1e-5 of sum |terms| of
+ * the per-token dot.  Q6_K / BF16: exact products, sums in another order.
  * ------------------------------------------------------------------------- */
 /* Bytes between consecutive Q8_K rows of a batch: g4_q8K_bytes(k) rounded
  * up to 64 (0 if k is not a positive multiple of 256). */
@@ -174,9 +177,11 @@ size_t g4_q8K_row_stride(int k);
 int g4_quantize_rows_q8_K(const float *x, void *y, int k, int m);
 /* o[t*d + r] = mm_quant_dot_rows row r on Q8_K row t (main.c:1558-1566,
  * vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K main.c:476-593), t < m, r < d:
- * the same integer block sums and scales on the fp16 matrix cores, fp32
- * partial sums in another order (within 1e-5 of sum |terms| of the per-token
- * dot).  Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
+ * the same integer block sums and scales on the fp16 matrix cores (every
+ * S_b, M_b exact: chains of at most 128 (Q4_K) / 64 (Q5_K) products, added
+ * as integers), the fp32 fold in another order (within 1e-5 of sum |terms|
+ * of the per-token dot).  Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8
+ * 16-byte aligned. */
 int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m, int type);
 /* g4_mm_batch_q8 for nseg (1..4) matrices of one type over the same Q8_K
  * rows in one launch (gate and up, Q and K): o[k][t*d[k] + r] for matrix
@@ -202,12 +207,23 @@ size_t g4_kq_image_bytes(int n, int d);
  * (g4_kq_image_bytes(n, d) bytes, 16-byte aligned) */
 int g4_kq_image(void *img, const void *w, int n, int d, int type);
 /* g4_mm_batch_q8 / g4_mm_batch_q8_multi on images instead of the quantized
- * tensors: the same integer block sums and the same fold, so the same
- * outputs (bit for bit while every block's partial sums stay below 2^24;
- * always within 1e-5 of sum |terms| of mm_quant_dot_rows, main.c:1558-1566) */
-int g4_mm_batch_img(float *o, const void *img, const void *q8, int n, int d, int m);
+ * tensors (type: the type the image was built from): the same exact integer
+ * block sums and the same fold, so g4_mm_batch_q8's outputs bit for bit
+ * (within 1e-5 of sum |terms| of mm_quant_dot_rows, main.c:1558-1566) */
+int g4_mm_batch_img(float *o, const void *img, const void *q8, int n, int d, int m, int type);
 int g4_mm_batch_img_multi(float *const *o, const void *const *img, const int *d, int nseg, const void *q8, int n,
-                          int m);
+                          int m, int type);
+/* g4_mm_batch_img with the tile given: 32*nt tokens x 32*nwv rows per
+ * workgroup, (nt, nwv) in (1, 2), (1, 4), (1, 8), (2, 4), (2, 8); shape sweeps */
+int g4_mm_batch_img_tile(float *o, const void *img, const void *q8, int n, int d, int m, int type, int nt, int nwv);
+/* Debug: the batched GEMM's own per-block integer sums, for m Q8_K rows
+ * (g4_q8K_row_stride(n) apart): S[(t*d + r)*nb + b] = S_b and M[...] = M_b
+ * of row r, token t, block b (nb = n/256), as the batched kernel forms them
+ * on the matrix cores (image 0: from the quantized tensor w; image 1: from
+ * its fp16 image) -- the sums of vec_dot_q4_K_q8_K / q5_K (main.c:500-523,
+ * 556-590) that g4_debug_block_sums gives per token. */
+int g4_debug_batch_block_sums(const void *w, int image, int n, int d, int m, int type, const void *q8, int32_t *S,
+                              int32_t *M);
 /* the fold of g4_mm_batch_q8_blocks' terms over the Q8_K rows q8 (n wide) ->
  * out[t*d + r]; with ple, out = gelu(fold) * ple[t*pstride + r] instead
  * (main.c:1989-1993, as g4_gelu_mul_rows); with q8o, also the Q8_K rows of
@@ -341,6 +357,18 @@ int g4_emb_lookup(float *o, const void *w, int type, int rows, int id, int dim);
  * next step's input and advance the position by one. */
 size_t g4_argmax_part_bytes(int n);
 int    g4_argmax(const float *v, int n, int *out, void *part, int *dtok, int *dpos);
+/* mm_argmax_row (main.c:1570-1667, logits_tied's lm_mode 2 at main.c:1784-1786,
+ * generate's fast_argmax main.c:2348) and the greedy pick after logits_tied
+ * (main.c:1788-1795, 2045-2049): the first index of the largest of
+ * v = W . x (cap <= 0) or cap * tanh(W . x / cap) (cap > 0) -> *out / *dtok
+ * (device ints, each optional), *dpos advanced if given.  v is written to
+ * logits (d floats, required).  Q6_K: the LM-head GEMV reduces its rows to
+ * per-workgroup argmax keys in the same launch (the reference's fused
+ * lm_mode 2); other types: g4_mm (q8: the Q8_K workspace for Q4_K / Q5_K),
+ * soft-cap, g4_argmax.  part: g4_mm_argmax_part_bytes(d). */
+size_t g4_mm_argmax_part_bytes(int d);
+int    g4_mm_argmax_row(const float *x, const void *w, int n, int d, int type, void *q8, float cap, float *logits,
+                        void *part, int *out, int *dtok, int *dpos);
 
 /* ---------------------------------------------------------------------------
  * Engine step kernels: fusions of consecutive statements of forward()

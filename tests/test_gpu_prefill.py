@@ -481,7 +481,7 @@ def test_mm_batch_img_vs_q8(lib, orc, qtype, n, d, m):
     ref = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
     for nt, nwv in [(0, 0), (1, 2), (1, 4), (1, 8), (2, 4), (2, 8)]:
         out = DBuf(lib, 4 * m * d)
-        lib.g4_mm_batch_img_tile(out.ptr, img.ptr, q8.ptr, n, d, m, nt, nwv)
+        lib.g4_mm_batch_img_tile(out.ptr, img.ptr, q8.ptr, n, d, m, qtype, nt, nwv)
         got = out.to_array(np.float32).reshape(m, d)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (nt, nwv)
     toks = range(m) if d * m <= 200_000 else sorted(set(range(0, m, 8)) | {1, 2, 3, m - 1})
@@ -506,7 +506,7 @@ def test_mm_batch_img_multi_prefill_shape(lib, orc, qtype):
     VPA = C.c_void_p * 2
     dd = (C.c_int * 2)(d, d)
     lib.g4_mm_batch_q8_multi(VPA(outs[0].ptr, outs[1].ptr), VPA(ws[0].ptr, ws[1].ptr), dd, 2, q8.ptr, n, m, qtype)
-    lib.g4_mm_batch_img_multi(VPA(outs[2].ptr, outs[3].ptr), VPA(imgs[0].ptr, imgs[1].ptr), dd, 2, q8.ptr, n, m)
+    lib.g4_mm_batch_img_multi(VPA(outs[2].ptr, outs[3].ptr), VPA(imgs[0].ptr, imgs[1].ptr), dd, 2, q8.ptr, n, m, qtype)
     for k in range(2):
         ref = outs[k].to_array(np.float32).reshape(m, d)
         got = outs[2 + k].to_array(np.float32).reshape(m, d)
@@ -521,4 +521,84 @@ def test_kq_image_args(lib):
     assert lib.L.g4_kq_image_bytes(100, 100) == 0
     buf = DBuf(lib, 4096)
     assert lib.L.g4_kq_image(buf.ptr, buf.ptr, 256, 1, 14) != 0       # Q6_K has no image
-    assert lib.L.g4_mm_batch_img_tile(buf.ptr, buf.ptr, buf.ptr, 256, 1, 1, 3, 4) != 0
+    assert lib.L.g4_mm_batch_img_tile(buf.ptr, buf.ptr, buf.ptr, 256, 1, 1, 12, 3, 4) != 0
+    assert lib.L.g4_mm_batch_img_tile(buf.ptr, buf.ptr, buf.ptr, 256, 1, 1, 14, 1, 4) != 0   # no Q6_K image
+    S = DBuf(lib, 64)
+    assert lib.L.g4_debug_batch_block_sums(buf.ptr, 0, 256, 1, 1, 14, buf.ptr, S.ptr, S.ptr) != 0
+    assert lib.L.g4_debug_batch_block_sums(buf.ptr, 0, 300, 1, 1, 12, buf.ptr, S.ptr, S.ptr) != 0
+
+
+def _saturated(rng, qtype, d, n):
+    """Q4_K / Q5_K rows whose blocks reach the largest integer sums: every
+    6-bit scale and min 63 (all scale bytes 0xff), every code 15 (Q4_K) or 31
+    (Q5_K); rows 0 .. d/2 - 1 saturated everywhere, the rest random with every
+    third block saturated."""
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    bs = synth.BLOCK_BYTES[qtype]
+    blk = raw.reshape(d, n // 256, bs)
+    sat = np.zeros((d, n // 256), bool)
+    sat[: d // 2] = True
+    sat[d // 2:, ::3] = True
+    code_end = bs                                    # scales 4..16, then (Q5_K: qh 16..48) and qs
+    blk[sat, 4:code_end] = 0xFF
+    return raw, sat
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_batch_block_sums_exact_saturated(lib, orc, qtype):
+    """The batched GEMM's own per-block integer sums S_b and M_b (from the
+    quantized tensor and from its fp16 image) equal the exact integers of
+    vec_dot_q4_K_q8_K / q5_K (main.c:500-523, 556-590) for every (token,
+    row, block), on blocks that reach |S_b| = 256 * 63 * 15 * 127 (Q4_K,
+    3.1e7) or 256 * 63 * 31 * 127 (Q5_K, 6.3e7), past fp32's 2^24 exact
+    range: constant-sign tokens (Q8_K codes all -127, or +127) against
+    saturated scales and codes.  They also equal the per-token GEMV's
+    g4_debug_block_sums, and the outputs meet the 1e-5 bar against the
+    oracle; the image GEMM's outputs equal the quantized GEMM's bit for bit."""
+    from g4 import DBuf, upload_quant
+    n, d, m = 2560, 256, 40
+    nb = n // 256
+    rng = np.random.default_rng(91 + qtype)
+    raw, sat = _saturated(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    x[0] = 1.0                                       # Q8_K codes all -127 (iscale = -127 / max)
+    x[1] = 1.0
+    x[1, ::256] = -1.0                               # the block maximum negative: the rest +127
+    x[2] = np.abs(x[2])                              # one sign, varied codes
+    x[3] = -np.abs(x[3]) * 7.0
+    x[4, :1280] = 2.0                                # half constant, half random
+    x[5] = 0.0                                       # d = 0 token
+    q8, qb = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    q8s = np.stack([orc.quantize_q8K(x[t]) for t in range(m)])
+    assert (q8s[0]["qs"] == -127).all() and (q8s[1]["qs"][:, 1:] == 127).all()
+    bsz = synth.BLOCK_BYTES[qtype]
+    eS = np.zeros((m, d, nb), np.int64)
+    eM = np.zeros((m, d, nb), np.int64)
+    for t in range(m):
+        for r in range(d):
+            eS[t, r], eM[t, r] = kq.kquant_block_sums(raw[r].reshape(-1, bsz), qtype, q8s[t])
+    big = np.abs(eS) > (1 << 24)
+    assert big.sum() > 1000 and np.abs(eS).max() >= (30_000_000 if qtype == 12 else 60_000_000)
+    for image in (0, 1):
+        src = _image(lib, w, qtype, n, d) if image else w
+        S, M = DBuf(lib, 4 * m * d * nb), DBuf(lib, 4 * m * d * nb)
+        lib.g4_debug_batch_block_sums(src.ptr, image, n, d, m, qtype, q8.ptr, S.ptr, M.ptr)
+        gS = S.to_array(np.int32).reshape(m, d, nb)
+        gM = M.to_array(np.int32).reshape(m, d, nb)
+        bad = np.argwhere(gS != eS)
+        assert bad.size == 0, f"image={image}: S_b differs at {len(bad)} (token, row, block), first {bad[:4].tolist()}"
+        assert np.array_equal(gM, eM), f"image={image}: M_b differs"
+    # the per-token decode GEMV's own sums are the same integers
+    for t in (0, 1, 3, 9):
+        S1, M1 = DBuf(lib, 4 * d * nb), DBuf(lib, 4 * d * nb)
+        lib.g4_debug_block_sums(w.ptr, n, d, qtype, q8.ptr + t * qb, S1.ptr, M1.ptr)
+        assert np.array_equal(S1.to_array(np.int32).reshape(d, nb), eS[t])
+        assert np.array_equal(M1.to_array(np.int32).reshape(d, nb), eM[t])
+    got = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    _check_q8(orc, raw, qtype, n, d, x, got, list(range(m)))
+    img = _image(lib, w, qtype, n, d)
+    for nt, nwv in [(0, 0), (1, 2), (1, 4), (2, 4)]:
+        out = DBuf(lib, 4 * m * d)
+        lib.g4_mm_batch_img_tile(out.ptr, img.ptr, q8.ptr, n, d, m, qtype, nt, nwv)
+        assert np.array_equal(out.to_array(np.float32).reshape(m, d).view(np.uint32), got.view(np.uint32)), (nt, nwv)

@@ -307,3 +307,44 @@ def test_residual_norm_rows(lib, n, narrow):
         lib.g4_download_q8K(q8.ptr + z * rs, P(ha), n)
         lib.g4_download_q8K(q1.ptr, P(hb), n)
         assert ha.tobytes() == hb.tobytes(), z
+
+
+@pytest.mark.parametrize("hd", [256, 512])
+def test_attn_decode_rows_peaked_small(lib, orc, hd):
+    """The prompt-chunk attention (hd 256: split-fp16 matrix cores; 512: fp32
+    ones) with small-magnitude queries (elements ~0.05, their fp16 low parts
+    subnormal) against large keys, so that the softmax is peaked and most
+    weights lie in 1e-3..1e-1 -- where a weight split without its factor 16
+    would keep only 2^-15 of relative precision -- compared with the oracle
+    at the engine's per-layer bar of 1e-5 of max|o| (V: unit rows, as the
+    RMS-normalised cache holds)."""
+    rng = np.random.default_rng(hd + 5)
+    n_heads, n_kv, window, ring, p0, m, G = 8, 2, 512, 512, 300, 200, 4
+    kvd, qd_ = n_kv * hd, n_heads * hd
+    T = p0 + m
+    sk = 3.0 / (0.05 * np.sqrt(hd))                  # score std 3 at scale 1
+    K = (rng.standard_normal((T, kvd)) * sk).astype(np.float32)
+    V = rng.standard_normal((T, kvd)).astype(np.float32)
+    q = (rng.standard_normal((m, qd_)) * 0.05).astype(np.float32)
+    kc = np.full((ring, kvd), np.nan, np.float32)
+    vc = np.full((ring, kvd), np.nan, np.float32)
+    for t in range(max(0, p0 - ring), p0):
+        kc[t % ring], vc[t % ring] = K[t], V[t]
+    pad = np.full((3, kvd), np.nan, np.float32)
+    kch, vch = np.concatenate([K[p0:], pad]), np.concatenate([V[p0:], pad])
+    part = empty(lib, m * lib.L.g4_attn_part_bytes(n_heads, hd, G))
+    out = empty(lib, 4 * m * qd_)
+    qd, kcd, vcd, kchd, vchd = dbuf(lib, q), dbuf(lib, kc), dbuf(lib, vc), dbuf(lib, kch), dbuf(lib, vch)
+    lib.g4_attn_decode_rows(qd.ptr, kcd.ptr, vcd.ptr, kchd.ptr, vchd.ptr, kvd, ring, p0, m, window, n_heads, n_kv, hd,
+                            F(1.0), G, part.ptr, out.ptr, None)
+    got = out.to_array(np.float32).reshape(m, qd_)
+    frac = []
+    for z in range(0, m, 7):
+        pos = p0 + z
+        t0 = max(0, pos + 1 - window)
+        want = orc.attn(q[z], K, V, kvd, t0, pos + 1 - t0, n_heads, n_kv, hd, 1.0)
+        assert rel_err(got[z], want) < 1e-5, z
+        s = (K[t0:pos + 1, :hd].astype(np.float64) @ q[z, :hd].astype(np.float64))
+        p = np.exp(s - s.max())
+        frac.append(np.mean((p > 1e-3) & (p < 1e-1)))
+    assert np.mean(frac) > 0.2, np.mean(frac)

@@ -216,13 +216,23 @@ def test_attn_dev_fused_quant(lib, orc):
 @pytest.mark.parametrize("hd,window,pos,G,store", [(256, 512, 700, 16, True), (256, 512, 100, 4, True),
                                                    (256, 512, 511, 16, True), (512, 0, 300, 10, True),
                                                    (512, 0, 37, 1, True), (256, 512, 900, 16, False),
-                                                   (512, 0, 640, 20, False)])
+                                                   (512, 0, 640, 20, False),
+                                                   # the engine's full layers at max_seq >= 4096: 128 chunks,
+                                                   # the eight-wave kernel
+                                                   (256, 0, 4999, 128, True), (256, 0, 4999, 128, False),
+                                                   (512, 0, 4999, 128, True), (512, 0, 4999, 128, False),
+                                                   (256, 0, 32767, 128, True), (256, 0, 32767, 128, False),
+                                                   (512, 0, 32767, 128, True), (512, 0, 32767, 128, False),
+                                                   (512, 0, 100, 128, True), (256, 0, 8191, 64, True)])
 def test_attn_decode_fused(lib, orc, hd, window, pos, G, store):
     """qkv_post + attention in one pass (main.c:1886-1950): raw Q/K/V of
     position pos, per-head norms, RoPE from the position's table, K/V append
     into the (ring or flat) cache, attention over the window -- against the
     oracle's norms, RoPE and attention over a flat cache.  store=False is a
-    shared-KV layer: nothing is appended and the cache already holds pos."""
+    shared-KV layer: nothing is appended and the cache already holds pos.
+    With 64 or more chunks (4 q heads per kv head) the launch takes the
+    eight-wave kernel, the one every full layer runs at contexts of 4096 and
+    more; pos 100 at G = 128 leaves most chunks empty."""
     rng = np.random.default_rng(hd + pos + G)
     nh, nkv, eps = 8, 2, 1e-6
     kv_dim = nkv * hd

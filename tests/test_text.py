@@ -242,3 +242,26 @@ def test_thinking_stream(pair):
             break
         s.push(t)
     assert forced == cend
+
+
+@pytest.mark.parametrize("count", [(1 << 62) + 3, (1 << 64) - 1, 1 << 40])
+def test_scores_count_bounded(tmp_path, count):
+    """A tokenizer.ggml.scores array whose 64-bit element count overruns the
+    file (including counts where count * 4 wraps around 2^64 to a small
+    number) is rejected as malformed, never read past the mapping."""
+    import struct
+
+    import g4
+    pieces = ["a", "b", "ab", "<eos>"]
+    p = str(tmp_path / "v.gguf")
+    synth.write_vocab_gguf(p, pieces, None, [0.0, -1.0, -2.0, -3.0], bos=0, eos=3)
+    g4.Vocab(p).close()                                 # the well-formed file opens
+    buf = bytearray(open(p, "rb").read())
+    key = b"tokenizer.ggml.scores"
+    at = buf.index(key) + len(key)
+    assert struct.unpack_from("<II", buf, at) == (9, 6)   # array of f32
+    assert struct.unpack_from("<Q", buf, at + 8)[0] == 4
+    struct.pack_into("<Q", buf, at + 8, count)
+    open(p, "wb").write(bytes(buf))
+    with pytest.raises(g4.G4Error):
+        g4.Vocab(p)
