@@ -20,6 +20,8 @@ Workloads (synthetic inputs, generated from fixed seeds on the host):
           matrices on the matrix cores (seed 1)
   prefill_e2e  batched prompt prefill through the engine at the E4B shape:
           511 tokens in one chunk (seed 4); roofline on the Q6_K GEMM (V, FFN down)
+  floors  probe kernels: a dependent launch with no work, streaming reads at
+          14.8 / 29.5 / 551.6 MB, a last-workgroup hand-off inside a kernel
   attn    ISWA decode attention step (norms, RoPE, K/V append, attention):
           sliding ring 512 and global T = 4096 / 32768 at head_dim 256 and 512
           (seed 3); value: the global T=32768 hd 256 case
@@ -896,9 +898,64 @@ def _time_steps(lib, step, args) -> float:
     return ms
 
 
+def bench_floors(lib, g4, synth, args):
+    """The floors the decode step's kernels are sized against (probe kernels
+    that compute nothing of the model): a dependent launch with no work, a
+    streaming read at the byte counts of the step's kernels (weights rotated
+    over more than the 256 MB Infinity Cache, so every launch reads HBM), and
+    a last-workgroup hand-off inside a kernel against the same kernel
+    without it.  Each is a graph of K launches timed with HIP events."""
+    L = lib.L
+    ncu, arch = C.c_int(), C.create_string_buffer(64)
+    lib.check(L.g4_device_info(C.byref(ncu), arch, 64))
+    cus = ncu.value
+    res_cfg = {"cus": cus}
+    # 1. chained empty kernels
+    for wg in (1, 256, 1024):
+        ms = _time_steps(lib, lambda i, wg=wg: L.g4_probe_empty(wg), args)
+        res_cfg[f"empty_launch_us_{wg}wg"] = round(ms * 1e3 / args.steps, 3)
+    # 2. streaming reads
+    sink = g4.DBuf(lib, 4 * 4096)
+    reads = {}
+    for mb, label in ((14.79, "14.8MB (Q4_K 10240x2560)"), (29.54, "29.5MB (gate|up 2x10240x2560)"),
+                      (551.6, "551.6MB (LM head Q6_K 262144x2560)")):
+        nbytes = int(mb * 1e6) // 16 * 16
+        ncp = _copies(nbytes)
+        bufs = [g4.DBuf(lib, nbytes) for _ in range(ncp)]
+        for b in bufs:
+            lib.check(L.g4_memset(b.ptr, 0, nbytes))
+        for wg in (4 * cus,):
+            ms = _time_steps(lib, lambda i, b=bufs, n=nbytes, wg=wg: L.g4_probe_read(b[i % len(b)].ptr, n, sink.ptr, wg),
+                             args)
+            us = ms * 1e3 / args.steps
+            reads[label] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1), "copies_rotated": ncp}
+        del bufs
+    # 3. last-workgroup hand-off
+    vals = g4.DBuf(lib, 4 * 4096)
+    cnt = g4.DBuf(lib, 256)
+    out = g4.DBuf(lib, 256)
+    lib.check(L.g4_memset(cnt.ptr, 0, 256))
+    hand = {}
+    for wg in (16, 256, 640):
+        t = []
+        for h in (0, 1):
+            ms = _time_steps(lib, lambda i, wg=wg, h=h: L.g4_probe_handoff(vals.ptr, cnt.ptr, out.ptr, wg, h), args)
+            t.append(ms * 1e3 / args.steps)
+        hand[f"{wg}wg"] = {"plain_us": round(t[0], 3), "handoff_us": round(t[1], 3), "cost_us": round(t[1] - t[0], 3)}
+    got = np.zeros(1, np.float32)
+    lib.check(L.g4_memcpy_d2h(got.ctypes.data, out.ptr, 4))
+    assert got[0] == sum(range(640)), got              # the last launch's hand-off summed every workgroup's value
+    big = reads["551.6MB (LM head Q6_K 262144x2560)"]
+    return {"value": big["GB_s"], "unit": "GB/s", "higher_is_better": True,
+            "ms_per_step": big["us"] / 1e3, "dtype": "f32",
+            "config": dict({"workload": "floors: chained empty launches, streaming reads, last-workgroup hand-off "
+                            "(graphs of K launches, HIP events)", "streaming_read": reads, "handoff": hand},
+                           **res_cfg)}
+
+
 WORKLOADS = {"decode": bench_decode, "gemv": bench_gemv, "gateup": bench_gateup, "lmhead": bench_lmhead,
              "copy": bench_copy, "prefill": bench_prefill, "prefill_e2e": bench_prefill_e2e, "attn": bench_attn,
-             "layer": bench_layer}
+             "layer": bench_layer, "floors": bench_floors}
 
 
 def main() -> int:

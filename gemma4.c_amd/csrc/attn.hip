@@ -1501,12 +1501,13 @@ void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
         else hipLaunchKernelGGL((attn_chunk_kernel<HD, 8, false>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
         return;
     }
-    // decode over long windows (64+ chunks, i.e. about one workgroup per CU
-    // for two kv heads): eight waves per workgroup, twice the rows in flight
-    // per CU.  hd 256: two register sets of 4 positions per wave (172 VGPRs);
-    // hd 512: one set (32K positions: 34.6 against 38.6 us at hd 256, 55.1
-    // against 56.1 us at hd 512, chunk + merge)
-    if (kp == 4 && a.G >= 64) {
+    // decode with 4 q heads per kv head: eight waves per workgroup, twice
+    // the rows in flight per CU.  hd 256: two register sets of 4 positions
+    // per wave (172 VGPRs); hd 512: one set.  Over 32K positions: 34.6
+    // against 38.6 us at hd 256, 55.1 against 56.1 us at hd 512 (chunk +
+    // merge); the E4B decode step with its 512-slot rings in 16 chunks:
+    // 2.258 against 2.292 ms
+    if (kp == 4) {
         if constexpr (HD == 256)
             hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true, 512, 4>), grid, dim3(512), attn_chunk_lds(HD, kp, 8),
                                g4_stream(), a);

@@ -120,6 +120,12 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Sum over the whole workgroup (blockDim.x a multiple of 64, <= 1024); every
 // thread gets the total.  red must hold 16 floats; it is reusable after return.
+// workgroup barrier for LDS hand-offs only: this wave's LDS operations are
+// complete, then s_barrier.  __syncthreads() also waits for every
+// outstanding global load; this keeps them in flight.  The asm is a
+// compiler barrier for memory operations as well.
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_sum(v);
@@ -307,6 +313,72 @@ __device__ __forceinline__ void residual_finish(const ResidualArgs& a, ResidualR
         for (int k = 0; k < EPT; k++) {
             const int i = tid + k * nt;
             if (i < n) buf[i] = xv[k];
+        }
+    }
+}
+
+// The same step with one float4 of each vector per thread (n/4 threads):
+// thread t owns elements 4t .. 4t+3, so wave w holds Q8_K block w.  Every
+// load is issued unconditionally (an absent vector is read from x in its
+// place and not used), and each norm's sum of squares takes one LDS-only
+// barrier: per thread ((a^2 + b^2) + c^2) + d^2, a wave butterfly, then the
+// waves' sums in wave order.  off: the row's offset (rows of n floats).
+struct Res4 {
+    float4 x, y, wp, wn;
+    float sc;
+};
+
+__device__ __forceinline__ void residual4_load(const ResidualArgs& a, Res4& r, size_t off) {
+    const int tid = threadIdx.x;
+    r.x = reinterpret_cast<const float4*>(a.x + off)[tid];
+    r.y = reinterpret_cast<const float4*>(a.y ? a.y + off : a.x + off)[tid];
+    r.wp = reinterpret_cast<const float4*>(a.y ? a.w_post : a.x)[tid];
+    r.wn = reinterpret_cast<const float4*>(a.w_next ? a.w_next : a.x)[tid];
+    r.sc = a.oscale ? a.oscale[0] : 1.0f;
+}
+
+// q: the thread's 4 values to quantize (qsrc 0: the normed vector, else x');
+// nv: the normed vector (x' without w_next).  store: x_out and xb2 are
+// written (one workgroup of a prologue kernel).  red: [2][16] floats of LDS.
+__device__ __forceinline__ void residual4_finish(const ResidualArgs& a, const Res4& r, float (*red)[16], bool store,
+                                                 size_t off, float q[4], float nv[4]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    float v[4] = {r.x.x, r.x.y, r.x.z, r.x.w};
+    if (a.y) {
+        const float y[4] = {r.y.x, r.y.y, r.y.z, r.y.w}, w[4] = {r.wp.x, r.wp.y, r.wp.z, r.wp.w};
+        float ss = ((y[0] * y[0] + y[1] * y[1]) + y[2] * y[2]) + y[3] * y[3];
+        ss = wave_sum(ss);
+        if (lane == 0) red[0][wave] = ss;
+        lds_sync();
+        float t = 0.0f;
+        for (int i = 0; i < nw; i++) t += red[0][i];
+        const float sy = 1.0f / sqrtf(t / (float)a.n + a.eps);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float u = v[k] + (y[k] * sy) * w[k];
+            if (a.oscale) u = u * r.sc;
+            v[k] = u;
+        }
+    }
+    if (store && a.x_out && (a.y || a.x_out != a.x))
+        reinterpret_cast<float4*>(a.x_out + off)[tid] = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) q[k] = nv[k] = v[k];
+    if (a.w_next) {
+        const float w[4] = {r.wn.x, r.wn.y, r.wn.z, r.wn.w};
+        float ss = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
+        ss = wave_sum(ss);
+        if (lane == 0) red[1][wave] = ss;
+        lds_sync();
+        float t = 0.0f;
+        for (int i = 0; i < nw; i++) t += red[1][i];
+        const float sx = 1.0f / sqrtf(t / (float)a.n + a.eps);
+#pragma unroll
+        for (int k = 0; k < 4; k++) nv[k] = (v[k] * sx) * w[k];
+        if (store && a.xb2) reinterpret_cast<float4*>(a.xb2 + off)[tid] = make_float4(nv[0], nv[1], nv[2], nv[3]);
+        if (a.qsrc == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[k] = nv[k];
         }
     }
 }

@@ -188,49 +188,46 @@ struct Stack2 {
     float* out6;
     int d6;
 };
-constexpr int kKs6 = 2;                 // Q6_K row split inside a prologue kernel
-constexpr int kRows6 = 32 / kKs6;       // Q6_K rows per 256-thread workgroup
+// Q6_K rows per prologue workgroup of wg threads: wg/8 lane groups, ks6 per row
+constexpr int q6_pro_rows(int wg, int ks6) { return wg / 8 / ks6; }
 
-// Q6_K rows of a prologue kernel's workgroup vb: 256 threads, kRows6 rows x
-// kKs6 slices, x = the fp32 vector the prologue leaves in pbuf; same lane
-// mapping and arithmetic as gemv_q6k_rows_kernel (below).  The weight loads
-// are issued before the prologue's arithmetic.
-template <int NB>
-__device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, const ResidualArgs& ra,
-                                                  ResidualRegs<NB>& rr, float* pbuf, float* red) {
-    constexpr int QB = (NB + kKs6 - 1) / kKs6;
+// Q6_K rows of a prologue kernel's workgroup vb: WG threads, q6_pro_rows(WG,
+// KS6) rows x KS6 slices, x = the fp32 normed vector (the prologue's nv, staged
+// here in pbuf); same lane mapping and arithmetic as gemv_q6k_rows_kernel
+// (below).  The weight loads are issued before the prologue's arithmetic.
+template <int NB, int WG, int KS6>
+__device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, const ResidualArgs& ra, const Res4& r4,
+                                                  float* pbuf, float (*red)[16]) {
+    constexpr int QB = (NB + KS6 - 1) / KS6;
+    constexpr int R6 = q6_pro_rows(WG, KS6);
     const int tid = threadIdx.x, L = tid & 7, g = tid >> 3, h = L >> 2, u = L & 3;
-    const int rr6 = g % kRows6, ks = g / kRows6;
-    const int row_ = vb * kRows6 + rr6, row = min(row_, st.d6 - 1);
+    const int rr6 = g % R6, ks = g / R6;
+    const int row_ = vb * R6 + rr6, row = min(row_, st.d6 - 1);
     const Q6KPlanes P = q6k_planes((size_t)st.d6 * NB);
     uint4 qlv[QB];
     uint2 qhv[QB], scv[QB];
     uint32_t dv[QB];
 #pragma unroll
     for (int i = 0; i < QB; i++) {
-        const int b = ks + i * kKs6;
-        if (b < NB) {
-            const size_t blk = (size_t)row * NB + b;
-            qlv[i] = *reinterpret_cast<const uint4*>(st.w6 + P.ql + blk * 128 + 16 * L);
-            qhv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.qh + blk * 64 + 8 * L);
-            scv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.sc + blk * 16 + 8 * h);
-            dv[i] = *reinterpret_cast<const uint16_t*>(st.w6 + P.d + blk * 2);
-        }
+        const size_t blk = (size_t)row * NB + min(ks + i * KS6, NB - 1);
+        qlv[i] = *reinterpret_cast<const uint4*>(st.w6 + P.ql + blk * 128 + 16 * L);
+        qhv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.qh + blk * 64 + 8 * L);
+        scv[i] = *reinterpret_cast<const uint2*>(st.w6 + P.sc + blk * 16 + 8 * h);
+        dv[i] = *reinterpret_cast<const uint16_t*>(st.w6 + P.d + blk * 2);
     }
-    residual_finish<NB>(ra, rr, pbuf, red, false);
-    __syncthreads();
-    // sums of the runs of 8 of x
+    float q[4], nv[4];
+    residual4_finish(ra, r4, red, false, 0, q, nv);
+    reinterpret_cast<float4*>(pbuf)[tid] = make_float4(nv[0], nv[1], nv[2], nv[3]);
+    // sums of the runs of 8 of x: this thread's 4 and its neighbour's
     float* x8 = pbuf + NB * 256 + ((NB * 292 + 15) & ~15) / 4;
-    for (int i = tid; i < NB * 32; i += blockDim.x) {
-        const float4 a = reinterpret_cast<const float4*>(pbuf)[2 * i];
-        const float4 b = reinterpret_cast<const float4*>(pbuf)[2 * i + 1];
-        x8[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-    }
-    __syncthreads();
+    const float s4 = (nv[0] + nv[1]) + (nv[2] + nv[3]);
+    const float o4 = __shfl_xor(s4, 1, 64);
+    if ((tid & 1) == 0) x8[tid >> 1] = s4 + o4;
+    lds_sync();
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < QB; i++) {
-        const int b = ks + i * kKs6;
+        const int b = ks + i * KS6;
         if (b < NB) {
             const uint4 ql = qlv[i];
             const uint2 qh = qhv[i], sc = scv[i];
@@ -267,12 +264,12 @@ __device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, cons
     acc += __shfl_xor(acc, 4, 64);
     float* part = x8 + NB * 32;
     if (L == 0) part[g] = acc;
-    __syncthreads();
-    if (tid < kRows6) {
-        float s = 0.0f;
+    lds_sync();
+    if (tid < R6) {
+        float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kKs6; j++) s += part[j * kRows6 + tid];
-        if (vb * kRows6 + tid < st.d6) st.out6[vb * kRows6 + tid] = s;
+        for (int j = 0; j < KS6; j++) sum += part[j * R6 + tid];
+        if (vb * R6 + tid < st.d6) st.out6[vb * R6 + tid] = sum;
     }
     (void)row_;
 }
@@ -287,7 +284,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                                                            const float* __restrict__ aux, const ResidualArgs ra,
                                                            const Stack2 st) {
     static_assert(!QIN || (WG == 64 && NB == 1), "the single-block input path runs one wave over one block");
-    static_assert(!PRO || (WG == 256 && NB > 0 && !DBG), "the prologue needs 256 threads and a fixed row length");
+    static_assert(!PRO || (WG == 64 * NB && NB > 0 && !DBG), "the prologue needs one wave per block");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
@@ -405,16 +402,17 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
         Raw raw[NH];
         if constexpr (PRO) {
             // the activations are produced here: residual step, norm and Q8_K
-            // by the whole workgroup into LDS (workgroup 0 also stores x_out,
-            // xb2 and q8), then read from LDS.  The step's small loads go
-            // first, the weight loads behind them, so the norm's arithmetic
+            // by the whole workgroup (one float4 of each vector per thread,
+            // wave w quantizes block w into LDS; workgroup 0 also stores
+            // x_out, xb2 and q8), then read from LDS.  The step's small loads
+            // go first, the weight loads behind them, so the norm's arithmetic
             // waits only for the former.  Workgroups past the K-quant rows
             // take the Q6_K tensor (st.w6) on the fp32 normed vector.
             constexpr int rpw = WG / GL;
             const int qk_wgs = (dtot + rpw - 1) / rpw;
             const bool vwg = st.w6 != nullptr && (int)blockIdx.x >= qk_wgs;
-            ResidualRegs<NB> rr;
-            residual_load<NB>(ra, rr);
+            Res4 r4;
+            residual4_load(ra, r4, 0);
             if (!vwg) {
                 // every group loads NH blocks (past the row's end: its last
                 // block again, not used), so the number of loads behind the
@@ -423,17 +421,17 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                 for (int i = 0; i < NH; i++) load_w(min(grp * NH + i, nb - 1), raw[i]);
             }
             extern __shared__ __align__(16) float pbuf[];   // NB*256 floats, the Q8_K blocks, [Q6_K: run sums]
-            __shared__ float red[16];
+            __shared__ float red[2][16];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf + NB * 256);
             if (vwg) {
-                q6k_prologue_rows<NB>(st, blockIdx.x - qk_wgs, ra, rr, pbuf, red);
+                q6k_prologue_rows<NB, WG, SPLIT>(st, blockIdx.x - qk_wgs, ra, r4, pbuf, red);
                 return;
             }
-            residual_finish<NB>(ra, rr, pbuf, red, blockIdx.x == 0);
-            __syncthreads();
-            quantize_blocks_wg(pbuf, q8l, NB);
-            if (blockIdx.x == 0 && ra.q8) quantize_blocks_wg(pbuf, ra.q8, NB);
-            __syncthreads();
+            float qv[4], nv[4];
+            residual4_finish(ra, r4, red, blockIdx.x == 0, 0, qv, nv);
+            quantize_block_wave(qv, tid & 63, q8l, NB, tid >> 6);
+            if (blockIdx.x == 0 && ra.q8) quantize_block_wave(qv, tid & 63, ra.q8, NB, tid >> 6);
+            lds_sync();
             const uint8_t* a_qs_l = q8l + 32 * l;
             const uint8_t* a_bs_l = q8l + q8k_bsums_off(NB) + 8 * k;
             const float* a_d_l = reinterpret_cast<const float*>(q8l + q8k_d_off(NB));
@@ -1027,20 +1025,37 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
                        S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{}, Stack2{});
 }
 
-// residual step + norm + Q8_K as the prologue of every workgroup (256
-// threads: four waves of 8/SPLIT rows each)
+// residual step + norm + Q8_K as the prologue of every workgroup (64 NB
+// threads: one wave per Q8_K block, each wave 8/SPLIT rows)
+template <bool Q5, int NMAT, int NB, int SPLIT>
+void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
+                      const Stack2& st) {
+    constexpr int WG = 64 * NB;
+    constexpr int rows_per_wg = WG / (8 * SPLIT);
+    const int rows = d + st.d;
+    // x, Q8_K, and for a Q6_K tensor the run sums of x and the partials
+    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15) + (size_t)NB * 32 * 4 +
+                       (size_t)WG / 8 * 4;
+    const int r6 = q6_pro_rows(WG, SPLIT);
+    const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + r6 - 1) / r6 : 0);
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, true>),
+                       dim3(wgs), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
+                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st);
+}
+
+// residual step + norm + Q8_K as the prologue of every workgroup (64 NB
+// threads: one wave per Q8_K block); a row takes 32 lanes (64 with two
+// matrices), i.e. 2 NB (NB) rows per workgroup.  At the E4B shape (n = 2560):
+// Q|K|V 7.2 us and the PLE gate 5.9 us per launch, against 9.0 / 7.1 us with
+// 16 lanes per row (four times fewer workgroups, each CU's SIMDs holding 2.5
+// waves of the work) and 8.0 / 6.4 us for the 256-thread form before it;
+// 64 lanes per row measured the same as 32 for the PLE gate and 8.4 us for
+// Q|K|V.
 template <bool Q5, int NMAT, int NB>
 void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                     const Stack2& st) {
-    constexpr int SPLIT = NMAT == 2 ? 4 : 2;
-    constexpr int rows_per_wg = 4 * 8 / SPLIT;
-    const int rows = d + st.d;
-    // x, Q8_K, and for a Q6_K tensor the run sums of x and 32 partials
-    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15) + (size_t)NB * 32 * 4 + 32 * 4;
-    const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + kRows6 - 1) / kRows6 : 0);
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, 256, true>),
-                       dim3(wgs), dim3(256), lds, g4_stream(), (const uint8_t*)w,
-                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st);
+    if constexpr (NMAT == 2 || NB > 10) launch_q45_pro_s<Q5, NMAT, NB, 8>(w, w2, o, d, aux, ra, st);
+    else launch_q45_pro_s<Q5, NMAT, NB, 4>(w, w2, o, d, aux, ra, st);
 }
 
 template <bool Q5, int NB>
@@ -1436,6 +1451,10 @@ static int mm_residual(const char* who, float* o, const void* w, const void* w2,
     G4_CHECK_ARG(!(y && x_out == x), "%s: x_out must not alias x when y is given", who);
     G4_CHECK_ARG(!(y && xb2 == y), "%s: xb2 must not alias y", who);
     G4_CHECK_ARG(!q8 || aligned16(q8), "%s: q8 must be 16-byte aligned", who);
+    // the prologue reads and writes the vectors as float4
+    G4_CHECK_ARG(aligned16(x) && (!x_out || aligned16(x_out)) && (!y || (aligned16(y) && aligned16(w_post))) &&
+                     (!w_next || aligned16(w_next)) && (!xb2 || aligned16(xb2)),
+                 "%s: x, x_out, y, w_post, w_next and xb2 must be 16-byte aligned", who);
     ResidualArgs ra{x, x_out, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
     const int nb = n / 256;
     const bool q5 = type == G4_Q5_K;

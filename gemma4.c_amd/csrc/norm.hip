@@ -62,6 +62,28 @@ __global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(ResidualArg
     }
 }
 
+// The same step with one float4 of each vector per thread (n/4 threads, n a
+// multiple of 256 up to 4096; residual4_load / residual4_finish): wave w
+// holds Q8_K block w and quantizes it from its registers (no LDS round trip),
+// with one LDS-only barrier per norm.  The residual prologues of
+// g4_mm_residual_q8 run the same code, so for these n every form of the step
+// gives the same bits.  Row z = blockIdx.x of m rows (x, y, xb2 n apart, q8
+// rows q8row bytes apart; m = 1: the decode step).
+__global__ __launch_bounds__(1024) void residual4_kernel(ResidualArgs a, size_t q8row) {
+    __shared__ float red[2][16];
+    const size_t off = (size_t)blockIdx.x * a.n;
+    Res4 r;
+    residual4_load(a, r, off);
+    float q[4], nv[4];
+    residual4_finish(a, r, red, true, off, q, nv);
+    if (a.q8) quantize_block_wave(q, threadIdx.x & 63, a.q8 + blockIdx.x * q8row, a.n / 256, threadIdx.x >> 6);
+}
+
+bool residual4_ok(const void* x, const void* y, const void* xb2, int n) {
+    auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    return n % 256 == 0 && n <= 4096 && al(x) && al(y) && al(xb2);
+}
+
 // row z = blockIdx.x of m rows of n (x, y, xb2 n apart; q8 rows q8row bytes
 // apart): the same step per row as residual_norm_kernel (same thread count
 // and reduction tree when launched with the same EPT and block size)
@@ -93,6 +115,10 @@ extern "C" int g4_residual_norm(float* x, const float* y, const float* w_post, c
     G4_CHECK_ARG(!q8 || n % 256 == 0, "residual_norm: n=%d not a multiple of 256 for Q8_K", n);
     G4_CHECK_ARG(!(q8 && qsrc == 0) || w_next, "residual_norm: quantizing xb2 needs w_next");
     ResidualArgs a{x, x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
+    if (residual4_ok(x, y, xb2, n) && (!y || ((uintptr_t)w_post & 15) == 0) && (!w_next || ((uintptr_t)w_next & 15) == 0)) {
+        hipLaunchKernelGGL(residual4_kernel, dim3(1), dim3(n / 4), 0, g4_stream(), a, (size_t)0);
+        return g4_check_launch("residual4_kernel");
+    }
     // EPT elements per thread, as few waves as cover n (n = 2560: 640 threads,
     // one wave per Q8_K block)
     const int ept = n <= kNormThreads ? 1 : n <= 4 * kNormThreads ? 4 : 16;
@@ -120,11 +146,14 @@ extern "C" int g4_residual_norm_rows(float* x, const float* y, const float* w_po
     ResidualArgs a{x, x, y, w_post, oscale, w_next, xb2, (uint8_t*)q8, qsrc, n, eps};
     const size_t q8row = g4_q8K_row_stride(n);
     const size_t lds = (size_t)n * 4;
-    if (narrow) {
-        const dim3 g(m), b(256);
-        if (n == 2048) hipLaunchKernelGGL(residual_rows_kernel<8>, g, b, lds, g4_stream(), a, q8row);
-        else if (n == 2560) hipLaunchKernelGGL(residual_rows_kernel<10>, g, b, lds, g4_stream(), a, q8row);
-        else hipLaunchKernelGGL(residual_rows_kernel<16>, g, b, lds, g4_stream(), a, q8row);
+    const bool four = residual4_ok(x, y, xb2, n) && (!y || ((uintptr_t)w_post & 15) == 0) &&
+                      (!w_next || ((uintptr_t)w_next & 15) == 0);
+    G4_CHECK_ARG(!narrow || four, "residual_norm_rows: the prologue layout needs 16-byte aligned x, y, xb2 and weights");
+    if (four) {
+        // the layout of g4_residual_norm and of the GEMV prologues for these
+        // n (narrow or not), so each row's bits are theirs
+        hipLaunchKernelGGL(residual4_kernel, dim3(m), dim3(n / 4), 0, g4_stream(), a, q8row);
+        return g4_check_launch("residual4_kernel");
     } else {
         const int ept = n <= kNormThreads ? 1 : n <= 4 * kNormThreads ? 4 : 16;
         const int nt = ((n + ept - 1) / ept + 63) / 64 * 64;

@@ -110,6 +110,9 @@ _SIGS = {
     "g4_argmax_part_bytes": (SZ, [I]),
     "g4_argmax": (I, [VP, I, VP, VP, VP, VP]),
     "g4_mm_argmax_part_bytes": (SZ, [I]),
+    "g4_probe_empty": (I, [I]),
+    "g4_probe_read": (I, [VP, SZ, VP, I]),
+    "g4_probe_handoff": (I, [VP, VP, VP, I, I]),
     "g4_mm_argmax_row": (I, [VP, VP, I, I, I, VP, F, VP, VP, VP, VP, VP]),
     "g4_residual_norm": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, F]),
     "g4_qkv_post": (I, [VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, F, F, VP, F, VP]),

@@ -275,9 +275,12 @@ int g4_ple_finish_rows(float *ple, const float *ctx, const void *ple_tok, int ty
 /* o[z][i] = gelu(g[z][i]) * u[z*ustride + i]: gelu(gate)*up (main.c:1976-1980)
  * and the PLE gate (main.c:1989-1993) */
 int g4_gelu_mul_rows(float *o, const float *g, const float *u, int d, int m, int ustride);
-/* g4_residual_norm on m rows of x (in place); narrow = 1 uses the thread
- * layout of g4_mm_residual_q8's prologue (n = 2048, 2560, 4096), narrow = 0
- * that of g4_residual_norm, so each row matches the decode step's bits */
+/* g4_residual_norm on m rows of x (in place), each row's bits those of the
+ * decode step: narrow = 1 matches the residual prologue of g4_mm_residual_q8
+ * (_pair, _qkv, and the single-tensor form; n = 2048, 2560, 4096, all
+ * pointers 16-byte aligned), narrow = 0 g4_residual_norm.  For 16-byte
+ * aligned rows with n a multiple of 256 up to 4096 the two layouts are the
+ * same (one float4 per thread). */
 int g4_residual_norm_rows(float *x, const float *y, const float *w_post, const float *oscale, const float *w_next,
                           float *xb2, void *q8, int qsrc, int n, float eps, int m, int narrow);
 /* RoPE (cos, sin) tables of positions pos0..pos0+m-1 (main.c:1725-1742), n_rot/2 pairs each */
@@ -463,6 +466,23 @@ int g4_graph_begin(void);
 int g4_graph_end(void **graph_exec);
 int g4_graph_launch(void *graph_exec);
 int g4_graph_destroy(void *graph_exec);
+
+/* ---------------------------------------------------------------------------
+ * Measurement probes (no counterpart in the reference; they compute nothing
+ * of the model): the floors the decode step is sized against, timed by
+ * bench.py --workload floors.
+ * ------------------------------------------------------------------------- */
+/* an empty kernel of `workgroups` 64-thread workgroups: a dependent launch's cost */
+int g4_probe_empty(int workgroups);
+/* a streaming read of `bytes` (16-byte aligned, a multiple of 16) with 1 KB
+ * per wave instruction over `workgroups` 256-thread workgroups; sink gets one
+ * float per workgroup */
+int g4_probe_read(const void *p, size_t bytes, float *sink, int workgroups);
+/* every workgroup stores a value; with handoff, each then releases it
+ * device-wide and counts itself in on *count (zero before the first launch;
+ * the last workgroup resets it) and the last one acquires and adds them into
+ * *out.  handoff = 0 is the same launch without the hand-off. */
+int g4_probe_handoff(float *vals, unsigned int *count, float *out, int workgroups, int handoff);
 
 #ifdef __cplusplus
 }
