@@ -1549,12 +1549,13 @@ int launch_attn(const AttnArgs& a) {
         return g4_check_launch("attn_rows_h16_kernel/attn_rows_mfma_kernel/attn_merge_kernel");
     }
     if (attn_chunk_lds(a.hd, kp) <= 65536) {
+        // no out: the partials only, merged by the caller (g4_mm_attn_merge)
         if (a.hd == 256) {
             launch_chunk<256>(a, kp, grid);
-            launch_merge<256>(a, dim3(a.n_heads, 1, zq));
+            if (a.out) launch_merge<256>(a, dim3(a.n_heads, 1, zq));
         } else {
             launch_chunk<512>(a, kp, grid);
-            launch_merge<512>(a, dim3(a.n_heads, 2, zq));
+            if (a.out) launch_merge<512>(a, dim3(a.n_heads, 2, zq));
         }
         return g4_check_launch("attn_chunk_kernel/attn_merge_kernel");
     }
@@ -1881,7 +1882,9 @@ extern "C" int g4_attn_decode_fused(const float* q_raw, const float* q_norm, con
                                     float* out, void* q8) {
     int rc = check_attn_shape("attn_decode_fused", n_heads, n_kv, hd, G, true);
     if (rc) return rc;
-    G4_CHECK_ARG(q_raw && q_norm && rope_tab && kc && vc && dpos && part && out, "attn_decode_fused: null pointer");
+    G4_CHECK_ARG(q_raw && q_norm && rope_tab && kc && vc && dpos && part, "attn_decode_fused: null pointer");
+    G4_CHECK_ARG(out || (!q8 && attn_chunk_lds(hd, n_heads / n_kv <= 1 ? 1 : n_heads / n_kv <= 2 ? 2 : n_heads / n_kv <= 4 ? 4 : 8) <= 65536),
+                 "attn_decode_fused: out is required with q8, or where the partials need the merge kernel");
     G4_CHECK_ARG(n_rot > 0 && n_rot % 2 == 0 && n_rot <= hd && (2 * kAttnThreads) % n_rot == 0,
                  "attn_decode_fused: n_rot=%d (hd %d; n_rot/2 must divide %d)", n_rot, hd, kAttnThreads);
     G4_CHECK_ARG(!k_raw || (v_raw && k_norm && kstore && vstore), "attn_decode_fused: incomplete K/V append arguments");

@@ -188,6 +188,18 @@ struct Stack2 {
     float* out6;
     int d6;
 };
+// attention merge prologue (PRO 2): the G chunk partials (o[256], max, sum)
+// of each head (head_dim 256, one Q8_K block per head) as attn_chunk_kernel
+// leaves them; out / q8: the merged vector and its Q8_K (workgroup 0, each
+// optional)
+struct MergeArgs {
+    const float* part;
+    float* out;
+    uint8_t* q8;
+    int G;
+};
+constexpr int kMergeMaxG = G4_MERGE_MAX_CHUNKS;   // chunks per head the merge prologue holds in registers
+
 // Q6_K rows per prologue workgroup of wg threads: wg/8 lane groups, ks6 per row
 constexpr int q6_pro_rows(int wg, int ks6) { return wg / 8 / ks6; }
 
@@ -274,7 +286,8 @@ __device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, cons
     (void)row_;
 }
 
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, bool PRO = false>
+// PRO 1: residual prologue (ra, st); PRO 2: attention merge prologue (mg)
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0>
 __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
                                                            const uint8_t* q8, float* __restrict__ out,
@@ -282,9 +295,10 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                                                            int32_t* __restrict__ dbgM, const float* __restrict__ xin,
                                                            uint8_t* __restrict__ q8_store,
                                                            const float* __restrict__ aux, const ResidualArgs ra,
-                                                           const Stack2 st) {
+                                                           const Stack2 st, const MergeArgs mg) {
     static_assert(!QIN || (WG == 64 && NB == 1), "the single-block input path runs one wave over one block");
     static_assert(!PRO || (WG == 64 * NB && NB > 0 && !DBG), "the prologue needs one wave per block");
+    static_assert(PRO != 2 || NMAT == 1, "the merge prologue feeds one matrix");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
@@ -294,9 +308,9 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
     // stays for its barriers; rows past the end compute the last row and do
     // not store.  Rows d.. d+st.d-1 (PRO only) belong to the stacked second
     // tensor.
-    const int dtot = d + (PRO ? st.d : 0);
+    const int dtot = d + (PRO == 1 ? st.d : 0);
     const int row = (PRO || QIN) ? min(row_, dtot - 1) : row_;
-    const bool sec = PRO && row >= d;
+    const bool sec = PRO == 1 && row >= d;
     const int dl = sec ? st.d : d, rl = sec ? row - d : row;
     const uint8_t* const wa = sec ? st.w : w0;
     float* const outp = sec ? st.out : out;
@@ -400,7 +414,70 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
     if (NB > 0) {
         // every load of this group's blocks first, then the integer work
         Raw raw[NH];
-        if constexpr (PRO) {
+        if constexpr (PRO == 2) {
+            // the attention output is merged here: wave h takes head h, lane
+            // L its dims 4L .. 4L+3, issuing every chunk's partial (m, l) and
+            // o loads and then its weight loads before anything waits; the
+            // merge is attn_merge_kernel's arithmetic in its order (max of the
+            // chunk maxima, f_g = exp(m_g - M) for chunks with weight, the
+            // wave-sum of l_g f_g, o = sum_g o_g f_g from g = 0, o / L), so the
+            // vector, its Q8_K (wave h: block h into LDS) and the outputs are
+            // the separate merge + GEMV's bits
+            const int lane = tid & 63, h = tid >> 6;
+            const int G = mg.G;
+            constexpr int RS = 256 + 2;   // partial row stride (floats)
+            const float* ph = mg.part + (size_t)h * G * RS;
+            const float2 ml = *reinterpret_cast<const float2*>(ph + (size_t)min(lane, G - 1) * RS + 256);
+            float2 oa[kMergeMaxG], ob[kMergeMaxG];
+#pragma unroll
+            for (int u = 0; u < kMergeMaxG; u++) {
+                const float* pr = ph + (size_t)min(u, G - 1) * RS + 4 * lane;
+                oa[u] = *reinterpret_cast<const float2*>(pr);
+                ob[u] = *reinterpret_cast<const float2*>(pr + 2);
+            }
+#pragma unroll
+            for (int i = 0; i < NH; i++) load_w(min(grp * NH + i, nb - 1), raw[i]);
+            const float mgv = lane < G ? ml.x : -INFINITY;
+            const float lgv = lane < G ? ml.y : 0.0f;
+            const float M = wave_max(mgv);
+            const float f = lane < G && lgv > 0.0f ? expf(mgv - M) : 0.0f;
+            const float L = wave_sum(lane < G ? 0.0f + lgv * f : 0.0f);
+            float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < kMergeMaxG; u++) {
+                if (u < G) {
+                    const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), u));
+                    o[0] = __builtin_fmaf(oa[u].x, fu, o[0]);
+                    o[1] = __builtin_fmaf(oa[u].y, fu, o[1]);
+                    o[2] = __builtin_fmaf(ob[u].x, fu, o[2]);
+                    o[3] = __builtin_fmaf(ob[u].y, fu, o[3]);
+                }
+            }
+            float r[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] = L > 0.0f ? o[c] / L : 0.0f;
+            extern __shared__ __align__(16) float pbuf[];
+            uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf);
+            quantize_block_wave(r, lane, q8l, NB, h);
+            if (blockIdx.x == 0) {
+                if (mg.out) reinterpret_cast<float4*>(mg.out)[tid] = make_float4(r[0], r[1], r[2], r[3]);
+                if (mg.q8) quantize_block_wave(r, lane, mg.q8, NB, h);
+            }
+            lds_sync();
+            const uint8_t* a_qs_l = q8l + 32 * l;
+            const uint8_t* a_bs_l = q8l + q8k_bsums_off(NB) + 8 * k;
+            const float* a_d_l = reinterpret_cast<const float*>(q8l + q8k_d_off(NB));
+#pragma unroll
+            for (int i = 0; i < NH; i++) {
+                const int b = grp * NH + i;
+                if (b < nb) {
+                    raw[i].a0 = *reinterpret_cast<const uint4*>(a_qs_l + b * 256);
+                    raw[i].a1 = *reinterpret_cast<const uint4*>(a_qs_l + b * 256 + 16);
+                    raw[i].bsw = *reinterpret_cast<const uint2*>(a_bs_l + b * 32);
+                    raw[i].yd = a_d_l[b];
+                }
+            }
+        } else if constexpr (PRO == 1) {
             // the activations are produced here: residual step, norm and Q8_K
             // by the whole workgroup (one float4 of each vector per thread,
             // wave w quantizes block w into LDS; workgroup 0 also stores
@@ -1022,7 +1099,7 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
     constexpr int rows_per_wg = 8 / SPLIT;
     hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, DBG, NB, SPLIT, QIN>), dim3((d + rows_per_wg - 1) / rows_per_wg),
                        dim3(64), 0, g4_stream(), (const uint8_t*)w0, (const uint8_t*)w1, (const uint8_t*)q8, o, nb, d,
-                       S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{}, Stack2{});
+                       S, M, xin, (uint8_t*)q8_store, aux, ResidualArgs{}, Stack2{}, MergeArgs{});
 }
 
 // residual step + norm + Q8_K as the prologue of every workgroup (64 NB
@@ -1038,9 +1115,23 @@ void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const floa
                        (size_t)WG / 8 * 4;
     const int r6 = q6_pro_rows(WG, SPLIT);
     const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + r6 - 1) / r6 : 0);
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, true>),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, 1>),
                        dim3(wgs), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
-                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st);
+                       (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st,
+                       MergeArgs{});
+}
+
+// attention merge + Q8_K as the prologue of every workgroup (64 NB threads:
+// wave h merges head h), then the GEMV with 32 lanes per row
+template <bool Q5, int NB>
+void launch_q45_merge(const void* w, float* o, int d, const MergeArgs& mg) {
+    constexpr int WG = 64 * NB, SPLIT = 4;
+    constexpr int rows_per_wg = WG / (8 * SPLIT);
+    const size_t lds = ((size_t)NB * 292 + 15) & ~(size_t)15;
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, 1, false, NB, SPLIT, false, WG, 2>),
+                       dim3((d + rows_per_wg - 1) / rows_per_wg), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
+                       nullptr, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, nullptr, ResidualArgs{},
+                       Stack2{}, mg);
 }
 
 // residual step + norm + Q8_K as the prologue of every workgroup (64 NB
@@ -1505,4 +1596,26 @@ extern "C" int g4_mm_residual_q8_qkv(float* o1, const void* w1, int d1, float* o
     return mm_residual("g4_mm_residual_q8_qkv", o1, w1, nullptr, n, d1, type, nullptr,
                        Stack2{(const uint8_t*)w2, o2, d2, (const uint8_t*)w3, o3, d3}, x, x_out, y, w_post, oscale,
                        w_next, xb2, q8, 0, eps);
+}
+
+// The attention output projection with the merge of the decode attention's
+// chunk partials as its prologue (n = n_heads * 256)
+extern "C" int g4_mm_attn_merge(float* o, const void* w, int n, int d, int type, const float* part, int G, int n_heads,
+                                int hd, float* q_out, void* q8) {
+    int rc = check_gemv("g4_mm_attn_merge", o, w, part, n, d);
+    if (rc) return rc;
+    G4_CHECK_ARG(hd == 256 && n_heads > 0 && n == n_heads * hd, "g4_mm_attn_merge: head_dim %d, %d heads, n=%d", hd,
+                 n_heads, n);
+    G4_CHECK_ARG(G >= 1 && G <= kMergeMaxG, "g4_mm_attn_merge: %d chunks (1..%d)", G, kMergeMaxG);
+    G4_CHECK_ARG(!q_out || aligned16(q_out), "g4_mm_attn_merge: q_out must be 16-byte aligned");
+    G4_CHECK_ARG(!q8 || aligned16(q8), "g4_mm_attn_merge: q8 must be 16-byte aligned");
+    const MergeArgs mg{part, q_out, (uint8_t*)q8, G};
+    const bool q5 = type == G4_Q5_K;
+    if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "g4_mm_attn_merge: type %d not supported", type);
+    switch (n_heads) {
+    case 8: q5 ? launch_q45_merge<true, 8>(w, o, d, mg) : launch_q45_merge<false, 8>(w, o, d, mg); break;
+    case 16: q5 ? launch_q45_merge<true, 16>(w, o, d, mg) : launch_q45_merge<false, 16>(w, o, d, mg); break;
+    default: return g4_fail(G4_ERR_ARG, "g4_mm_attn_merge: %d heads (8 or 16)", n_heads);
+    }
+    return g4_check_launch("gemv_q45_rows_kernel<merge>");
 }

@@ -110,6 +110,7 @@ _SIGS = {
     "g4_argmax_part_bytes": (SZ, [I]),
     "g4_argmax": (I, [VP, I, VP, VP, VP, VP]),
     "g4_mm_argmax_part_bytes": (SZ, [I]),
+    "g4_mm_attn_merge": (I, [VP, VP, I, I, I, VP, I, I, I, VP, VP]),
     "g4_probe_empty": (I, [I]),
     "g4_probe_read": (I, [VP, SZ, VP, I]),
     "g4_probe_handoff": (I, [VP, VP, VP, I, I]),

@@ -158,6 +158,17 @@ int g4_mm_residual_q8_qkv(float *o1, const void *w1, int d1, float *o2, const vo
                           const void *w3, int d3, int type3, int n, int type, const float *x, float *x_out,
                           const float *y, const float *w_post, const float *oscale, const float *w_next, float *xb2,
                           void *q8, float eps);
+/* The attention block's end and the output projection in one launch
+ * (main.c:1909-1950 then main.c:1955): the G chunk partials that
+ * g4_attn_decode_fused left in part (out and q8 NULL) are merged per head by
+ * log-sum-exp exactly as its own merge does (same operations and order, so
+ * the same vector), quantized to Q8_K and multiplied by W (Q4_K / Q5_K, d
+ * rows of n = n_heads * hd) as g4_mm_quant_dot_rows: o[d].  q_out (n floats)
+ * and q8 (g4_q8K_bytes(n)) optionally receive the merged vector and its
+ * Q8_K.  head_dim 256 only, n_heads 8 or 16, G <= G4_MERGE_MAX_CHUNKS. */
+#define G4_MERGE_MAX_CHUNKS 16
+int g4_mm_attn_merge(float *o, const void *w, int n, int d, int type, const float *part, int G, int n_heads, int hd,
+                     float *q_out, void *q8);
 
 /* ---------------------------------------------------------------------------
  * Batched prefill GEMM.  The reference has none: generate() runs forward()
@@ -408,7 +419,9 @@ int    g4_attn_decode_dev(const float *q, const float *kc, const float *vc, int 
  * k_norm and rotated, V without weight) and stored at slot pos (pos % ring
  * when ring > 0) of kstore/vstore, and the attention over kc/vc (the cache
  * read: this layer's own, or the donor's on shared-KV layers) uses them for
- * position pos.  n_rot/2 must divide 256.  Otherwise as g4_attn_decode_dev. */
+ * position pos.  n_rot/2 must divide 256.  Otherwise as g4_attn_decode_dev;
+ * with out and q8 NULL only the chunk partials are written to part (G chunks
+ * per head, g4_attn_part_bytes), for g4_mm_attn_merge to merge. */
 int    g4_attn_decode_fused(const float *q_raw, const float *q_norm, const float *k_raw, const float *v_raw,
                             const float *k_norm, float *kstore, float *vstore, const float *kc, const float *vc,
                             int kv_stride, int ring, const int *dpos, int window, int n_heads, int n_kv, int hd,

@@ -292,6 +292,100 @@ def test_attn_decode_fused(lib, orc, hd, window, pos, G, store):
     assert h.tobytes() == orc.quantize_q8K(got).tobytes()
 
 
+
+@pytest.mark.parametrize("nh,nkv,window,pos,G,store,qtype,d", [(8, 2, 512, 700, 16, True, 12, 2560),
+                                                              (8, 2, 512, 900, 16, False, 12, 2560),
+                                                              (8, 2, 512, 100, 4, True, 13, 2560),
+                                                              (8, 2, 0, 37, 1, True, 12, 200),
+                                                              (16, 2, 512, 600, 16, True, 12, 2560),
+                                                              (16, 4, 0, 333, 11, False, 13, 1000)])
+def test_attn_merge_o_prologue(lib, orc, nh, nkv, window, pos, G, store, qtype, d):
+    """The attention's end and the output projection in one launch
+    (main.c:1909-1950 then the O mm, main.c:1955): g4_attn_decode_fused leaves
+    only the chunk partials, g4_mm_attn_merge merges them per head in every
+    workgroup and runs the Q4_K/Q5_K GEMV on their Q8_K.  The merged vector
+    is within 1e-4 of the oracle's attention and bit-equal to the separate
+    merge kernel's, its Q8_K is quantize_row_q8_K of it, and the outputs equal
+    the oracle's mm_quant_dot_rows on that Q8_K bit for bit."""
+    from g4 import upload_quant
+    hd, eps = 256, 1e-6
+    rng = np.random.default_rng(nh + pos + G + qtype)
+    kv_dim, n = nkv * hd, nh * hd
+    base = 1e4 if window else 1e6
+    q_norm = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    k_norm = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    flat_k = rng.standard_normal((pos + 1, kv_dim)).astype(np.float32)
+    flat_v = rng.standard_normal((pos + 1, kv_dim)).astype(np.float32)
+    q = rng.standard_normal(n).astype(np.float32)
+    k = rng.standard_normal(kv_dim).astype(np.float32)
+    v = rng.standard_normal(kv_dim).astype(np.float32)
+    qn = q.copy()
+    orc.L.or_rmsnorm_head_inplace(P(qn), P(q_norm), nh, hd, C.c_float(eps))
+    qn = orc.rope(qn, nh, hd, hd, pos, base, None)
+    if store:
+        kk = k.copy()
+        orc.L.or_rmsnorm_head_inplace(P(kk), P(k_norm), nkv, hd, C.c_float(eps))
+        flat_k[pos] = orc.rope(kk, nkv, hd, hd, pos, base, None)
+        vv = v.copy()
+        orc.L.or_rmsnorm_head_noweight_inplace(P(vv), nkv, hd, C.c_float(eps))
+        flat_v[pos] = vv
+    t_start = max(0, pos + 1 - window) if window else 0
+    want = orc.attn(qn, flat_k, flat_v, kv_dim, t_start, pos + 1 - t_start, nh, nkv, hd, 1.0)
+    slots = window if window else pos + 1
+    cache_k = np.full((slots, kv_dim), 7.0, np.float32)
+    cache_v = np.full((slots, kv_dim), -7.0, np.float32)
+    for t in range(t_start, pos + (0 if store else 1)):
+        cache_k[t % slots], cache_v[t % slots] = flat_k[t], flat_v[t]
+    kc, vc = dbuf(lib, cache_k), dbuf(lib, cache_v)
+    dpos = dbuf(lib, np.array([pos], np.int32))
+    tab = empty(lib, 4 * hd)
+    lib.g4_rope_table(tab.ptr, dpos.ptr, 0, hd, C.c_float(base), C.c_float(1.0), None)
+    qd, kd, vd = dbuf(lib, q), dbuf(lib, k), dbuf(lib, v)
+    qnd, knd = dbuf(lib, q_norm), dbuf(lib, k_norm)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    part = empty(lib, lib.L.g4_attn_part_bytes(nh, hd, G))
+
+    def attn(out, q8):
+        lib.g4_attn_decode_fused(qd.ptr, qnd.ptr, kd.ptr if store else None, vd.ptr if store else None,
+                                 knd.ptr if store else None, kc.ptr if store else None, vc.ptr if store else None,
+                                 kc.ptr, vc.ptr, kv_dim, window, dpos.ptr, window, nh, nkv, hd, hd, tab.ptr,
+                                 C.c_float(eps), C.c_float(1.0), G, part.ptr, out, q8)
+
+    # the separate merge kernel, then the plain GEMV on its Q8_K
+    o_sep, q8_sep, y_sep = empty(lib, 4 * n), empty(lib, lib.L.g4_q8K_bytes(n)), empty(lib, 4 * d)
+    attn(o_sep.ptr, q8_sep.ptr)
+    lib.g4_mm_quant_dot_rows(y_sep.ptr, w.ptr, n, d, qtype, q8_sep.ptr)
+    # partials only (the append is repeated with the same row), merged in the GEMV
+    o_m, q8_m, y_m = empty(lib, 4 * n), empty(lib, lib.L.g4_q8K_bytes(n)), empty(lib, 4 * d)
+    attn(None, None)
+    lib.g4_mm_attn_merge(y_m.ptr, w.ptr, n, d, qtype, part.ptr, G, nh, hd, o_m.ptr, q8_m.ptr)
+    got = o_m.to_array(np.float32)
+    assert rel_err(got, want) < 1e-4
+    assert np.array_equal(got.view(np.uint32), o_sep.to_array(np.float32).view(np.uint32))
+    h = np.zeros(n // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8_m.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(got).tobytes()
+    y = y_m.to_array(np.float32)
+    assert np.array_equal(y.view(np.uint32), orc.mm_quant_dot_rows(raw, n, d, qtype, h).view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), y_sep.to_array(np.float32).view(np.uint32))
+    # without the optional stores the outputs are the same
+    y2 = empty(lib, 4 * d)
+    lib.g4_mm_attn_merge(y2.ptr, w.ptr, n, d, qtype, part.ptr, G, nh, hd, None, None)
+    assert np.array_equal(y2.to_array(np.float32).view(np.uint32), y.view(np.uint32))
+
+
+def test_attn_merge_o_prologue_rejects(lib):
+    from g4 import DBuf, G4Error
+    b = DBuf(lib, 1 << 20)
+    for args in [(b.ptr, b.ptr, 2048, 2560, 12, b.ptr, 17, 8, 256, None, None),    # too many chunks
+                 (b.ptr, b.ptr, 4096, 2560, 12, b.ptr, 8, 8, 512, None, None),     # head_dim 512
+                 (b.ptr, b.ptr, 3072, 2560, 12, b.ptr, 8, 12, 256, None, None),    # 12 heads
+                 (b.ptr, b.ptr, 2048, 2560, 14, b.ptr, 8, 8, 256, None, None)]:    # Q6_K
+        with pytest.raises(G4Error):
+            lib.g4_mm_attn_merge(*args)
+
+
 # ---------------------------------------------------------------------------
 # embedding lookup, PLE, GELU gate, argmax
 # ---------------------------------------------------------------------------
