@@ -61,13 +61,7 @@ __device__ __forceinline__ void rope_head_lds_tab(float* seg, int hd, int n_rot,
 __global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ tab, const int* dpos, int pos, int npair,
                                                          float ts, float fs, const float* __restrict__ ff) {
     const int p = dpos ? *dpos : pos;
-    for (int j = threadIdx.x; j < npair; j += blockDim.x) {
-        const float f = ff ? ff[j] : 1.0f;   // in flight during the product chain
-        float theta = (float)p;
-        for (int i = 0; i < j; i++) theta *= ts;
-        const float angle = (fs * theta) / f;
-        tab[j] = make_float2(cosf(angle), sinf(angle));
-    }
+    for (int j = threadIdx.x; j < npair; j += blockDim.x) tab[j] = rope_pair_cs(p, j, ts, fs, ff);
 }
 
 // rows: position pos0 + blockIdx.x -> tab + blockIdx.x * npair
@@ -75,13 +69,7 @@ __global__ __launch_bounds__(256) void rope_table_rows_kernel(float2* __restrict
                                                               float fs, const float* __restrict__ ff) {
     const int p = pos0 + blockIdx.x;
     float2* t = tab + (size_t)blockIdx.x * npair;
-    for (int j = threadIdx.x; j < npair; j += blockDim.x) {
-        const float f = ff ? ff[j] : 1.0f;   // in flight during the product chain
-        float theta = (float)p;
-        for (int i = 0; i < j; i++) theta *= ts;
-        const float angle = (fs * theta) / f;
-        t[j] = make_float2(cosf(angle), sinf(angle));
-    }
+    for (int j = threadIdx.x; j < npair; j += blockDim.x) t[j] = rope_pair_cs(p, j, ts, fs, ff);
 }
 
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ vec, int hd, int n_rot, int pos, float ts,

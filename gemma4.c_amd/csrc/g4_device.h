@@ -78,6 +78,17 @@ __device__ __forceinline__ void unpack_scales(const uint32_t s0, const uint32_t 
 }
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xff; }
 
+// ---- RoPE angles (main.c:1725-1742) ------------------------------------------
+// (cos, sin) of pair j at position p: the reference's angle chain theta_0 = p,
+// theta_j = theta_{j-1} * ts (one rounding per step), angle = (fs * theta_j) / ff[j]
+__device__ __forceinline__ float2 rope_pair_cs(int p, int j, float ts, float fs, const float* __restrict__ ff) {
+    const float f = ff ? ff[j] : 1.0f;   // in flight during the product chain
+    float theta = (float)p;
+    for (int i = 0; i < j; i++) theta *= ts;
+    const float angle = (fs * theta) / f;
+    return make_float2(cosf(angle), sinf(angle));
+}
+
 // ---- cross-lane helpers (64-wide wavefronts) --------------------------------
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) { return __shfl_xor(v, mask, 64); }

@@ -38,6 +38,31 @@ __global__ __launch_bounds__(256) void emb_lookup_kernel(float* __restrict__ o, 
     o[i] = use_scale ? v * scale : v;
 }
 
+// the decode step's inputs in one launch: workgroups 0 .. ceil(dim/256)-1
+// take emb_lookup_kernel's elements, the next two the (cos, sin) tables of
+// the two RoPE variants at position *dpos (rope_table_kernel's values)
+struct RopeTab {
+    float2* tab;
+    const float* ff;
+    float ts;
+    int npair;
+};
+__global__ __launch_bounds__(256) void emb_rope_kernel(float* __restrict__ o, const void* w, int type, int rows, int dim,
+                                                       const int* dtok, float scale, const int* dpos, float fs,
+                                                       RopeTab ta, RopeTab tb) {
+    const int ne = (dim + 255) / 256;
+    if ((int)blockIdx.x >= ne) {
+        const RopeTab& t = blockIdx.x == ne ? ta : tb;
+        const int p = *dpos;
+        for (int j = threadIdx.x; j < t.npair; j += 256) t.tab[j] = rope_pair_cs(p, j, t.ts, fs, t.ff);
+        return;
+    }
+    const int id = *dtok;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim || id < 0 || id >= rows) return;
+    o[i] = table_elem(w, type, rows, dim, id, i) * scale;
+}
+
 // token z = blockIdx.y of a prompt chunk -> row z of o
 __global__ __launch_bounds__(256) void emb_lookup_rows_kernel(float* __restrict__ o, const void* w, int type, int rows,
                                                               int dim, const int* __restrict__ dtok, float scale) {
@@ -254,6 +279,21 @@ extern "C" int g4_emb_lookup_dev(float* o, const void* w, int type, int rows, co
     hipLaunchKernelGGL(emb_lookup_kernel, dim3((dim + 255) / 256), dim3(256), 0, g4_stream(), o, w, type, rows, dim,
                        dtok, 0, 1, scale);
     return g4_check_launch("emb_lookup_kernel");
+}
+
+extern "C" int g4_emb_lookup_rope(float* o, const void* w, int type, int rows, const int* dtok, int dim, float scale,
+                                  const int* dpos, float* tab_a, int n_rot_a, float base_a, const float* ff_a,
+                                  float* tab_b, int n_rot_b, float base_b, const float* ff_b, float freq_scale) {
+    G4_CHECK_ARG(o && w && dtok && dim > 0 && rows > 0 && dpos, "g4_emb_lookup_rope: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    G4_CHECK_ARG(tab_a && tab_b && n_rot_a > 0 && n_rot_a % 2 == 0 && n_rot_a <= 2048 && n_rot_b > 0 &&
+                     n_rot_b % 2 == 0 && n_rot_b <= 2048,
+                 "g4_emb_lookup_rope: bad RoPE table arguments");
+    const RopeTab ta{(float2*)tab_a, ff_a, powf(base_a, -2.0f / (float)n_rot_a), n_rot_a / 2};
+    const RopeTab tb{(float2*)tab_b, ff_b, powf(base_b, -2.0f / (float)n_rot_b), n_rot_b / 2};
+    hipLaunchKernelGGL(emb_rope_kernel, dim3((dim + 255) / 256 + 2), dim3(256), 0, g4_stream(), o, w, type, rows, dim,
+                       dtok, scale, dpos, freq_scale, ta, tb);
+    return g4_check_launch("emb_rope_kernel");
 }
 
 extern "C" int g4_ple_finish(float* ple, const float* ctx, const void* ple_tok, int type, int rows, const float* proj_norm,

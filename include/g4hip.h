@@ -429,6 +429,13 @@ int    g4_attn_decode_fused(const float *q_raw, const float *q_norm, const float
                             float *out, void *q8);
 /* x = emb_lookup(w, *dtok) * scale (main.c:1849-1854) */
 int g4_emb_lookup_dev(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale);
+/* The decode step's inputs in one launch: g4_emb_lookup_dev(o, ..., scale)
+ * and g4_rope_table(tab_a, dpos, 0, n_rot_a, base_a, freq_scale, ff_a) and
+ * g4_rope_table(tab_b, ...) at the position *dpos -- the same values as the
+ * three calls (main.c:1849-1854, 1725-1742). */
+int g4_emb_lookup_rope(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale,
+                       const int *dpos, float *tab_a, int n_rot_a, float base_a, const float *ff_a, float *tab_b,
+                       int n_rot_b, float base_b, const float *ff_b, float freq_scale);
 /* build_ple after its projection (main.c:1751-1777): ple[l*pd+i] =
  * (emb(ple_tok, tok)[l*pd+i]*sc_tok + rmsnorm(ctx[l*pd..]*sc_ctx, norm)[i]) * mix;
  * tok = *dtok if dtok else tok. */

@@ -405,6 +405,35 @@ def test_emb_lookup_bitexact(lib, orc, qtype):
     assert lib.L.g4_emb_lookup(out.ptr, w.ptr, qtype, rows, rows, dim) == 1   # G4_ERR_ARG, id out of range
 
 
+
+@pytest.mark.parametrize("qtype,pos", [(14, 0), (12, 519), (14, 32767)])
+def test_emb_lookup_rope(lib, orc, qtype, pos):
+    """The decode step's inputs in one launch: the embedding row times its
+    scale, bit-exact against the oracle's emb_lookup, and both RoPE tables
+    (sliding: n_rot 256, base 1e4; full: n_rot 512, base 1e6 with freq
+    factors) equal, bit for bit, to g4_rope_table's at the same position."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(qtype + pos)
+    rows, dim, tok, scale = 300, 2560, 123, np.float32(np.sqrt(2560.0))
+    raw = synth.rand_kquant(rng, qtype, rows, dim)
+    w = upload_quant(lib, raw, qtype, dim, rows)
+    ff = rng.uniform(1.0, 4.0, 256).astype(np.float32)
+    ffd = dbuf(lib, ff)
+    dtok, dpos = dbuf(lib, np.array([tok], np.int32)), dbuf(lib, np.array([pos], np.int32))
+    out, ta, tb = DBuf(lib, 4 * dim), DBuf(lib, 4 * 256), DBuf(lib, 4 * 512)
+    lib.g4_emb_lookup_rope(out.ptr, w.ptr, qtype, rows, dtok.ptr, dim, C.c_float(scale), dpos.ptr, ta.ptr, 256,
+                           C.c_float(1e4), None, tb.ptr, 512, C.c_float(1e6), ffd.ptr, C.c_float(1.0))
+    want = np.empty(dim, np.float32)
+    assert orc.L.or_emb_lookup(P(want), P(raw), qtype, tok, dim) == 0
+    assert np.array_equal(out.to_array(np.float32).view(np.uint32), (want * scale).view(np.uint32))
+    ra, rb = DBuf(lib, 4 * 256), DBuf(lib, 4 * 512)
+    lib.g4_rope_table(ra.ptr, dpos.ptr, 0, 256, C.c_float(1e4), C.c_float(1.0), None)
+    lib.g4_rope_table(rb.ptr, dpos.ptr, 0, 512, C.c_float(1e6), C.c_float(1.0), ffd.ptr)
+    assert np.array_equal(ta.to_array(np.float32).view(np.uint32), ra.to_array(np.float32).view(np.uint32))
+    assert np.array_equal(tb.to_array(np.float32).view(np.uint32), rb.to_array(np.float32).view(np.uint32))
+    if pos == 0:   # angle 0: (1, 0) pairs
+        assert np.array_equal(ta.to_array(np.float32).reshape(-1, 2), np.tile([1.0, 0.0], (128, 1)).astype(np.float32))
+
 def test_ple_finish(lib, orc):
     from g4 import DBuf, upload_quant
     rng = np.random.default_rng(5)
