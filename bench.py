@@ -917,7 +917,8 @@ def bench_floors(lib, g4, synth, args):
     # 2. streaming reads
     sink = g4.DBuf(lib, 4 * 4096)
     reads = {}
-    for mb, label in ((14.79, "14.8MB (Q4_K 10240x2560)"), (29.54, "29.5MB (gate|up 2x10240x2560)"),
+    for mb, label in ((2.95, "2.95MB (O Q4_K 2560x2048)"), (14.79, "14.8MB (Q4_K 10240x2560)"),
+                      (21.54, "21.5MB (FFN down Q6_K 2560x10240)"), (29.54, "29.5MB (gate|up 2x10240x2560)"),
                       (551.6, "551.6MB (LM head Q6_K 262144x2560)")):
         nbytes = int(mb * 1e6) // 16 * 16
         ncp = _copies(nbytes)
@@ -930,21 +931,26 @@ def bench_floors(lib, g4, synth, args):
             us = ms * 1e3 / args.steps
             reads[label] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1), "copies_rotated": ncp}
         del bufs
-    # 3. last-workgroup hand-off
-    vals = g4.DBuf(lib, 4 * 4096)
+    # 3. last-workgroup hand-off: 16 values per workgroup, fenced and as
+    # device-scope atomics, against the same launch without it
+    vals = g4.DBuf(lib, 4 * 16 * 640)
     cnt = g4.DBuf(lib, 256)
     out = g4.DBuf(lib, 256)
     lib.check(L.g4_memset(cnt.ptr, 0, 256))
     hand = {}
-    for wg in (16, 256, 640):
-        t = []
-        for h in (0, 1):
-            ms = _time_steps(lib, lambda i, wg=wg, h=h: L.g4_probe_handoff(vals.ptr, cnt.ptr, out.ptr, wg, h), args)
-            t.append(ms * 1e3 / args.steps)
-        hand[f"{wg}wg"] = {"plain_us": round(t[0], 3), "handoff_us": round(t[1], 3), "cost_us": round(t[1] - t[0], 3)}
     got = np.zeros(1, np.float32)
-    lib.check(L.g4_memcpy_d2h(got.ctypes.data, out.ptr, 4))
-    assert got[0] == sum(range(640)), got              # the last launch's hand-off summed every workgroup's value
+    for wg in (13, 32, 160, 256, 640):
+        t = []
+        for mode in (0, 1, 2):
+            ms = _time_steps(lib, lambda i, wg=wg, mode=mode: L.g4_probe_handoff(vals.ptr, cnt.ptr, out.ptr, wg, mode),
+                             args)
+            t.append(ms * 1e3 / args.steps)
+            if mode:
+                lib.check(L.g4_memcpy_d2h(got.ctypes.data, out.ptr, 4))
+                want = float(np.sum(np.arange(16 * wg, dtype=np.float64)))
+                assert abs(float(got[0]) - want) <= 1e-6 * want, (got, want)   # every value seen
+        hand[f"{wg}wg"] = {"plain_us": round(t[0], 3), "fenced_us": round(t[1], 3), "atomic_us": round(t[2], 3),
+                           "cost_fenced_us": round(t[1] - t[0], 3), "cost_atomic_us": round(t[2] - t[0], 3)}
     big = reads["551.6MB (LM head Q6_K 262144x2560)"]
     return {"value": big["GB_s"], "unit": "GB/s", "higher_is_better": True,
             "ms_per_step": big["us"] / 1e3, "dtype": "f32",

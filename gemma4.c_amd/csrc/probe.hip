@@ -36,30 +36,54 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const float4* __restric
     if (threadIdx.x == 0) sink[blockIdx.x] = acc;
 }
 
-// every workgroup writes one value, makes it visible device-wide (release)
-// and counts itself in; the workgroup that arrives last (acquire) adds the
-// values and resets the counter for the next launch: the in-kernel
-// alternative to a second launch.  handoff = 0: the same kernel without the
-// release, the counter and the last workgroup's pass (the baseline).
-__global__ __launch_bounds__(64) void probe_handoff_kernel(float* __restrict__ vals, unsigned int* __restrict__ count,
-                                                           float* __restrict__ out, int handoff) {
-    __shared__ bool last;
-    if (threadIdx.x == 0) vals[blockIdx.x] = (float)blockIdx.x;
-    if (!handoff) return;
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const unsigned int t = atomicAdd(count, 1u);
-        last = t == gridDim.x - 1;
+// every workgroup writes kHandVals values and counts itself in; the one
+// that arrives last reads every value (all its loads issued at once) and
+// resets the counter for the next launch: the in-kernel alternative to a
+// second launch.  mode 0: the stores only (the baseline); 1: plain stores,
+// a device-scope release fence before the count and an acquire after it;
+// 2: the values stored and read as device-scope relaxed atomics (coherent
+// without the L2 write-back of a release fence), the count issued once the
+// stores have completed.
+constexpr int kHandVals = 16;
+constexpr int kHandMaxPerThread = 40;   // 640 workgroups x 16 values over 256 threads
+__global__ __launch_bounds__(256) void probe_handoff_kernel(float* __restrict__ vals, unsigned int* __restrict__ count,
+                                                            float* __restrict__ out, int mode) {
+    __shared__ int last;
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const float v = (float)(blockIdx.x * kHandVals + tid);
+    float* const dst = vals + blockIdx.x * kHandVals + tid;
+    if (mode == 2) {
+        if (tid < kHandVals) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (tid < kHandVals) {
+        *dst = v;
+    }
+    if (mode == 0) return;
+    if (mode == 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        if (mode == 1) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
+    if (mode == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int n = gridDim.x * kHandVals;
+    float x[kHandMaxPerThread];
+#pragma unroll
+    for (int j = 0; j < kHandMaxPerThread; j++) {
+        const int i = min(tid + 256 * j, n - 1);
+        x[j] = mode == 2 ? __hip_atomic_load(vals + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : vals[i];
+    }
     float s = 0.0f;
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += 64) s += __hip_atomic_load(vals + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int j = 0; j < kHandMaxPerThread; j++) s += tid + 256 * j < n ? x[j] : 0.0f;
     s = wave_sum(s);
-    if (threadIdx.x == 0) {
-        *out = s;
-        atomicExch(count, 0u);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        *out = (red[0] + red[1]) + (red[2] + red[3]);
+        __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -82,8 +106,10 @@ extern "C" int g4_probe_read(const void* p, size_t bytes, float* sink, int workg
     return g4_check_launch("probe_read_kernel");
 }
 
-extern "C" int g4_probe_handoff(float* vals, unsigned int* count, float* out, int workgroups, int handoff) {
-    G4_CHECK_ARG(vals && count && out && workgroups > 0, "g4_probe_handoff: bad arguments");
-    hipLaunchKernelGGL(probe_handoff_kernel, dim3(workgroups), dim3(64), 0, g4_stream(), vals, count, out, handoff);
+extern "C" int g4_probe_handoff(float* vals, unsigned int* count, float* out, int workgroups, int mode) {
+    G4_CHECK_ARG(vals && count && out && workgroups > 0 && workgroups * kHandVals <= 256 * kHandMaxPerThread &&
+                     mode >= 0 && mode <= 2,
+                 "g4_probe_handoff: bad arguments (workgroups %d, mode %d)", workgroups, mode);
+    hipLaunchKernelGGL(probe_handoff_kernel, dim3(workgroups), dim3(256), 0, g4_stream(), vals, count, out, mode);
     return g4_check_launch("probe_handoff_kernel");
 }

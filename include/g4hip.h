@@ -498,11 +498,14 @@ int g4_probe_empty(int workgroups);
  * per wave instruction over `workgroups` 256-thread workgroups; sink gets one
  * float per workgroup */
 int g4_probe_read(const void *p, size_t bytes, float *sink, int workgroups);
-/* every workgroup stores a value; with handoff, each then releases it
- * device-wide and counts itself in on *count (zero before the first launch;
- * the last workgroup resets it) and the last one acquires and adds them into
- * *out.  handoff = 0 is the same launch without the hand-off. */
-int g4_probe_handoff(float *vals, unsigned int *count, float *out, int workgroups, int handoff);
+/* every 256-thread workgroup stores 16 values (vals: 16 per workgroup,
+ * workgroups <= 640); mode 1: each then releases them device-wide (fence)
+ * and counts itself in on *count (zero before the first launch; the last
+ * workgroup resets it), and the last one acquires, loads every value at once
+ * and adds them into *out; mode 2: the same with the values stored and
+ * loaded as device-scope relaxed atomics and no fences; mode 0: the stores
+ * only. */
+int g4_probe_handoff(float *vals, unsigned int *count, float *out, int workgroups, int mode);
 
 #ifdef __cplusplus
 }
