@@ -10,30 +10,29 @@
 // token's activations (no split over tokens or K that depends on the batch),
 // so a prompt gives the same bits in any chunking.
 //
-// Q4_K / Q5_K (mm_batch_kq32_kernel).  The reference's dot per block is
+// Q4_K / Q5_K (mm_batch_kq8_kernel).  The reference's dot per block is
 //   y.d * d * sum_j sc_j * sum_e q_e * q8_e  -  y.d * dmin * sum_j m_j * bs_j
 // (vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K, main.c:476-529, 531-593; bs_j =
-// the two 16-element bsums of sub-block j).  The first sum, S_b, runs on
-// v_mfma_f32_32x32x16_f16 with the sub-block scale folded into the weight
-// operand: sc * q <= 63 * 31 is an integer below 2048 and |q8| <= 128, so
-// every product is exact.  A whole block can reach |S_b| = 256 * 63 * 15 *
-// 128 (Q4_K, 3.1e7) or 256 * 63 * 31 * 128 (Q5_K, 6.4e7), past 2^24, so the
-// sixteen 16-long K steps are chained in pieces whose partial sums cannot
-// leave the exact range (kChainSteps: Q4_K 8 steps = 128 products, at most
-// 1.55e7; Q5_K 4 steps = 64 products, at most 1.60e7): every chain is an
-// exact integer whatever order the matrix core adds in.  Q4_K's two chains
-// are added in fp32 (both exact, so the sum is the exact S_b rounded once,
-// the same value as the int32 sum converted); Q5_K's four are converted and
-// added as int32.  The min sum M_b (|M_b| <= 16 * 63 * 2048, exact) is two
-// 8-long MFMAs, and the block is folded into the fp32 accumulator with three
-// VALU operations per output.  MODE 2 stores the int32 S_b and M_b of every
-// (token, row, block) instead (g4_debug_batch_block_sums).  The weights are the B
-// operand, so a lane's outputs share one weight row and its d, dmin and
-// scales come from the block header the lane loads itself.  Work split: a
-// 256-thread workgroup owns 128 weight rows (32 per wave) x 32 NT tokens;
-// per block it stages its tokens' activations in LDS as fp16 in the MFMA K
-// order, and each wave builds its weight operands (codes * scale as fp16) in
-// registers from 64 contiguous bytes per lane, loaded one block ahead.
+// the two 16-element bsums of sub-block j).  The inner sums run on the int8
+// matrix cores, v_mfma_i32_32x32x32_i8, one product per sub-block (K = its
+// 32 codes: the 4/5-bit q against the int8 q8), exact in int32; the 6-bit
+// sub-block scale cannot ride in an int8 operand (sc * q reaches 1953), so
+// S_b = sum_j sc_j * acc_j is formed in int32 (|S_b| <= 256 * 63 * 31 * 128
+// = 6.4e7).  The min sum M_b (|M_b| <= 16 * 63 * 2048, exact) is two
+// v_mfma_f32_32x32x8_f16 on the bsums and mins, and the block is folded into
+// the fp32 accumulator with three VALU operations per output:
+// fma(y.d, fma(d, S_b, -(dmin * M_b)), acc).  MODE 2 stores the int32 S_b
+// and M_b of every (token, row, block) instead (g4_debug_batch_block_sums).
+// The weights are the B operand, so a lane's outputs share one weight row
+// and its d, dmin and scales come from the block header the lane loads
+// itself.  Work split: a workgroup of 4 or 5 waves owns 32 weight rows per
+// wave x 32 tokens; per block it stages its tokens' Q8_K codes in LDS as
+// they are, each sub-block's 32 positions contiguous, and each wave builds
+// its weight operands (nibbles as bytes) in registers from 64 contiguous
+// bytes per lane, loaded one block ahead.  Against the same kernel on the
+// fp16 matrix cores (codes * scale as fp16, chained in exact pieces): the
+// same bits, Q4_K 4-12 % and Q5_K 11-25 % less time at the E4B prompt
+// shapes (511 tokens).
 //
 // Q6_K (mm_batch_q6s_kernel).  The reference dequantizes each weight to
 // d * sc * (q - 32) in fp32 (exact: 11 + 7 + 5 significant bits) and
@@ -79,14 +78,6 @@ __device__ __forceinline__ uint2 i8x4_to_h4(uint32_t w) {
     const h2_t c = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const h2_t lo = bits_h2(__builtin_amdgcn_perm(kMagic, u, kSelLo)) + c;
     const h2_t hi = bits_h2(__builtin_amdgcn_perm(kMagic, u, kSelHi)) + c;
-    return make_uint2(h2_bits(lo), h2_bits(hi));
-}
-
-// four codes c (one per byte, < 256) -> four fp16 c * s, exactly:
-// fma(1024 + c, s, -1024 s) is c * s (an integer < 2048) before rounding
-__device__ __forceinline__ uint2 codes_to_h4(uint32_t c, h2_t s, h2_t ns) {
-    const h2_t lo = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(kMagic, c, kSelLo)), s, ns);
-    const h2_t hi = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(kMagic, c, kSelHi)), s, ns);
     return make_uint2(h2_bits(lo), h2_bits(hi));
 }
 
@@ -192,24 +183,33 @@ __device__ __forceinline__ void store_block_sums(int32_t* So, int32_t* Mo, const
     }
 }
 
+// ---- Q4_K / Q5_K on the int8 matrix cores (mm_batch_kq8_kernel) ----------
+// Lane (i, kg) of a wave owns weight row 32 w + i and, in every sub-block,
+// positions 16 kg .. 16 kg + 15: of the device qs plane it loads words
+// 16 kg .. 16 kg + 15 of the block (bytes 16 kg .. 16 kg + 15 of each 32-byte
+// chunk c, whose low nibbles are sub-block 2c and high nibbles 2c + 1), so
+// word q of chunk c gives positions 16 kg + 4q .. +3 of both sub-blocks.
+// The activations are staged per token with position p of sub-block j at
+// byte 32 j + p, so lane half kg's A operand is one 16-byte LDS read.
+constexpr int kKq8Tok = 272;   // LDS bytes per staged token: 256 codes + pad
+
 // MODE 0: the outputs.  MODE 1 (PB): one block per workgroup (blockIdx.y),
 // whose per-block term u (before the token's Q8_K d) is stored instead of
 // folded: out gets nb slices of m x d.  MODE 2 (DB): every block's int32 S_b
 // and M_b into S = o[0] and M = o[1], each [m][d][nb] (one segment).
 template <bool Q5, int NT, int NWV, int MODE = 0>
-__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq32_kernel(
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_kq8_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
     constexpr bool PB = MODE == 1, DB = MODE == 2;
-    constexpr int CS = kChainSteps<Q5>;
     constexpr int NTH = 64 * NWV;
     constexpr int TOK = 32 * NT;
-    constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;   // (token, Q8_K lane) units of 32 bytes per thread
-    constexpr int BQ = (TOK * 4 + NTH - 1) / NTH;    // 8-byte bsums quarters per thread
-    // two stages: block b + 1's activations are staged half-way through
-    // block b's products, so one barrier per block suffices
-    __shared__ __align__(16) uint8_t sA[2][TOK * kKqTok];
+    constexpr int UPT = (TOK * 8 + NTH - 1) / NTH;
+    constexpr int BQ = (TOK * 4 + NTH - 1) / NTH;
+    __shared__ __align__(16) uint8_t sA[2][TOK * kKq8Tok];
     __shared__ __align__(16) uint8_t sS[2][TOK * kKqBs];
     __shared__ __align__(16) float sD[2][TOK];
+    typedef int i4v_t __attribute__((ext_vector_type(4)));
+    typedef int i16v_t __attribute__((ext_vector_type(16)));
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = lane & 31, kg = lane >> 5;
@@ -227,21 +227,19 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     const int tokb = by * TOK;
     const size_t nblk = (size_t)d * nb;
     const size_t hdr_off = (Q5 ? 160 : 128) * nblk, qh_off = 128 * nblk;
-    const size_t q8row = ((size_t)nb * 292 + 63) & ~(size_t)63;   // q8_row_stride
+    const size_t q8row = ((size_t)nb * 292 + 63) & ~(size_t)63;
     const size_t rB = (size_t)min(row, d - 1) * nb;
 
     struct WRaw {
-        uint4 qs[4];     // device qs words 16kg .. 16kg+15 of the block
-        uint4 qh;        // Q5_K: qh bytes 16kg .. 16kg+15 (positions 4l..4l+3)
-        uint4 hdr;       // d, dmin, scales
+        uint4 qs[4];
+        uint4 qh;
+        uint4 hdr;
     };
     struct XRaw {
         uint4 a0[UPT], a1[UPT];
         uint2 bs[BQ];
         float yd;
     };
-    // buffer loads: a per-lane 32-bit offset fixed for the kernel and the
-    // block's offset in a scalar register (loads past the end read zero)
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(hdr_off + 16 * nblk), kBufWord3);
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q8, (short)0, (int)(m * q8row), kBufWord3);
@@ -264,9 +262,6 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         if (Q5) r.qh = buf_load16(rw, vqh, b * 32);
         r.hdr = buf_load16(rw, vhdr, b * 16);
     };
-    // unit u = tid + 256 j: token u >> 3, Q8_K device lane u & 7 (32 bytes:
-    // words (h, jj) = sub-block 2jj + h, positions 4l'..4l'+3); tokens past
-    // m repeat the last one (their outputs are not stored)
     auto load_x = [&](int b, XRaw& r) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
@@ -277,20 +272,20 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < BQ; j++) r.bs[j] = buf_load8(rq, vbs[j], b * 32);
         r.yd = __uint_as_float(buf_load4(rq, vyd, b * 4));
     };
-    // unit (t, l'): for jj = 0..3 the K step s = 4 (l' & 3) + jj, group
-    // kg = l' >> 2 entry [cvt(word (0, jj)), cvt(word (1, jj))]
+    // unit (t, l'): device Q8_K words 8l' + 4h + jj hold sub-block 2jj + h,
+    // positions 4l' .. 4l'+3; staged at 32 (2jj + h) + 4l' of the token's row
     auto stage = [&](const XRaw& r, int st) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
             const int u = tid + j * NTH, lq = u & 7;
             if (UPT * NTH != TOK * 8 && u >= TOK * 8) continue;
-            uint8_t* dst = sA[st] + (u >> 3) * kKqTok + 128 * (lq & 3) + 16 * (lq >> 2);
-            const uint32_t a0[4] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w};
-            const uint32_t a1[4] = {r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
+            uint8_t* dst = sA[st] + (u >> 3) * kKq8Tok + 4 * lq;
+            const uint32_t wd[8] = {r.a0[j].x, r.a0[j].y, r.a0[j].z, r.a0[j].w,
+                                    r.a1[j].x, r.a1[j].y, r.a1[j].z, r.a1[j].w};
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const uint2 l = i8x4_to_h4(a0[jj]), hh = i8x4_to_h4(a1[jj]);
-                *reinterpret_cast<uint4*>(dst + 32 * jj) = make_uint4(l.x, l.y, hh.x, hh.y);
+            for (int k = 0; k < 8; k++) {   // k = 4h + jj
+                const int h = k >> 2, jj = k & 3;
+                *reinterpret_cast<uint32_t*>(dst + 32 * (2 * jj + h)) = wd[k];
             }
         }
 #pragma unroll
@@ -311,8 +306,12 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[nt][v] = 0.0f;
     f16v_t zero;
+    i16v_t izero;
 #pragma unroll
-    for (int v = 0; v < 16; v++) zero[v] = 0.0f;
+    for (int v = 0; v < 16; v++) {
+        zero[v] = 0.0f;
+        izero[v] = 0;
+    }
 
     // one block from stage st: after the barrier (block b's activations are
     // in st, and every wave is done with the other stage), the next block's
@@ -325,52 +324,38 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     auto block = [&](int b, int st, const WRaw& wc, WRaw& wnext) {
         lds_barrier();
         if (!PB) load_w(min(b + 1, nb - 1), wnext);
-
-        // scales of row i: sub-blocks 2j, 2j+1 as exact fp16 multipliers
         uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
         unpack_scales(wc.hdr.y, wc.hdr.z, wc.hdr.w, sc_lo, sc_hi, mn_lo, mn_hi);
-        h2_t SA[4], SB[4], NA[4], NB[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t scw = j < 2 ? sc_lo : sc_hi;
-            const int sh = 16 * (j & 1);
-            const _Float16 sa = (_Float16)(float)((scw >> sh) & 0xffu), sb = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
-            SA[j] = h2_t{sa, sa};
-            SB[j] = h2_t{sb, sb};
-            NA[j] = h2_t{(_Float16)(-1024.0f) * sa, (_Float16)(-1024.0f) * sa};
-            NB[j] = h2_t{(_Float16)(-1024.0f) * sb, (_Float16)(-1024.0f) * sb};
-        }
-
-        // S: the running chain; P: Q4_K's first chain; SI: Q5_K's int32 sum
-        f16v_t S[NT], P[NT];
         int SI[NT][16];
-        const uint8_t* at0 = sA[st] + i * kKqTok + 16 * kg;
+        const uint8_t* at0 = sA[st] + i * kKq8Tok + 16 * kg;
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-            if (!PB && s == 8 && b + 1 < b1) {
+        for (int sb = 0; sb < 8; sb++) {
+            if (!PB && sb == 4 && b + 1 < b1) {
                 stage(xn, st ^ 1);
                 load_x(min(b + 2, nb - 1), xn);
             }
-            const int j = s & 3;
-            const uint4 Q = wc.qs[s >> 2];
-            const uint32_t word = j == 0 ? Q.x : j == 1 ? Q.y : j == 2 ? Q.z : Q.w;
-            uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
-            if (Q5) {
-                const uint32_t hw = (s >> 2) == 0 ? wc.qh.x : (s >> 2) == 1 ? wc.qh.y : (s >> 2) == 2 ? wc.qh.z : wc.qh.w;
-                lo |= ((hw >> (2 * j)) & 0x01010101u) << 4;
-                hi |= ((hw >> (2 * j + 1)) & 0x01010101u) << 4;
+            const int c = sb >> 1, h = sb & 1;
+            uint32_t cw[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t word = c == 0 ? wc.qs[q].x : c == 1 ? wc.qs[q].y : c == 2 ? wc.qs[q].z : wc.qs[q].w;
+                uint32_t v = h ? (word >> 4) & 0x0f0f0f0fu : word & 0x0f0f0f0fu;
+                if (Q5) {
+                    const uint32_t hw = q == 0 ? wc.qh.x : q == 1 ? wc.qh.y : q == 2 ? wc.qh.z : wc.qh.w;
+                    v |= ((hw >> sb) & 0x01010101u) << 4;
+                }
+                cw[q] = v;
             }
-            const uint2 al = codes_to_h4(lo, SA[j], NA[j]), ah = codes_to_h4(hi, SB[j], NB[j]);
-            const h8_t B = __builtin_bit_cast(h8_t, make_uint4(al.x, al.y, ah.x, ah.y));
+            const i4v_t B = {(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+            const int scv = byte_of(sb < 4 ? sc_lo : sc_hi, sb & 3);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const h8_t A = *reinterpret_cast<const h8_t*>(at0 + 32 * nt * kKqTok + 32 * s);
-                S[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, s % CS == 0 ? zero : S[nt], 0, 0, 0);
-                chain_end<Q5>(s, S[nt], P[nt], SI[nt]);
+                const i4v_t A = *reinterpret_cast<const i4v_t*>(at0 + 32 * nt * kKq8Tok + 32 * sb);
+                const i16v_t Z = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, izero, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) SI[nt][v] = (sb == 0 ? 0 : SI[nt][v]) + __mul24(scv, Z[v]);
             }
         }
-        // min sums (bsums 4kg.. and 8+4kg..: sub-blocks 2kg, 2kg+1, 4+2kg,
-        // 5+2kg) and the block's scales
         const int msh = 16 * kg;
         const _Float16 m0 = (_Float16)(float)((mn_lo >> msh) & 0xffu), m1 = (_Float16)(float)((mn_lo >> (msh + 8)) & 0xffu);
         const _Float16 m4 = (_Float16)(float)((mn_hi >> msh) & 0xffu), m5 = (_Float16)(float)((mn_hi >> (msh + 8)) & 0xffu);
@@ -383,8 +368,16 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
             f16v_t M = __builtin_amdgcn_mfma_f32_32x32x8f16(A1, Bm1, zero, 0, 0, 0);
             M = __builtin_amdgcn_mfma_f32_32x32x8f16(A2, Bm2, M, 0, 0, 0);
             if (DB) {
-                store_block_sums<Q5>(reinterpret_cast<int32_t*>(sg.o[0]), reinterpret_cast<int32_t*>(sg.o[1]), S[nt],
-                                     P[nt], SI[nt], M, row, d, tokb + 32 * nt + 4 * kg, m, nb, b);
+                if (row < d) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int tok = tokb + 32 * nt + 8 * (v >> 2) + 4 * kg + (v & 3);
+                        if (tok >= m) continue;
+                        const size_t o = ((size_t)tok * d + row) * nb + b;
+                        reinterpret_cast<int32_t*>(sg.o[0])[o] = SI[nt][v];
+                        reinterpret_cast<int32_t*>(sg.o[1])[o] = (int)M[v];
+                    }
+                }
                 continue;
             }
 #pragma unroll
@@ -394,7 +387,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const int v = 4 * a + c;
-                    const float u = __builtin_fmaf(dx, chain_block_sum<Q5>(S[nt], P[nt], SI[nt], v), -(dmx * M[v]));
+                    const float u = __builtin_fmaf(dx, (float)SI[nt][v], -(dmx * M[v]));
                     acc[nt][v] = PB ? u : __builtin_fmaf(y4[c], u, acc[nt][v]);
                 }
             }
@@ -409,7 +402,6 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
         block(b, 0, w0, w1);
         if (b + 1 < b1) block(b + 1, 1, w1, w0);
     }
-
     if (!DB && row < d) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
@@ -421,38 +413,24 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
-template <bool Q5, int NT, int NWV>
-void launch_mm_batch32(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
+template <bool Q5, int NT, int NWV, int MODE = 0>
+void launch_mm_batch8(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
     const int gy = (m + 32 * NT - 1) / (32 * NT);
-    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, NT, NWV>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(), sg, q8,
-                       nb, m);
-}
-
-template <bool Q5>
-void launch_mm_batch32_blocks(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
-    const int gy = (m + 31) / 32;
-    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, 1>), dim3(sg.g0[sg.n] * gy, nb), dim3(256), 0, g4_stream(), sg,
-                       q8, nb, m);
-}
-
-template <bool Q5>
-void launch_mm_batch32_sums(const KqSegs& sg, const uint8_t* q8, int nb, int m) {
-    const int gy = (m + 31) / 32;
-    hipLaunchKernelGGL((mm_batch_kq32_kernel<Q5, 1, 4, 2>), dim3(sg.g0[sg.n] * gy), dim3(256), 0, g4_stream(), sg, q8, nb,
-                       m);
+    hipLaunchKernelGGL((mm_batch_kq8_kernel<Q5, NT, NWV, MODE>), dim3(sg.g0[sg.n] * gy), dim3(64 * NWV), 0, g4_stream(),
+                       sg, q8, nb, m);
 }
 
 // ---- Q4_K / Q5_K through fp16 weight images (mm_batch_img_kernel) --------
-// The in-register weight decode of mm_batch_kq32_kernel (nibbles, Q5_K high
-// bits, scale multiply, fp16 packing) is most of its vector instructions and
-// sets its pace.  An image does that decode once per matrix, when the model
+// The in-register weight decode of a quantized-tensor kernel (nibbles, Q5_K
+// high bits, the scales) is most of its vector instructions and sets its
+// pace.  An image does that decode once per matrix, when the model
 // is loaded: every weight's sc * q (the 6-bit sub-block scale times the
 // 4/5-bit code, an integer <= 63 * 31, exact in fp16) stored as the B operand
 // of v_mfma_f32_32x32x16_f16, plus per row and block d, dmin and the mins.
-// The block sums are the same integers, chained in the same exact pieces as
-// in mm_batch_kq32_kernel (kChainSteps: Q4_K two chains, Q5_K four, so the
-// K order inside the matrix cores does not matter), and the fold the same
-// three fp32 steps, so the outputs are mm_batch_kq32_kernel's bits; the
+// The block sums are the same integers, chained in exact pieces (kChainSteps:
+// Q4_K two chains of 128 products, Q5_K four of 64, each below 2^24 whatever
+// order the matrix core adds in), and the fold the same three fp32 steps, so
+// the outputs are mm_batch_kq8_kernel's bits; the
 // kernel's loop is MFMAs, LDS reads of the activations and the block fold.
 // The image does not record its type: the caller names it (Q5_K needs the
 // shorter chains).
@@ -518,7 +496,7 @@ __global__ __launch_bounds__(256) void kq_image_kernel(const uint8_t* __restrict
 }
 
 // NWV waves of 32 rows (one image row group each) x 32 NT tokens per
-// workgroup; segments as in mm_batch_kq32_kernel, in units of 32 NWV rows
+// workgroup; segments as in mm_batch_kq8_kernel, in units of 32 NWV rows
 // LDS slot (16 bytes) of step s, lane half kg inside a token's row: the two
 // halves of a step 128 bytes apart, so that the lanes (i, 0) and (i, 1) of
 // one 128-bit read fall in different banks (2 s + kg, the plain order, had
@@ -526,7 +504,7 @@ __global__ __launch_bounds__(256) void kq_image_kernel(const uint8_t* __restrict
 __device__ __forceinline__ int img_slot(int s, int kg) { return (s & 7) + 8 * kg + 16 * (s >> 3); }
 
 // MODE 0: the outputs; MODE 2: every block's int32 S_b and M_b, as
-// mm_batch_kq32_kernel's MODE 2
+// mm_batch_kq8_kernel's MODE 2
 template <bool Q5, int NT, int NWV, int MODE = 0>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) void mm_batch_img_kernel(
     const KqSegs sg, const uint8_t* __restrict__ q8, int nb, int m) {
@@ -1390,13 +1368,13 @@ extern "C" int g4_mm_batch_q8_multi(float* const* o, const void* const* w, const
     sg.g0[nseg] = (int)gx;
     G4_CHECK_ARG(gx * ((m + 32 * kKqNT - 1) / (32 * kKqNT)) < (1LL << 31), "g4_mm_batch_q8: %d tokens too many", m);
     if (type == G4_Q4_K) {
-        if (nwv == 5) launch_mm_batch32<false, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
-        else launch_mm_batch32<false, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
+        if (nwv == 5) launch_mm_batch8<false, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
+        else launch_mm_batch8<false, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
     } else {
-        if (nwv == 5) launch_mm_batch32<true, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
-        else launch_mm_batch32<true, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
+        if (nwv == 5) launch_mm_batch8<true, kKqNT, 5>(sg, (const uint8_t*)q8, nb, m);
+        else launch_mm_batch8<true, kKqNT, 4>(sg, (const uint8_t*)q8, nb, m);
     }
-    return g4_check_launch("mm_batch_kq32_kernel");
+    return g4_check_launch("mm_batch_kq8_kernel");
 }
 
 extern "C" int g4_mm_batch_q8(float* o, const void* w, const void* q8, int n, int d, int m, int type) {
@@ -1419,9 +1397,14 @@ extern "C" int g4_mm_batch_q8_blocks(float* u, const void* w, const void* q8, in
     sg.g0[0] = 0;
     sg.g0[1] = (d + 127) / 128;
     G4_CHECK_ARG((long long)sg.g0[1] * ((m + 31) / 32) < (1LL << 31), "g4_mm_batch_q8_blocks: %d tokens too many", m);
-    if (type == G4_Q4_K) launch_mm_batch32_blocks<false>(sg, (const uint8_t*)q8, nb, m);
-    else launch_mm_batch32_blocks<true>(sg, (const uint8_t*)q8, nb, m);
-    return g4_check_launch("mm_batch_kq32_kernel (per block)");
+    const int gy = (m + 31) / 32;
+    if (type == G4_Q4_K)
+        hipLaunchKernelGGL((mm_batch_kq8_kernel<false, 1, 4, 1>), dim3(sg.g0[1] * gy, nb), dim3(256), 0, g4_stream(), sg,
+                           (const uint8_t*)q8, nb, m);
+    else
+        hipLaunchKernelGGL((mm_batch_kq8_kernel<true, 1, 4, 1>), dim3(sg.g0[1] * gy, nb), dim3(256), 0, g4_stream(), sg,
+                           (const uint8_t*)q8, nb, m);
+    return g4_check_launch("mm_batch_kq8_kernel (per block)");
 }
 
 extern "C" size_t g4_kq_image_bytes(int n, int d) {
@@ -1531,7 +1514,7 @@ extern "C" int g4_mm_batch_img_tile(float* o, const void* img, const void* q8, i
 }
 
 // every block's int32 S_b and M_b as the batched kernels form them: S and M
-// are [m][d][n/256]; image 0: the quantized tensor w (mm_batch_kq32_kernel),
+// are [m][d][n/256]; image 0: the quantized tensor w (mm_batch_kq8_kernel),
 // 1: its fp16 image (mm_batch_img_kernel, one-wave row groups of 32 tokens)
 extern "C" int g4_debug_batch_block_sums(const void* w, int image, int n, int d, int m, int type, const void* q8,
                                          int32_t* S, int32_t* M) {
@@ -1554,9 +1537,9 @@ extern "C" int g4_debug_batch_block_sums(const void* w, int image, int n, int d,
     const uint8_t* q = (const uint8_t*)q8;
     if (!image) {
         sg.g0[1] = (d + 127) / 128;
-        if (type == G4_Q4_K) launch_mm_batch32_sums<false>(sg, q, nb, m);
-        else launch_mm_batch32_sums<true>(sg, q, nb, m);
-        return g4_check_launch("mm_batch_kq32_kernel (block sums)");
+        if (type == G4_Q4_K) launch_mm_batch8<false, 1, 4, 2>(sg, q, nb, m);
+        else launch_mm_batch8<true, 1, 4, 2>(sg, q, nb, m);
+        return g4_check_launch("mm_batch_kq8_kernel (block sums)");
     }
     sg.g0[1] = (d + 127) / 128;
     if (type == G4_Q4_K) launch_mm_batch_img<false, 1, 4, 2>(sg, q, nb, m);

@@ -188,11 +188,10 @@ size_t g4_q8K_row_stride(int k);
 int g4_quantize_rows_q8_K(const float *x, void *y, int k, int m);
 /* o[t*d + r] = mm_quant_dot_rows row r on Q8_K row t (main.c:1558-1566,
  * vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K main.c:476-593), t < m, r < d:
- * the same integer block sums and scales on the fp16 matrix cores (every
- * S_b, M_b exact: chains of at most 128 (Q4_K) / 64 (Q5_K) products, added
- * as integers), the fp32 fold in another order (within 1e-5 of sum |terms|
- * of the per-token dot).  Q4_K / Q5_K only (others: G4_ERR_TYPE); o, w, q8
- * 16-byte aligned. */
+ * the same integer block sums and scales, the code sums on the int8 matrix
+ * cores (every S_b, M_b exact in int32), the fp32 fold in another order
+ * (within 1e-5 of sum |terms| of the per-token dot).  Q4_K / Q5_K only
+ * (others: G4_ERR_TYPE); o, w, q8 16-byte aligned. */
 int g4_mm_batch_q8(float *o, const void *w, const void *q8, int n, int d, int m, int type);
 /* g4_mm_batch_q8 for nseg (1..4) matrices of one type over the same Q8_K
  * rows in one launch (gate and up, Q and K): o[k][t*d[k] + r] for matrix

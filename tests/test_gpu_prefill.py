@@ -580,7 +580,7 @@ def test_batch_block_sums_exact_saturated(lib, orc, qtype):
             eS[t, r], eM[t, r] = kq.kquant_block_sums(raw[r].reshape(-1, bsz), qtype, q8s[t])
     big = np.abs(eS) > (1 << 24)
     assert big.sum() > 1000 and np.abs(eS).max() >= (30_000_000 if qtype == 12 else 60_000_000)
-    for image in (0, 1):
+    for image in (0, 1):   # 0: the int8 matrix-core kernel on w; 1: the fp16 image kernel
         src = _image(lib, w, qtype, n, d) if image else w
         S, M = DBuf(lib, 4 * m * d * nb), DBuf(lib, 4 * m * d * nb)
         lib.g4_debug_batch_block_sums(src.ptr, image, n, d, m, qtype, q8.ptr, S.ptr, M.ptr)
@@ -602,3 +602,28 @@ def test_batch_block_sums_exact_saturated(lib, orc, qtype):
         out = DBuf(lib, 4 * m * d)
         lib.g4_mm_batch_img_tile(out.ptr, img.ptr, q8.ptr, n, d, m, qtype, nt, nwv)
         assert np.array_equal(out.to_array(np.float32).reshape(m, d).view(np.uint32), got.view(np.uint32)), (nt, nwv)
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+@pytest.mark.parametrize("n,d,m", [(2560, 2048, 511), (2560, 10240, 511), (2560, 256, 511), (2048, 2560, 511),
+                                   (2560, 2560, 1), (512, 100, 33), (256, 40, 5), (4096, 520, 64)])
+def test_mm_batch_q8_int8_equals_fp16_image(lib, orc, qtype, n, d, m):
+    """The quantized-tensor GEMM (int8 matrix cores: one v_mfma_i32_32x32x32_i8
+    per sub-block, scales applied in int32) and the fp16 image GEMM (sc * q
+    folded into fp16 operands, chained in exact pieces) form the same integer
+    block sums and the same fold: the same bits at the E4B prompt shapes and
+    ragged ones, and sampled tokens meet the 1e-5 bar against the oracle's
+    per-token mm_quant_dot_rows."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(n + d + m + qtype)
+    raw = synth.rand_kquant(rng, qtype, d, n)
+    w = upload_quant(lib, raw, qtype, n, d)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    q8, _ = _q8rows(lib, DBuf.from_array(lib, x), n, m)
+    got = _mm_q8(lib, w, q8.ptr, n, d, m, qtype)
+    img = _image(lib, w, qtype, n, d)
+    oi = DBuf(lib, 4 * m * d)
+    lib.g4_mm_batch_img(oi.ptr, img.ptr, q8.ptr, n, d, m, qtype)
+    gi = oi.to_array(np.float32).reshape(m, d)
+    assert np.array_equal(gi.view(np.uint32), got.view(np.uint32)), np.argwhere(gi != got)[:8]
+    _check_q8(orc, raw, qtype, n, d, x, got, sorted({0, m // 2, m - 1}))
