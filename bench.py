@@ -334,7 +334,8 @@ def cpu_layer_baseline(raws, shapes, layer_bytes):
                       f"mm_quant_rows), median of {len(ts)} runs, OpenMP {thr} threads"}
 
 
-FP16_MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 matrix peak (the instruction the prefill GEMM issues)
+FP16_MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 matrix peak (the image and split-Q6_K prefill GEMMs)
+INT8_MFMA_PEAK_TOPS = 5000.0     # MI355X dense int8 matrix peak (the Q4_K/Q5_K prefill GEMM on the quantized tensors)
 
 # one E4B sliding-window layer's Q4_K matrices (rows d, inputs n): Q, K, O,
 # gate, up, PLE inp_gate, PLE proj
@@ -394,7 +395,7 @@ def bench_prefill(lib, g4, synth, args):
     res = {
         "value": round(m / per_step, 1), "unit": "tok/s (one layer's Q4_K GEMMs)", "higher_is_better": True,
         "ms_per_step": ms / args.steps,
-        "dtype": "u4 x int8 -> exact fp16 matrix products (gate/up: fp16 sc*q images), fp32 block combine",
+        "dtype": "u4 x int8 -> int32 matrix products (gate/up: fp16 sc*q images), fp32 block combine",
         "config": {"workload": "batched prefill GEMM: 512 tokens x one E4B SWA layer's Q4_K matrices "
                                "(Q|K 2048+512, O 2560<-2048, gate|up 2x10240 on images, PLE 256/2560) (seed 1)",
                    "tokens": m, "layer_tflops": round(ops / per_step / 1e12, 2)},
@@ -460,7 +461,8 @@ def bench_prefill_e2e(lib, g4, synth, args):
     name = "mm_batch_q6s_kernel<Q6_K> (V and FFN down of one 511-token chunk)"
     res = {
         "value": round(m / sec, 1), "unit": "tok/s", "higher_is_better": True, "ms_per_step": sec * 1e3,
-        "dtype": "u4/u5 x int8 exact fp16 matrix products (Q4_K/Q5_K), split-fp16 matrix products (Q6_K), "
+        "dtype": "u4/u5 x int8 -> int32 matrix products (Q4_K/Q5_K; gate/up on fp16 sc*q images), split-fp16 "
+                 "matrix products (Q6_K), "
                  "fp32 matrix products (bf16), fp32 glue",
         "config": {"workload": "synthetic E4B-shape batched prefill (42 layers, hidden 2560, FFN 10240, 8q/2kv heads, "
                                "head_dim 256/512, window 512, Q4_K_M mix, seed 4): 511 prompt tokens in one chunk",
@@ -820,13 +822,22 @@ def bench_decode(lib, g4, synth, args):
     }
     # matrix-core use of the batched prefill: algorithmic GEMM flops of the
     # 511 tokens over the prefill's wall time, and the share of that time the
-    # issued matrix-core work would take at its instructions' peaks (fp16
-    # MFMA for the K-quant GEMMs: one issued flop per flop for Q4_K/Q5_K,
-    # three for the split Q6_K; fp32 MFMA for the bf16 PLE projection)
+    # issued matrix-core work would take at its instructions' peaks: int8
+    # MFMA for the Q4_K/Q5_K GEMMs on the quantized tensors (one issued op
+    # per op), fp16 MFMA for the FFN gate/up on their fp16 images (one per
+    # flop) and for the split Q6_K (three per flop), fp32 MFMA for the bf16
+    # PLE projection
     mm = synth.prefill_matmuls(synth.E4B)
     flops = sum(2.0 * n * d for _, _, n, d in mm) * (n_prompt - 1)
-    issued_s = sum(2.0 * n * d * (n_prompt - 1) * (3 if t == g4.Q6_K else 1) /
-                   ((FP32_MFMA_PEAK_TFLOPS if t == synth.BF16 else FP16_MFMA_PEAK_TFLOPS) * 1e12) for _, t, n, d in mm)
+
+    def peak(name, t):
+        if t == synth.BF16:
+            return FP32_MFMA_PEAK_TFLOPS
+        if t in (g4.Q4_K, g4.Q5_K) and not name.endswith(("ffn_gate.weight", "ffn_up.weight")):
+            return INT8_MFMA_PEAK_TOPS
+        return FP16_MFMA_PEAK_TFLOPS
+    issued_s = sum(2.0 * n * d * (n_prompt - 1) * (3 if t == g4.Q6_K else 1) / (peak(nm, t) * 1e12)
+                   for nm, t, n, d in mm)
     res["config"]["prefill_gemm_tflops"] = round(flops / t_prefill / 1e12, 1)
     res["config"]["prefill_mfma_util"] = round(issued_s / t_prefill, 4)
     _log("dominant-kernel roofline")
