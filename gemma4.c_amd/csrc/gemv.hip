@@ -286,8 +286,10 @@ __device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, cons
     (void)row_;
 }
 
-// PRO 1: residual prologue (ra, st); PRO 2: attention merge prologue (mg)
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0>
+// PRO 1: residual prologue (ra, st); PRO 2: attention merge prologue (mg).
+// LG: the lane groups of a row hand their block values to group 0 through
+// LDS (one write and one read per block) instead of lane shuffles.
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0, bool LG = false>
 __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
                                                            const uint8_t* q8, float* __restrict__ out,
@@ -554,6 +556,35 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             }
         }
         if (DBG) return;
+        if constexpr (LG && SPLIT > 1 && NB > 0) {
+            // a row's SPLIT groups lie in one wave (GL divides 64), whose LDS
+            // operations complete in order: no barrier between the writes
+            // and group 0's reads, which run the fp32 steps in block order
+            constexpr int RW = WG / GL;
+            static_assert(64 % GL == 0, "a row's lane groups must share a wave");
+            __shared__ uint4 gth[RW][NMAT][NB][8];
+            const int rw = tid / GL;
+#pragma unroll
+            for (int i = 0; i < NH; i++) {
+                const int b = grp * NH + i;
+                if (b < NB) {
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++)
+                        gth[rw][m][b][l] = make_uint4((uint32_t)S[m][i], (uint32_t)P[m][i], __float_as_uint(D[m][i]),
+                                                      __float_as_uint(DM[m][i]));
+                }
+            }
+            if (grp == 0) {
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const uint4 e = gth[rw][m][b][l];
+                        step(m, (int32_t)e.x, (int32_t)e.y, __uint_as_float(e.z), __uint_as_float(e.w));
+                    }
+                }
+            }
+        } else {
 #pragma unroll
         for (int gs = 0; gs < SPLIT; gs++) {
 #pragma unroll
@@ -573,6 +604,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
                     }
                 }
             }
+        }
         }
     } else {
         for (int b = 0; b < nb; b++) {
@@ -1104,7 +1136,7 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
 
 // residual step + norm + Q8_K as the prologue of every workgroup (64 NB
 // threads: one wave per Q8_K block, each wave 8/SPLIT rows)
-template <bool Q5, int NMAT, int NB, int SPLIT>
+template <bool Q5, int NMAT, int NB, int SPLIT, bool LG = false>
 void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                       const Stack2& st) {
     constexpr int WG = 64 * NB;
@@ -1115,20 +1147,21 @@ void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const floa
                        (size_t)WG / 8 * 4;
     const int r6 = q6_pro_rows(WG, SPLIT);
     const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + r6 - 1) / r6 : 0);
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, 1>),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, 1, LG>),
                        dim3(wgs), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
                        (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st,
                        MergeArgs{});
 }
 
 // attention merge + Q8_K as the prologue of every workgroup (64 NB threads:
-// wave h merges head h), then the GEMV with 32 lanes per row
+// wave h merges head h), then the GEMV with 32 lanes per row (the lane
+// groups' block values gathered through LDS)
 template <bool Q5, int NB>
 void launch_q45_merge(const void* w, float* o, int d, const MergeArgs& mg) {
     constexpr int WG = 64 * NB, SPLIT = 4;
     constexpr int rows_per_wg = WG / (8 * SPLIT);
     const size_t lds = ((size_t)NB * 292 + 15) & ~(size_t)15;
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, 1, false, NB, SPLIT, false, WG, 2>),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, 1, false, NB, SPLIT, false, WG, 2, true>),
                        dim3((d + rows_per_wg - 1) / rows_per_wg), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
                        nullptr, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, nullptr, ResidualArgs{},
                        Stack2{}, mg);
@@ -1141,12 +1174,14 @@ void launch_q45_merge(const void* w, float* o, int d, const MergeArgs& mg) {
 // 16 lanes per row (four times fewer workgroups, each CU's SIMDs holding 2.5
 // waves of the work) and 8.0 / 6.4 us for the 256-thread form before it;
 // 64 lanes per row measured the same as 32 for the PLE gate and 8.4 us for
-// Q|K|V.
+// Q|K|V.  With 32 lanes per row the four lane groups hand their block values
+// to group 0 through LDS: decode step 2.214 against 2.227 ms with lane
+// shuffles (64 lanes per row: 2.257 with LDS, 2.281 with shuffles).
 template <bool Q5, int NMAT, int NB>
 void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                     const Stack2& st) {
     if constexpr (NMAT == 2 || NB > 10) launch_q45_pro_s<Q5, NMAT, NB, 8>(w, w2, o, d, aux, ra, st);
-    else launch_q45_pro_s<Q5, NMAT, NB, 4>(w, w2, o, d, aux, ra, st);
+    else launch_q45_pro_s<Q5, NMAT, NB, 4, true>(w, w2, o, d, aux, ra, st);
 }
 
 template <bool Q5, int NB>

@@ -392,6 +392,52 @@ def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
     assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), np.flatnonzero(g != r)[:8]
 
 
+@pytest.mark.parametrize("cancel", [0.0, 0.9, 0.999])
+def test_residual_step_norms_when_the_step_cancels(lib, orc, cancel):
+    """The two norms of a residual step (post_norm + residual + out_scale,
+    then the next attn_norm, main.c:1995-2003, 1878) when the step cancels
+    most of x: inputs with x = -cancel * (y s_y) w + noise drive x' toward
+    zero, and the normed vector must stay within 4e-6 of the float64 RMSNorm
+    of the x' the kernel itself stored (its second sum of squares is that of
+    x', not of x and the step), in the single-workgroup step and in the GEMV
+    prologue, which give the same bits."""
+    from g4 import DBuf, upload_quant
+    n, d = 2560, 256
+    rng = np.random.default_rng(int(cancel * 1000) + 5)
+    y = (rng.standard_normal(n) * 4).astype(np.float32)
+    wp = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    wn = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    sy = 1.0 / np.sqrt(np.mean(y.astype(np.float64) ** 2) + 1e-6)
+    x = (-cancel * (y * sy) * wp + 0.01 * rng.standard_normal(n)).astype(np.float32)
+    osc = np.array([0.9], np.float32)
+    xd, yd, wpd, wnd, od = (DBuf.from_array(lib, a) for a in (x, y, wp, wn, osc))
+    eps = C.c_float(1e-6)
+    raw = synth.rand_kquant(rng, 12, d, n)
+    w = upload_quant(lib, raw, 12, n, d)
+    outs = []
+    for form in ("step", "prologue"):
+        xo, xb2, q8 = DBuf(lib, 4 * n), DBuf(lib, 4 * n), DBuf(lib, lib.L.g4_q8K_bytes(n))
+        if form == "step":
+            x2 = DBuf.from_array(lib, x)
+            lib.g4_residual_norm(x2.ptr, yd.ptr, wpd.ptr, od.ptr, wnd.ptr, xb2.ptr, q8.ptr, 0, n, eps)
+            gx = x2.to_array(np.float32)
+        else:
+            out = DBuf(lib, 4 * d)
+            lib.g4_mm_residual_q8(out.ptr, w.ptr, None, n, d, 12, None, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, od.ptr,
+                                  wnd.ptr, xb2.ptr, q8.ptr, 0, eps)
+            gx = xo.to_array(np.float32)
+        gv = xb2.to_array(np.float32)
+        x64 = gx.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-6) * wn
+        assert rel_err(gv, want) < 4e-6, form
+        h = np.zeros(n // 256, Q8K_DTYPE)
+        lib.g4_download_q8K(q8.ptr, P(h), n)
+        assert h.tobytes() == orc.quantize_q8K(gv).tobytes()
+        outs.append((gx, gv))
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))
+
+
 def test_mm_residual_q8_rejects_alias(lib):
     from g4 import DBuf, G4Error
     b = DBuf(lib, 4 * 4096)
