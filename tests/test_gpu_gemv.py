@@ -390,6 +390,15 @@ def test_mm_residual_q8(lib, orc, qtype, n, d, mode):
         lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
     g, r = out.to_array(np.float32), ref.to_array(np.float32)
     assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), np.flatnonzero(g != r)[:8]
+    # and against the oracle: mm_quant_dot_rows on the stored Q8_K bit for bit,
+    # the GELU epilogues within 1e-6 of the oracle's gelu (device tanhf)
+    dot = orc.mm_quant_dot_rows(raw, n, d, qtype, h)
+    if mode in ("ffn", "ple"):
+        other = orc.mm_quant_dot_rows(up_raw, n, d, qtype, h) if mode == "ffn" else mul
+        want = np.array([orc.L.or_gelu(C.c_float(v)) for v in dot], np.float32) * other
+        assert rel_err(g, want) < 1e-6
+    else:
+        assert np.array_equal(g.view(np.uint32), dot.view(np.uint32))
 
 
 @pytest.mark.parametrize("cancel", [0.0, 0.9, 0.999])
@@ -448,8 +457,9 @@ def test_mm_residual_q8_rejects_alias(lib):
 
 @pytest.mark.parametrize("qtype,d1,d2", [(12, 2048, 512), (13, 200, 70), (12, 4096, 1024)])
 def test_mm_residual_q8_pair(lib, orc, qtype, d1, d2):
-    """Two GEMVs stacked in one prologue launch (Q and K): each output equal,
-    bit for bit, to mm_quant_dot_rows on the stored Q8_K."""
+    """Two GEMVs stacked in one prologue launch (Q and K): the stored Q8_K is
+    quantize_row_q8_K of the stored normed vector, and each output equals,
+    bit for bit, the GPU's and the oracle's mm_quant_dot_rows on it."""
     from g4 import DBuf, upload_quant
     n = 2560
     rng = np.random.default_rng(d1 + d2 + qtype)
@@ -465,19 +475,25 @@ def test_mm_residual_q8_pair(lib, orc, qtype, d1, d2):
     lib.g4_mm_residual_q8_pair(o1.ptr, w1.ptr, d1, o2.ptr, w2.ptr, d2, n, qtype, xd.ptr, xo.ptr, yd.ptr, wpd.ptr, None,
                                wnd.ptr, xb2.ptr, q8.ptr, 0, C.c_float(1e-6))
     assert rel_err(xo.to_array(np.float32), x + orc.rmsnorm(y, wp)) < 2e-6
-    for o, w, d in ((o1, w1, d1), (o2, w2, d2)):
+    h = np.zeros(n // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(xb2.to_array(np.float32)).tobytes()
+    for o, w, d, raw in ((o1, w1, d1, r1), (o2, w2, d2, r2)):
         ref = DBuf(lib, 4 * d)
         lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
         g, r = o.to_array(np.float32), ref.to_array(np.float32)
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (d, np.flatnonzero(g != r)[:8])
+        want = orc.mm_quant_dot_rows(raw, n, d, qtype, h)
+        assert np.array_equal(g.view(np.uint32), want.view(np.uint32)), (d, np.flatnonzero(g != want)[:8])
 
 
 @pytest.mark.parametrize("qtype,d1,d2,d3", [(12, 2048, 512, 512), (13, 200, 70, 90), (12, 4096, 1024, 1024)])
 def test_mm_residual_q8_qkv(lib, orc, qtype, d1, d2, d3):
     """Q, K (K-quant, stacked) and V (Q6_K on the fp32 normed vector) in one
-    prologue launch: Q and K bit-exact against mm_quant_dot_rows on the stored
-    Q8_K; V against the oracle's mm_quant_rows on the stored normed vector
-    to 1e-5 of sum |w*x|."""
+    prologue launch: Q and K bit-exact against the GPU's and the oracle's
+    mm_quant_dot_rows on the stored Q8_K (itself quantize_row_q8_K of the
+    stored normed vector); V against the oracle's mm_quant_rows on the stored
+    normed vector to 1e-5 of sum |w*x|."""
     from g4 import DBuf, upload_quant
     n = 2560
     rng = np.random.default_rng(d1 + d2 + d3 + qtype)
@@ -499,11 +515,16 @@ def test_mm_residual_q8_qkv(lib, orc, qtype, d1, d2, d3):
     assert rel_err(xo.to_array(np.float32), want_x) < 2e-6
     xb = xb2.to_array(np.float32)
     assert rel_err(xb, orc.rmsnorm(want_x, wn)) < 4e-6
-    for o, w, d in ((o1, w1, d1), (o2, w2, d2)):
+    h = np.zeros(n // 256, Q8K_DTYPE)
+    lib.g4_download_q8K(q8.ptr, P(h), n)
+    assert h.tobytes() == orc.quantize_q8K(xb2.to_array(np.float32)).tobytes()
+    for o, w, d, raw in ((o1, w1, d1, r1), (o2, w2, d2, r2)):
         ref = DBuf(lib, 4 * d)
         lib.g4_mm_quant_dot_rows(ref.ptr, w.ptr, n, d, qtype, q8.ptr)
         g, r = o.to_array(np.float32), ref.to_array(np.float32)
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (d, np.flatnonzero(g != r)[:8])
+        want = orc.mm_quant_dot_rows(raw, n, d, qtype, h)
+        assert np.array_equal(g.view(np.uint32), want.view(np.uint32)), (d, np.flatnonzero(g != want)[:8])
     want = orc.mm_quant_rows(xb, r3, n, d3, 14)
     W = np.abs(kq.dequant_f64(r3.reshape(-1, 210), 14).reshape(d3, n))
     mag = W @ np.abs(xb.astype(np.float64))
