@@ -829,12 +829,16 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
 // never drain the next batch.  The first two batches are issued before x is
 // staged.  AM: also the first-index maximum of the outputs (as stored, after
 // the soft-cap) over this workgroup's rows as an argmax key in part[block].
+constexpr int kQ6XsBlk = 256 + 8;   // LDS floats per block of x in gemv_q6k_rows_kernel
+
 template <int KS, bool SOFTCAP, bool AM = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void gemv_q6k_rows_kernel(
     const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                             float* __restrict__ out, int nb, int d, float cap,
                                                             unsigned long long* __restrict__ part_am) {
-    // LDS: x (n floats), the sums of its runs of 8 (n/8 floats), [32] partials
+    // LDS: x (n floats, 4 floats of padding after every 128: a block's two
+    // halves, read by lanes h = 0 and 1 of a group at once, then fall in
+    // different banks), the sums of its runs of 8 (n/8 floats), [32] partials
     extern __shared__ __align__(16) float xs[];
     __shared__ unsigned long long red[4];
     constexpr int RPW = 32 / KS;
@@ -843,7 +847,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     const int rr = g % RPW, ks = g / RPW;
     const size_t nblk = (size_t)d * nb;
     const Q6KPlanes P = q6k_planes(nblk);
-    float* x8 = xs + nb * 256;
+    float* x8 = xs + nb * kQ6XsBlk;
     float* part = x8 + nb * 32;
     const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
     const int ngroups = (d + RPW - 1) / RPW;
@@ -889,7 +893,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
     }
     // i covers elements 4i..4i+3; pairs of float4 make one run of 8
     auto stage = [&](int i, const float4& v) {
-        reinterpret_cast<float4*>(xs)[i] = v;
+        reinterpret_cast<float4*>(xs)[i + (i >> 5)] = v;
         const float s4 = (v.x + v.y) + (v.z + v.w);
         const float o4 = __shfl_xor(s4, 1, 64);
         if ((i & 1) == 0) x8[i >> 1] = s4 + o4;
@@ -920,7 +924,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void g
                 const uint4 ql = bt.ql[i];
                 const uint2 qh = bt.qh[i], sc = bt.sc[i];
                 const float df = half_bits_to_f32(bt.dv[i]);
-                const float* xb = xs + b * 256 + 128 * h + 8 * u;
+                const float* xb = xs + b * kQ6XsBlk + (128 + 4) * h + 8 * u;
                 const float* sb8 = x8 + b * 32 + 16 * h + u;
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
@@ -1099,6 +1103,149 @@ __global__ __launch_bounds__(8 * kQ6SliceMaxNb) void gemv_q6k_kslice_kernel(cons
     }
 }
 
+// ------------------------------------------------------------------------
+// Q6_K x fp32 with x held in registers (the LM head: many rows of NB blocks)
+// ------------------------------------------------------------------------
+// A workgroup of 8*NB*kXrRpi threads.  Thread t takes row slot r = t/(8 NB)
+// of every pass and slot (b, L) = ((t mod 8NB)/8, t mod 8) of every row it
+// visits: the 32 weights 128h + 32k + 8u + e of block b (L = 4h+u, the lane
+// mapping of gemv_q6k_rows_kernel), so the 32 elements of x it multiplies
+// and their four run sums stay in registers for the whole launch (no LDS
+// reads of x, which gemv_q6k_rows_kernel pays once per weight).  A pass
+// covers kXrRpi rows; eight passes make a batch of 8*kXrRpi rows whose
+// block partials (each summed over its 8 lanes) go to LDS; after a barrier
+// one thread per row in one wave (a different wave each batch) add each row's NB
+// partials, apply the soft-cap, store and (AM) keep the argmax key.  Batches are dealt to the workgroups round
+// robin (d a multiple of the batch); each thread keeps kXrPf
+// passes of weight loads in flight (past the last pass: the last one again,
+// so no load sits under a branch).
+// Same per-block arithmetic as gemv_q6k_rows_kernel (fp32 tolerance of the
+// reference's sequential sums).
+constexpr int kXrRpi = 8, kXrPf = 4, kXrRow = 12;
+
+template <int NB, bool SOFTCAP, bool AM>
+__global__ __launch_bounds__(8 * NB * kXrRpi) void gemv_q6k_xreg_kernel(const uint8_t* __restrict__ w,
+                                                                       const float* __restrict__ x,
+                                                                       float* __restrict__ out, int d, float cap,
+                                                                       unsigned long long* __restrict__ part_am) {
+    constexpr int NT = 8 * NB * kXrRpi;
+    constexpr int BR = 8 * kXrRpi;   // rows per batch
+    static_assert(NB <= kXrRow && NT % 64 == 0 && BR <= 64, "a row's partials fit one LDS row; whole waves");
+    static_assert(8 % kXrPf == 0, "the step loop covers whole batches (8 passes)");
+    __shared__ __align__(16) float part[2][BR][kXrRow];
+    __shared__ unsigned long long red[NT / 64];
+    const int t = threadIdx.x, r = t / (8 * NB), s = t - r * (8 * NB), b = s >> 3, L = s & 7, h = L >> 2, u = L & 3;
+    const int nbatch = d / BR;
+    const int mine = (int)blockIdx.x < nbatch ? (nbatch - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int nsteps = 8 * mine;
+    unsigned long long best = 0;   // argmax key of this thread's rows
+    if (nsteps > 0) {
+        const Q6KPlanes P = q6k_planes((size_t)d * NB);
+        // x of this thread (runs k = 0..3 of 8 elements at b*256 + 128h + 32k + 8u)
+        float4 xa[4], xb[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4* xp = reinterpret_cast<const float4*>(x + b * 256 + 128 * h + 32 * k + 8 * u);
+            xa[k] = xp[0];
+            xb[k] = xp[1];
+        }
+        struct Wt {
+            uint4 ql;
+            uint2 qh, sc;
+            uint32_t dv;
+        };
+        // a pass's first block (uniform) plus this thread's offsets: the rows
+        // are whole batches (d a multiple of BR), so no row is clamped
+        const uint32_t rb = (uint32_t)(r * NB + b);
+        const uint32_t o_ql = rb * 128u + 16u * L, o_qh = rb * 64u + 8u * L, o_sc = rb * 16u + 8u * h, o_d = rb * 2u;
+        auto load = [&](int j, Wt& q) {
+            j = min(j, nsteps - 1);
+            const size_t pb = ((size_t)((int)blockIdx.x + (j >> 3) * (int)gridDim.x) * BR + (j & 7) * kXrRpi) * NB;
+            q.ql = *reinterpret_cast<const uint4*>(w + P.ql + pb * 128 + o_ql);
+            q.qh = *reinterpret_cast<const uint2*>(w + P.qh + pb * 64 + o_qh);
+            q.sc = *reinterpret_cast<const uint2*>(w + P.sc + pb * 16 + o_sc);
+            q.dv = *reinterpret_cast<const uint16_t*>(w + P.d + pb * 2 + o_d);
+        };
+        Wt ring[kXrPf];
+#pragma unroll
+        for (int p = 0; p < kXrPf; p++) load(p, ring[p]);
+        float s8[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            s8[k] = ((xa[k].x + xa[k].y) + (xa[k].z + xa[k].w)) + ((xb[k].x + xb[k].y) + (xb[k].z + xb[k].w));
+        const float inv = SOFTCAP ? 1.0f / cap : 0.0f;
+        for (int j0 = 0; j0 < nsteps; j0 += kXrPf) {
+#pragma unroll
+            for (int p = 0; p < kXrPf; p++) {
+                const int j = j0 + p;
+                const Wt& q = ring[p];
+                const float df = half_bits_to_f32(q.dv);
+                float acc = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const uint32_t qa = (kk & 1) ? q.ql.z : q.ql.x;   // codes e = 0..3
+                    const uint32_t qb = (kk & 1) ? q.ql.w : q.ql.y;   // codes e = 4..7
+                    const uint32_t la = kk < 2 ? (qa & 0x0f0f0f0fu) : ((qa >> 4) & 0x0f0f0f0fu);
+                    const uint32_t lb = kk < 2 ? (qb & 0x0f0f0f0fu) : ((qb >> 4) & 0x0f0f0f0fu);
+                    const uint32_t ca = la | (((q.qh.x >> (2 * kk)) & 0x03030303u) << 4);   // q in [0, 63]
+                    const uint32_t cb = lb | (((q.qh.y >> (2 * kk)) & 0x03030303u) << 4);
+                    // sum_e x_e (q_e - 32) = sum_e x_e q_e - 32 * sum_e x_e
+                    float dot = xa[kk].x * (float)(ca & 0xff);
+                    dot = __builtin_fmaf(xa[kk].y, (float)((ca >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(xa[kk].z, (float)((ca >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(xa[kk].w, (float)(ca >> 24), dot);
+                    dot = __builtin_fmaf(xb[kk].x, (float)(cb & 0xff), dot);
+                    dot = __builtin_fmaf(xb[kk].y, (float)((cb >> 8) & 0xff), dot);
+                    dot = __builtin_fmaf(xb[kk].z, (float)((cb >> 16) & 0xff), dot);
+                    dot = __builtin_fmaf(xb[kk].w, (float)(cb >> 24), dot);
+                    dot = __builtin_fmaf(-32.0f, s8[kk], dot);
+                    // scale of sub-block (u >> 1) + 2kk: word kk >> 1, byte (u >> 1) + 2 (kk & 1)
+                    const int8_t s8i = (int8_t)byte_of(kk < 2 ? q.sc.x : q.sc.y, (u >> 1) + 2 * (kk & 1));
+                    acc = __builtin_fmaf(df * (float)s8i, dot, acc);
+                }
+                // the slot's next pass, into the registers just read (a load
+                // into other registers would be copied back across the loop
+                // edge, which waits for it)
+                load(j + kXrPf, ring[p]);
+                // the block's 8 lanes (quad xor 1, 2, then the two quads)
+                acc += dpp_f<kDppXor1>(acc);
+                acc += dpp_f<kDppXor2>(acc);
+                acc += dpp_f<kDppHalfMirror>(acc);
+                float(*pb)[kXrRow] = part[(j >> 3) & 1];
+                if (L == 0) pb[(j & 7) * kXrRpi + r][b] = acc;
+                if ((j & 7) == 7) {
+                    // the batch's rows: every partial is in LDS.  Lanes 0..BR-1
+                    // of one wave add them, the wave taking turns by batch so
+                    // that no wave falls behind the others at the barriers
+                    lds_sync();
+                    const int tr = t - 64 * ((j >> 3) % (NT / 64));
+                    if (tr >= 0 && tr < BR) {
+                        const float* pr = pb[tr];
+                        float v[NB];
+#pragma unroll
+                        for (int i = 0; i < NB; i++) v[i] = pr[i];
+#pragma unroll
+                        for (int m = 1; m < NB; m <<= 1)
+#pragma unroll
+                            for (int i = 0; i + m < NB; i += 2 * m) v[i] += v[i + m];
+                        const int row = ((int)blockIdx.x + (j >> 3) * (int)gridDim.x) * BR + tr;
+                        const float o = SOFTCAP ? cap * tanhf(v[0] * inv) : v[0];
+                        out[row] = o;
+                        if (AM) {
+                            const unsigned long long key = argmax_key(o, row);
+                            best = key > best ? key : best;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (AM) {
+        best = block_max_u64(best, red);
+        if (t == 0) part_am[blockIdx.x] = best;
+    }
+}
+
 }  // namespace g4
 
 // ------------------------------------------------------------------------
@@ -1231,13 +1378,28 @@ void launch_q6_ks(const void* w, const float* x, float* o, int nb, int d, float 
     const int ngroups = (d + 32 / KS - 1) / (32 / KS);
     int grid = 4 * g4_num_cus();
     if (grid > ngroups) grid = ngroups;
-    const size_t lds = (size_t)nb * 1024 + (size_t)nb * 128 + 32 * 4;
+    const size_t lds = (size_t)nb * kQ6XsBlk * 4 + (size_t)nb * 128 + 32 * 4;
     hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP>), dim3(grid), dim3(256), lds, g4_stream(),
                        (const uint8_t*)w, x, o, nb, d, cap, nullptr);
 }
 
+// the register-x kernel for rows of 10 blocks (the LM head at hidden 2560)
+// once there are enough rows for two workgroups per CU; returns the grid,
+// 0 when it does not apply
+constexpr int kXrWgPerCu = 1;
+template <bool SOFTCAP, bool AM>
+int launch_q6_xreg(const void* w, const float* x, float* o, int nb, int d, float cap, unsigned long long* part) {
+    const int nbatch = d / (8 * kXrRpi);
+    const int grid = kXrWgPerCu * g4_num_cus();
+    if (nb != 10 || d % (8 * kXrRpi) || nbatch < grid) return 0;
+    hipLaunchKernelGGL((gemv_q6k_xreg_kernel<10, SOFTCAP, AM>), dim3(grid), dim3(8 * 10 * kXrRpi), 0, g4_stream(),
+                       (const uint8_t*)w, x, o, d, cap, part);
+    return grid;
+}
+
 template <bool SOFTCAP>
 int launch_q6_f32(const void* w, const float* x, float* o, int nb, int d, float cap) {
+    if (launch_q6_xreg<SOFTCAP, false>(w, x, o, nb, d, cap, nullptr)) return g4_check_launch("gemv_q6k_xreg_kernel");
     if (!SOFTCAP && nb <= kQ6SliceMaxNb && nb % 8 == 0) {
         hipLaunchKernelGGL((gemv_q6k_kslice_kernel<kQ6SliceRows>), dim3((d + kQ6SliceRows - 1) / kQ6SliceRows),
                            dim3(8 * nb), 0, g4_stream(), (const uint8_t*)w, x, o, nb, d);
@@ -1433,7 +1595,7 @@ int launch_q6_am(const void* w, const float* x, float* o, int nb, int d, float c
     const int ngroups = (d + 32 / KS - 1) / (32 / KS);
     int grid = 4 * g4_num_cus();
     if (grid > ngroups) grid = ngroups;
-    const size_t lds = (size_t)nb * 1024 + (size_t)nb * 128 + 32 * 4;
+    const size_t lds = (size_t)nb * kQ6XsBlk * 4 + (size_t)nb * 128 + 32 * 4;
     hipLaunchKernelGGL((gemv_q6k_rows_kernel<KS, SOFTCAP, true>), dim3(grid), dim3(256), lds, g4_stream(),
                        (const uint8_t*)w, x, o, nb, d, cap, part);
     return grid;
@@ -1441,6 +1603,7 @@ int launch_q6_am(const void* w, const float* x, float* o, int nb, int d, float c
 
 template <bool SOFTCAP>
 int launch_q6_am_ks(const void* w, const float* x, float* o, int nb, int d, float cap, unsigned long long* part) {
+    if (const int g = launch_q6_xreg<SOFTCAP, true>(w, x, o, nb, d, cap, part)) return g;
     const int target = 2 * g4_num_cus();
     if ((d + 31) / 32 >= target) return launch_q6_am<SOFTCAP, 1>(w, x, o, nb, d, cap, part);
     if ((d + 15) / 16 >= target) return launch_q6_am<SOFTCAP, 2>(w, x, o, nb, d, cap, part);

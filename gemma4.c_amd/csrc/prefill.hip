@@ -1050,7 +1050,7 @@ __global__ __launch_bounds__(256) void gelu_mul_split_kernel(const float* __rest
 // 16 nt + i; B operand (weights): Wh or Wl of the same elements of row
 // 16 rt + i.  Result lane (g, i): tokens 16 nt + 4g + v of
 // row 16 rt + i.
-constexpr int kXsStride = kSplitBlk + 16;   // LDS bytes per staged token
+constexpr int kXsStride = kSplitBlk + 32;   // LDS bytes per staged token
 
 // 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (the
 // LDS address is wave-uniform: it goes to M0).  A plain device function: in

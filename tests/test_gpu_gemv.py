@@ -171,10 +171,10 @@ def test_q6K_f32_gemv(lib, orc, n, d):
 
 @pytest.mark.parametrize("d", [4096, 16384, 262144])
 def test_q6K_softcap(lib, orc, d):
-    """logits_tied's GEMV + soft-cap.  262144 rows is the LM head itself: at
-    that size the launch picks one row group per workgroup and a grid-stride
-    loop (the instantiation the decode step runs); 16384 and 4096 rows take
-    the K-sliced forms."""
+    """logits_tied's GEMV + soft-cap.  262144 and 16384 rows (at n = 2560)
+    take the kernel with x held in registers, batches of 64 rows dealt to the
+    workgroups (262144 rows is the LM head itself, the instantiation the
+    decode step runs); 4096 rows takes the K-sliced LDS form."""
     from g4 import DBuf, upload_quant
     n = 2560
     rng = np.random.default_rng(2 + d)
