@@ -188,15 +188,16 @@ struct Stack2 {
     float* out6;
     int d6;
 };
-// attention merge prologue (PRO 2): the G chunk partials (o[256], max, sum)
-// of each head (head_dim 256, one Q8_K block per head) as attn_chunk_kernel
-// leaves them; out / q8: the merged vector and its Q8_K (workgroup 0, each
-// optional)
+// attention merge prologue (PRO 2): the G chunk partials (o[hd], max, sum)
+// of each head (head_dim 256 or 512: hb = hd / 256 Q8_K blocks per head) as
+// attn_chunk_kernel leaves them; out / q8: the merged vector and its Q8_K
+// (workgroup 0, each optional)
 struct MergeArgs {
     const float* part;
     float* out;
     uint8_t* q8;
     int G;
+    int hb;
 };
 constexpr int kMergeMaxG = G4_MERGE_MAX_CHUNKS;   // chunks per head the merge prologue holds in registers
 
@@ -417,23 +418,25 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
         // every load of this group's blocks first, then the integer work
         Raw raw[NH];
         if constexpr (PRO == 2) {
-            // the attention output is merged here: wave h takes head h, lane
-            // L its dims 4L .. 4L+3, issuing every chunk's partial (m, l) and
-            // o loads and then its weight loads before anything waits; the
-            // merge is attn_merge_kernel's arithmetic in its order (max of the
-            // chunk maxima, f_g = exp(m_g - M) for chunks with weight, the
-            // wave-sum of l_g f_g, o = sum_g o_g f_g from g = 0, o / L), so the
-            // vector, its Q8_K (wave h: block h into LDS) and the outputs are
-            // the separate merge + GEMV's bits
-            const int lane = tid & 63, h = tid >> 6;
-            const int G = mg.G;
-            constexpr int RS = 256 + 2;   // partial row stride (floats)
+            // the attention output is merged here: wave v takes block v of
+            // the vector (head v / hb, its dims 256 (v mod hb) + 4L .. +3 on
+            // lane L), issuing every chunk's partial (m, l) and o loads and
+            // then its weight loads before anything waits; the merge is
+            // attn_merge_kernel's arithmetic in its order (max of the chunk
+            // maxima, f_g = exp(m_g - M) for chunks with weight, the wave-sum
+            // of l_g f_g, o = sum_g o_g f_g from g = 0, o / L), so the vector,
+            // its Q8_K (wave v: block v into LDS) and the outputs are the
+            // separate merge + GEMV's bits
+            const int lane = tid & 63, v = tid >> 6;
+            const int G = mg.G, hb = mg.hb;
+            const int h = hb == 1 ? v : v >> 1, half = v - h * hb;
+            const int RS = 256 * hb + 2;   // partial row stride (floats)
             const float* ph = mg.part + (size_t)h * G * RS;
-            const float2 ml = *reinterpret_cast<const float2*>(ph + (size_t)min(lane, G - 1) * RS + 256);
+            const float2 ml = *reinterpret_cast<const float2*>(ph + (size_t)min(lane, G - 1) * RS + 256 * hb);
             float2 oa[kMergeMaxG], ob[kMergeMaxG];
 #pragma unroll
             for (int u = 0; u < kMergeMaxG; u++) {
-                const float* pr = ph + (size_t)min(u, G - 1) * RS + 4 * lane;
+                const float* pr = ph + (size_t)min(u, G - 1) * RS + 256 * half + 4 * lane;
                 oa[u] = *reinterpret_cast<const float2*>(pr);
                 ob[u] = *reinterpret_cast<const float2*>(pr + 2);
             }
@@ -460,10 +463,10 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             for (int c = 0; c < 4; c++) r[c] = L > 0.0f ? o[c] / L : 0.0f;
             extern __shared__ __align__(16) float pbuf[];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf);
-            quantize_block_wave(r, lane, q8l, NB, h);
+            quantize_block_wave(r, lane, q8l, NB, v);
             if (blockIdx.x == 0) {
                 if (mg.out) reinterpret_cast<float4*>(mg.out)[tid] = make_float4(r[0], r[1], r[2], r[3]);
-                if (mg.q8) quantize_block_wave(r, lane, mg.q8, NB, h);
+                if (mg.q8) quantize_block_wave(r, lane, mg.q8, NB, v);
             }
             lds_sync();
             const uint8_t* a_qs_l = q8l + 32 * l;
@@ -1301,8 +1304,8 @@ void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const floa
 }
 
 // attention merge + Q8_K as the prologue of every workgroup (64 NB threads:
-// wave h merges head h), then the GEMV with 32 lanes per row (the lane
-// groups' block values gathered through LDS)
+// wave v merges block v of the vector), then the GEMV with 32 lanes per row
+// (the lane groups' block values gathered through LDS)
 template <bool Q5, int NB>
 void launch_q45_merge(const void* w, float* o, int d, const MergeArgs& mg) {
     constexpr int WG = 64 * NB, SPLIT = 4;
@@ -1802,18 +1805,18 @@ extern "C" int g4_mm_attn_merge(float* o, const void* w, int n, int d, int type,
                                 int hd, float* q_out, void* q8) {
     int rc = check_gemv("g4_mm_attn_merge", o, w, part, n, d);
     if (rc) return rc;
-    G4_CHECK_ARG(hd == 256 && n_heads > 0 && n == n_heads * hd, "g4_mm_attn_merge: head_dim %d, %d heads, n=%d", hd,
-                 n_heads, n);
+    G4_CHECK_ARG((hd == 256 || hd == 512) && n_heads > 0 && n == n_heads * hd,
+                 "g4_mm_attn_merge: head_dim %d, %d heads, n=%d", hd, n_heads, n);
     G4_CHECK_ARG(G >= 1 && G <= kMergeMaxG, "g4_mm_attn_merge: %d chunks (1..%d)", G, kMergeMaxG);
     G4_CHECK_ARG(!q_out || aligned16(q_out), "g4_mm_attn_merge: q_out must be 16-byte aligned");
     G4_CHECK_ARG(!q8 || aligned16(q8), "g4_mm_attn_merge: q8 must be 16-byte aligned");
-    const MergeArgs mg{part, q_out, (uint8_t*)q8, G};
+    const MergeArgs mg{part, q_out, (uint8_t*)q8, G, hd / 256};
     const bool q5 = type == G4_Q5_K;
     if (type != G4_Q4_K && !q5) return g4_fail(G4_ERR_TYPE, "g4_mm_attn_merge: type %d not supported", type);
-    switch (n_heads) {
+    switch (n / 256) {
     case 8: q5 ? launch_q45_merge<true, 8>(w, o, d, mg) : launch_q45_merge<false, 8>(w, o, d, mg); break;
     case 16: q5 ? launch_q45_merge<true, 16>(w, o, d, mg) : launch_q45_merge<false, 16>(w, o, d, mg); break;
-    default: return g4_fail(G4_ERR_ARG, "g4_mm_attn_merge: %d heads (8 or 16)", n_heads);
+    default: return g4_fail(G4_ERR_ARG, "g4_mm_attn_merge: %d heads of %d (n = 2048 or 4096)", n_heads, hd);
     }
     return g4_check_launch("gemv_q45_rows_kernel<merge>");
 }

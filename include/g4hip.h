@@ -165,7 +165,8 @@ int g4_mm_residual_q8_qkv(float *o1, const void *w1, int d1, float *o2, const vo
  * the same vector), quantized to Q8_K and multiplied by W (Q4_K / Q5_K, d
  * rows of n = n_heads * hd) as g4_mm_quant_dot_rows: o[d].  q_out (n floats)
  * and q8 (g4_q8K_bytes(n)) optionally receive the merged vector and its
- * Q8_K.  head_dim 256 only, n_heads 8 or 16, G <= G4_MERGE_MAX_CHUNKS. */
+ * Q8_K.  n = n_heads * hd of 2048 or 4096 (head_dim 256 or 512),
+ * G <= G4_MERGE_MAX_CHUNKS. */
 #define G4_MERGE_MAX_CHUNKS 16
 int g4_mm_attn_merge(float *o, const void *w, int n, int d, int type, const float *part, int G, int n_heads, int hd,
                      float *q_out, void *q8);

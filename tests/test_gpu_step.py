@@ -293,22 +293,26 @@ def test_attn_decode_fused(lib, orc, hd, window, pos, G, store):
 
 
 
-@pytest.mark.parametrize("nh,nkv,window,pos,G,store,qtype,d", [(8, 2, 512, 700, 16, True, 12, 2560),
-                                                              (8, 2, 512, 900, 16, False, 12, 2560),
-                                                              (8, 2, 512, 100, 4, True, 13, 2560),
-                                                              (8, 2, 0, 37, 1, True, 12, 200),
-                                                              (16, 2, 512, 600, 16, True, 12, 2560),
-                                                              (16, 4, 0, 333, 11, False, 13, 1000)])
-def test_attn_merge_o_prologue(lib, orc, nh, nkv, window, pos, G, store, qtype, d):
+@pytest.mark.parametrize("nh,nkv,hd,window,pos,G,store,qtype,d", [(8, 2, 256, 512, 700, 16, True, 12, 2560),
+                                                                 (8, 2, 256, 512, 900, 16, False, 12, 2560),
+                                                                 (8, 2, 256, 512, 100, 4, True, 13, 2560),
+                                                                 (8, 2, 256, 0, 37, 1, True, 12, 200),
+                                                                 (16, 2, 256, 512, 600, 16, True, 12, 2560),
+                                                                 (16, 4, 256, 0, 333, 11, False, 13, 1000),
+                                                                 (8, 2, 512, 0, 700, 16, True, 12, 2560),
+                                                                 (8, 2, 512, 0, 1023, 16, False, 13, 2560),
+                                                                 (8, 2, 512, 0, 5, 3, True, 12, 300)])
+def test_attn_merge_o_prologue(lib, orc, nh, nkv, hd, window, pos, G, store, qtype, d):
     """The attention's end and the output projection in one launch
     (main.c:1909-1950 then the O mm, main.c:1955): g4_attn_decode_fused leaves
     only the chunk partials, g4_mm_attn_merge merges them per head in every
-    workgroup and runs the Q4_K/Q5_K GEMV on their Q8_K.  The merged vector
-    is within 1e-4 of the oracle's attention and bit-equal to the separate
-    merge kernel's, its Q8_K is quantize_row_q8_K of it, and the outputs equal
-    the oracle's mm_quant_dot_rows on that Q8_K bit for bit."""
+    workgroup and runs the Q4_K/Q5_K GEMV on their Q8_K (head_dim 256: one
+    Q8_K block per head; 512, the global layers': two).  The merged vector is
+    within 1e-4 of the oracle's attention and bit-equal to the separate merge
+    kernel's, its Q8_K is quantize_row_q8_K of it, and the outputs equal the
+    oracle's mm_quant_dot_rows on that Q8_K bit for bit."""
     from g4 import upload_quant
-    hd, eps = 256, 1e-6
+    eps = 1e-6
     rng = np.random.default_rng(nh + pos + G + qtype)
     kv_dim, n = nkv * hd, nh * hd
     base = 1e4 if window else 1e6
@@ -379,7 +383,8 @@ def test_attn_merge_o_prologue_rejects(lib):
     from g4 import DBuf, G4Error
     b = DBuf(lib, 1 << 20)
     for args in [(b.ptr, b.ptr, 2048, 2560, 12, b.ptr, 17, 8, 256, None, None),    # too many chunks
-                 (b.ptr, b.ptr, 4096, 2560, 12, b.ptr, 8, 8, 512, None, None),     # head_dim 512
+                 (b.ptr, b.ptr, 2048, 2560, 12, b.ptr, 8, 16, 128, None, None),    # head_dim 128
+                 (b.ptr, b.ptr, 6144, 2560, 12, b.ptr, 8, 12, 512, None, None),    # 12 heads of 512
                  (b.ptr, b.ptr, 3072, 2560, 12, b.ptr, 8, 12, 256, None, None),    # 12 heads
                  (b.ptr, b.ptr, 2048, 2560, 14, b.ptr, 8, 8, 256, None, None)]:    # Q6_K
         with pytest.raises(G4Error):
