@@ -260,9 +260,10 @@ size_t g4_split_rows_bytes(int n, int m);
 int g4_split_rows_f16(const float *x, void *xs, int n, int m);
 /* o[t*d + r] = mm_quant_rows row r of split row t (main.c:1539-1556) for a
  * planar Q6_K w: the exact products sc * (q - 32) * (hi + lo) on the fp16
- * matrix cores (sc split as 16a + b), the block's d and the row's 2^s in
- * fp32; within 1e-5 of sum |w x| of the reference's fp32 dot.  Q6_K only
- * (others: G4_ERR_TYPE). */
+ * matrix cores (the integer weight split exactly into its fp16 rounding Wh
+ * and the rest Wl in {-1, 0, 1}: Wh hi + Wh lo + Wl hi), the block's d and
+ * the row's 2^s in fp32; within 1e-5 of sum |w x| of the reference's fp32
+ * dot.  Q6_K only (others: G4_ERR_TYPE). */
 int g4_mm_batch_split(float *o, const void *w, const void *xs, int n, int d, int m, int type);
 /* g4_gelu_mul_rows (o = gelu(g) * u, rows of n, u rows ustride floats apart)
  * followed by g4_split_rows_f16 of o in one launch, without o: the split rows
