@@ -527,7 +527,7 @@ def cpu_prefill_baseline(raw, n, d, tokens: int = 4):
                       f"{len(ts)} runs, OpenMP {thr} threads"}
 
 
-LMHEAD_KERNEL = "gemv_q6k_rows_kernel<Q6_K, softcap> 262144x2560"
+LMHEAD_KERNEL = "gemv_q6k_xreg_kernel<Q6_K, softcap> 262144x2560"
 
 
 def bench_lmhead(lib, g4, synth, args):
