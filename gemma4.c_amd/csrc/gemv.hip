@@ -667,20 +667,22 @@ __device__ __forceinline__ int dot2_i16(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2_t, a), __builtin_bit_cast(s2_t, b), c, false);
 }
 
-// PRO: a 256-thread workgroup of four such waves whose Q8_K vector is made
-// by the workgroup itself: the residual step, norm and Q8_K of ResidualArgs
-// (its loads issued first, then every wave's header and weight loads, so the
-// norm's arithmetic runs while the weights stream in), into LDS; workgroup 0
-// also stores the residual stream, xb2 and the Q8_K when asked.
+// PRO: a workgroup of NB such waves (64 NB threads, n = 256 NB) whose Q8_K
+// vector is made by the workgroup itself: the residual step, norm and Q8_K
+// of ResidualArgs with one float4 of each vector per thread and block w
+// quantized by wave w (its loads issued first, then every wave's header and
+// weight loads, so the norm's arithmetic runs while the weights stream in),
+// into LDS; workgroup 0 also stores the residual stream, xb2 and the Q8_K
+// when asked.
 template <bool Q5, int NB, int NMAT, bool PRO = false>
-__global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const uint8_t* __restrict__ w0,
+__global__ __launch_bounds__(PRO ? 64 * NB : 64) void gemv_q45_stream_kernel(const uint8_t* __restrict__ w0,
                                                                          const uint8_t* __restrict__ w1,
                                                                          const uint8_t* __restrict__ q8,
                                                                          float* __restrict__ out, int d,
                                                                          const float* __restrict__ aux,
                                                                          const ResidualArgs ra) {
     constexpr int RPW = 8 / NMAT;                 // rows per wave
-    constexpr int NWV = PRO ? 4 : 1;              // waves per workgroup
+    constexpr int NWV = PRO ? NB : 1;             // waves per workgroup
     constexpr int Q8B = NB * 292;                 // device Q8_K bytes
     constexpr int Q8C = Q8B / 16, Q8T = (Q8B - Q8C * 16) / 4;
     constexpr int QPL = PRO ? 0 : (Q8C + 63) / 64;
@@ -693,8 +695,8 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
     const uint32_t nblk = (uint32_t)d * NB;
     const uint32_t hdr_off = (Q5 ? 160u : 128u) * nblk, qh_off = 128u * nblk;   // q4k_planes / q5k_planes
 
-    [[maybe_unused]] ResidualRegs<NB> rr;
-    if constexpr (PRO) residual_load<NB>(ra, rr);
+    [[maybe_unused]] Res4 r4;
+    if constexpr (PRO) residual4_load(ra, r4, 0);
     // the Q8_K vector is staged in LDS (the same for every wave)
     uint4 qv[QPL > 0 ? QPL : 1];
     uint32_t tv = 0u;
@@ -722,12 +724,12 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
     }
     __builtin_amdgcn_sched_barrier(0);   // all loads issued before the LDS stores wait for the first ones
     if constexpr (PRO) {
-        __shared__ __align__(16) float pbuf[NB * 256];
-        __shared__ float red[16];
-        residual_finish<NB>(ra, rr, pbuf, red, blockIdx.x == 0);
-        __syncthreads();
-        quantize_blocks_wg(pbuf, sq, NB);
-        if (blockIdx.x == 0 && ra.q8) quantize_blocks_wg(pbuf, ra.q8, NB);
+        // one float4 of each vector per thread, wave w quantizes block w
+        __shared__ float red[2][16];
+        float qv[4], nv[4];
+        residual4_finish(ra, r4, red, blockIdx.x == 0, 0, qv, nv);
+        quantize_block_wave(qv, lane, sq, NB, wv);
+        if (blockIdx.x == 0 && ra.q8) quantize_block_wave(qv, lane, ra.q8, NB, wv);
     } else {
 #pragma unroll
         for (int j = 0; j < QPL; j++) {
@@ -736,7 +738,11 @@ __global__ __launch_bounds__(PRO ? 256 : 64) void gemv_q45_stream_kernel(const u
         }
         if (lane < Q8T) reinterpret_cast<uint32_t*>(sq + Q8C * 16)[lane] = tv;
     }
-    __syncthreads();
+    // (with the prologue an LDS-only barrier: __syncthreads() would also wait
+    // for every weight load, so no block's dot could start before the last
+    // one had landed)
+    if constexpr (PRO) lds_sync();
+    else __syncthreads();
 
     // byte selectors of the two mins (m_2k, m_2k+1 of min lane k), as int16 pairs
     const uint32_t selA = (k & 1) ? 0x0c020c02u : 0x0c000c00u;
@@ -1338,9 +1344,9 @@ template <bool Q5, int NB>
 void launch_q45_pro_nm(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                        const Stack2& st) {
     if (w2 && !st.w && !st.w6) {
-        // gate|up: the streaming kernel, four waves of 4 rows x {gate, up}
-        hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, NB, 2, true>), dim3((d + 15) / 16), dim3(256), 0, g4_stream(),
-                           (const uint8_t*)w, (const uint8_t*)w2, nullptr, o, d, nullptr, ra);
+        // gate|up: the streaming kernel, NB waves of 4 rows x {gate, up}
+        hipLaunchKernelGGL((gemv_q45_stream_kernel<Q5, NB, 2, true>), dim3((d + 4 * NB - 1) / (4 * NB)), dim3(64 * NB), 0,
+                           g4_stream(), (const uint8_t*)w, (const uint8_t*)w2, nullptr, o, d, nullptr, ra);
     } else if (w2) {
         launch_q45_pro<Q5, 2, NB>(w, w2, o, d, nullptr, ra, st);
     } else {
