@@ -1351,8 +1351,19 @@ void launch_q45_merge(const void* w, float* o, int d, const MergeArgs& mg) {
 template <bool Q5, int NMAT, int NB>
 void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                     const Stack2& st) {
-    if constexpr (NMAT == 2 || NB > 10) launch_q45_pro_s<Q5, NMAT, NB, 8>(w, w2, o, d, aux, ra, st);
-    else launch_q45_pro_s<Q5, NMAT, NB, 4, true>(w, w2, o, d, aux, ra, st);
+    if constexpr (NMAT == 2 || NB > 10) {
+        launch_q45_pro_s<Q5, NMAT, NB, 8>(w, w2, o, d, aux, ra, st);
+    } else {
+        // 16 lanes per row where 32 would need more workgroups than there
+        // are CUs: a ten-wave workgroup fills a CU's wave slots, so the
+        // excess ran as a second round of prologues (the global layers'
+        // Q|K|V, 4096 + 1024 + 1024 rows: 308 workgroups, 11.5 us)
+        constexpr int WG = 64 * NB;
+        const int wgs4 = (d + st.d + WG / 32 - 1) / (WG / 32) +
+                         (st.w6 ? (st.d6 + q6_pro_rows(WG, 4) - 1) / q6_pro_rows(WG, 4) : 0);
+        if (wgs4 > g4_num_cus()) launch_q45_pro_s<Q5, NMAT, NB, 2, true>(w, w2, o, d, aux, ra, st);
+        else launch_q45_pro_s<Q5, NMAT, NB, 4, true>(w, w2, o, d, aux, ra, st);
+    }
 }
 
 template <bool Q5, int NB>
