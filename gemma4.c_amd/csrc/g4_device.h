@@ -440,6 +440,51 @@ __device__ inline float dequant_elem(const uint8_t* __restrict__ w, int type, si
     return d1 * (float)q - m1;
 }
 
+// ---- BF16 x fp32 rows (mm_bf16, main.c:1529-1537) ---------------------------
+// A wave's RPW rows of nch 16-byte chunks (8 bf16 each), chunk lane + 64c of
+// row r in v[r][c] (zero past nch), against x in LDS: lane partial sums in
+// chunk order, then the wave sum.  Every lane gets each row's dot.
+template <int RPW, int CPL>
+__device__ __forceinline__ void bf16_rows_dot(const uint4 (&v)[RPW][CPL], const float* xs, int nch, int lane,
+                                              float (&res)[RPW]) {
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const int ch = lane + 64 * c;
+            if (ch < nch) {
+                const float4 xa = reinterpret_cast<const float4*>(xs)[2 * ch];
+                const float4 xb = reinterpret_cast<const float4*>(xs)[2 * ch + 1];
+                acc = __builtin_fmaf(xa.x, bf16_to_f32(v[r][c].x & 0xffffu), acc);
+                acc = __builtin_fmaf(xa.y, bf16_to_f32(v[r][c].x >> 16), acc);
+                acc = __builtin_fmaf(xa.z, bf16_to_f32(v[r][c].y & 0xffffu), acc);
+                acc = __builtin_fmaf(xa.w, bf16_to_f32(v[r][c].y >> 16), acc);
+                acc = __builtin_fmaf(xb.x, bf16_to_f32(v[r][c].z & 0xffffu), acc);
+                acc = __builtin_fmaf(xb.y, bf16_to_f32(v[r][c].z >> 16), acc);
+                acc = __builtin_fmaf(xb.z, bf16_to_f32(v[r][c].w & 0xffffu), acc);
+                acc = __builtin_fmaf(xb.w, bf16_to_f32(v[r][c].w >> 16), acc);
+            }
+        }
+        res[r] = wave_sum(acc);
+    }
+}
+
+// the loads of those rows (rows past d and chunks past nch: zero)
+template <int RPW, int CPL>
+__device__ __forceinline__ void bf16_rows_load(const uint16_t* __restrict__ w, int n, int d, int row0, int lane,
+                                               uint4 (&v)[RPW][CPL]) {
+    const int nch = n / 8;
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const int ch = lane + 64 * c, row = row0 + r;
+            v[r][c] = (row < d && ch < nch) ? reinterpret_cast<const uint4*>(w + (size_t)row * n)[ch]
+                                            : make_uint4(0, 0, 0, 0);
+        }
+}
+
 // Q8_K of the nb blocks in buf (LDS) into y (global or LDS, device layout),
 // one wave per block
 __device__ __forceinline__ void quantize_blocks_wg(const float* buf, uint8_t* y, int nb) {

@@ -114,40 +114,16 @@ __global__ __launch_bounds__(kWG) void gemv_bf16_kernel(const uint16_t* __restri
     extern __shared__ __align__(16) uint8_t smem[];
     float* xs = reinterpret_cast<float*>(smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int nch = n / 8;
     const int row0 = (blockIdx.x * 4 + wave) * RPW;
     uint4 v[RPW][CPL];
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-#pragma unroll
-        for (int c = 0; c < CPL; c++) {
-            const int ch = lane + 64 * c, row = row0 + r;
-            v[r][c] = (row < d && ch < nch) ? reinterpret_cast<const uint4*>(w + (size_t)row * n)[ch] : make_uint4(0, 0, 0, 0);
-        }
+    bf16_rows_load<RPW, CPL>(w, n, d, row0, lane, v);
     for (int k = tid; k < n / 4; k += kWG) reinterpret_cast<float4*>(xs)[k] = reinterpret_cast<const float4*>(x)[k];
     __syncthreads();
+    float res[RPW];
+    bf16_rows_dot<RPW, CPL>(v, xs, n / 8, lane, res);
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < CPL; c++) {
-            const int ch = lane + 64 * c;
-            if (ch < nch) {
-                const float4 xa = reinterpret_cast<const float4*>(xs)[2 * ch];
-                const float4 xb = reinterpret_cast<const float4*>(xs)[2 * ch + 1];
-                acc = __builtin_fmaf(xa.x, bf16_to_f32(v[r][c].x & 0xffffu), acc);
-                acc = __builtin_fmaf(xa.y, bf16_to_f32(v[r][c].x >> 16), acc);
-                acc = __builtin_fmaf(xa.z, bf16_to_f32(v[r][c].y & 0xffffu), acc);
-                acc = __builtin_fmaf(xa.w, bf16_to_f32(v[r][c].y >> 16), acc);
-                acc = __builtin_fmaf(xb.x, bf16_to_f32(v[r][c].z & 0xffffu), acc);
-                acc = __builtin_fmaf(xb.y, bf16_to_f32(v[r][c].z >> 16), acc);
-                acc = __builtin_fmaf(xb.z, bf16_to_f32(v[r][c].w & 0xffffu), acc);
-                acc = __builtin_fmaf(xb.w, bf16_to_f32(v[r][c].w >> 16), acc);
-            }
-        }
-        acc = wave_sum(acc);
-        if (lane == 0 && row0 + r < d) out[row0 + r] = acc;
-    }
+    for (int r = 0; r < RPW; r++)
+        if (lane == 0 && row0 + r < d) out[row0 + r] = res[r];
 }
 
 // ------------------------------------------------------------------------

@@ -63,6 +63,45 @@ __global__ __launch_bounds__(256) void emb_rope_kernel(float* __restrict__ o, co
     o[i] = table_elem(w, type, rows, dim, id, i) * scale;
 }
 
+// ... and the PLE context projection of the same row (main.c:1747-1750:
+// ctx = W . x, W bf16 [d x dim]) in the same launch: workgroups [0, gx)
+// take 8 rows of ctx each (4 waves x 2 rows, gemv_bf16_kernel's dot: the
+// same bits), issue their weight loads, then rebuild x = table row * scale
+// in LDS themselves (emb_rope_kernel's values) while the weights are in
+// flight; workgroup 0 also stores x.  Workgroups gx and gx + 1 write the two
+// RoPE tables.
+template <int RPW, int CPL>
+__global__ __launch_bounds__(256) void emb_ple_kernel(float* __restrict__ o, const void* emb, int type, int rows,
+                                                      int dim, const int* dtok, float scale,
+                                                      const uint16_t* __restrict__ w, float* __restrict__ ctx, int d,
+                                                      const int* dpos, float fs, RopeTab ta, RopeTab tb) {
+    const int gx = (d + 4 * RPW - 1) / (4 * RPW);
+    if ((int)blockIdx.x >= gx) {
+        const RopeTab& t = (int)blockIdx.x == gx ? ta : tb;
+        const int p = *dpos;
+        for (int j = threadIdx.x; j < t.npair; j += 256) t.tab[j] = rope_pair_cs(p, j, t.ts, fs, t.ff);
+        return;
+    }
+    extern __shared__ __align__(16) float xs[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row0 = (blockIdx.x * 4 + wave) * RPW;
+    uint4 v[RPW][CPL];
+    bf16_rows_load<RPW, CPL>(w, dim, d, row0, lane, v);
+    const int id = *dtok;
+    const bool ok = id >= 0 && id < rows;
+    for (int i = tid; i < dim; i += 256) {
+        const float e = ok ? table_elem(emb, type, rows, dim, id, i) * scale : 0.0f;
+        xs[i] = e;
+        if (blockIdx.x == 0 && ok) o[i] = e;
+    }
+    lds_sync();
+    float res[RPW];
+    bf16_rows_dot<RPW, CPL>(v, xs, dim / 8, lane, res);
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+        if (lane == 0 && row0 + r < d) ctx[row0 + r] = res[r];
+}
+
 // token z = blockIdx.y of a prompt chunk -> row z of o
 __global__ __launch_bounds__(256) void emb_lookup_rows_kernel(float* __restrict__ o, const void* w, int type, int rows,
                                                               int dim, const int* __restrict__ dtok, float scale) {
@@ -294,6 +333,35 @@ extern "C" int g4_emb_lookup_rope(float* o, const void* w, int type, int rows, c
     hipLaunchKernelGGL(emb_rope_kernel, dim3((dim + 255) / 256 + 2), dim3(256), 0, g4_stream(), o, w, type, rows, dim,
                        dtok, scale, dpos, freq_scale, ta, tb);
     return g4_check_launch("emb_rope_kernel");
+}
+
+extern "C" int g4_emb_lookup_rope_ple(float* o, const void* w, int type, int rows, const int* dtok, int dim,
+                                      float scale, const int* dpos, float* tab_a, int n_rot_a, float base_a,
+                                      const float* ff_a, float* tab_b, int n_rot_b, float base_b, const float* ff_b,
+                                      float freq_scale, float* ctx, const void* w_ctx, int d_ctx) {
+    G4_CHECK_ARG(o && w && dtok && dim > 0 && rows > 0 && dpos && ctx && w_ctx && d_ctx > 0,
+                 "g4_emb_lookup_rope_ple: bad arguments");
+    G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
+    G4_CHECK_ARG(dim % 8 == 0 && dim <= 4096 && ((uintptr_t)w_ctx & 15) == 0,
+                 "g4_emb_lookup_rope_ple: dim=%d (a multiple of 8, <= 4096), w_ctx 16-byte aligned", dim);
+    G4_CHECK_ARG(tab_a && tab_b && n_rot_a > 0 && n_rot_a % 2 == 0 && n_rot_a <= 2048 && n_rot_b > 0 &&
+                     n_rot_b % 2 == 0 && n_rot_b <= 2048,
+                 "g4_emb_lookup_rope_ple: bad RoPE table arguments");
+    const RopeTab ta{(float2*)tab_a, ff_a, powf(base_a, -2.0f / (float)n_rot_a), n_rot_a / 2};
+    const RopeTab tb{(float2*)tab_b, ff_b, powf(base_b, -2.0f / (float)n_rot_b), n_rot_b / 2};
+    // four rows per wave (every workgroup rebuilds x: fewer, larger ones);
+    // 16-byte chunks per lane: dim / 512 rounded up
+    const size_t lds = (size_t)dim * 4;
+    const uint16_t* wp = (const uint16_t*)w_ctx;
+    auto go = [&](auto kern, int rpw) {
+        hipLaunchKernelGGL(kern, dim3((d_ctx + 4 * rpw - 1) / (4 * rpw) + 2), dim3(256), lds, g4_stream(), o, w, type,
+                           rows, dim, dtok, scale, wp, ctx, d_ctx, dpos, freq_scale, ta, tb);
+    };
+    const int cpl = (dim / 8 + 63) / 64;
+    if (cpl <= 4) go(emb_ple_kernel<4, 4>, 4);
+    else if (cpl <= 5) go(emb_ple_kernel<4, 5>, 4);
+    else go(emb_ple_kernel<2, 8>, 2);
+    return g4_check_launch("emb_ple_kernel");
 }
 
 extern "C" int g4_ple_finish(float* ple, const float* ctx, const void* ple_tok, int type, int rows, const float* proj_norm,

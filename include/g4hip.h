@@ -437,6 +437,14 @@ int g4_emb_lookup_dev(float *o, const void *w, int type, int rows, const int *dt
 int g4_emb_lookup_rope(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale,
                        const int *dpos, float *tab_a, int n_rot_a, float base_a, const float *ff_a, float *tab_b,
                        int n_rot_b, float base_b, const float *ff_b, float freq_scale);
+/* ... and the PLE context projection of build_ple on the same row
+ * (main.c:1749-1750: ctx = mm_bf16(w_ctx, o), w_ctx bf16 [d_ctx x dim]) in
+ * the same launch: the same values as g4_emb_lookup_rope followed by
+ * g4_mm_bf16(ctx, o, w_ctx, dim, d_ctx).  dim a multiple of 8, <= 4096. */
+int g4_emb_lookup_rope_ple(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale,
+                           const int *dpos, float *tab_a, int n_rot_a, float base_a, const float *ff_a, float *tab_b,
+                           int n_rot_b, float base_b, const float *ff_b, float freq_scale, float *ctx,
+                           const void *w_ctx, int d_ctx);
 /* build_ple after its projection (main.c:1751-1777): ple[l*pd+i] =
  * (emb(ple_tok, tok)[l*pd+i]*sc_tok + rmsnorm(ctx[l*pd..]*sc_ctx, norm)[i]) * mix;
  * tok = *dtok if dtok else tok. */

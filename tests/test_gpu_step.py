@@ -439,6 +439,43 @@ def test_emb_lookup_rope(lib, orc, qtype, pos):
     if pos == 0:   # angle 0: (1, 0) pairs
         assert np.array_equal(ta.to_array(np.float32).reshape(-1, 2), np.tile([1.0, 0.0], (128, 1)).astype(np.float32))
 
+@pytest.mark.parametrize("qtype,pos,d_ctx", [(14, 519, 10752), (12, 0, 1000), (14, 32767, 8)])
+def test_emb_lookup_rope_ple(lib, orc, qtype, pos, d_ctx):
+    """The step's inputs with the bf16 PLE context projection in the same
+    launch: x, both RoPE tables and ctx equal, bit for bit, to
+    g4_emb_lookup_rope followed by g4_mm_bf16 on its x; x against the
+    oracle's emb_lookup and ctx within 1e-5 of the oracle's mm_bf16
+    (normalised by sum |w x|).  d_ctx 10752 is E4B's 42 x 256."""
+    from g4 import DBuf, upload_quant
+    rng = np.random.default_rng(qtype + pos + d_ctx)
+    rows, dim, tok, scale = 300, 2560, 123, np.float32(np.sqrt(2560.0))
+    raw = synth.rand_kquant(rng, qtype, rows, dim)
+    w = upload_quant(lib, raw, qtype, dim, rows)
+    wc_raw = synth.rand_bf16(rng, d_ctx, dim)
+    wc = dbuf(lib, wc_raw)
+    ff = rng.uniform(1.0, 4.0, 256).astype(np.float32)
+    ffd = dbuf(lib, ff)
+    dtok, dpos = dbuf(lib, np.array([tok], np.int32)), dbuf(lib, np.array([pos], np.int32))
+    out, ta, tb, ctx = DBuf(lib, 4 * dim), DBuf(lib, 4 * 256), DBuf(lib, 4 * 512), DBuf(lib, 4 * d_ctx)
+    lib.g4_emb_lookup_rope_ple(out.ptr, w.ptr, qtype, rows, dtok.ptr, dim, C.c_float(scale), dpos.ptr, ta.ptr, 256,
+                               C.c_float(1e4), None, tb.ptr, 512, C.c_float(1e6), ffd.ptr, C.c_float(1.0), ctx.ptr,
+                               wc.ptr, d_ctx)
+    out2, ta2, tb2, ctx2 = DBuf(lib, 4 * dim), DBuf(lib, 4 * 256), DBuf(lib, 4 * 512), DBuf(lib, 4 * d_ctx)
+    lib.g4_emb_lookup_rope(out2.ptr, w.ptr, qtype, rows, dtok.ptr, dim, C.c_float(scale), dpos.ptr, ta2.ptr, 256,
+                           C.c_float(1e4), None, tb2.ptr, 512, C.c_float(1e6), ffd.ptr, C.c_float(1.0))
+    lib.g4_mm_bf16(ctx2.ptr, out2.ptr, wc.ptr, dim, d_ctx)
+    for a, b in ((out, out2), (ta, ta2), (tb, tb2), (ctx, ctx2)):
+        assert np.array_equal(a.to_array(np.uint32), b.to_array(np.uint32))
+    want = np.empty(dim, np.float32)
+    assert orc.L.or_emb_lookup(P(want), P(raw), qtype, tok, dim) == 0
+    x = want * scale
+    assert np.array_equal(out.to_array(np.float32).view(np.uint32), x.view(np.uint32))
+    Wf = (wc_raw.astype(np.uint32) << 16).view(np.float32).reshape(d_ctx, dim).astype(np.float64)
+    want_c = Wf @ x.astype(np.float64)
+    mag = np.abs(Wf) @ np.abs(x.astype(np.float64))
+    assert np.max(np.abs(ctx.to_array(np.float32) - want_c) / mag) < 1e-5
+
+
 def test_ple_finish(lib, orc):
     from g4 import DBuf, upload_quant
     rng = np.random.default_rng(5)
