@@ -266,7 +266,8 @@ __device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, cons
 // PRO 1: residual prologue (ra, st); PRO 2: attention merge prologue (mg).
 // LG: the lane groups of a row hand their block values to group 0 through
 // LDS (one write and one read per block) instead of lane shuffles.
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0, bool LG = false>
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0, bool LG = false,
+          int KS6 = SPLIT>
 __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
                                                            const uint8_t* __restrict__ w1,
                                                            const uint8_t* q8, float* __restrict__ out,
@@ -482,7 +483,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             __shared__ float red[2][16];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf + NB * 256);
             if (vwg) {
-                q6k_prologue_rows<NB, WG, SPLIT>(st, blockIdx.x - qk_wgs, ra, r4, pbuf, red);
+                q6k_prologue_rows<NB, WG, KS6>(st, blockIdx.x - qk_wgs, ra, r4, pbuf, red);
                 return;
             }
             float qv[4], nv[4];
@@ -1283,7 +1284,7 @@ void launch_q45_nb(const void* w0, const void* w1, const void* q8, float* o, int
 
 // residual step + norm + Q8_K as the prologue of every workgroup (64 NB
 // threads: one wave per Q8_K block, each wave 8/SPLIT rows)
-template <bool Q5, int NMAT, int NB, int SPLIT, bool LG = false>
+template <bool Q5, int NMAT, int NB, int SPLIT, bool LG = false, int KS6 = SPLIT>
 void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const float* aux, const ResidualArgs& ra,
                       const Stack2& st) {
     constexpr int WG = 64 * NB;
@@ -1292,9 +1293,9 @@ void launch_q45_pro_s(const void* w, const void* w2, float* o, int d, const floa
     // x, Q8_K, and for a Q6_K tensor the run sums of x and the partials
     const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15) + (size_t)NB * 32 * 4 +
                        (size_t)WG / 8 * 4;
-    const int r6 = q6_pro_rows(WG, SPLIT);
+    const int r6 = q6_pro_rows(WG, KS6);
     const int wgs = (rows + rows_per_wg - 1) / rows_per_wg + (st.w6 ? (st.d6 + r6 - 1) / r6 : 0);
-    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, 1, LG>),
+    hipLaunchKernelGGL((gemv_q45_rows_kernel<Q5, NMAT, false, NB, SPLIT, false, WG, 1, LG, KS6>),
                        dim3(wgs), dim3(WG), lds, g4_stream(), (const uint8_t*)w,
                        (const uint8_t*)w2, nullptr, o, NB, d, nullptr, nullptr, nullptr, nullptr, aux, ra, st,
                        MergeArgs{});
@@ -1330,14 +1331,15 @@ void launch_q45_pro(const void* w, const void* w2, float* o, int d, const float*
     if constexpr (NMAT == 2 || NB > 10) {
         launch_q45_pro_s<Q5, NMAT, NB, 8>(w, w2, o, d, aux, ra, st);
     } else {
-        // 16 lanes per row where 32 would need more workgroups than there
-        // are CUs: a ten-wave workgroup fills a CU's wave slots, so the
+        // 16 lanes per K-quant row where 32 would need more workgroups than
+        // there are CUs: a ten-wave workgroup fills a CU's wave slots, so the
         // excess ran as a second round of prologues (the global layers'
-        // Q|K|V, 4096 + 1024 + 1024 rows: 308 workgroups, 11.5 us)
+        // Q|K|V, 4096 + 1024 + 1024 rows: 308 workgroups, 11.5 us; 180 with
+        // the Q6_K V rows still on four slices each)
         constexpr int WG = 64 * NB;
         const int wgs4 = (d + st.d + WG / 32 - 1) / (WG / 32) +
                          (st.w6 ? (st.d6 + q6_pro_rows(WG, 4) - 1) / q6_pro_rows(WG, 4) : 0);
-        if (wgs4 > g4_num_cus()) launch_q45_pro_s<Q5, NMAT, NB, 2, true>(w, w2, o, d, aux, ra, st);
+        if (wgs4 > g4_num_cus()) launch_q45_pro_s<Q5, NMAT, NB, 2, true, 4>(w, w2, o, d, aux, ra, st);
         else launch_q45_pro_s<Q5, NMAT, NB, 4, true>(w, w2, o, d, aux, ra, st);
     }
 }
