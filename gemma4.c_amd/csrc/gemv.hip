@@ -266,24 +266,27 @@ __device__ __forceinline__ void q6k_prologue_rows(const Stack2& st, int vb, cons
 // PRO 1: residual prologue (ra, st); PRO 2: attention merge prologue (mg).
 // LG: the lane groups of a row hand their block values to group 0 through
 // LDS (one write and one read per block) instead of lane shuffles.
-template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0, bool LG = false,
-          int KS6 = SPLIT>
-__global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
-                                                           const uint8_t* __restrict__ w1,
-                                                           const uint8_t* q8, float* __restrict__ out,
-                                                           int nb_rt, int d, int32_t* __restrict__ dbgS,
-                                                           int32_t* __restrict__ dbgM, const float* __restrict__ xin,
-                                                           uint8_t* __restrict__ q8_store,
-                                                           const float* __restrict__ aux, const ResidualArgs ra,
-                                                           const Stack2 st, const MergeArgs mg) {
+//
+// The body runs as workgroup bid with thread index tid (a workgroup of WG
+// threads); q8s: 292 bytes of LDS for the QIN path's Q8_K block; xload(t):
+// the QIN input float4 of lane t (XL: read after the weight loads are
+// issued instead of before); put(o, row, v) stores an output.
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG, int PRO, bool LG, int KS6, bool XL,
+          typename XIn, typename Put>
+__device__ __forceinline__ void q45_rows_body(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                              const uint8_t* q8, float* __restrict__ out, int nb_rt, int d,
+                                              int32_t* __restrict__ dbgS, int32_t* __restrict__ dbgM,
+                                              uint8_t* __restrict__ q8_store, const float* __restrict__ aux,
+                                              const ResidualArgs& ra, const Stack2& st, const MergeArgs& mg, int bid,
+                                              int tid, uint8_t* q8s, XIn&& xload, Put&& put) {
     static_assert(!QIN || (WG == 64 && NB == 1), "the single-block input path runs one wave over one block");
     static_assert(!PRO || (WG == 64 * NB && NB > 0 && !DBG), "the prologue needs one wave per block");
     static_assert(PRO != 2 || NMAT == 1, "the merge prologue feeds one matrix");
     constexpr int GL = 8 * SPLIT;                               // lanes per row
     constexpr int NH = NB > 0 ? (NB + SPLIT - 1) / SPLIT : 1;   // blocks per group (unrolled case)
     const int nb = NB > 0 ? NB : nb_rt;
-    const int tid = threadIdx.x, l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
-    const int row_ = blockIdx.x * (WG / GL) + tid / GL;
+    const int l = tid & 7, k = l & 3, grp = SPLIT > 1 ? (tid >> 3) & (SPLIT - 1) : 0;
+    const int row_ = bid * (WG / GL) + tid / GL;
     // with the prologue (or the input quantized in the wave) every thread
     // stays for its barriers; rows past the end compute the last row and do
     // not store.  Rows d.. d+st.d-1 (PRO only) belong to the stacked second
@@ -441,7 +444,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             extern __shared__ __align__(16) float pbuf[];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf);
             quantize_block_wave(r, lane, q8l, NB, v);
-            if (blockIdx.x == 0) {
+            if (bid == 0) {
                 if (mg.out) reinterpret_cast<float4*>(mg.out)[tid] = make_float4(r[0], r[1], r[2], r[3]);
                 if (mg.q8) quantize_block_wave(r, lane, mg.q8, NB, v);
             }
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             // take the Q6_K tensor (st.w6) on the fp32 normed vector.
             constexpr int rpw = WG / GL;
             const int qk_wgs = (dtot + rpw - 1) / rpw;
-            const bool vwg = st.w6 != nullptr && (int)blockIdx.x >= qk_wgs;
+            const bool vwg = st.w6 != nullptr && bid >= qk_wgs;
             Res4 r4;
             residual4_load(ra, r4, 0);
             if (!vwg) {
@@ -483,13 +486,13 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             __shared__ float red[2][16];
             uint8_t* q8l = reinterpret_cast<uint8_t*>(pbuf + NB * 256);
             if (vwg) {
-                q6k_prologue_rows<NB, WG, KS6>(st, blockIdx.x - qk_wgs, ra, r4, pbuf, red);
+                q6k_prologue_rows<NB, WG, KS6>(st, bid - qk_wgs, ra, r4, pbuf, red);
                 return;
             }
             float qv[4], nv[4];
-            residual4_finish(ra, r4, red, blockIdx.x == 0, 0, qv, nv);
+            residual4_finish(ra, r4, red, bid == 0, 0, qv, nv);
             quantize_block_wave(qv, tid & 63, q8l, NB, tid >> 6);
-            if (blockIdx.x == 0 && ra.q8) quantize_block_wave(qv, tid & 63, ra.q8, NB, tid >> 6);
+            if (bid == 0 && ra.q8) quantize_block_wave(qv, tid & 63, ra.q8, NB, tid >> 6);
             lds_sync();
             const uint8_t* a_qs_l = q8l + 32 * l;
             const uint8_t* a_bs_l = q8l + q8k_bsums_off(NB) + 8 * k;
@@ -509,12 +512,13 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
             // 256 inputs into LDS (workgroup 0 also stores them) while the
             // weights are in flight (the load counter retires in order: the
             // quantize waits only for what was issued before the weights)
-            const float4 f = reinterpret_cast<const float4*>(xin)[tid];
+            float4 f;
+            if constexpr (!XL) f = xload(tid);
             load_w(0, raw[0]);
-            __shared__ __align__(16) uint8_t q8s[292];
+            if constexpr (XL) f = xload(tid);
             const float v[4] = {f.x, f.y, f.z, f.w};
             quantize_block_wave(v, tid, q8s, 1, 0);
-            if (blockIdx.x == 0 && q8_store) quantize_block_wave(v, tid, q8_store, 1, 0);
+            if (bid == 0 && q8_store) quantize_block_wave(v, tid, q8_store, 1, 0);
             __syncthreads();
             raw[0].a0 = *reinterpret_cast<const uint4*>(q8s + 32 * l);
             raw[0].a1 = *reinterpret_cast<const uint4*>(q8s + 32 * l + 16);
@@ -615,9 +619,103 @@ __global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __rest
         }
     }
     if (l == 0 && grp == 0 && row_ < dtot) {
-        if (NMAT == 2) outp[rl] = gelu_ref(r[0]) * r[NMAT - 1];
-        else outp[rl] = aux ? gelu_ref(r[0]) * aux_v : r[0];
+        if (NMAT == 2) put(outp, rl, gelu_ref(r[0]) * r[NMAT - 1]);
+        else put(outp, rl, aux ? gelu_ref(r[0]) * aux_v : r[0]);
     }
+}
+
+template <bool Q5, int NMAT, bool DBG, int NB, int SPLIT, bool QIN, int WG = 64, int PRO = 0, bool LG = false,
+          int KS6 = SPLIT>
+__global__ __launch_bounds__(WG) void gemv_q45_rows_kernel(const uint8_t* __restrict__ w0,
+                                                           const uint8_t* __restrict__ w1,
+                                                           const uint8_t* q8, float* __restrict__ out,
+                                                           int nb_rt, int d, int32_t* __restrict__ dbgS,
+                                                           int32_t* __restrict__ dbgM, const float* __restrict__ xin,
+                                                           uint8_t* __restrict__ q8_store,
+                                                           const float* __restrict__ aux, const ResidualArgs ra,
+                                                           const Stack2 st, const MergeArgs mg) {
+    __shared__ __align__(16) uint8_t q8s[QIN ? 292 : 16];
+    q45_rows_body<Q5, NMAT, DBG, NB, SPLIT, QIN, WG, PRO, LG, KS6, false>(
+        w0, w1, q8, out, nb_rt, d, dbgS, dbgM, q8_store, aux, ra, st, mg, blockIdx.x, threadIdx.x, q8s,
+        [&](int t) { return reinterpret_cast<const float4*>(xin)[t]; },
+        [](float* o, int row, float v) { o[row] = v; });
+}
+
+// ------------------------------------------------------------------------
+// The PLE gate and projection of a decode layer in one launch
+// (main.c:1982-1994)
+// ------------------------------------------------------------------------
+// Workgroups [0, P) are g4_mm_residual_q8's PLE-gate workgroups (the
+// residual step of the FFN output, Q8_K of x', gelu(gate . q8) * ple: the
+// same bits), each storing its values as (value, sequence) pairs, one 64-bit
+// device-scope store per value.  Workgroups [P, P + C) run the projection,
+// one wave per 8 rows as the single-block-input GEMV does (mm() quantizing
+// the 256 gate values: the same bits); each wave issues its weight block and
+// then polls the pairs until all 256 carry this call's sequence number.  A
+// pair is written and read whole, so no flag, fence or store
+// acknowledgement is waited for; the sequence number (*seq, which the caller
+// changes between calls on one buffer) keeps an earlier call's values from
+// counting.  The gate workgroups have the lowest ids and are dispatched
+// first; a poll gives up after kPleSpins rounds and sets the error word.
+constexpr int kPleNB = 10;                 // n / 256: one wave per Q8_K block
+constexpr int kPleGateRows = 64 * kPleNB / 32;   // gate rows per workgroup (32 lanes a row)
+constexpr int kPleProjRows = 8 * kPleNB;   // projection rows per workgroup (8 a wave)
+constexpr uint32_t kPleSpins = 1u << 20;
+
+__host__ __device__ inline size_t ple_pair_words(int pd) { return ((size_t)pd + 1) & ~(size_t)1; }
+
+template <bool Q5G, bool Q5P>
+__global__ __launch_bounds__(64 * kPleNB) void ple_fused_kernel(const uint8_t* __restrict__ wg,
+                                                              const uint8_t* __restrict__ wp, float* __restrict__ y,
+                                                              int pd, int dp, const float* __restrict__ mul,
+                                                              const ResidualArgs ra, unsigned long long* pairs,
+                                                              const uint32_t* seq) {
+    const int P = (pd + kPleGateRows - 1) / kPleGateRows;
+    const uint32_t sq = *seq;
+    if ((int)blockIdx.x < P) {
+        q45_rows_body<Q5G, 1, false, kPleNB, 4, false, 64 * kPleNB, 1, true, 4, false>(
+            wg, nullptr, nullptr, nullptr, kPleNB, pd, nullptr, nullptr, nullptr, mul, ra, Stack2{}, MergeArgs{},
+            blockIdx.x, threadIdx.x, nullptr, [](int) { return make_float4(0.0f, 0.0f, 0.0f, 0.0f); },
+            [&](float*, int row, float v) {
+                __hip_atomic_store(pairs + row, ((unsigned long long)sq << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            });
+        return;
+    }
+    __shared__ __align__(16) uint8_t q8s[kPleNB][292];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t* err = reinterpret_cast<uint32_t*>(pairs + ple_pair_words(pd));
+    q45_rows_body<Q5P, 1, false, 1, 1, true, 64, 0, false, 1, true>(
+        wp, nullptr, nullptr, y, 1, dp, nullptr, nullptr, nullptr, nullptr, ResidualArgs{}, Stack2{}, MergeArgs{},
+        ((int)blockIdx.x - P) * kPleNB + wave, lane, q8s[wave],
+        [&](int t) {
+            // wave 0 polls (lane t: values 4t .. 4t+3, the float4 the
+            // single-block path quantizes; pd = 256, checked by the launcher)
+            // and hands the values to the other waves through LDS
+            __shared__ __align__(16) float gv[256];
+            if (wave == 0) {
+                unsigned long long a[4];
+                for (uint32_t spins = 0;; spins++) {
+                    bool ok = true;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        a[j] = __hip_atomic_load(pairs + 4 * t + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ok = ok && (uint32_t)(a[j] >> 32) == sq;
+                    }
+                    if (__all(ok)) break;
+                    if (spins >= kPleSpins) {
+                        if (t == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                reinterpret_cast<float4*>(gv)[t] = make_float4(__uint_as_float((uint32_t)a[0]), __uint_as_float((uint32_t)a[1]),
+                                                              __uint_as_float((uint32_t)a[2]), __uint_as_float((uint32_t)a[3]));
+            }
+            lds_sync();
+            return reinterpret_cast<const float4*>(gv)[t];
+        },
+        [](float* o, int row, float v) { o[row] = v; });
 }
 
 // ------------------------------------------------------------------------
@@ -1829,4 +1927,41 @@ extern "C" int g4_mm_attn_merge(float* o, const void* w, int n, int d, int type,
     default: return g4_fail(G4_ERR_ARG, "g4_mm_attn_merge: %d heads of %d (n = 2048 or 4096)", n_heads, hd);
     }
     return g4_check_launch("gemv_q45_rows_kernel<merge>");
+}
+
+// The PLE gate and projection of a decode layer in one launch (see
+// ple_fused_kernel): pairs holds g4_ple_pairs_bytes(pd) bytes, zeroed before
+// the first call.
+extern "C" size_t g4_ple_pairs_bytes(int pd) { return pd > 0 ? ple_pair_words(pd) * 8 + 16 : 0; }
+
+extern "C" int g4_mm_ple_gate_proj(float* y, const void* w_proj, int type_proj, int d_proj, const void* w_gate,
+                                   int type_gate, int n, int pd, const float* mul, const float* x, float* x_out,
+                                   const float* y_in, const float* w_post, float eps, void* pairs,
+                                   const uint32_t* seq) {
+    const char* who = "g4_mm_ple_gate_proj";
+    G4_CHECK_ARG(y && w_proj && w_gate && mul && x && x_out && y_in && w_post && pairs && seq, "%s: null pointer", who);
+    G4_CHECK_ARG(n == 256 * kPleNB && pd == 256 && d_proj > 0, "%s: n=%d pd=%d d_proj=%d (n = %d, pd = 256)", who, n,
+                 pd, d_proj, 256 * kPleNB);
+    G4_CHECK((type_gate == G4_Q4_K || type_gate == G4_Q5_K) && (type_proj == G4_Q4_K || type_proj == G4_Q5_K),
+             G4_ERR_TYPE, "%s: types %d / %d not supported", who, type_gate, type_proj);
+    G4_CHECK_ARG(aligned16(w_proj) && aligned16(w_gate) && aligned16(x) && aligned16(x_out) && aligned16(y_in) &&
+                     aligned16(w_post) && aligned16(pairs),
+                 "%s: weights, x, x_out, y_in, w_post and pairs must be 16-byte aligned", who);
+    G4_CHECK_ARG(x_out != x && (const float*)y != x && y != x_out && (const float*)y != y_in,
+                 "%s: x_out must differ from x, y from x, x_out and y_in", who);
+    const ResidualArgs ra{x, x_out, y_in, w_post, nullptr, nullptr, nullptr, nullptr, 1, n, eps};
+    constexpr int NB = kPleNB, WG = 64 * NB;
+    const size_t lds = (size_t)NB * 256 * 4 + (((size_t)NB * 292 + 15) & ~(size_t)15) + (size_t)NB * 32 * 4 +
+                       (size_t)WG / 8 * 4;
+    const int wgs = (pd + kPleGateRows - 1) / kPleGateRows + (d_proj + kPleProjRows - 1) / kPleProjRows;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(wgs), dim3(WG), lds, g4_stream(), (const uint8_t*)w_gate, (const uint8_t*)w_proj,
+                           y, pd, d_proj, mul, ra, (unsigned long long*)pairs, seq);
+    };
+    const bool q5g = type_gate == G4_Q5_K, q5p = type_proj == G4_Q5_K;
+    if (!q5g && !q5p) go(ple_fused_kernel<false, false>);
+    else if (!q5g) go(ple_fused_kernel<false, true>);
+    else if (!q5p) go(ple_fused_kernel<true, false>);
+    else go(ple_fused_kernel<true, true>);
+    return g4_check_launch("ple_fused_kernel");
 }

@@ -68,14 +68,16 @@ __global__ __launch_bounds__(256) void emb_rope_kernel(float* __restrict__ o, co
 // take 8 rows of ctx each (4 waves x 2 rows, gemv_bf16_kernel's dot: the
 // same bits), issue their weight loads, then rebuild x = table row * scale
 // in LDS themselves (emb_rope_kernel's values) while the weights are in
-// flight; workgroup 0 also stores x.  Workgroups gx and gx + 1 write the two
-// RoPE tables.
+// flight; workgroup 0 also stores x (and advances the step's sequence word
+// *seq, if given).  Workgroups gx and gx + 1 write the two RoPE tables.
 template <int RPW, int CPL>
 __global__ __launch_bounds__(256) void emb_ple_kernel(float* __restrict__ o, const void* emb, int type, int rows,
                                                       int dim, const int* dtok, float scale,
                                                       const uint16_t* __restrict__ w, float* __restrict__ ctx, int d,
-                                                      const int* dpos, float fs, RopeTab ta, RopeTab tb) {
+                                                      const int* dpos, float fs, RopeTab ta, RopeTab tb,
+                                                      uint32_t* seq) {
     const int gx = (d + 4 * RPW - 1) / (4 * RPW);
+    if (seq && blockIdx.x == 0 && threadIdx.x == 0) *seq += 1u;
     if ((int)blockIdx.x >= gx) {
         const RopeTab& t = (int)blockIdx.x == gx ? ta : tb;
         const int p = *dpos;
@@ -338,7 +340,7 @@ extern "C" int g4_emb_lookup_rope(float* o, const void* w, int type, int rows, c
 extern "C" int g4_emb_lookup_rope_ple(float* o, const void* w, int type, int rows, const int* dtok, int dim,
                                       float scale, const int* dpos, float* tab_a, int n_rot_a, float base_a,
                                       const float* ff_a, float* tab_b, int n_rot_b, float base_b, const float* ff_b,
-                                      float freq_scale, float* ctx, const void* w_ctx, int d_ctx) {
+                                      float freq_scale, float* ctx, const void* w_ctx, int d_ctx, uint32_t* seq) {
     G4_CHECK_ARG(o && w && dtok && dim > 0 && rows > 0 && dpos && ctx && w_ctx && d_ctx > 0,
                  "g4_emb_lookup_rope_ple: bad arguments");
     G4_CHECK(table_type_ok(type), G4_ERR_TYPE, "Unsupported emb type %d", type);
@@ -355,7 +357,7 @@ extern "C" int g4_emb_lookup_rope_ple(float* o, const void* w, int type, int row
     const uint16_t* wp = (const uint16_t*)w_ctx;
     auto go = [&](auto kern, int rpw) {
         hipLaunchKernelGGL(kern, dim3((d_ctx + 4 * rpw - 1) / (4 * rpw) + 2), dim3(256), lds, g4_stream(), o, w, type,
-                           rows, dim, dtok, scale, wp, ctx, d_ctx, dpos, freq_scale, ta, tb);
+                           rows, dim, dtok, scale, wp, ctx, d_ctx, dpos, freq_scale, ta, tb, seq);
     };
     const int cpl = (dim / 8 + 63) / 64;
     if (cpl <= 4) go(emb_ple_kernel<4, 4>, 4);

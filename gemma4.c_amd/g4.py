@@ -123,7 +123,9 @@ _SIGS = {
     "g4_attn_decode_fused": (I, [VP, VP, VP, VP, VP, VP, VP, VP, VP, I, I, VP, I, I, I, I, I, VP, F, F, I, VP, VP, VP]),
     "g4_emb_lookup_dev": (I, [VP, VP, I, I, VP, I, F]),
     "g4_emb_lookup_rope": (I, [VP, VP, I, I, VP, I, F, VP, VP, I, F, VP, VP, I, F, VP, F]),
-    "g4_emb_lookup_rope_ple": (I, [VP, VP, I, I, VP, I, F, VP, VP, I, F, VP, VP, I, F, VP, F, VP, VP, I]),
+    "g4_emb_lookup_rope_ple": (I, [VP, VP, I, I, VP, I, F, VP, VP, I, F, VP, VP, I, F, VP, F, VP, VP, I, VP]),
+    "g4_ple_pairs_bytes": (SZ, [I]),
+    "g4_mm_ple_gate_proj": (I, [VP, VP, I, I, VP, I, I, I, VP, VP, VP, VP, VP, F, VP, VP]),
     "g4_ple_finish": (I, [VP, VP, VP, I, I, VP, VP, I, I, I, F, F, F, F]),
     "g4_gelu_mul_quant": (I, [VP, VP, I, VP]),
     "g4_store_i32x2": (I, [VP, I, I]),

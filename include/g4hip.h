@@ -171,6 +171,27 @@ int g4_mm_residual_q8_qkv(float *o1, const void *w1, int d1, float *o2, const vo
 int g4_mm_attn_merge(float *o, const void *w, int n, int d, int type, const float *part, int G, int n_heads, int hd,
                      float *q_out, void *q8);
 
+/* The PLE gate and projection of a decode layer in one launch
+ * (main.c:1982-1994): the residual step of g4_mm_residual_q8 with qsrc 1
+ * (post_ffw_norm of y_in into x_out = x + norm(y_in) * w_post, Q8_K of
+ * x_out), g = gelu(w_gate . q8) * mul (pd rows, the PLE gate), then
+ * y = mm(w_proj, g) (d_proj rows of one block: g quantized to Q8_K as mm()
+ * does) -- the same bits as g4_mm_residual_q8(g, w_gate, NULL, n, pd, ...,
+ * mul, ..., qsrc 1) followed by g4_mm(y, g, w_proj, pd, d_proj, ...).  The
+ * gate values cross workgroups as (value, *seq) pairs in `pairs`
+ * (g4_ple_pairs_bytes(pd) bytes of device memory, zeroed before the first
+ * call): *seq must differ between calls that share `pairs` and must not be
+ * 0 (g4_emb_lookup_rope_ple advances such a word once per decode step; give
+ * each layer its own pairs).  The word after the pairs becomes nonzero if a
+ * call's projection could not read the gate values (never expected; its y
+ * is then invalid).  n = 2560, pd = 256 only; gate and projection Q4_K or
+ * Q5_K.  No counterpart in the reference, which runs the two as separate
+ * mm() calls. */
+size_t g4_ple_pairs_bytes(int pd);
+int g4_mm_ple_gate_proj(float *y, const void *w_proj, int type_proj, int d_proj, const void *w_gate, int type_gate,
+                        int n, int pd, const float *mul, const float *x, float *x_out, const float *y_in,
+                        const float *w_post, float eps, void *pairs, const uint32_t *seq);
+
 /* ---------------------------------------------------------------------------
  * Batched prefill GEMM.  The reference has none: generate() runs forward()
  * once per prompt token (main.c:2366-2384), so for m tokens it performs m
@@ -440,11 +461,13 @@ int g4_emb_lookup_rope(float *o, const void *w, int type, int rows, const int *d
 /* ... and the PLE context projection of build_ple on the same row
  * (main.c:1749-1750: ctx = mm_bf16(w_ctx, o), w_ctx bf16 [d_ctx x dim]) in
  * the same launch: the same values as g4_emb_lookup_rope followed by
- * g4_mm_bf16(ctx, o, w_ctx, dim, d_ctx).  dim a multiple of 8, <= 4096. */
+ * g4_mm_bf16(ctx, o, w_ctx, dim, d_ctx).  dim a multiple of 8, <= 4096.
+ * seq (nullable): a device word the launch increments by one (the step's
+ * sequence number for g4_mm_ple_gate_proj). */
 int g4_emb_lookup_rope_ple(float *o, const void *w, int type, int rows, const int *dtok, int dim, float scale,
                            const int *dpos, float *tab_a, int n_rot_a, float base_a, const float *ff_a, float *tab_b,
                            int n_rot_b, float base_b, const float *ff_b, float freq_scale, float *ctx,
-                           const void *w_ctx, int d_ctx);
+                           const void *w_ctx, int d_ctx, uint32_t *seq);
 /* build_ple after its projection (main.c:1751-1777): ple[l*pd+i] =
  * (emb(ple_tok, tok)[l*pd+i]*sc_tok + rmsnorm(ctx[l*pd..]*sc_ctx, norm)[i]) * mix;
  * tok = *dtok if dtok else tok. */

@@ -591,3 +591,48 @@ def test_softcap(lib):
     inv = np.float32(1.0) / np.float32(30.0)
     want = 30.0 * np.tanh((v * inv).astype(np.float64))
     assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) < 2e-6
+
+
+@pytest.mark.parametrize("qg,qp", [(12, 12), (13, 12), (12, 13)])
+def test_mm_ple_gate_proj(lib, orc, qg, qp):
+    """The PLE gate and projection in one launch (g4_mm_ple_gate_proj):
+    y and x_out equal, bit for bit, to g4_mm_residual_q8 (qsrc 1, gelu * mul)
+    followed by g4_mm on the 256 gate values, over three calls on one pairs
+    buffer with the sequence word advanced between them (new inputs each
+    time, so values left from an earlier call would show); y also against
+    the oracle: mm_quant_dot_rows of the projection on quantize_row_q8_K of
+    the gate values."""
+    from g4 import DBuf, upload_quant
+    n, pd, dp = 2560, 256, 2560
+    rng = np.random.default_rng(70 + qg + 3 * qp)
+    g_raw = synth.rand_kquant(rng, qg, pd, n)
+    p_raw = synth.rand_kquant(rng, qp, dp, pd)
+    wg, wp = upload_quant(lib, g_raw, qg, n, pd), upload_quant(lib, p_raw, qp, pd, dp)
+    pairs = DBuf(lib, lib.L.g4_ple_pairs_bytes(pd))
+    lib.g4_memset(pairs.ptr, 0, lib.L.g4_ple_pairs_bytes(pd))
+    seq = dbuf(lib, np.array([0], np.uint32))
+    eps = C.c_float(1e-6)
+    for call in range(3):
+        lib.g4_memcpy_h2d(seq.ptr, P(np.array([call + 1], np.uint32)), 4)
+        x = rng.standard_normal(n).astype(np.float32)
+        y_in = (rng.standard_normal(n) * 4).astype(np.float32)
+        wpost = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        mul = rng.standard_normal(pd).astype(np.float32)
+        xd, yd, wpd, muld = dbuf(lib, x), dbuf(lib, y_in), dbuf(lib, wpost), dbuf(lib, mul)
+        xo, y = DBuf(lib, 4 * n), DBuf(lib, 4 * dp)
+        lib.g4_mm_ple_gate_proj(y.ptr, wp.ptr, qp, dp, wg.ptr, qg, n, pd, muld.ptr, xd.ptr, xo.ptr, yd.ptr, wpd.ptr,
+                                eps, pairs.ptr, seq.ptr)
+        xo2, g2, y2 = DBuf(lib, 4 * n), DBuf(lib, 4 * pd), DBuf(lib, 4 * dp)
+        q8a, q8b = DBuf(lib, lib.L.g4_q8K_bytes(n)), DBuf(lib, lib.L.g4_q8K_bytes(pd))
+        lib.g4_mm_residual_q8(g2.ptr, wg.ptr, None, n, pd, qg, muld.ptr, xd.ptr, xo2.ptr, yd.ptr, wpd.ptr, None, None,
+                              None, q8a.ptr, 1, eps)
+        lib.g4_mm(y2.ptr, g2.ptr, wp.ptr, pd, dp, qp, q8b.ptr, 0)
+        lib.g4_sync()
+        assert np.array_equal(y.to_array(np.uint32), y2.to_array(np.uint32)), f"call {call}: y"
+        assert np.array_equal(xo.to_array(np.uint32), xo2.to_array(np.uint32)), f"call {call}: x_out"
+        words = pairs.to_array(np.uint32)
+        assert np.all(words[1:2 * pd:2] == call + 1) and words[2 * pd] == 0
+        assert np.array_equal(words[0:2 * pd:2], g2.to_array(np.uint32))
+    g = g2.to_array(np.float32)
+    want = orc.mm_quant_dot_rows(p_raw, pd, dp, qp, orc.quantize_q8K(g))
+    assert np.array_equal(y.to_array(np.float32).view(np.uint32), want.view(np.uint32))

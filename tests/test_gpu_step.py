@@ -457,15 +457,17 @@ def test_emb_lookup_rope_ple(lib, orc, qtype, pos, d_ctx):
     ffd = dbuf(lib, ff)
     dtok, dpos = dbuf(lib, np.array([tok], np.int32)), dbuf(lib, np.array([pos], np.int32))
     out, ta, tb, ctx = DBuf(lib, 4 * dim), DBuf(lib, 4 * 256), DBuf(lib, 4 * 512), DBuf(lib, 4 * d_ctx)
+    seq = dbuf(lib, np.array([41], np.uint32))
     lib.g4_emb_lookup_rope_ple(out.ptr, w.ptr, qtype, rows, dtok.ptr, dim, C.c_float(scale), dpos.ptr, ta.ptr, 256,
                                C.c_float(1e4), None, tb.ptr, 512, C.c_float(1e6), ffd.ptr, C.c_float(1.0), ctx.ptr,
-                               wc.ptr, d_ctx)
+                               wc.ptr, d_ctx, seq.ptr)
     out2, ta2, tb2, ctx2 = DBuf(lib, 4 * dim), DBuf(lib, 4 * 256), DBuf(lib, 4 * 512), DBuf(lib, 4 * d_ctx)
     lib.g4_emb_lookup_rope(out2.ptr, w.ptr, qtype, rows, dtok.ptr, dim, C.c_float(scale), dpos.ptr, ta2.ptr, 256,
                            C.c_float(1e4), None, tb2.ptr, 512, C.c_float(1e6), ffd.ptr, C.c_float(1.0))
     lib.g4_mm_bf16(ctx2.ptr, out2.ptr, wc.ptr, dim, d_ctx)
     for a, b in ((out, out2), (ta, ta2), (tb, tb2), (ctx, ctx2)):
         assert np.array_equal(a.to_array(np.uint32), b.to_array(np.uint32))
+    assert seq.to_array(np.uint32)[0] == 42   # advanced once
     want = np.empty(dim, np.float32)
     assert orc.L.or_emb_lookup(P(want), P(raw), qtype, tok, dim) == 0
     x = want * scale
