@@ -773,7 +773,9 @@ __host__ __device__ inline size_t attn_chunk_lds(int hd, int kvm_pow2, int nw = 
 // reduced (decode: few workgroups, each one's latency counts); without it
 // the register count allows twice the workgroups per CU (prompt-chunk rows:
 // thousands of workgroups, occupancy counts)
-template <int HD, int KVM, bool DB, int NTH = kAttnThreads, int PPW_ = 0>
+// FZ: 0 the fused norms decided at run time (a.q_norm), 1 fused (known at
+// compile time: the SPL form below), 2 not fused
+template <int HD, int KVM, bool DB, int NTH = kAttnThreads, int PPW_ = 0, int FZ = 0>
 __global__ __launch_bounds__(NTH) void attn_chunk_kernel(AttnArgs a) {
     if (a.qrows) attn_query_row(a, false);
     constexpr int W = HD / 128;
@@ -786,18 +788,37 @@ __global__ __launch_bounds__(NTH) void attn_chunk_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];   // [NW][KVM][HD] o, then [NW][KVM] (max, sum)
     const int c = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvm = a.n_heads / a.n_kv;
-    const bool fuse = a.q_norm != nullptr;
+    const bool fuse = FZ == 1 || (FZ == 0 && a.q_norm != nullptr);
     const bool append = fuse && a.kraw != nullptr;
 
     // q heads of this kv head (heads past kvm repeat the last one; unused),
     // the norm weights, the RoPE pairs and the raw K/V of this position:
-    // issued first, so their arithmetic waits only for them
+    // issued first, so their arithmetic waits only for them.  SPL (fused, a
+    // wave for each vector): wave w < KVM takes q head w, wave KVM this
+    // position's K, wave KVM + 1 its V; each normalises (and rotates) its
+    // vector alone and every wave reads all of them back from LDS, instead of
+    // every wave repeating the KVM + 2 norms
+    constexpr bool SPL = FZ == 1 && NW >= KVM + 2;
     HVec<HD> q[KVM];
-#pragma unroll
-    for (int h = 0; h < KVM; h++) q[h].load(a.q + (size_t)(kvh * kvm + min(h, kvm - 1)) * HD, lane);
-    HVec<HD> wq, wk, kn, vn;
+    HVec<HD> wq, wk, kn, vn, mine, wmine;
     float2 rc[W];
-    if (fuse) {
+    const int wvu = __builtin_amdgcn_readfirstlane(wave);   // the wave index as a scalar
+    if (SPL && fuse) {
+        // every wave loads one vector and one weight vector (no load under a
+        // condition: the pointers are selected per wave)
+        const bool kv_wave = append && (wvu == KVM || wvu == KVM + 1);
+        const float* src = wvu < KVM ? a.q + (size_t)(kvh * kvm + min(wvu, kvm - 1)) * HD
+                           : kv_wave ? (wvu == KVM ? a.kraw : a.vraw) + (size_t)kvh * HD
+                                     : a.q;
+        mine.load(src, lane);
+        wmine.load(wvu == KVM && append ? a.k_norm : a.q_norm, lane);
+#pragma unroll
+        for (int i = 0; i < W; i++) rc[i] = a.tab[min(W * lane + i, a.n_rot / 2 - 1)];
+    } else {
+#pragma unroll
+        for (int h = 0; h < KVM; h++) q[h].load(a.q + (size_t)(kvh * kvm + min(h, kvm - 1)) * HD, lane);
+    }
+    if (!SPL && fuse) {
         wq.load(a.q_norm, lane);
 #pragma unroll
         // every lane loads a pair (clamped: n_rot >= 2 is checked at
@@ -835,29 +856,50 @@ __global__ __launch_bounds__(NTH) void attn_chunk_kernel(AttnArgs a) {
     const float* kbase = a.kc + (size_t)kvh * HD;
     const float* vbase = a.vc + (size_t)kvh * HD;
     HVec<HD> kr[PPW], vr[PPW], kr2[DB ? PPW : 1], vr2[DB ? PPW : 1];
+    // an empty chunk (cnt 0) loads one row it will not use, in bounds: slot 0
+    // of a ring, else the window's last position (so the first round's loads
+    // are issued unconditionally: behind a branch the compiler made the
+    // norms below wait for them)
+    const int t_last = t0 + max(nwin, 1) - 1;
     auto load_kv = [&](HVec<HD>* K, HVec<HD>* Vv, int r) {
 #pragma unroll
         for (int p = 0; p < PPW; p++) {
-            const int i = min(r * NW * PPW + wave * PPW + p, cnt - 1);
-            const int t = cb + i;   // position (position mode; prompt-chunk rows only)
+            const int i = min(r * NW * PPW + wave * PPW + p, max(cnt - 1, 0));
+            const int t = cnt > 0 ? cb + i : t_last;   // position (position mode; prompt-chunk rows only)
             if (a.kchunk && t >= a.p0) {
                 const size_t off = (size_t)(t - a.p0) * a.kv_stride + (size_t)kvh * HD;
                 K[p].load(a.kchunk + off, lane);
                 Vv[p].load(a.vchunk + off, lane);
             } else {
-                K[p].load(kbase + (size_t)slot_of(i) * a.kv_stride, lane);
-                Vv[p].load(vbase + (size_t)slot_of(i) * a.kv_stride, lane);
+                const int sl = cnt > 0 ? slot_of(i) : slotm ? 0 : attn_slot(a, t_last);
+                K[p].load(kbase + (size_t)sl * a.kv_stride, lane);
+                Vv[p].load(vbase + (size_t)sl * a.kv_stride, lane);
             }
         }
     };
-    if (cnt > 0) load_kv(kr, vr, 0);
+    load_kv(kr, vr, 0);
     // the position (slot mode: not needed by the loads above)
     const int dpv = slotm ? *a.dpos : 0;
     __builtin_amdgcn_sched_barrier(0);   // the loads are in flight before anything waits
 
     // per-head norms and RoPE (q; this position's K and V, whichever
     // workgroup turns out to own the position)
-    if (fuse) {
+    if (SPL && fuse) {
+        __shared__ __align__(16) float stg[SPL ? (KVM + 2) * HD : 1];
+        if (wvu < KVM || (append && wvu < KVM + 2)) {
+            const bool isv = wvu == KVM + 1;
+            norm_vec<HD>(mine, isv ? nullptr : &wmine, a.eps);
+            if (!isv) rope_vec<HD>(mine, rc, lane, a.n_rot);
+            mine.store(stg + wvu * HD, lane);
+        }
+        lds_sync();
+#pragma unroll
+        for (int h = 0; h < KVM; h++) q[h].load(stg + h * HD, lane);
+        if (append) {
+            kn.load(stg + KVM * HD, lane);
+            vn.load(stg + (KVM + 1) * HD, lane);
+        }
+    } else if (fuse) {
 #pragma unroll
         for (int h = 0; h < KVM; h++) {
             norm_vec<HD>(q[h], &wq, a.eps);
@@ -1496,12 +1538,14 @@ void launch_chunk(const AttnArgs& a, int kp, const dim3& grid) {
     // merge); the E4B decode step with its 512-slot rings in 16 chunks:
     // 2.258 against 2.292 ms
     if (kp == 4) {
-        if constexpr (HD == 256)
-            hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true, 512, 4>), grid, dim3(512), attn_chunk_lds(HD, kp, 8),
-                               g4_stream(), a);
-        else
-            hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false, 512>), grid, dim3(512), attn_chunk_lds(HD, kp, 8),
-                               g4_stream(), a);
+        const size_t l8 = attn_chunk_lds(HD, kp, 8);
+        if constexpr (HD == 256) {
+            if (a.q_norm) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true, 512, 4, 1>), grid, dim3(512), l8, g4_stream(), a);
+            else hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, true, 512, 4, 2>), grid, dim3(512), l8, g4_stream(), a);
+        } else {
+            if (a.q_norm) hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false, 512, 0, 1>), grid, dim3(512), l8, g4_stream(), a);
+            else hipLaunchKernelGGL((attn_chunk_kernel<HD, 4, false, 512, 0, 2>), grid, dim3(512), l8, g4_stream(), a);
+        }
         return;
     }
     if (kp == 1) hipLaunchKernelGGL((attn_chunk_kernel<HD, 1, true>), grid, dim3(kAttnThreads), lds, g4_stream(), a);
