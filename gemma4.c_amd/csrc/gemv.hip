@@ -422,21 +422,25 @@ __device__ __forceinline__ void q45_rows_body(const uint8_t* __restrict__ w0, co
             }
 #pragma unroll
             for (int i = 0; i < NH; i++) load_w(min(grp * NH + i, nb - 1), raw[i]);
+            __builtin_amdgcn_sched_barrier(0);   // every load issued before the merge waits
             const float mgv = lane < G ? ml.x : -INFINITY;
             const float lgv = lane < G ? ml.y : 0.0f;
             const float M = wave_max(mgv);
             const float f = lane < G && lgv > 0.0f ? expf(mgv - M) : 0.0f;
             const float L = wave_sum(lane < G ? 0.0f + lgv * f : 0.0f);
             float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            // chunk 0 always counts (G >= 1) and the chunks past G are
+            // selected away rather than skipped: under a branch the compiler
+            // moved chunk 0's loads into it and waited there for every load
+            // issued before (the weights)
 #pragma unroll
             for (int u = 0; u < kMergeMaxG; u++) {
-                if (u < G) {
-                    const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), u));
-                    o[0] = __builtin_fmaf(oa[u].x, fu, o[0]);
-                    o[1] = __builtin_fmaf(oa[u].y, fu, o[1]);
-                    o[2] = __builtin_fmaf(ob[u].x, fu, o[2]);
-                    o[3] = __builtin_fmaf(ob[u].y, fu, o[3]);
-                }
+                const float fu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), u));
+                const bool on = u == 0 || u < G;
+                o[0] = on ? __builtin_fmaf(oa[u].x, fu, o[0]) : o[0];
+                o[1] = on ? __builtin_fmaf(oa[u].y, fu, o[1]) : o[1];
+                o[2] = on ? __builtin_fmaf(ob[u].x, fu, o[2]) : o[2];
+                o[3] = on ? __builtin_fmaf(ob[u].y, fu, o[3]) : o[3];
             }
             float r[4];
 #pragma unroll
