@@ -1126,6 +1126,66 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
+// The same merge for 32 < G <= 128 with 1024 threads: thread (c, dim), c =
+// tid / 256, takes chunks c, c + 4, ..., so a workgroup has four times the
+// loads of the 256-thread form in flight (32 a thread, all issued first, on
+// clamped indices); the four chunk groups' sums are added through LDS in a
+// fixed order.  The barriers wait for LDS only, so the partial loads stay in
+// flight while the chunk weights are formed.
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_merge_wide_kernel(AttnArgs a) {
+    if (a.qrows) attn_query_row(a, true);
+    constexpr int CG = 4, MR = 32;
+    __shared__ float fw[CG * MR];
+    __shared__ float redm[16], redl[16];
+    __shared__ __align__(16) float po[CG][256];
+    __shared__ __align__(16) float mo[256];
+    const int h = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x, c = tid >> 8, t = tid & 255;
+    const int G = a.G;
+    const float* ph = a.part + (size_t)h * G * (HD + 2);
+    const int dd = slice * 256 + t;
+    const float* pd = ph + dd;
+    float v[MR];
+#pragma unroll
+    for (int u = 0; u < MR; u++) v[u] = pd[(size_t)min(c + CG * u, G - 1) * (HD + 2)];
+    const int gi = min(tid, G - 1);
+    const float mr = ph[(size_t)gi * (HD + 2) + HD], lr = ph[(size_t)gi * (HD + 2) + HD + 1];
+    const float mg = tid < G ? mr : -INFINITY, lg = tid < G ? lr : 0.0f;
+    const float wm = wave_max(mg);
+    if ((tid & 63) == 0) redm[tid >> 6] = wm;
+    lds_sync();
+    float M = redm[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) M = fmaxf(M, redm[i]);
+    const float f = tid < G && lg > 0.0f ? expf(mg - M) : 0.0f;
+    if (tid < CG * MR) fw[tid] = f;
+    const float wl = wave_sum(lg * f);
+    if ((tid & 63) == 0) redl[tid >> 6] = wl;
+    lds_sync();
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) L += redl[i];
+    float o = 0.0f;
+#pragma unroll
+    for (int u = 0; u < MR; u++) o = c + CG * u < G ? __builtin_fmaf(v[u], fw[c + CG * u], o) : o;
+    po[c][t] = o;
+    lds_sync();
+    if (c == 0) {
+        const float sum = (po[0][t] + po[1][t]) + (po[2][t] + po[3][t]);
+        const float r = L > 0.0f ? sum / L : 0.0f;
+        a.out[(size_t)h * HD + dd] = r;
+        mo[t] = r;
+    }
+    if (a.q8) {
+        lds_sync();
+        if (tid < 64) {
+            const float4 f4 = reinterpret_cast<const float4*>(mo)[tid];
+            const float v4[4] = {f4.x, f4.y, f4.z, f4.w};
+            quantize_block_wave(v4, tid, a.q8, a.n_heads * HD / 256, h * (HD / 256) + slice);
+        }
+    }
+}
+
 // ---- query rows of a prompt chunk on the matrix cores ---------------------
 // The same partials as attn_chunk_kernel's query-row mode (one (o, max, sum)
 // per row, q head and chunk, merged by attn_merge_kernel), for 16 query rows
@@ -1558,6 +1618,7 @@ template <int HD>
 void launch_merge(const AttnArgs& a, const dim3& grid) {
     if (a.G <= 16) hipLaunchKernelGGL((attn_merge_kernel<HD, 16>), grid, dim3(256), 0, g4_stream(), a);
     else if (a.G <= 32) hipLaunchKernelGGL((attn_merge_kernel<HD, 32>), grid, dim3(256), 0, g4_stream(), a);
+    else if (a.G <= 128) hipLaunchKernelGGL((attn_merge_wide_kernel<HD>), grid, dim3(1024), 0, g4_stream(), a);
     else hipLaunchKernelGGL((attn_merge_kernel<HD, 128>), grid, dim3(256), 0, g4_stream(), a);
 }
 
