@@ -658,7 +658,7 @@ def _attn_chunks(cap: int) -> int:
     return G
 
 
-ATTN_KERNEL = "attn_chunk_kernel + attn_merge_kernel (global T=32768, hd 256)"
+ATTN_KERNEL = "attn_chunk_kernel + attn_merge_wide_kernel (global T=32768, hd 256)"
 
 
 def bench_attn(lib, g4, synth, args):
