@@ -637,7 +637,25 @@ def _gate_up_roofline(lib, g4, synth, n_launch: int = 200):
     per = ms / 1e3 / n_launch
     algo = 2 * g_raw.nbytes + lib.L.g4_q8K_bytes(n) + 4 * d
     name = "gemv_q45_stream_kernel<gate|up, GELU> 2x10240x2560 Q4_K"
-    return dict(roofline(algo, per, name), kernel=name, bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
+    res = dict(roofline(algo, per, name), kernel=name, bytes_per_launch=algo, us_per_launch=round(per * 1e6, 3))
+
+    # the same GEMV as the decode step runs it: the post-attention residual
+    # step, ffn_norm and Q8_K as every workgroup's prologue (g4_mm_residual_q8)
+    vecs = [g4.DBuf.from_array(lib, rng.standard_normal(n).astype(np.float32)) for _ in range(4)]
+    xr, yr, wp, wn = vecs
+    xo = g4.DBuf(lib, 4 * n)
+
+    def step_pro(i):
+        L.g4_mm_residual_q8(hb.ptr, gs[i % ncp].ptr, us[i % ncp].ptr, n, d, g4.Q4_K, None, xr.ptr, xo.ptr, yr.ptr,
+                            wp.ptr, None, wn.ptr, None, None, 0, 1e-6)
+    ms = _time_steps(lib, step_pro, A)
+    per_p = ms / 1e3 / n_launch
+    algo_p = 2 * g_raw.nbytes + 5 * 4 * n + 4 * d
+    rp = roofline(algo_p, per_p, "")
+    res["in_step"] = {"kernel": "gemv_q45_stream_kernel<gate|up, GELU, residual prologue> 2x10240x2560 Q4_K",
+                      "achieved": rp["achieved"], "frac": rp["frac"], "bytes_per_launch": algo_p,
+                      "us_per_launch": round(per_p * 1e6, 3)}
+    return res
 
 
 # ISWA decode attention (8 q / 2 kv heads): (name, positions read, head_dim,
